@@ -1,0 +1,76 @@
+"""Loader for the gfx950 Weaver library (``libaether_weaver.so``).
+
+The reference loads its kernels from a metallib whose path build.rs exports
+(``WeaverEngine::new(metallib_path)``, nexus-core/src/weaver.rs:85-95,
+build.rs:75).  Here the kernels live in a shared library built in-tree by
+``aether_nexus_amd.build``; its path can be overridden with ``AETHER_WEAVER_LIB``.
+A missing library is an error: there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+LIB_NAME = "libaether_weaver.so"
+DEFAULT_LIB = PKG_DIR / LIB_NAME
+
+_c_int = ctypes.c_int
+_vp = ctypes.c_void_p
+_sz = ctypes.c_size_t
+_u32 = ctypes.c_uint32
+_u64 = ctypes.c_uint64
+
+#: Every function declared in include/aether_weaver.h with its ctypes signature.
+SIGNATURES = {
+    "aw_abi_version": (_u32, []),
+    "aw_abi_struct_sizes": (None, [ctypes.POINTER(_sz)]),
+    "aw_status_string": (ctypes.c_char_p, [_c_int]),
+    "aw_validate_params": (_c_int, [_vp, _sz, _sz, _sz, _vp, _sz, _vp, _sz, _sz, _sz, ctypes.c_char_p, _sz]),
+    "aw_decode_plan": (_c_int, [_vp, _vp, ctypes.c_char_p, _sz]),
+    "aw_engine_create": (_c_int, [_c_int, ctypes.POINTER(_vp)]),
+    "aw_engine_destroy": (None, [_vp]),
+    "aw_engine_last_error": (ctypes.c_char_p, [_vp]),
+    "aw_engine_device_name": (ctypes.c_char_p, [_vp]),
+    "aw_engine_max_threads_per_threadgroup": (_u64, [_vp]),
+    "aw_decode": (_c_int, [_vp, _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _vp, _vp, _sz]),
+    "aw_decode_device": (_c_int, [_vp, _vp, _vp]),
+    "aw_engine_check_device_errors": (_c_int, [_vp, _vp]),
+    "aw_debug_gather_codes": (_c_int, [_vp, _vp, _sz, _vp, _u32, _u32, _vp, _vp, _vp, _vp]),
+    "aw_engine_set_profiling": (_c_int, [_vp, _c_int]),
+    "aw_engine_stage_stats": (_c_int, [_vp, _c_int, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_u64)]),
+    "aw_engine_reset_stage_stats": (_c_int, [_vp]),
+}
+
+_cache: dict[str, ctypes.CDLL] = {}
+
+
+def lib_path(path: str | os.PathLike | None = None) -> Path:
+    if path is not None:
+        return Path(path)
+    env = os.environ.get("AETHER_WEAVER_LIB")
+    return Path(env) if env else DEFAULT_LIB
+
+
+def load(path: str | os.PathLike | None = None) -> ctypes.CDLL:
+    """Load the library and declare every exported signature.
+
+    Raises ``FileNotFoundError`` when the library was not built and ``OSError``
+    when it cannot be loaded, like ``new_library_with_file`` failing in the
+    reference (weaver.rs:89)."""
+    p = lib_path(path).resolve()
+    key = str(p)
+    if key in _cache:
+        return _cache[key]
+    if not p.is_file():
+        raise FileNotFoundError(
+            f"{p} not found: build it with `python -c 'import __graft_entry__ as g; g.build()'` "
+            "(hipcc --offload-arch=gfx950); there is no CPU fallback")
+    lib = ctypes.CDLL(key)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _cache[key] = lib
+    return lib

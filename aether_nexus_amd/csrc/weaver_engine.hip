@@ -1,0 +1,865 @@
+// weaver_engine.hip — C ABI of the gfx950 Weaver decode library.
+//
+// Replaces WeaverEngine (nexus-core/src/weaver.rs:31-322): engine creation,
+// the reference-compatible host-slice decode, plus a device-resident batched
+// entry point.  Kernels live in weaver_kernels.hpp.  There is no CPU fallback:
+// without a gfx950 device every compute entry point returns an error.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/aether_weaver.h"
+#include "weaver_kernels.hpp"
+
+static_assert(sizeof(aw_sparse_code) == 16, "SparseCode is 16 bytes (types.rs:227)");
+static_assert(sizeof(aw_weaver_params) == 48, "WeaverParams is 12 x u32 (types.rs:351-374)");
+static_assert(offsetof(aw_weaver_params, hot_count) == 20, "WeaverParams field order");
+static_assert(offsetof(aw_weaver_params, sparsity_k) == 32, "WeaverParams field order");
+
+namespace {
+
+constexpr uint32_t kBlock = aw::kBlockTokens;
+constexpr size_t kAlign = 256;
+
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+uint32_t cdiv(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) / b); }
+
+void put_msg(char* msg, size_t len, const char* fmt, ...) {
+    if (!msg || !len) return;
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(msg, len, fmt, ap);
+    va_end(ap);
+}
+
+struct DevBuf {
+    void* ptr = nullptr;
+    size_t cap = 0;
+};
+
+// Grow-only device buffer (weaver.rs:252-255 reallocates only on overflow).
+int ensure(DevBuf& b, size_t bytes, std::string& err) {
+    if (bytes <= b.cap && b.ptr) return AW_OK;
+    if (b.ptr) (void)hipFree(b.ptr);
+    b.ptr = nullptr;
+    b.cap = 0;
+    size_t want = std::max<size_t>(align_up(bytes, kAlign), kAlign);
+    hipError_t e = hipMalloc(&b.ptr, want);
+    if (e != hipSuccess) {
+        err = std::string("hipMalloc(") + std::to_string(want) + ") failed: " + hipGetErrorString(e);
+        b.ptr = nullptr;
+        return AW_E_HIP;
+    }
+    b.cap = want;
+    return AW_OK;
+}
+
+// Workspace sub-allocation offsets for one request.
+struct Layout {
+    aw_decode_plan_info info{};
+    uint32_t rc = 4;       // cold rows per work-group
+    uint32_t n_chunks = 1; // ceil(R / rc)
+    uint32_t n_ar = 1;     // atom ranges of the finish
+    uint32_t atoms_per_range = 0;
+    uint32_t tiles_per_group = 0, rows_per_group = 0, n_groups = 0;
+    size_t off_ql = 0, off_hm = 0, off_hl = 0, off_ho = 0;
+    size_t off_cm = 0, off_cl = 0, off_ca = 0, off_cw = 0, off_ocp = 0;
+};
+
+bool supported_head_dim(uint32_t d) { return d == 64 || d == 128; }
+
+// Largest cold row chunk (1, 2 or 4) whose LDS tables fit.
+uint32_t pick_rc(uint32_t R, uint32_t A, size_t max_lds) {
+    uint32_t rc = R >= 4 ? 4 : (R >= 2 ? 2 : 1);
+    while (rc > 1 && aw::cold_smem_bytes(A, (int)rc) > max_lds) rc /= 2;
+    return rc;
+}
+
+int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, Layout* L, char* msg, size_t mlen) {
+    if (!d) {
+        put_msg(msg, mlen, "null descriptor");
+        return AW_E_INVALID_ARG;
+    }
+    if (d->layers == 0 || d->batch == 0 || d->queries == 0) {
+        put_msg(msg, mlen, "layers, batch and queries must be >= 1");
+        return AW_E_INVALID_ARG;
+    }
+    if (d->kv_heads == 0 || d->q_heads == 0 || d->q_heads % d->kv_heads) {
+        put_msg(msg, mlen, "q_heads (%u) must be a positive multiple of kv_heads (%u)", d->q_heads, d->kv_heads);
+        return AW_E_INVALID_ARG;
+    }
+    if (!supported_head_dim(d->head_dim)) {
+        put_msg(msg, mlen, "head_dim %u unsupported (64 or 128)", d->head_dim);
+        return AW_E_UNSUPPORTED;
+    }
+    const uint32_t G = d->q_heads / d->kv_heads;
+    const uint64_t R64 = (uint64_t)G * d->queries;
+    if (R64 > 64) {
+        put_msg(msg, mlen, "gqa_group*queries = %llu exceeds 64 query rows per kv head",
+                (unsigned long long)R64);
+        return AW_E_UNSUPPORTED;
+    }
+    const uint32_t R = (uint32_t)R64;
+    if (d->refs_stride < (uint64_t)d->hot_count + d->cold_count) {
+        put_msg(msg, mlen, "refs_stride %u < hot_count + cold_count", d->refs_stride);
+        return AW_E_INVALID_ARG;
+    }
+    if (!(d->scale == d->scale) || std::isinf(d->scale)) {
+        put_msg(msg, mlen, "scale must be finite");
+        return AW_E_INVALID_ARG;
+    }
+    if (d->cold_count > 0) {
+        if (d->dict_size == 0 || d->dict_size > 65536 || d->dict_size % 16) {
+            put_msg(msg, mlen, "dict_size %u must be a multiple of 16 in [16, 65536]", d->dict_size);
+            return AW_E_UNSUPPORTED;
+        }
+        if (d->dict_heads != 1 && d->dict_heads != d->kv_heads) {
+            put_msg(msg, mlen, "dict_heads must be 1 (shared) or kv_heads");
+            return AW_E_INVALID_ARG;
+        }
+    }
+    const uint64_t n_lbg = (uint64_t)d->layers * d->batch * d->kv_heads;
+    const uint32_t HD = d->head_dim, A = d->dict_size;
+    Layout& o = *L;
+    o = Layout{};
+    o.info.rows_per_kv_head = R;
+    o.info.computes_q_latent = (d->cold_count > 0 && d->q_latent == nullptr) ? 1u : 0u;
+
+    // Hot: ~8 waves per CU, >= 64 tokens per wave, splits <= kMaxSplits.
+    if (d->hot_count > 0) {
+        const uint64_t n_tok = (uint64_t)d->hot_count * kBlock;
+        uint64_t want = cdiv((uint64_t)n_cu * 8, n_lbg);
+        uint64_t cap = std::max<uint64_t>(1, cdiv(n_tok, 64));
+        uint64_t S = std::max<uint64_t>(1, std::min<uint64_t>({want, cap, (uint64_t)aw::kMaxSplits}));
+        uint64_t tps = align_up(cdiv(n_tok, S), 32);
+        o.info.hot_tokens_per_split = (uint32_t)tps;
+        o.info.hot_splits = cdiv(n_tok, tps);
+    }
+    // Cold: one work-group per CU at a time (LDS bound); >= 1024 tokens per split.
+    if (d->cold_count > 0) {
+        o.rc = pick_rc(R, A, max_lds);
+        if (aw::cold_smem_bytes(A, (int)o.rc) > max_lds) {
+            put_msg(msg, mlen, "dict_size %u needs %zu bytes of LDS, device allows %zu", A,
+                    aw::cold_smem_bytes(A, (int)o.rc), max_lds);
+            return AW_E_UNSUPPORTED;
+        }
+        o.n_chunks = cdiv(R, o.rc);
+        const uint64_t n_tok = (uint64_t)d->cold_count * kBlock;
+        const uint64_t items = n_lbg * o.n_chunks;
+        uint64_t want = cdiv((uint64_t)n_cu * 2, items);
+        uint64_t cap = std::max<uint64_t>(1, cdiv(n_tok, 1024));
+        uint64_t S = std::max<uint64_t>(1, std::min<uint64_t>({want, cap, (uint64_t)aw::kMaxSplits}));
+        uint64_t tps = align_up(cdiv(n_tok, S), 16);
+        o.info.cold_tokens_per_split = (uint32_t)tps;
+        o.info.cold_splits = cdiv(n_tok, tps);
+        o.info.cold_row_chunk = o.rc;
+        // Finish tiles: groups of rows that share one dictionary.
+        const uint32_t dh = d->dict_heads;
+        const uint32_t hg = dh == 1 ? d->kv_heads : 1;
+        o.rows_per_group = d->batch * hg * R;
+        o.tiles_per_group = cdiv(o.rows_per_group, 16);
+        o.n_groups = d->layers * dh;
+        const uint64_t tiles = (uint64_t)o.tiles_per_group * o.n_groups;
+        uint32_t n_ar = 1;
+        if (tiles < (uint64_t)n_cu / 2) n_ar = (uint32_t)std::min<uint64_t>(cdiv(n_cu, tiles), cdiv(A, 128));
+        o.atoms_per_range = (uint32_t)align_up(cdiv(A, n_ar), 32);
+        o.n_ar = cdiv(A, o.atoms_per_range);
+    }
+
+    // Workspace layout.
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        size_t at = off;
+        off = align_up(off + bytes, kAlign);
+        return at;
+    };
+    if (o.info.computes_q_latent) o.off_ql = take(n_lbg * A * R * 2);
+    if (o.info.hot_splits) {
+        const uint64_t n = n_lbg * o.info.hot_splits * R;
+        o.off_hm = take(n * 4);
+        o.off_hl = take(n * 4);
+        o.off_ho = take(n * HD * 4);
+    }
+    if (o.info.cold_splits) {
+        const uint64_t n = n_lbg * o.info.cold_splits * R;
+        o.off_cm = take(n * 4);
+        o.off_cl = take(n * 4);
+        o.off_ca = take(n * 4);
+        o.off_cw = take(n * A * 4);
+        if (o.n_ar > 1) o.off_ocp = take(n_lbg * R * o.n_ar * HD * 4);
+    }
+    o.info.workspace_bytes = off;
+    return AW_OK;
+}
+
+} // namespace
+
+// ------------------------------------------------------------------ engine
+
+struct aw_engine {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::string name, last_error;
+    uint64_t max_threads = 0;
+    size_t max_lds = 0;
+    uint32_t n_cu = 0;
+    DevBuf q, ql, hot, cold, refs, dict, out; // aw_decode copies (weaver.rs:40-46)
+    DevBuf ws;                                // per-request scratch
+    uint32_t* err = nullptr;                  // device error word
+    bool profiling = false;
+    struct Pending {
+        int stage;
+        hipEvent_t a, b;
+    };
+    std::vector<Pending> pending;
+    std::vector<hipEvent_t> free_events;
+    double stage_ms[AW_STAGE_COUNT] = {};
+    uint64_t stage_n[AW_STAGE_COUNT] = {};
+};
+
+namespace {
+
+int fail(aw_engine* e, int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    if (e) e->last_error = buf;
+    return code;
+}
+
+int hip_fail(aw_engine* e, hipError_t err, const char* what) {
+    return fail(e, AW_E_HIP, "%s: %s", what, hipGetErrorString(err));
+}
+
+#define AW_HIP(e, call)                                              \
+    do {                                                             \
+        hipError_t _err = (call);                                    \
+        if (_err != hipSuccess) return hip_fail((e), _err, #call);   \
+    } while (0)
+
+hipEvent_t take_event(aw_engine* e) {
+    if (!e->free_events.empty()) {
+        hipEvent_t ev = e->free_events.back();
+        e->free_events.pop_back();
+        return ev;
+    }
+    hipEvent_t ev = nullptr;
+    if (hipEventCreate(&ev) != hipSuccess) return nullptr;
+    return ev;
+}
+
+// Resolve finished event pairs into the per-stage totals.
+void drain_events(aw_engine* e) {
+    for (auto& p : e->pending) {
+        float ms = 0.0f;
+        if (hipEventSynchronize(p.b) == hipSuccess && hipEventElapsedTime(&ms, p.a, p.b) == hipSuccess) {
+            e->stage_ms[p.stage] += ms;
+            e->stage_n[p.stage] += 1;
+        }
+        e->free_events.push_back(p.a);
+        e->free_events.push_back(p.b);
+    }
+    e->pending.clear();
+}
+
+struct StageTimer {
+    aw_engine* e;
+    int stage;
+    hipStream_t s;
+    hipEvent_t a = nullptr, b = nullptr;
+    StageTimer(aw_engine* e_, int st, hipStream_t s_) : e(e_), stage(st), s(s_) {
+        if (!e->profiling) return;
+        if (e->pending.size() > 8192) drain_events(e);
+        a = take_event(e);
+        b = take_event(e);
+        if (a && b) (void)hipEventRecord(a, s);
+    }
+    ~StageTimer() {
+        if (!a || !b) return;
+        (void)hipEventRecord(b, s);
+        e->pending.push_back({stage, a, b});
+    }
+};
+
+template <int HD>
+int launch_project(aw_engine* e, const aw_decode_desc* d, const Layout& o, uint16_t* ql, hipStream_t st) {
+    aw::ProjArgs a{};
+    a.q = d->q;
+    a.dict = d->dict;
+    a.ql = ql;
+    a.batch = d->batch;
+    a.queries = d->queries;
+    a.q_heads = d->q_heads;
+    a.kv_heads = d->kv_heads;
+    a.gqa = d->q_heads / d->kv_heads;
+    a.rows_r = o.info.rows_per_kv_head;
+    a.dict_size = d->dict_size;
+    a.dict_heads = d->dict_heads;
+    a.rows_per_group = d->batch * d->queries * (d->dict_heads == 1 ? d->q_heads : a.gqa);
+    a.dict_layer = (uint64_t)d->dict_heads * d->dict_size * HD;
+    const uint32_t rows = a.rows_per_group;
+    StageTimer t(e, AW_STAGE_PROJECT, st);
+    const dim3 block(64);
+    const uint32_t gz = d->layers * d->dict_heads;
+    if (rows <= 16) {
+        hipLaunchKernelGGL((aw::project_kernel<HD, 1, 1>), dim3(cdiv(d->dict_size, 16), cdiv(rows, 16), gz), block,
+                           0, st, a);
+    } else if (rows <= 32) {
+        hipLaunchKernelGGL((aw::project_kernel<HD, 2, 1>), dim3(cdiv(d->dict_size, 16), cdiv(rows, 32), gz), block,
+                           0, st, a);
+    } else if (rows <= 512) {
+        hipLaunchKernelGGL((aw::project_kernel<HD, 4, 2>), dim3(cdiv(d->dict_size, 32), cdiv(rows, 64), gz), block,
+                           0, st, a);
+    } else {
+        hipLaunchKernelGGL((aw::project_kernel<HD, 4, 4>), dim3(cdiv(d->dict_size, 64), cdiv(rows, 64), gz), block,
+                           0, st, a);
+    }
+    AW_HIP(e, hipGetLastError());
+    return AW_OK;
+}
+
+template <int HD>
+int launch_hot(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* ws, hipStream_t st) {
+    aw::HotArgs a{};
+    a.q = d->q;
+    a.hot_k = d->hot_k;
+    a.hot_v = d->hot_v;
+    a.refs = d->refs;
+    a.seq_hot = d->seq_hot;
+    a.part_m = (float*)(ws + o.off_hm);
+    a.part_l = (float*)(ws + o.off_hl);
+    a.part_o = (float*)(ws + o.off_ho);
+    a.err = e->err;
+    a.batch = d->batch;
+    a.queries = d->queries;
+    a.q_heads = d->q_heads;
+    a.kv_heads = d->kv_heads;
+    a.gqa = d->q_heads / d->kv_heads;
+    a.rows_r = o.info.rows_per_kv_head;
+    a.hot_count = d->hot_count;
+    a.refs_stride = d->refs_stride;
+    a.splits = o.info.hot_splits;
+    a.tokens_per_split = o.info.hot_tokens_per_split;
+    a.causal = (d->flags & AW_F_CAUSAL) ? 1u : 0u;
+    a.scale_log2 = d->scale * aw::kLog2e;
+    a.hot_blocks = d->hot_blocks;
+    a.hot_layer = d->hot_blocks * kBlock * d->kv_heads * HD;
+    a.refs_layer = (uint64_t)d->batch * d->refs_stride;
+    const uint64_t grid = (uint64_t)d->layers * d->batch * d->kv_heads * a.splits;
+    if (grid > 0x7FFFFFFFull) return fail(e, AW_E_UNSUPPORTED, "hot grid too large");
+    StageTimer t(e, AW_STAGE_HOT, st);
+    const uint32_t R = a.rows_r;
+    if (R <= 16)
+        hipLaunchKernelGGL((aw::hot_kernel<HD, 1>), dim3((uint32_t)grid), dim3(64), 0, st, a);
+    else if (R <= 32)
+        hipLaunchKernelGGL((aw::hot_kernel<HD, 2>), dim3((uint32_t)grid), dim3(64), 0, st, a);
+    else
+        hipLaunchKernelGGL((aw::hot_kernel<HD, 4>), dim3((uint32_t)grid), dim3(64), 0, st, a);
+    AW_HIP(e, hipGetLastError());
+    return AW_OK;
+}
+
+constexpr int kColdCPT = 4;
+
+int launch_cold(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* ws, hipStream_t st) {
+    aw::ColdArgs a{};
+    const uint32_t HD = d->head_dim, A = d->dict_size, G = d->q_heads / d->kv_heads;
+    const uint32_t R = o.info.rows_per_kv_head;
+    a.cold = (const aw::uint4_t*)d->cold;
+    a.refs = d->refs;
+    a.seq_cold = d->seq_cold;
+    a.part_m = (float*)(ws + o.off_cm);
+    a.part_l = (float*)(ws + o.off_cl);
+    a.part_amax = (float*)(ws + o.off_ca);
+    a.part_w = (float*)(ws + o.off_cw);
+    a.err = e->err;
+    a.batch = d->batch;
+    a.kv_heads = d->kv_heads;
+    a.gqa = G;
+    a.rows_r = R;
+    a.hot_count = d->hot_count;
+    a.cold_count = d->cold_count;
+    a.refs_stride = d->refs_stride;
+    a.dict_size = A;
+    a.splits = o.info.cold_splits;
+    a.tokens_per_split = o.info.cold_tokens_per_split;
+    a.n_chunks = o.n_chunks;
+    a.n_units = (uint32_t)((uint64_t)d->layers * d->batch * o.n_chunks * a.splits);
+    a.scale_log2 = d->scale * aw::kLog2e;
+    a.cold_blocks = d->cold_blocks;
+    a.cold_layer = d->cold_blocks * kBlock * d->kv_heads;
+    a.refs_layer = (uint64_t)d->batch * d->refs_stride;
+    if (o.info.computes_q_latent) { // [lbg][A][R]
+        a.ql = (const uint16_t*)(ws + o.off_ql);
+        a.s_lb = (uint64_t)d->kv_heads * A * R;
+        a.s_g = (uint64_t)A * R;
+        a.s_q = G;
+        a.s_j = 1;
+        a.s_a = R;
+    } else { // caller's [L][B][Q][Hq][A]
+        a.ql = d->q_latent;
+        a.s_lb = (uint64_t)d->queries * d->q_heads * A;
+        a.s_g = (uint64_t)G * A;
+        a.s_q = (uint64_t)d->q_heads * A;
+        a.s_j = A;
+        a.s_a = 1;
+    }
+    (void)HD;
+    const uint64_t grid = (uint64_t)cdiv(a.n_units, 8) * 8 * d->kv_heads;
+    if (grid > 0x7FFFFFFFull) return fail(e, AW_E_UNSUPPORTED, "cold grid too large");
+    const size_t smem = aw::cold_smem_bytes(A, (int)o.rc);
+    StageTimer t(e, AW_STAGE_COLD, st);
+    switch (o.rc) {
+    case 4:
+        hipLaunchKernelGGL((aw::cold_kernel<4, kColdCPT>), dim3((uint32_t)grid), dim3(aw::kColdThreads), smem, st, a);
+        break;
+    case 2:
+        hipLaunchKernelGGL((aw::cold_kernel<2, kColdCPT>), dim3((uint32_t)grid), dim3(aw::kColdThreads), smem, st, a);
+        break;
+    default:
+        hipLaunchKernelGGL((aw::cold_kernel<1, kColdCPT>), dim3((uint32_t)grid), dim3(aw::kColdThreads), smem, st, a);
+        break;
+    }
+    AW_HIP(e, hipGetLastError());
+    return AW_OK;
+}
+
+template <int HD>
+int launch_finish(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* ws, hipStream_t st) {
+    aw::FinishArgs a{};
+    a.dict = d->dict;
+    a.cold_m = (const float*)(ws + o.off_cm);
+    a.cold_l = (const float*)(ws + o.off_cl);
+    a.cold_w = (const float*)(ws + o.off_cw);
+    a.cold_amax = (const float*)(ws + o.off_ca);
+    if (o.info.hot_splits) {
+        a.hot_m = (const float*)(ws + o.off_hm);
+        a.hot_l = (const float*)(ws + o.off_hl);
+        a.hot_o = (const float*)(ws + o.off_ho);
+    }
+    a.ocp = o.n_ar > 1 ? (float*)(ws + o.off_ocp) : nullptr;
+    a.out = d->out;
+    a.batch = d->batch;
+    a.queries = d->queries;
+    a.q_heads = d->q_heads;
+    a.kv_heads = d->kv_heads;
+    a.gqa = d->q_heads / d->kv_heads;
+    a.rows_r = o.info.rows_per_kv_head;
+    a.dict_size = d->dict_size;
+    a.dict_heads = d->dict_heads;
+    a.rows_per_group = o.rows_per_group;
+    a.tiles_per_group = o.tiles_per_group;
+    a.cold_splits = o.info.cold_splits;
+    a.hot_splits = o.info.hot_splits;
+    a.n_ar = o.n_ar;
+    a.atoms_per_range = o.atoms_per_range;
+    a.dict_layer = (uint64_t)d->dict_heads * d->dict_size * HD;
+    const uint64_t gx = (uint64_t)o.tiles_per_group * o.n_groups;
+    if (gx > 0x7FFFFFFFull) return fail(e, AW_E_UNSUPPORTED, "finish grid too large");
+    StageTimer t(e, AW_STAGE_FINISH, st);
+    hipLaunchKernelGGL((aw::finish_kernel<HD>), dim3((uint32_t)gx, o.n_ar), dim3(64 * aw::kFinishWaves), 0, st, a);
+    AW_HIP(e, hipGetLastError());
+    return AW_OK;
+}
+
+template <int HD>
+int launch_merge(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* ws, hipStream_t st) {
+    aw::MergeArgs a{};
+    const bool cold = o.info.cold_splits > 0;
+    a.cold_m = cold ? (const float*)(ws + o.off_cm) : nullptr;
+    a.cold_l = cold ? (const float*)(ws + o.off_cl) : nullptr;
+    a.cold_amax = cold ? (const float*)(ws + o.off_ca) : nullptr;
+    a.ocp = cold ? (const float*)(ws + o.off_ocp) : nullptr;
+    if (o.info.hot_splits) {
+        a.hot_m = (const float*)(ws + o.off_hm);
+        a.hot_l = (const float*)(ws + o.off_hl);
+        a.hot_o = (const float*)(ws + o.off_ho);
+    }
+    a.out = d->out;
+    a.batch = d->batch;
+    a.queries = d->queries;
+    a.q_heads = d->q_heads;
+    a.kv_heads = d->kv_heads;
+    a.gqa = d->q_heads / d->kv_heads;
+    a.rows_r = o.info.rows_per_kv_head;
+    a.cold_splits = o.info.cold_splits;
+    a.hot_splits = o.info.hot_splits;
+    a.n_ar = o.n_ar;
+    a.total_rows = (uint64_t)d->layers * d->batch * d->kv_heads * a.rows_r;
+    const uint64_t gx = cdiv(a.total_rows, 16);
+    if (gx > 0x7FFFFFFFull) return fail(e, AW_E_UNSUPPORTED, "merge grid too large");
+    StageTimer t(e, AW_STAGE_MERGE, st);
+    hipLaunchKernelGGL((aw::merge_kernel<HD>), dim3((uint32_t)gx), dim3(256), 0, st, a);
+    AW_HIP(e, hipGetLastError());
+    return AW_OK;
+}
+
+template <int HD>
+int run_pipeline(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* ws, hipStream_t st) {
+    int rc = AW_OK;
+    const bool cold = o.info.cold_splits > 0;
+    if (cold && o.info.computes_q_latent)
+        if ((rc = launch_project<HD>(e, d, o, (uint16_t*)(ws + o.off_ql), st))) return rc;
+    if (o.info.hot_splits)
+        if ((rc = launch_hot<HD>(e, d, o, ws, st))) return rc;
+    if (cold) {
+        if ((rc = launch_cold(e, d, o, ws, st))) return rc;
+        if ((rc = launch_finish<HD>(e, d, o, ws, st))) return rc;
+        if (o.n_ar > 1)
+            if ((rc = launch_merge<HD>(e, d, o, ws, st))) return rc;
+    } else {
+        if ((rc = launch_merge<HD>(e, d, o, ws, st))) return rc;
+    }
+    return AW_OK;
+}
+
+int decode_device(aw_engine* e, const aw_decode_desc* d, hipStream_t st) {
+    Layout o;
+    char msg[256] = {0};
+    int rc = plan(d, e->max_lds, e->n_cu, &o, msg, sizeof msg);
+    if (rc) return fail(e, rc, "%s", msg);
+    if (!d->out || !d->q) return fail(e, AW_E_INVALID_ARG, "q and out are required");
+    if (d->hot_count && (!d->hot_k || !d->refs)) return fail(e, AW_E_INVALID_ARG, "hot_k and refs are required");
+    if (d->cold_count && (!d->cold || !d->refs || !d->dict))
+        return fail(e, AW_E_INVALID_ARG, "cold, refs and dict are required");
+    if (d->cold_count && ((uintptr_t)d->cold & 15u))
+        return fail(e, AW_E_ALIGN, "cold pool pointer is not 16-byte aligned");
+    if ((rc = ensure(e->ws, o.info.workspace_bytes, e->last_error))) return rc;
+    char* ws = (char*)e->ws.ptr;
+    return d->head_dim == 64 ? run_pipeline<64>(e, d, o, ws, st) : run_pipeline<128>(e, d, o, ws, st);
+}
+
+template <typename F>
+int check_kernel(aw_engine* e, F* fn, const char* name) {
+    hipFuncAttributes attr;
+    hipError_t err = hipFuncGetAttributes(&attr, (const void*)fn);
+    if (err != hipSuccess)
+        return fail(e, AW_E_LOAD, "kernel %s has no code object for this device: %s", name, hipGetErrorString(err));
+    return AW_OK;
+}
+
+} // namespace
+
+// ------------------------------------------------------------- C ABI
+
+extern "C" {
+
+uint32_t aw_abi_version(void) { return AW_ABI_VERSION; }
+
+void aw_abi_struct_sizes(size_t sizes[4]) {
+    sizes[0] = sizeof(aw_sparse_code);
+    sizes[1] = sizeof(aw_weaver_params);
+    sizes[2] = sizeof(aw_decode_desc);
+    sizes[3] = sizeof(aw_decode_plan_info);
+}
+
+const char* aw_status_string(int status) {
+    switch (status) {
+    case AW_OK: return "ok";
+    case AW_E_INVALID_ARG: return "invalid argument";
+    case AW_E_ALIGN: return "misaligned SparseCode pointer";
+    case AW_E_OOB: return "block ref or atom index out of range";
+    case AW_E_HIP: return "HIP runtime error";
+    case AW_E_LOAD: return "kernels not available for this device";
+    case AW_E_UNSUPPORTED: return "unsupported request";
+    default: return "unknown status";
+    }
+}
+
+int aw_validate_params(const aw_weaver_params* p, size_t n_q_exact, size_t n_q_latent, size_t n_hot_pool,
+                       const aw_sparse_code* cold_pool, size_t n_cold_pool, const uint32_t* loom_refs,
+                       size_t n_loom_refs, size_t n_dictionary, size_t n_out, char* msg, size_t mlen) {
+    if (!p) {
+        put_msg(msg, mlen, "null params");
+        return AW_E_INVALID_ARG;
+    }
+    if (p->block_size != kBlock) {
+        put_msg(msg, mlen, "block_size %u, only 16 is supported (ModelDims::BLOCK_SIZE)", p->block_size);
+        return AW_E_UNSUPPORTED;
+    }
+    if (p->sparsity_k != 4) {
+        put_msg(msg, mlen, "sparsity_k %u, a SparseCode holds exactly 4 terms", p->sparsity_k);
+        return AW_E_UNSUPPORTED;
+    }
+    if (p->kv_heads == 0 || p->gqa_group == 0 || (uint64_t)p->gqa_group * p->kv_heads != p->q_heads) {
+        put_msg(msg, mlen, "gqa_group (%u) * kv_heads (%u) != q_heads (%u)", p->gqa_group, p->kv_heads, p->q_heads);
+        return AW_E_INVALID_ARG;
+    }
+    if (!supported_head_dim(p->head_dim)) {
+        put_msg(msg, mlen, "head_dim %u unsupported (64 or 128)", p->head_dim);
+        return AW_E_UNSUPPORTED;
+    }
+    if (p->gqa_group > 64) {
+        put_msg(msg, mlen, "gqa_group %u exceeds 64", p->gqa_group);
+        return AW_E_UNSUPPORTED;
+    }
+    const uint64_t HD = p->head_dim, Hkv = p->kv_heads;
+    if (n_q_exact < (uint64_t)p->q_heads * HD) {
+        put_msg(msg, mlen, "q_exact holds %zu values, needs %llu", n_q_exact,
+                (unsigned long long)p->q_heads * HD);
+        return AW_E_INVALID_ARG;
+    }
+    if (n_out < (uint64_t)p->q_heads * HD) {
+        put_msg(msg, mlen, "output holds %zu values, needs %llu", n_out, (unsigned long long)p->q_heads * HD);
+        return AW_E_INVALID_ARG;
+    }
+    const uint64_t nrefs = (uint64_t)p->hot_count + p->cold_count;
+    if (n_loom_refs < nrefs || (nrefs && !loom_refs)) {
+        put_msg(msg, mlen, "loom_refs holds %zu refs, needs hot_count + cold_count = %llu", n_loom_refs,
+                (unsigned long long)nrefs);
+        return AW_E_INVALID_ARG;
+    }
+    const uint64_t hot_blocks = n_hot_pool / (kBlock * Hkv * HD);
+    for (uint32_t b = 0; b < p->hot_count; ++b) {
+        const uint32_t phys = loom_refs[b] & aw::kRefMask;
+        if (phys >= hot_blocks) {
+            put_msg(msg, mlen, "hot ref %u -> block %u, hot pool holds %llu blocks", b, phys,
+                    (unsigned long long)hot_blocks);
+            return AW_E_OOB;
+        }
+    }
+    if (p->cold_count) {
+        if (p->dict_size == 0 || p->dict_size > 65536 || p->dict_size % 16) {
+            put_msg(msg, mlen, "dict_size %u must be a multiple of 16 in [16, 65536]", p->dict_size);
+            return AW_E_UNSUPPORTED;
+        }
+        if (n_q_latent != 0 && n_q_latent < (uint64_t)p->q_heads * p->dict_size) {
+            put_msg(msg, mlen, "q_latent holds %zu values, needs %llu (or 0 to compute it)", n_q_latent,
+                    (unsigned long long)p->q_heads * p->dict_size);
+            return AW_E_INVALID_ARG;
+        }
+        if (n_dictionary < Hkv * p->dict_size * HD) {
+            put_msg(msg, mlen, "dictionary holds %zu values, needs kv_heads*dict_size*head_dim = %llu", n_dictionary,
+                    (unsigned long long)(Hkv * p->dict_size * HD));
+            return AW_E_INVALID_ARG;
+        }
+        if (!cold_pool) {
+            put_msg(msg, mlen, "cold pool is empty but cold_count = %u", p->cold_count);
+            return AW_E_INVALID_ARG;
+        }
+        if ((uintptr_t)cold_pool & 15u) {
+            put_msg(msg, mlen, "cold pool pointer is not 16-byte aligned");
+            return AW_E_ALIGN;
+        }
+        const uint64_t cold_blocks = n_cold_pool / (kBlock * Hkv);
+        for (uint32_t b = 0; b < p->cold_count; ++b) {
+            const uint32_t phys = loom_refs[p->hot_count + b] & aw::kRefMask;
+            if (phys >= cold_blocks) {
+                put_msg(msg, mlen, "cold ref %u -> block %u, cold pool holds %llu blocks", b, phys,
+                        (unsigned long long)cold_blocks);
+                return AW_E_OOB;
+            }
+            const aw_sparse_code* c = cold_pool + (uint64_t)phys * kBlock * Hkv;
+            for (uint64_t i = 0; i < kBlock * Hkv; ++i)
+                for (int k = 0; k < 4; ++k)
+                    if (c[i].indices[k] >= p->dict_size) {
+                        put_msg(msg, mlen, "cold block %u code %llu: atom index %u >= dict_size %u", phys,
+                                (unsigned long long)i, c[i].indices[k], p->dict_size);
+                        return AW_E_OOB;
+                    }
+        }
+    }
+    return AW_OK;
+}
+
+int aw_decode_plan(const aw_decode_desc* desc, aw_decode_plan_info* info, char* msg, size_t mlen) {
+    Layout o;
+    // Host-side planning assumes the MI355X limits: 160 KiB LDS per work-group, 256 CUs.
+    int rc = plan(desc, 160 * 1024, 256, &o, msg, mlen);
+    if (rc == AW_OK && info) *info = o.info;
+    return rc;
+}
+
+int aw_engine_create(int device, aw_engine** out) {
+    if (!out) return AW_E_INVALID_ARG;
+    *out = nullptr;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count == 0) return AW_E_HIP;
+    if (device < 0 || device >= count) return AW_E_INVALID_ARG;
+    aw_engine* e = new aw_engine();
+    e->device = device;
+    hipDeviceProp_t prop;
+    if (hipSetDevice(device) != hipSuccess || hipGetDeviceProperties(&prop, device) != hipSuccess) {
+        delete e;
+        return AW_E_HIP;
+    }
+    e->name = prop.name;
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        delete e;
+        return AW_E_LOAD;
+    }
+    e->max_threads = (uint64_t)prop.maxThreadsPerBlock;
+    e->max_lds = prop.sharedMemPerBlock;
+    e->n_cu = (uint32_t)prop.multiProcessorCount;
+    int rc = AW_OK;
+    if (!rc) rc = check_kernel(e, aw::hot_kernel<128, 1>, "hot_kernel");
+    if (!rc) rc = check_kernel(e, aw::cold_kernel<4, kColdCPT>, "cold_kernel");
+    if (!rc) rc = check_kernel(e, aw::finish_kernel<128>, "finish_kernel");
+    if (rc) {
+        delete e;
+        return rc;
+    }
+    // Let the cold kernel use the device's full LDS.
+    (void)hipFuncSetAttribute((const void*)aw::cold_kernel<4, kColdCPT>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                        (int)e->max_lds);
+    (void)hipFuncSetAttribute((const void*)aw::cold_kernel<2, kColdCPT>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                        (int)e->max_lds);
+    (void)hipFuncSetAttribute((const void*)aw::cold_kernel<1, kColdCPT>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                        (int)e->max_lds);
+    if (hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking) != hipSuccess ||
+        hipMalloc((void**)&e->err, 256) != hipSuccess || hipMemset(e->err, 0, 256) != hipSuccess) {
+        aw_engine_destroy(e);
+        return AW_E_HIP;
+    }
+    *out = e;
+    return AW_OK;
+}
+
+void aw_engine_destroy(aw_engine* e) {
+    if (!e) return;
+    (void)hipSetDevice(e->device);
+    if (e->stream) (void)hipStreamSynchronize(e->stream);
+    drain_events(e);
+    for (hipEvent_t ev : e->free_events) (void)hipEventDestroy(ev);
+    for (DevBuf* b : {&e->q, &e->ql, &e->hot, &e->cold, &e->refs, &e->dict, &e->out, &e->ws})
+        if (b->ptr) (void)hipFree(b->ptr);
+    if (e->err) (void)hipFree(e->err);
+    if (e->stream) (void)hipStreamDestroy(e->stream);
+    delete e;
+}
+
+const char* aw_engine_last_error(const aw_engine* e) { return e ? e->last_error.c_str() : "null engine"; }
+const char* aw_engine_device_name(const aw_engine* e) { return e ? e->name.c_str() : ""; }
+uint64_t aw_engine_max_threads_per_threadgroup(const aw_engine* e) { return e ? e->max_threads : 0; }
+
+int aw_decode(aw_engine* e, const uint16_t* q_exact, size_t n_q_exact, const uint16_t* q_latent, size_t n_q_latent,
+              const uint16_t* hot_pool, size_t n_hot_pool, const aw_sparse_code* cold_pool, size_t n_cold_pool,
+              const uint32_t* loom_refs, size_t n_loom_refs, const uint16_t* dictionary, size_t n_dictionary,
+              const aw_weaver_params* p, uint16_t* out, size_t n_out) {
+    if (!e) return AW_E_INVALID_ARG;
+    char msg[256] = {0};
+    int rc = aw_validate_params(p, n_q_exact, n_q_latent, n_hot_pool, cold_pool, n_cold_pool, loom_refs,
+                                n_loom_refs, n_dictionary, n_out, msg, sizeof msg);
+    if (rc) return fail(e, rc, "%s", msg);
+    if (!q_exact || !out) return fail(e, AW_E_INVALID_ARG, "q_exact and out are required");
+    AW_HIP(e, hipSetDevice(e->device));
+    const uint64_t HD = p->head_dim;
+    // Copy the slices into the persistent buffers (weaver.rs:155-196); empty slices are skipped.
+    auto fill = [&](DevBuf& b, const void* src, size_t bytes) -> int {
+        if (!bytes) return AW_OK;
+        int r = ensure(b, bytes, e->last_error);
+        if (r) return r;
+        AW_HIP(e, hipMemcpyAsync(b.ptr, src, bytes, hipMemcpyHostToDevice, e->stream));
+        return AW_OK;
+    };
+    const bool cold = p->cold_count > 0;
+    const bool hot = p->hot_count > 0;
+    if ((rc = fill(e->q, q_exact, (size_t)p->q_heads * HD * 2))) return rc;
+    if (cold && n_q_latent)
+        if ((rc = fill(e->ql, q_latent, (size_t)p->q_heads * p->dict_size * 2))) return rc;
+    if (hot && (rc = fill(e->hot, hot_pool, n_hot_pool * 2))) return rc;
+    if (cold && (rc = fill(e->cold, cold_pool, n_cold_pool * sizeof(aw_sparse_code)))) return rc;
+    if ((rc = fill(e->refs, loom_refs, ((size_t)p->hot_count + p->cold_count) * 4))) return rc;
+    if (cold && (rc = fill(e->dict, dictionary, (size_t)p->kv_heads * p->dict_size * HD * 2))) return rc;
+    if ((rc = ensure(e->out, (size_t)p->q_heads * HD * 2, e->last_error))) return rc;
+
+    aw_decode_desc d{};
+    d.layers = d.batch = d.queries = 1;
+    d.q_heads = p->q_heads;
+    d.kv_heads = p->kv_heads;
+    d.head_dim = p->head_dim;
+    d.dict_size = cold ? p->dict_size : 0;
+    d.dict_heads = p->kv_heads; // reference layout [kv_heads][dict_size][head_dim]
+    d.hot_count = p->hot_count;
+    d.cold_count = p->cold_count;
+    d.refs_stride = p->hot_count + p->cold_count;
+    d.flags = 0;
+    d.scale = 1.0f; // the reference applies no score scale
+    d.hot_blocks = hot ? n_hot_pool / (kBlock * p->kv_heads * HD) : 0;
+    d.cold_blocks = cold ? n_cold_pool / (kBlock * p->kv_heads) : 0;
+    d.q = (const uint16_t*)e->q.ptr;
+    d.q_latent = (cold && n_q_latent) ? (const uint16_t*)e->ql.ptr : nullptr;
+    d.hot_k = hot ? (const uint16_t*)e->hot.ptr : nullptr;
+    d.hot_v = nullptr;
+    d.cold = cold ? (const aw_sparse_code*)e->cold.ptr : nullptr;
+    d.refs = (const uint32_t*)e->refs.ptr;
+    d.dict = cold ? (const uint16_t*)e->dict.ptr : nullptr;
+    d.out = (uint16_t*)e->out.ptr;
+    if ((rc = decode_device(e, &d, e->stream))) return rc;
+    AW_HIP(e, hipMemcpyAsync(out, e->out.ptr, (size_t)p->q_heads * HD * 2, hipMemcpyDeviceToHost, e->stream));
+    AW_HIP(e, hipStreamSynchronize(e->stream)); // commit + wait_until_completed (weaver.rs:227-228)
+    return aw_engine_check_device_errors(e, e->stream);
+}
+
+int aw_decode_device(aw_engine* e, const aw_decode_desc* desc, void* stream) {
+    if (!e) return AW_E_INVALID_ARG;
+    AW_HIP(e, hipSetDevice(e->device));
+    hipStream_t st = stream ? (hipStream_t)stream : e->stream;
+    return decode_device(e, desc, st);
+}
+
+int aw_engine_check_device_errors(aw_engine* e, void* stream) {
+    if (!e) return AW_E_INVALID_ARG;
+    AW_HIP(e, hipSetDevice(e->device));
+    hipStream_t st = stream ? (hipStream_t)stream : e->stream;
+    uint32_t word = 0;
+    AW_HIP(e, hipMemcpyAsync(&word, e->err, 4, hipMemcpyDeviceToHost, st));
+    AW_HIP(e, hipStreamSynchronize(st));
+    if (!word) return AW_OK;
+    AW_HIP(e, hipMemsetAsync(e->err, 0, 4, st));
+    AW_HIP(e, hipStreamSynchronize(st));
+    return fail(e, AW_E_OOB, "device saw out-of-range input:%s%s%s (the affected tokens or terms were skipped)",
+                (word & aw::kErrHotRef) ? " hot block ref" : "", (word & aw::kErrColdRef) ? " cold block ref" : "",
+                (word & aw::kErrAtom) ? " atom index" : "");
+}
+
+int aw_debug_gather_codes(aw_engine* e, const aw_sparse_code* codes, size_t n, const uint16_t* dict,
+                          uint32_t dict_size, uint32_t head_dim, uint32_t* idx, float* coef, uint16_t* atoms,
+                          void* stream) {
+    if (!e) return AW_E_INVALID_ARG;
+    if (!n) return AW_OK;
+    if (!codes || !dict || !idx || !coef || !atoms || !head_dim || !dict_size)
+        return fail(e, AW_E_INVALID_ARG, "null pointer or zero size");
+    if ((uintptr_t)codes & 15u) return fail(e, AW_E_ALIGN, "codes pointer is not 16-byte aligned");
+    AW_HIP(e, hipSetDevice(e->device));
+    hipStream_t st = stream ? (hipStream_t)stream : e->stream;
+    const uint64_t threads = (uint64_t)n * 4;
+    hipLaunchKernelGGL(aw::gather_codes_kernel, dim3(cdiv(threads, 256)), dim3(256), 0, st,
+                       (const aw::uint4_t*)codes, (uint64_t)n, dict, dict_size, head_dim, idx, coef, atoms, e->err);
+    AW_HIP(e, hipGetLastError());
+    return AW_OK;
+}
+
+int aw_engine_set_profiling(aw_engine* e, int enable) {
+    if (!e) return AW_E_INVALID_ARG;
+    e->profiling = enable != 0;
+    return AW_OK;
+}
+
+int aw_engine_stage_stats(aw_engine* e, int stage, double* total_ms, uint64_t* launches) {
+    if (!e || stage < 0 || stage >= AW_STAGE_COUNT) return AW_E_INVALID_ARG;
+    drain_events(e);
+    if (total_ms) *total_ms = e->stage_ms[stage];
+    if (launches) *launches = e->stage_n[stage];
+    return AW_OK;
+}
+
+int aw_engine_reset_stage_stats(aw_engine* e) {
+    if (!e) return AW_E_INVALID_ARG;
+    drain_events(e);
+    for (int i = 0; i < AW_STAGE_COUNT; ++i) {
+        e->stage_ms[i] = 0;
+        e->stage_n[i] = 0;
+    }
+    return AW_OK;
+}
+
+} // extern "C"

@@ -1,0 +1,1005 @@
+// weaver_kernels.hpp — gfx950 (CDNA4) kernels of the Weaver decode path.
+//
+// The reference computes Weaver decode in one Metal kernel, one 32-thread
+// group per query head, walking every hot token and then every cold token
+// serially with an online softmax (nexus-core/src/weaver_kernel.metal:118-240).
+// Here the same math is split into stages shaped for MI355X:
+//
+//   project_kernel  q_latent = q . D^T on MFMA (v_mfma_f32_16x16x32_f16).
+//                   The identity the reference assumes for its q_latent input
+//                   (weaver_kernel.metal:184-190, docs/YELLOWPAPER.md:84-92).
+//   hot_kernel      exact attention over the f16 hot pool, split-K over the
+//                   token axis.  One wave owns one (sequence, kv head, token
+//                   range) and all G*Q query rows of that kv head, so each K/V
+//                   row is read from HBM once for the whole GQA group
+//                   (the reference re-reads it per query head).  S^T = K Q^T and
+//                   O^T += V^T P^T both run on MFMA; K == V unless a separate V
+//                   pool is given (weaver_kernel.metal:162-166).
+//   cold_kernel     attention on the SparseCodes without decompression: scores
+//                   from the LDS-resident q_latent table (metal:186-190), and
+//                   instead of rebuilding V per token (metal:206-219) the
+//                   softmax weight times each coefficient is accumulated into a
+//                   per-atom bin in LDS.  sum_t p_t V_t = sum_a bin[a] D[a].
+//   finish_kernel   bin . D on MFMA (fp32 bins split into two f16 terms),
+//                   optionally fused with the log-sum-exp merge.
+//   merge_kernel    log-sum-exp merge of hot and cold partials, f16 output
+//                   (metal:226-239: zero output when nothing is visible).
+//
+// Scores are carried in the log2 domain (score * scale * log2(e)) so every
+// exponential is one v_exp_f32.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace aw {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t uint4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t uint2_t __attribute__((ext_vector_type(2)));
+
+constexpr uint32_t kBlockTokens = 16;      // tokens per block (ModelDims::BLOCK_SIZE)
+constexpr uint32_t kRefMask = 0x7FFFFFFFu; // weaver_kernel.metal:145,174
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kColdThreads = 512;
+constexpr int kFinishWaves = 4;
+constexpr int kMaxSplits = 64;
+constexpr float kColdSlack = 12.0f; // log2 headroom of a cold work-group's running reference
+
+// Error bits written to the engine's device error word.
+constexpr uint32_t kErrHotRef = 1u, kErrColdRef = 2u, kErrAtom = 4u;
+
+__device__ inline float4_t mfma16x16x32(half8_t a, half8_t b, float4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ inline half8_t as_h8(uint4_t v) { return __builtin_bit_cast(half8_t, v); }
+__device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ inline float h2f_bits(uint32_t bits16) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+}
+__device__ inline void flag_error(uint32_t* err, uint32_t bit) {
+    __hip_atomic_fetch_or(err, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline float wave_max(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m));
+    return v;
+}
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+    return v;
+}
+
+// ---------------------------------------------------------------- arguments
+
+struct ProjArgs {
+    const uint16_t* q;    // [L][B][Q][Hq][HD]
+    const uint16_t* dict; // [L][dict_heads][A][HD]
+    uint16_t* ql;         // [L*B*Hkv][A][R] f16
+    uint32_t batch, queries, q_heads, kv_heads, gqa, rows_r;
+    uint32_t dict_size, dict_heads;
+    uint32_t rows_per_group; // B*Q*(dict_heads==1 ? Hq : G)
+    uint64_t dict_layer;     // elements per layer
+};
+
+struct HotArgs {
+    const uint16_t* q;
+    const uint16_t* hot_k;
+    const uint16_t* hot_v; // may be null (K == V)
+    const uint32_t* refs;
+    const uint32_t* seq_hot;
+    float* part_m; // [lbg][S][R]
+    float* part_l;
+    float* part_o; // [lbg][S][R][HD]
+    uint32_t* err;
+    uint32_t batch, queries, q_heads, kv_heads, gqa, rows_r;
+    uint32_t hot_count, refs_stride, splits, tokens_per_split, causal;
+    float scale_log2;
+    uint64_t hot_blocks, hot_layer, refs_layer;
+};
+
+struct ColdArgs {
+    const uint16_t* ql; // q_latent, addressed through the strides below
+    const uint4_t* cold;
+    const uint32_t* refs;
+    const uint32_t* seq_cold;
+    float* part_m; // [lbg][S][R]
+    float* part_l;
+    float* part_w;   // [lbg][S][R][A]
+    float* part_amax; // [lbg][S][R]: max_a |bin[a]|
+    uint32_t* err;
+    uint32_t batch, kv_heads, gqa, rows_r;
+    uint32_t hot_count, cold_count, refs_stride, dict_size;
+    uint32_t splits, tokens_per_split, n_chunks, n_units;
+    float scale_log2;
+    uint64_t cold_blocks, cold_layer, refs_layer;
+    // q_latent element (lb, g, q, j, a) = ql[lb*s_lb + g*s_g + q*s_q + j*s_j + a*s_a]
+    uint64_t s_lb, s_g, s_q, s_j, s_a;
+};
+
+struct FinishArgs {
+    const uint16_t* dict;
+    const float* cold_m;
+    const float* cold_l;
+    const float* cold_w;
+    const float* cold_amax;
+    const float* hot_m;
+    const float* hot_l;
+    const float* hot_o;
+    float* ocp; // [lbg*R + r][n_ar][HD] when n_ar > 1
+    uint16_t* out;
+    uint32_t batch, queries, q_heads, kv_heads, gqa, rows_r;
+    uint32_t dict_size, dict_heads, rows_per_group, tiles_per_group;
+    uint32_t cold_splits, hot_splits, n_ar, atoms_per_range;
+    uint64_t dict_layer;
+};
+
+struct MergeArgs {
+    const float* cold_m;
+    const float* cold_l;
+    const float* cold_amax;
+    const float* ocp; // [rows][n_ar][HD] or null (no cold)
+    const float* hot_m;
+    const float* hot_l;
+    const float* hot_o;
+    uint16_t* out;
+    uint32_t batch, queries, q_heads, kv_heads, gqa, rows_r;
+    uint32_t cold_splits, hot_splits, n_ar;
+    uint64_t total_rows; // L*B*Hkv*R
+};
+
+// ------------------------------------------------------------ q . D^T (MFMA)
+//
+// One wave computes a (16*MR rows) x (16*NA atoms) tile with K = HD.
+// Operand layouts of v_mfma_f32_16x16x32_f16 (lane l, li = l%16, lg = l/16):
+//   A[i][k]: lane holds row li, k = 8*lg .. 8*lg+7   -> 16 contiguous bytes of a q row
+//   B[k][j]: lane holds col li, k = 8*lg .. 8*lg+7   -> 16 contiguous bytes of a D row
+//   C[i][j]: lane holds rows 4*lg .. 4*lg+3, col li
+// Rows of one group share one dictionary: group = (layer, dict head); inside a
+// group row i enumerates (b, q, head) with head over Hq (shared dictionary) or
+// over the G heads of kv head dg (per-kv-head dictionary).
+template <int HD, int MR, int NA>
+__global__ __launch_bounds__(64) void project_kernel(ProjArgs a) {
+    constexpr int KS = HD / 32;
+    const int lane = threadIdx.x, li = lane & 15, lg = lane >> 4;
+    const uint32_t group = blockIdx.z;
+    const uint32_t l = group / a.dict_heads, dg = group % a.dict_heads;
+    const uint32_t h_per = a.dict_heads == 1 ? a.q_heads : a.gqa;
+    const uint32_t row0 = blockIdx.y * 16 * MR, atom0 = blockIdx.x * 16 * NA;
+    const uint16_t* dict = a.dict + l * a.dict_layer + (uint64_t)dg * a.dict_size * HD;
+
+    half8_t aop[MR][KS];
+#pragma unroll
+    for (int mr = 0; mr < MR; ++mr) {
+        const uint32_t i = row0 + 16 * mr + li;
+        if (i < a.rows_per_group) {
+            const uint32_t b = i / (a.queries * h_per), rem = i % (a.queries * h_per);
+            const uint32_t q = rem / h_per, h = dg * a.gqa + rem % h_per;
+            const uint16_t* p = a.q + ((((uint64_t)l * a.batch + b) * a.queries + q) * a.q_heads + h) * HD;
+#pragma unroll
+            for (int j = 0; j < KS; ++j) aop[mr][j] = as_h8(*(const uint4_t*)(p + 32 * j + 8 * lg));
+        } else {
+#pragma unroll
+            for (int j = 0; j < KS; ++j) aop[mr][j] = (half8_t)(_Float16)0;
+        }
+    }
+    float4_t acc[MR][NA];
+#pragma unroll
+    for (int na = 0; na < NA; ++na) {
+        const uint32_t at = atom0 + 16 * na + li;
+        half8_t bop[KS];
+#pragma unroll
+        for (int j = 0; j < KS; ++j)
+            bop[j] = at < a.dict_size ? as_h8(*(const uint4_t*)(dict + (uint64_t)at * HD + 32 * j + 8 * lg))
+                                      : (half8_t)(_Float16)0;
+#pragma unroll
+        for (int mr = 0; mr < MR; ++mr) {
+            acc[mr][na] = (float4_t)0.0f;
+#pragma unroll
+            for (int j = 0; j < KS; ++j) acc[mr][na] = mfma16x16x32(aop[mr][j], bop[j], acc[mr][na]);
+        }
+    }
+    // Store as f16 into ql[lbg][atom][r], r = q*G + (h % G).
+    const bool packed = (a.gqa % 4) == 0; // then C rows 4*lg..+3 are 4 consecutive r of one (b,q,g)
+#pragma unroll
+    for (int mr = 0; mr < MR; ++mr) {
+        const uint32_t ib = row0 + 16 * mr + 4 * lg;
+#pragma unroll
+        for (int na = 0; na < NA; ++na) {
+            const uint32_t at = atom0 + 16 * na + li;
+            if (at >= a.dict_size) continue;
+            if (packed) {
+                if (ib >= a.rows_per_group) continue;
+                const uint32_t b = ib / (a.queries * h_per), rem = ib % (a.queries * h_per);
+                const uint32_t q = rem / h_per, h = dg * a.gqa + rem % h_per;
+                const uint32_t g = h / a.gqa, r = q * a.gqa + h % a.gqa;
+                const uint64_t lbg = ((uint64_t)l * a.batch + b) * a.kv_heads + g;
+                half4_t v;
+                v[0] = (_Float16)acc[mr][na][0];
+                v[1] = (_Float16)acc[mr][na][1];
+                v[2] = (_Float16)acc[mr][na][2];
+                v[3] = (_Float16)acc[mr][na][3];
+                *(half4_t*)(a.ql + (lbg * a.dict_size + at) * a.rows_r + r) = v;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t i = ib + e;
+                    if (i >= a.rows_per_group) continue;
+                    const uint32_t b = i / (a.queries * h_per), rem = i % (a.queries * h_per);
+                    const uint32_t q = rem / h_per, h = dg * a.gqa + rem % h_per;
+                    const uint32_t g = h / a.gqa, r = q * a.gqa + h % a.gqa;
+                    const uint64_t lbg = ((uint64_t)l * a.batch + b) * a.kv_heads + g;
+                    a.ql[(lbg * a.dict_size + at) * a.rows_r + r] =
+                        __builtin_bit_cast(uint16_t, (_Float16)acc[mr][na][e]);
+                }
+            }
+        }
+    }
+}
+
+// ------------------------------------------------- hot pool, split-K (MFMA)
+//
+// Work item = (lbg, split); one wave; the wave holds all R = G*Q query rows of
+// its kv head in RT tiles of 16.  Per chunk of 32 tokens (two 16-token blocks):
+//   S^T[token][row] = K Q^T: A = K (lane: token li of block tb, dims 8*lg+32j..)
+//                            B = Q^T (lane: row li, same dims), 4 k-steps at HD=128
+//   -> lane holds scores of tokens 4*lg+e (e<4) of each block for row li, so
+//      the P^T operand of the second product is already in the lane:
+//      k-index 8*lg+e' <-> token 4*lg+e' (e'<4) / 16+4*lg+(e'-4) (e'>=4).
+//   O^T[dim][row] += V^T P^T: A = V^T (lane: dim 16*nb+li, the 8 tokens above),
+//      gathered from the chunk staged in LDS.
+// LDS pitch HD+4 halves (66 words at HD=128) puts the four token rows 4*lg+e'
+// of one read on disjoint 8-bank groups.
+template <int HD, int RT>
+__global__ __launch_bounds__(64) void hot_kernel(HotArgs a) {
+    constexpr int KS = HD / 32, NB = HD / 16, P = HD + 4;
+    __shared__ __attribute__((aligned(16))) _Float16 lds[32 * P];
+    const int lane = threadIdx.x, li = lane & 15, lg = lane >> 4;
+    const uint32_t s = blockIdx.x % a.splits, lbg = blockIdx.x / a.splits;
+    const uint32_t g = lbg % a.kv_heads, lb = lbg / a.kv_heads, l = lb / a.batch;
+    uint32_t nh = a.hot_count;
+    if (a.seq_hot) nh = min(nh, a.seq_hot[lb]);
+    const uint32_t n_tok = nh * kBlockTokens;
+    const uint32_t t_begin = s * a.tokens_per_split;
+    const uint32_t t_end = min(t_begin + a.tokens_per_split, n_tok);
+    const uint32_t R = a.rows_r;
+
+    half8_t qop[RT][KS];
+    int lim[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        const uint32_t r = 16 * rt + li;
+        if (r < R) {
+            const uint32_t q = r / a.gqa, h = g * a.gqa + r % a.gqa;
+            const uint16_t* p = a.q + (((uint64_t)lb * a.queries + q) * a.q_heads + h) * HD;
+#pragma unroll
+            for (int j = 0; j < KS; ++j) qop[rt][j] = as_h8(*(const uint4_t*)(p + 32 * j + 8 * lg));
+            lim[rt] = a.causal ? (int)n_tok - (int)a.queries + 1 + (int)q : (int)n_tok;
+        } else {
+#pragma unroll
+            for (int j = 0; j < KS; ++j) qop[rt][j] = (half8_t)(_Float16)0;
+            lim[rt] = 0;
+        }
+    }
+
+    float m_run[RT], l_run[RT];
+    float4_t oacc[RT][NB];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        m_run[rt] = -INFINITY;
+        l_run[rt] = 0.0f;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) oacc[rt][nb] = (float4_t)0.0f;
+    }
+
+    const uint16_t* kbase = a.hot_k + (uint64_t)l * a.hot_layer;
+    const uint16_t* vbase = a.hot_v ? a.hot_v + (uint64_t)l * a.hot_layer : nullptr;
+    const uint32_t* refs = a.refs + (uint64_t)l * a.refs_layer + (uint64_t)(lb % a.batch) * a.refs_stride;
+
+    // Resolve the two blocks of chunk c0 and load this lane's K pieces.
+    auto load_chunk = [&](uint32_t c0, uint4_t (&kr)[2][KS], uint64_t (&rowoff)[2], bool (&ok)[2]) {
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) {
+            const bool in = c0 + 16 * tb < t_end;
+            const uint32_t ref = in ? (refs[c0 / 16 + tb] & kRefMask) : 0u;
+            ok[tb] = in && ref < a.hot_blocks;
+            if (in && !ok[tb]) flag_error(a.err, kErrHotRef);
+            rowoff[tb] = (((uint64_t)ref * kBlockTokens + li) * a.kv_heads + g) * HD + 8 * lg;
+#pragma unroll
+            for (int j = 0; j < KS; ++j)
+                kr[tb][j] = ok[tb] ? *(const uint4_t*)(kbase + rowoff[tb] + 32 * j) : (uint4_t)0u;
+        }
+    };
+
+    uint4_t kcur[2][KS];
+    uint64_t offcur[2];
+    bool okcur[2];
+    if (t_begin < t_end) load_chunk(t_begin, kcur, offcur, okcur);
+
+    for (uint32_t c0 = t_begin; c0 < t_end; c0 += 32) {
+        uint4_t knext[2][KS];
+        uint64_t offnext[2];
+        bool oknext[2];
+        const bool more = c0 + 32 < t_end;
+        if (more) load_chunk(c0 + 32, knext, offnext, oknext);
+
+        // S^T = K Q^T
+        float4_t sacc[RT][2];
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int tb = 0; tb < 2; ++tb) {
+                sacc[rt][tb] = (float4_t)0.0f;
+#pragma unroll
+                for (int j = 0; j < KS; ++j)
+                    sacc[rt][tb] = mfma16x16x32(as_h8(kcur[tb][j]), qop[rt][j], sacc[rt][tb]);
+            }
+
+        // Stage V (= K unless a V pool is given) in LDS as [token][dim].
+        __syncthreads();
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+            for (int j = 0; j < KS; ++j) {
+                uint4_t v = kcur[tb][j];
+                if (vbase) v = okcur[tb] ? *(const uint4_t*)(vbase + offcur[tb] + 32 * j) : (uint4_t)0u;
+                _Float16* dst = lds + (16 * tb + li) * P + 32 * j + 8 * lg;
+                *(uint2_t*)dst = (uint2_t){v[0], v[1]};
+                *(uint2_t*)(dst + 4) = (uint2_t){v[2], v[3]};
+            }
+        __syncthreads();
+
+        // Online softmax per query row (row li of each tile).
+        half8_t pop[RT];
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+            float sv[8];
+            float mx = -INFINITY;
+#pragma unroll
+            for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int tok = (int)(c0 + 16 * tb + 4 * lg + e);
+                    const bool v = okcur[tb] && tok < lim[rt];
+                    sv[4 * tb + e] = v ? sacc[rt][tb][e] * a.scale_log2 : -INFINITY;
+                    mx = fmaxf(mx, sv[4 * tb + e]);
+                }
+            mx = fmaxf(mx, __shfl_xor(mx, 16));
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            const float mnew = fmaxf(m_run[rt], mx);
+            float alpha = 1.0f, psum = 0.0f;
+            if (mnew != -INFINITY) {
+                alpha = fast_exp2(m_run[rt] - mnew);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float p = fast_exp2(sv[e] - mnew);
+                    psum += p;
+                    pop[rt][e] = (_Float16)p;
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) pop[rt][e] = (_Float16)0;
+            }
+            l_run[rt] = l_run[rt] * alpha + psum;
+            m_run[rt] = mnew;
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) oacc[rt][nb] *= alpha;
+        }
+
+        // O^T += V^T P^T
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+            half8_t vop;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int row = e < 4 ? 4 * lg + e : 16 + 4 * lg + (e - 4);
+                vop[e] = lds[row * P + 16 * nb + li];
+            }
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) oacc[rt][nb] = mfma16x16x32(vop, pop[rt], oacc[rt][nb]);
+        }
+
+        if (more) {
+#pragma unroll
+            for (int tb = 0; tb < 2; ++tb) {
+                offcur[tb] = offnext[tb];
+                okcur[tb] = oknext[tb];
+#pragma unroll
+                for (int j = 0; j < KS; ++j) kcur[tb][j] = knext[tb][j];
+            }
+        }
+    }
+
+    const uint64_t pbase = ((uint64_t)lbg * a.splits + s) * R;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        float lt = l_run[rt] + __shfl_xor(l_run[rt], 16);
+        lt += __shfl_xor(lt, 32);
+        const uint32_t r = 16 * rt + li;
+        if (r < R) {
+            if (lg == 0) {
+                a.part_m[pbase + r] = m_run[rt];
+                a.part_l[pbase + r] = lt;
+            }
+            float* po = a.part_o + (pbase + r) * HD;
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) *(float4_t*)(po + 16 * nb + 4 * lg) = oacc[rt][nb];
+        }
+    }
+}
+
+// ----------------------------------------------- cold pool, scores + bins
+//
+// Work item = (layer*batch+seq, chunk of RC query rows, split) x kv head g.
+// LDS: q_latent table [A][RC] f16, bins [A][RC] f32, reduction scratch.
+// Each thread scores CPT codes per tile (one 16-byte load each, next tile
+// prefetched).  The work-group keeps one reference maximum per row; weights
+// are 2^(s - ref) with s <= ref + kColdSlack, and the bins and partial sums are
+// rescaled only when a tile exceeds the reference by more than the slack.
+// The kv heads of one (sequence, chunk, split) are placed on one XCD (work
+// groups are dealt round-robin over the 8 XCDs), so the 128-byte lines that
+// interleave their 16-byte codes are fetched from HBM once per XCD L2.
+template <int RC, int CPT>
+__global__ __launch_bounds__(kColdThreads) void cold_kernel(ColdArgs a) {
+    constexpr int NT = kColdThreads, NW = NT / 64;
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t x = blockIdx.x % 8u, k = blockIdx.x / 8u;
+    const uint32_t g = k % a.kv_heads;
+    const uint32_t u = (k / a.kv_heads) * 8u + x;
+    if (u >= a.n_units) return;
+    const uint32_t s = u % a.splits, uc = u / a.splits;
+    const uint32_t c = uc % a.n_chunks, lb = uc / a.n_chunks;
+    const uint32_t l = lb / a.batch;
+    const uint64_t lbg = (uint64_t)lb * a.kv_heads + g;
+    const uint32_t A = a.dict_size, R = a.rows_r;
+    uint32_t nc = a.cold_count;
+    if (a.seq_cold) nc = min(nc, a.seq_cold[lb]);
+    const uint32_t n_tok = nc * kBlockTokens;
+    const uint32_t t_begin = s * a.tokens_per_split;
+    const uint32_t t_end = min(t_begin + a.tokens_per_split, n_tok);
+    const uint64_t pbase = (lbg * a.splits + s) * R;
+
+    if (t_begin >= t_end) {
+        if (tid < RC) {
+            const uint32_t r = c * RC + tid;
+            if (r < R) {
+                a.part_m[pbase + r] = -INFINITY;
+                a.part_l[pbase + r] = 0.0f;
+                a.part_amax[pbase + r] = 0.0f;
+            }
+        }
+        return;
+    }
+
+    const uint32_t qtab_bytes = (A * RC * 2 + 15) & ~15u;
+    _Float16* qtab = (_Float16*)smem;
+    float* bins = (float*)(smem + qtab_bytes);
+    float* red = bins + (uint64_t)A * RC; // [2][NW][RC]
+
+    // q_latent rows of this chunk into LDS; rows past R are zero.
+    for (uint32_t at = tid; at < A; at += NT) {
+#pragma unroll
+        for (int rr = 0; rr < RC; ++rr) {
+            const uint32_t r = c * RC + rr;
+            uint16_t bits = 0;
+            if (r < R)
+                bits = a.ql[(uint64_t)lb * a.s_lb + g * a.s_g + (r / a.gqa) * a.s_q + (r % a.gqa) * a.s_j +
+                            (uint64_t)at * a.s_a];
+            qtab[at * RC + rr] = __builtin_bit_cast(_Float16, bits);
+        }
+    }
+    for (uint32_t i = tid; i < A * RC; i += NT) bins[i] = 0.0f;
+    __syncthreads();
+
+    const uint32_t* refs =
+        a.refs + (uint64_t)l * a.refs_layer + (uint64_t)(lb % a.batch) * a.refs_stride + a.hot_count;
+    const uint4_t* cold = a.cold + (uint64_t)l * a.cold_layer;
+
+    auto load_tile = [&](uint32_t t0, uint4_t (&buf)[CPT], bool (&ok)[CPT]) {
+#pragma unroll
+        for (int kk = 0; kk < CPT; ++kk) {
+            const uint32_t t = t0 + kk * NT + tid;
+            bool v = t < t_end;
+            if (v) {
+                const uint32_t ref = refs[t >> 4] & kRefMask;
+                if (ref >= a.cold_blocks) {
+                    flag_error(a.err, kErrColdRef);
+                    v = false;
+                } else {
+                    buf[kk] = cold[((uint64_t)ref * kBlockTokens + (t & 15u)) * a.kv_heads + g];
+                }
+            }
+            ok[kk] = v;
+        }
+    };
+
+    float mref[RC], lpart[RC];
+#pragma unroll
+    for (int rr = 0; rr < RC; ++rr) {
+        mref[rr] = -INFINITY;
+        lpart[rr] = 0.0f;
+    }
+
+    uint4_t cur[CPT];
+    bool curv[CPT];
+    load_tile(t_begin, cur, curv);
+    int par = 0;
+    for (uint32_t t0 = t_begin; t0 < t_end; t0 += NT * CPT, par ^= 1) {
+        uint4_t nxt[CPT];
+        bool nxtv[CPT];
+        const bool more = t0 + NT * CPT < t_end;
+        if (more) load_tile(t0 + NT * CPT, nxt, nxtv);
+
+        // Decode codes and score them (metal:182-190).
+        float sc[CPT][RC];
+        uint32_t ia[CPT][4];
+        float cf[CPT][4];
+        float tmax[RC];
+#pragma unroll
+        for (int rr = 0; rr < RC; ++rr) tmax[rr] = -INFINITY;
+#pragma unroll
+        for (int kk = 0; kk < CPT; ++kk) {
+            const uint4_t cw = cur[kk];
+            ia[kk][0] = cw[0] & 0xFFFFu;
+            ia[kk][1] = cw[0] >> 16;
+            ia[kk][2] = cw[1] & 0xFFFFu;
+            ia[kk][3] = cw[1] >> 16;
+            cf[kk][0] = h2f_bits(cw[2] & 0xFFFFu);
+            cf[kk][1] = h2f_bits(cw[2] >> 16);
+            cf[kk][2] = h2f_bits(cw[3] & 0xFFFFu);
+            cf[kk][3] = h2f_bits(cw[3] >> 16);
+#pragma unroll
+            for (int rr = 0; rr < RC; ++rr) sc[kk][rr] = 0.0f;
+            if (curv[kk]) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if (ia[kk][j] >= A) {
+                        flag_error(a.err, kErrAtom);
+                        ia[kk][j] = 0;
+                        cf[kk][j] = 0.0f;
+                    }
+                    const _Float16* qp = qtab + ia[kk][j] * RC;
+                    if constexpr (RC == 4) {
+                        const half4_t qv = *(const half4_t*)qp;
+#pragma unroll
+                        for (int rr = 0; rr < 4; ++rr) sc[kk][rr] += cf[kk][j] * (float)qv[rr];
+                    } else {
+#pragma unroll
+                        for (int rr = 0; rr < RC; ++rr) sc[kk][rr] += cf[kk][j] * (float)qp[rr];
+                    }
+                }
+#pragma unroll
+                for (int rr = 0; rr < RC; ++rr) {
+                    sc[kk][rr] *= a.scale_log2;
+                    tmax[rr] = fmaxf(tmax[rr], sc[kk][rr]);
+                }
+            }
+        }
+        // Work-group maximum of this tile.
+#pragma unroll
+        for (int rr = 0; rr < RC; ++rr) {
+            const float wm = wave_max(tmax[rr]);
+            if (lane == 0) red[(par * NW + wave) * RC + rr] = wm;
+        }
+        __syncthreads();
+        bool rescale = false;
+        float fac[RC];
+#pragma unroll
+        for (int rr = 0; rr < RC; ++rr) {
+            float tm = -INFINITY;
+#pragma unroll
+            for (int w = 0; w < NW; ++w) tm = fmaxf(tm, red[(par * NW + w) * RC + rr]);
+            fac[rr] = 1.0f;
+            if (tm != -INFINITY && (mref[rr] == -INFINITY || tm > mref[rr] + kColdSlack)) {
+                if (mref[rr] != -INFINITY) {
+                    fac[rr] = fast_exp2(mref[rr] - tm);
+                    rescale = true;
+                }
+                mref[rr] = tm;
+                lpart[rr] *= fac[rr];
+            }
+        }
+        if (rescale) { // uniform across the work-group
+            for (uint32_t at = tid; at < A; at += NT)
+#pragma unroll
+                for (int rr = 0; rr < RC; ++rr) bins[at * RC + rr] *= fac[rr];
+            __syncthreads();
+        }
+        // Softmax weights into the per-atom bins.
+#pragma unroll
+        for (int kk = 0; kk < CPT; ++kk) {
+            if (!curv[kk]) continue;
+            float p[RC];
+#pragma unroll
+            for (int rr = 0; rr < RC; ++rr) {
+                p[rr] = fast_exp2(sc[kk][rr] - mref[rr]);
+                lpart[rr] += p[rr];
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                float* bp = bins + ia[kk][j] * RC;
+#pragma unroll
+                for (int rr = 0; rr < RC; ++rr)
+                    __hip_atomic_fetch_add(bp + rr, p[rr] * cf[kk][j], __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_WORKGROUP);
+            }
+        }
+        if (more) {
+#pragma unroll
+            for (int kk = 0; kk < CPT; ++kk) {
+                cur[kk] = nxt[kk];
+                curv[kk] = nxtv[kk];
+            }
+        }
+    }
+    __syncthreads();
+
+    // Bins out as rows [r][A]; track max |bin| per row for the f16 split of the finish.
+    float amax[RC];
+#pragma unroll
+    for (int rr = 0; rr < RC; ++rr) amax[rr] = 0.0f;
+    for (uint32_t at = tid; at < A; at += NT) {
+#pragma unroll
+        for (int rr = 0; rr < RC; ++rr) {
+            const uint32_t r = c * RC + rr;
+            const float v = bins[at * RC + rr];
+            amax[rr] = fmaxf(amax[rr], fabsf(v));
+            if (r < R) a.part_w[(pbase + r) * A + at] = v;
+        }
+    }
+    // Reduce lpart (sum) and amax (max) over the work-group.
+    float* red2 = red + 2 * NW * RC; // [NW][2*RC]
+#pragma unroll
+    for (int rr = 0; rr < RC; ++rr) {
+        const float ls = wave_sum(lpart[rr]);
+        const float am = wave_max(amax[rr]);
+        if (lane == 0) {
+            red2[wave * 2 * RC + rr] = ls;
+            red2[wave * 2 * RC + RC + rr] = am;
+        }
+    }
+    __syncthreads();
+    if (tid < RC) {
+        const uint32_t r = c * RC + tid;
+        if (r < R) {
+            float ls = 0.0f, am = 0.0f;
+            for (int w = 0; w < NW; ++w) {
+                ls += red2[w * 2 * RC + tid];
+                am = fmaxf(am, red2[w * 2 * RC + RC + tid]);
+            }
+            a.part_m[pbase + r] = mref[tid];
+            a.part_l[pbase + r] = ls;
+            a.part_amax[pbase + r] = am;
+        }
+    }
+}
+
+// Shared-memory bytes of cold_kernel<RC> for a dictionary of A atoms.
+inline size_t cold_smem_bytes(uint32_t A, int RC) {
+    const size_t qtab = ((size_t)A * RC * 2 + 15) & ~(size_t)15;
+    const int NW = kColdThreads / 64;
+    return qtab + (size_t)A * RC * 4 + (size_t)(2 * NW * RC + NW * 2 * RC) * 4;
+}
+
+// ----------------------------------------------- per-row merge factors
+//
+// For one row (lbg, r): cold splits combine to max Mc and sum Lc; the bins are
+// pre-multiplied by 2^(m_s - Mc) / Lc * scl with scl a power of two that keeps
+// the largest combined bin below 2^14, so the hi/lo f16 split of each bin keeps
+// ~22 significant bits.  Hot splits combine to Mh, Lh with factors 2^(m_s - Mh).
+struct RowFactors {
+    float Mc, Lc, inv_scl, Mh, Lh;
+};
+
+__device__ inline void cold_row_factors(const float* cm, const float* cl, const float* camax, uint32_t S,
+                                        uint64_t base, uint32_t R, float* fac_out, float& Mc, float& Lc,
+                                        float& inv_scl) {
+    Mc = -INFINITY;
+    for (uint32_t s = 0; s < S; ++s)
+        if (cl[base + (uint64_t)s * R] > 0.0f) Mc = fmaxf(Mc, cm[base + (uint64_t)s * R]);
+    Lc = 0.0f;
+    float bound = 0.0f;
+    for (uint32_t s = 0; s < S; ++s) {
+        const float l = cl[base + (uint64_t)s * R];
+        const float f = l > 0.0f ? fast_exp2(cm[base + (uint64_t)s * R] - Mc) : 0.0f;
+        Lc += f * l;
+        bound += f * camax[base + (uint64_t)s * R];
+    }
+    float scl = 1.0f;
+    if (Lc > 0.0f && bound > 0.0f) {
+        int e = ilogbf(bound / Lc) + 1;
+        e = max(-100, min(100, e));
+        scl = ldexpf(1.0f, 14 - e);
+    }
+    inv_scl = 1.0f / scl;
+    if (fac_out)
+        for (uint32_t s = 0; s < S; ++s) {
+            const float l = cl[base + (uint64_t)s * R];
+            fac_out[s] = l > 0.0f ? fast_exp2(cm[base + (uint64_t)s * R] - Mc) / Lc * scl : 0.0f;
+        }
+}
+
+__device__ inline void hot_row_factors(const float* hm, const float* hl, uint32_t S, uint64_t base, uint32_t R,
+                                       float* fac_out, float& Mh, float& Lh) {
+    Mh = -INFINITY;
+    for (uint32_t s = 0; s < S; ++s)
+        if (hl[base + (uint64_t)s * R] > 0.0f) Mh = fmaxf(Mh, hm[base + (uint64_t)s * R]);
+    Lh = 0.0f;
+    for (uint32_t s = 0; s < S; ++s) {
+        const float l = hl[base + (uint64_t)s * R];
+        const float f = l > 0.0f ? fast_exp2(hm[base + (uint64_t)s * R] - Mh) : 0.0f;
+        Lh += f * l;
+        fac_out[s] = f;
+    }
+}
+
+// out = (wh*Oh + wc*Lc*Oc) / (wh*Lh + wc*Lc); zero when nothing was visible.
+__device__ inline float merge_value(float oh, float Mh, float Lh, float oc, float Mc, float Lc) {
+    const float M = fmaxf(Lh > 0.0f ? Mh : -INFINITY, Lc > 0.0f ? Mc : -INFINITY);
+    if (M == -INFINITY) return 0.0f;
+    const float wh = Lh > 0.0f ? fast_exp2(Mh - M) : 0.0f;
+    const float wc = Lc > 0.0f ? fast_exp2(Mc - M) : 0.0f;
+    const float den = wh * Lh + wc * Lc;
+    return den > 0.0f ? (wh * oh + wc * Lc * oc) / den : 0.0f;
+}
+
+// ------------------------------------------------------ bins . D (MFMA)
+//
+// Work-group = 16 rows sharing one dictionary x one atom range; 4 waves split
+// the range in chunks of 32 atoms.  O^T[dim][row] += D^T W^T with
+//   B = W^T (lane: row li, atoms a0+4*lg+{0..3} and a0+16+4*lg+{0..3}: two
+//       16-byte loads per cold split, combined with the split factors),
+//       split into hi + lo f16 terms -> two MFMAs,
+//   A = D^T (lane: dim 16*nb+li, the same 8 atoms) gathered from a 32-atom
+//       dictionary chunk staged in LDS (pitch HD+4 halves).
+// With one atom range the log-sum-exp merge runs here too; otherwise the
+// partial cold outputs go to `ocp` for merge_kernel.
+template <int HD>
+__global__ __launch_bounds__(64 * kFinishWaves) void finish_kernel(FinishArgs a) {
+    constexpr int NB = HD / 16, P = HD + 4, NWF = kFinishWaves;
+    constexpr int DTILE = 32 * P;                           // halves per wave
+    constexpr int SMEM_D = NWF * DTILE * 2;                 // bytes
+    constexpr int SMEM_R = NWF * 16 * HD * 4;               // bytes
+    constexpr int SMEM = SMEM_D > SMEM_R ? SMEM_D : SMEM_R; // the two phases alias
+    __shared__ __attribute__((aligned(16))) unsigned char sbuf[SMEM];
+    __shared__ float s_cfac[16][kMaxSplits];
+    __shared__ float s_hfac[16][kMaxSplits];
+    __shared__ RowFactors s_rf[16];
+    __shared__ uint64_t s_row[16]; // lbg*R + r, or ~0 for padding rows
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, li = lane & 15, lg = lane >> 4;
+    const uint32_t group = blockIdx.x / a.tiles_per_group, tile = blockIdx.x % a.tiles_per_group;
+    const uint32_t ar = blockIdx.y;
+    const uint32_t l = group / a.dict_heads, dg = group % a.dict_heads;
+    const uint32_t R = a.rows_r, A = a.dict_size;
+    const uint32_t hg = a.dict_heads == 1 ? a.kv_heads : 1;
+
+    if (tid < 16) {
+        const uint32_t i = tile * 16 + tid;
+        uint64_t rowid = ~0ull;
+        if (i < a.rows_per_group) {
+            const uint32_t b = i / (hg * R), rem = i % (hg * R);
+            const uint32_t g = a.dict_heads == 1 ? rem / R : dg, r = rem % R;
+            const uint64_t lbg = ((uint64_t)l * a.batch + b) * a.kv_heads + g;
+            rowid = lbg * R + r;
+            const uint64_t cbase = lbg * a.cold_splits * R + r;
+            RowFactors rf;
+            cold_row_factors(a.cold_m, a.cold_l, a.cold_amax, a.cold_splits, cbase, R, s_cfac[tid], rf.Mc, rf.Lc,
+                             rf.inv_scl);
+            rf.Mh = -INFINITY;
+            rf.Lh = 0.0f;
+            if (a.hot_splits) {
+                const uint64_t hbase = lbg * a.hot_splits * R + r;
+                hot_row_factors(a.hot_m, a.hot_l, a.hot_splits, hbase, R, s_hfac[tid], rf.Mh, rf.Lh);
+            }
+            s_rf[tid] = rf;
+        }
+        s_row[tid] = rowid;
+    }
+    __syncthreads();
+
+    // This lane's B-operand row.
+    const uint64_t myrow = s_row[li];
+    const bool rowok = myrow != ~0ull;
+    const uint64_t lbg_me = rowok ? myrow / R : 0, r_me = rowok ? myrow % R : 0;
+    const uint16_t* dict = a.dict + (uint64_t)l * a.dict_layer + (uint64_t)dg * A * HD;
+    _Float16* dtile = (_Float16*)sbuf + wave * DTILE;
+
+    float4_t acc[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[nb] = (float4_t)0.0f;
+
+    const uint32_t a_begin = ar * a.atoms_per_range;
+    const uint32_t a_end = min(a_begin + a.atoms_per_range, A);
+    const uint32_t n_ch = (a_end - a_begin + 31) / 32;
+    const uint32_t iters = (n_ch + NWF - 1) / NWF;
+    for (uint32_t it = 0; it < iters; ++it) {
+        const uint32_t ch = it * NWF + wave;
+        const uint32_t a0 = a_begin + ch * 32;
+        const bool active = ch < n_ch;
+        __syncthreads();
+        if (active) {
+            // Dictionary chunk [32 atoms][HD] into this wave's LDS tile.
+            constexpr int PIECES = 32 * HD / 8;
+#pragma unroll
+            for (int pc = lane; pc < PIECES; pc += 64) {
+                const int at = pc / (HD / 8), col = (pc % (HD / 8)) * 8;
+                uint4_t v = (uint4_t)0u;
+                if (a0 + at < a_end) v = *(const uint4_t*)(dict + (uint64_t)(a0 + at) * HD + col);
+                _Float16* dst = dtile + at * P + col;
+                *(uint2_t*)dst = (uint2_t){v[0], v[1]};
+                *(uint2_t*)(dst + 4) = (uint2_t){v[2], v[3]};
+            }
+        }
+        __syncthreads();
+        if (active) {
+            float w8[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) w8[e] = 0.0f;
+            if (rowok) {
+                for (uint32_t s = 0; s < a.cold_splits; ++s) {
+                    const float f = s_cfac[li][s];
+                    if (f == 0.0f) continue;
+                    const float* wrow = a.cold_w + ((lbg_me * a.cold_splits + s) * R + r_me) * A;
+#pragma unroll
+                    for (int half = 0; half < 2; ++half) {
+                        const uint32_t at = a0 + 16 * half + 4 * lg;
+                        if (at < a_end) {
+                            const float4_t v = *(const float4_t*)(wrow + at);
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) w8[4 * half + e] += f * v[e];
+                        }
+                    }
+                }
+            }
+            half8_t hi, lo;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                hi[e] = (_Float16)w8[e];
+                lo[e] = (_Float16)(w8[e] - (float)hi[e]);
+            }
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                half8_t dop;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int row = e < 4 ? 4 * lg + e : 16 + 4 * lg + (e - 4);
+                    dop[e] = dtile[row * P + 16 * nb + li];
+                }
+                acc[nb] = mfma16x16x32(dop, hi, acc[nb]);
+                acc[nb] = mfma16x16x32(dop, lo, acc[nb]);
+            }
+        }
+    }
+    __syncthreads();
+    // Cross-wave reduction: red[wave][row][dim].
+    float* red = (float*)sbuf;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+        *(float4_t*)(red + (wave * 16 + li) * HD + 16 * nb + 4 * lg) = acc[nb];
+    __syncthreads();
+
+    constexpr int DPT = HD / 16; // dims per thread: 256 threads over 16 rows x HD
+    const int row = tid / 16, d0 = (tid % 16) * DPT;
+    const uint64_t rowid = s_row[row];
+    if (rowid == ~0ull) return;
+    const RowFactors rf = s_rf[row];
+    float oc[DPT];
+#pragma unroll
+    for (int e = 0; e < DPT; ++e) {
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NWF; ++w) v += red[(w * 16 + row) * HD + d0 + e];
+        oc[e] = v * rf.inv_scl;
+    }
+    if (a.n_ar > 1) {
+        float* dst = a.ocp + (rowid * a.n_ar + ar) * HD + d0;
+#pragma unroll
+        for (int e = 0; e < DPT; ++e) dst[e] = oc[e];
+        return;
+    }
+    const uint64_t lbg = rowid / R, r = rowid % R;
+    float oh[DPT];
+#pragma unroll
+    for (int e = 0; e < DPT; ++e) oh[e] = 0.0f;
+    for (uint32_t s = 0; s < a.hot_splits; ++s) {
+        const float f = s_hfac[row][s];
+        if (f == 0.0f) continue;
+        const float* src = a.hot_o + ((lbg * a.hot_splits + s) * R + r) * HD + d0;
+#pragma unroll
+        for (int e = 0; e < DPT; ++e) oh[e] += f * src[e];
+    }
+    const uint64_t lb = lbg / a.kv_heads, g = lbg % a.kv_heads;
+    const uint64_t q = r / a.gqa, h = g * a.gqa + r % a.gqa;
+    uint16_t* o = a.out + ((lb * a.queries + q) * a.q_heads + h) * HD + d0;
+#pragma unroll
+    for (int e = 0; e < DPT; ++e)
+        o[e] = __builtin_bit_cast(uint16_t, (_Float16)merge_value(oh[e], rf.Mh, rf.Lh, oc[e], rf.Mc, rf.Lc));
+}
+
+// --------------------------------------------------- log-sum-exp merge
+//
+// 16 rows (row id lbg*R + r) per 256-thread work-group; used when there is no
+// cold pool or when the cold output was split over several atom ranges.
+template <int HD>
+__global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
+    __shared__ float s_hfac[16][kMaxSplits];
+    __shared__ RowFactors s_rf[16];
+    const int tid = threadIdx.x;
+    const uint64_t row0 = (uint64_t)blockIdx.x * 16;
+    const uint32_t R = a.rows_r;
+    if (tid < 16) {
+        const uint64_t rowid = row0 + tid;
+        RowFactors rf;
+        rf.Mc = -INFINITY;
+        rf.Lc = 0.0f;
+        rf.inv_scl = 1.0f;
+        rf.Mh = -INFINITY;
+        rf.Lh = 0.0f;
+        if (rowid < a.total_rows) {
+            const uint64_t lbg = rowid / R, r = rowid % R;
+            if (a.ocp)
+                cold_row_factors(a.cold_m, a.cold_l, a.cold_amax, a.cold_splits, lbg * a.cold_splits * R + r, R,
+                                 nullptr, rf.Mc, rf.Lc, rf.inv_scl);
+            if (a.hot_splits)
+                hot_row_factors(a.hot_m, a.hot_l, a.hot_splits, lbg * a.hot_splits * R + r, R, s_hfac[tid], rf.Mh,
+                                rf.Lh);
+        }
+        s_rf[tid] = rf;
+    }
+    __syncthreads();
+    constexpr int DPT = HD / 16;
+    const int row = tid / 16, d0 = (tid % 16) * DPT;
+    const uint64_t rowid = row0 + row;
+    if (rowid >= a.total_rows) return;
+    const RowFactors rf = s_rf[row];
+    const uint64_t lbg = rowid / R, r = rowid % R;
+    float oc[DPT], oh[DPT];
+#pragma unroll
+    for (int e = 0; e < DPT; ++e) {
+        oc[e] = 0.0f;
+        oh[e] = 0.0f;
+    }
+    if (a.ocp)
+        for (uint32_t ar = 0; ar < a.n_ar; ++ar) {
+            const float* src = a.ocp + (rowid * a.n_ar + ar) * HD + d0;
+#pragma unroll
+            for (int e = 0; e < DPT; ++e) oc[e] += src[e];
+        }
+    for (uint32_t s = 0; s < a.hot_splits; ++s) {
+        const float f = s_hfac[row][s];
+        if (f == 0.0f) continue;
+        const float* src = a.hot_o + ((lbg * a.hot_splits + s) * R + r) * HD + d0;
+#pragma unroll
+        for (int e = 0; e < DPT; ++e) oh[e] += f * src[e];
+    }
+    const uint64_t lb = lbg / a.kv_heads, g = lbg % a.kv_heads;
+    const uint64_t q = r / a.gqa, h = g * a.gqa + r % a.gqa;
+    uint16_t* o = a.out + ((lb * a.queries + q) * a.q_heads + h) * HD + d0;
+#pragma unroll
+    for (int e = 0; e < DPT; ++e)
+        o[e] = __builtin_bit_cast(uint16_t, (_Float16)merge_value(oh[e], rf.Mh, rf.Lh, oc[e], rf.Mc, rf.Lc));
+}
+
+// ------------------------------------------------ codec check (bit-exact)
+__global__ void gather_codes_kernel(const uint4_t* codes, uint64_t n, const uint16_t* dict, uint32_t A,
+                                    uint32_t HD, uint32_t* idx, float* coef, uint16_t* atoms, uint32_t* err) {
+    const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= n * 4) return;
+    const uint64_t i = t / 4;
+    const uint32_t k = t % 4;
+    const uint4_t cw = codes[i];
+    const uint32_t word = k < 2 ? cw[0] : cw[1];
+    const uint32_t at = (k & 1) ? word >> 16 : word & 0xFFFFu;
+    const uint32_t cword = k < 2 ? cw[2] : cw[3];
+    const uint32_t cbits = (k & 1) ? cword >> 16 : cword & 0xFFFFu;
+    idx[t] = at;
+    coef[t] = h2f_bits(cbits);
+    if (at >= A) flag_error(err, kErrAtom);
+    for (uint32_t j = 0; j < HD; ++j) atoms[t * HD + j] = at < A ? dict[(uint64_t)at * HD + j] : (uint16_t)0xFFFFu;
+}
+
+} // namespace aw

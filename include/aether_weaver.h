@@ -1,0 +1,243 @@
+/*
+ * aether_weaver.h — C ABI of the MI355X (gfx950) Weaver decode library.
+ *
+ * Weaver decode is GQA decode attention over two KV pools:
+ *   - a hot pool of exact f16 rows, blocks of 16 tokens  [blocks][16][kv_heads][head_dim];
+ *   - a cold pool of 16-byte SparseCodes (4 dictionary atom indices + 4 f16
+ *     coefficients per token and kv head)              [blocks][16][kv_heads],
+ *     attended directly on the codes, without decompression.
+ * Blocks are addressed through a block table ("loom refs"): hot refs first,
+ * then cold refs; the physical block is ref & 0x7FFFFFFF.
+ *
+ * The reference dispatches one Metal kernel through a Rust engine:
+ *   nexus-core/src/weaver.rs:85        WeaverEngine::new(metallib_path)
+ *   nexus-core/src/weaver.rs:139-237   WeaverEngine::decode(q_exact, q_latent, hot_pool,
+ *                                        cold_pool, loom_refs, dictionary, params)
+ *   nexus-core/src/weaver.rs:314-321   device_name(), max_threads_per_threadgroup()
+ *   nexus-core/src/weaver_kernel.metal:118-240  weaver_decode (8 buffer bindings)
+ * Each entry point below names the reference interface it replaces.  All
+ * pointers are plain host or device pointers; no framework types cross this
+ * boundary.  Every function returns AW_OK (0) or a negative AW_E_* code; the
+ * engine keeps a text description of the last failure (aw_engine_last_error).
+ *
+ * Threading: calls on one engine must be serialised by the caller (the
+ * reference's decode takes &mut self, weaver.rs:139).  Use one engine per
+ * host thread, or lock around it.
+ */
+#ifndef AETHER_WEAVER_H
+#define AETHER_WEAVER_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AW_ABI_VERSION 1u
+
+/* ---- status codes -------------------------------------------------------- */
+#define AW_OK             0
+#define AW_E_INVALID_ARG (-1) /* bad geometry, null pointer, short buffer          */
+#define AW_E_ALIGN       (-2) /* SparseCode pointer not 16-byte aligned            */
+#define AW_E_OOB         (-3) /* block ref or atom index beyond its buffer         */
+#define AW_E_HIP         (-4) /* HIP runtime failure (no device, launch, copy ...) */
+#define AW_E_LOAD        (-5) /* kernels for this device are not in the library    */
+#define AW_E_UNSUPPORTED (-6) /* valid request this build does not implement       */
+
+/* ---- reference layouts ---------------------------------------------------- */
+
+/* One token's compressed K(=V) row for one kv head: V = sum_k coeffs[k] * D[indices[k]].
+ * 16 bytes, little-endian: u16 indices[4] at bytes 0-7, IEEE binary16 coeffs[4]
+ * at bytes 8-15.  Replaces SparseCode (nexus-core/src/types.rs:218-228,
+ * weaver_kernel.metal:34-37).  Coefficients are carried as raw binary16 bits. */
+typedef struct aw_sparse_code {
+    uint16_t indices[4];
+    uint16_t coeffs[4];
+} aw_sparse_code;
+
+/* Dispatch parameters, 12 x u32 = 48 bytes in the reference field order.
+ * Replaces WeaverParams (nexus-core/src/types.rs:351-374, weaver_kernel.metal:40-51).
+ * hot_count / cold_count are numbers of 16-token blocks. */
+typedef struct aw_weaver_params {
+    uint32_t q_heads;
+    uint32_t kv_heads;
+    uint32_t head_dim;
+    uint32_t block_size;  /* must be 16 */
+    uint32_t gqa_group;   /* q_heads / kv_heads */
+    uint32_t hot_count;
+    uint32_t cold_count;
+    uint32_t dict_size;
+    uint32_t sparsity_k;  /* must be 4 */
+    uint32_t _pad[3];
+} aw_weaver_params;
+
+/* ---- device-resident, batched / multi-query request ------------------------ */
+
+/* Flags for aw_decode_desc.flags. */
+#define AW_F_CAUSAL 1u /* query j of Q sees hot tokens p < n_hot_tokens - Q + 1 + j
+                          (the rule of nexus-core/src/ops.metal:549); cold tokens are
+                          all older than the drafts and always visible */
+
+/* One decode call over L layers x B sequences x Q query tokens.  All pointers
+ * are DEVICE pointers.  Element layouts (f16 = raw binary16 bits):
+ *   q        [L][B][Q][q_heads][head_dim]
+ *   q_latent [L][B][Q][q_heads][dict_size] or NULL (then q . D^T is computed
+ *            on the device, fp32 accumulation, stored as f16 like the
+ *            reference's q_latent buffer, weaver_kernel.metal:111)
+ *   hot_k    [L][hot_blocks][16][kv_heads][head_dim]
+ *   hot_v    same as hot_k, or NULL: V is the K row (reference, metal:162-166)
+ *   cold     [L][cold_blocks][16][kv_heads]   (16-byte aligned)
+ *   refs     [L][B][refs_stride]: hot refs [0, hot_count), cold refs
+ *            [hot_count, hot_count + cold_count) of each sequence
+ *   seq_hot, seq_cold  optional [L][B] per-sequence block counts
+ *            (<= hot_count / cold_count); NULL = every sequence uses the maximum
+ *   dict     [L][dict_heads][dict_size][head_dim]; dict_heads is 1 (one shared
+ *            dictionary) or kv_heads (the reference's per-kv-head dictionary,
+ *            weaver_kernel.metal:212-215)
+ *   out      [L][B][Q][q_heads][head_dim]
+ * scale multiplies every score; 1.0 reproduces the reference, which applies
+ * none (weaver_kernel.metal:153-160,186-190). */
+typedef struct aw_decode_desc {
+    uint32_t layers, batch, queries;
+    uint32_t q_heads, kv_heads, head_dim;
+    uint32_t dict_size, dict_heads;
+    uint32_t hot_count, cold_count;   /* max blocks per sequence */
+    uint32_t refs_stride;             /* >= hot_count + cold_count */
+    uint32_t flags;
+    float    scale;
+    uint32_t _reserved;
+    uint64_t hot_blocks, cold_blocks; /* pool capacity per layer, in blocks */
+    const uint16_t*       q;
+    const uint16_t*       q_latent;
+    const uint16_t*       hot_k;
+    const uint16_t*       hot_v;
+    const aw_sparse_code* cold;
+    const uint32_t*       refs;
+    const uint32_t*       seq_hot;
+    const uint32_t*       seq_cold;
+    const uint16_t*       dict;
+    uint16_t*             out;
+} aw_decode_desc;
+
+/* How a request is split across the GPU; filled by aw_decode_plan. */
+typedef struct aw_decode_plan_info {
+    uint32_t rows_per_kv_head;   /* R = gqa_group * queries */
+    uint32_t hot_splits;         /* work items per (layer, seq, kv head) on the hot pool */
+    uint32_t hot_tokens_per_split;
+    uint32_t cold_splits;
+    uint32_t cold_tokens_per_split;
+    uint32_t cold_row_chunk;     /* query rows binned together in one cold work-group */
+    uint32_t computes_q_latent;  /* 1 when q . D^T runs on the device */
+    uint32_t _reserved;
+    uint64_t workspace_bytes;    /* device scratch this request needs */
+} aw_decode_plan_info;
+
+/* Kernel stages, for aw_engine_stage_stats. */
+#define AW_STAGE_PROJECT 0 /* q_latent = q . D^T (MFMA) */
+#define AW_STAGE_HOT     1 /* split-K exact attention over the hot pool (MFMA) */
+#define AW_STAGE_COLD    2 /* scores on the codes + per-atom softmax-weight bins */
+#define AW_STAGE_FINISH  3 /* bins . D (MFMA); fused log-sum-exp merge when it fits */
+#define AW_STAGE_MERGE   4 /* log-sum-exp merge of hot and cold partials, f16 out */
+#define AW_STAGE_COUNT   5
+
+typedef struct aw_engine aw_engine;
+
+/* ---- pure host functions (no GPU needed) ---------------------------------- */
+
+/* ABI version and sizeof() of the public structs, for bindings to check their
+ * layouts: sizes[0..3] = aw_sparse_code, aw_weaver_params, aw_decode_desc,
+ * aw_decode_plan_info.  No reference counterpart. */
+uint32_t aw_abi_version(void);
+void     aw_abi_struct_sizes(size_t sizes[4]);
+
+/* Text for a status code.  No reference counterpart (the reference returns String). */
+const char* aw_status_string(int status);
+
+/* Validate reference parameters against the slice lengths that
+ * WeaverEngine::decode receives (weaver.rs:139-148), including every block ref
+ * and every referenced atom index.  The reference validates nothing and reads
+ * past short buffers; this library rejects such calls before launch.
+ * msg (may be NULL) receives a description of the first failure. */
+int aw_validate_params(const aw_weaver_params* params,
+                       size_t n_q_exact, size_t n_q_latent, size_t n_hot_pool,
+                       const aw_sparse_code* cold_pool, size_t n_cold_pool,
+                       const uint32_t* loom_refs, size_t n_loom_refs,
+                       size_t n_dictionary, size_t n_out,
+                       char* msg, size_t msg_len);
+
+/* Validate a device request's geometry and report how it will be split and how
+ * much scratch it needs.  Reads only the numeric fields of desc. */
+int aw_decode_plan(const aw_decode_desc* desc, aw_decode_plan_info* info,
+                   char* msg, size_t msg_len);
+
+/* ---- engine ------------------------------------------------------------------ */
+
+/* Replaces WeaverEngine::new (weaver.rs:85-132): selects HIP device `device`,
+ * checks that the library holds gfx950 kernels for it, creates the engine's
+ * stream and persistent buffers.  The reference's metallib path becomes the
+ * path of this shared library, which the host loads (dlopen) before calling. */
+int  aw_engine_create(int device, aw_engine** out);
+void aw_engine_destroy(aw_engine* engine);
+
+/* Last failure on this engine (engine-owned, valid until the next call). */
+const char* aw_engine_last_error(const aw_engine* engine);
+
+/* Replaces WeaverEngine::device_name (weaver.rs:314-316). */
+const char* aw_engine_device_name(const aw_engine* engine);
+
+/* Replaces WeaverEngine::max_threads_per_threadgroup (weaver.rs:319-321). */
+uint64_t aw_engine_max_threads_per_threadgroup(const aw_engine* engine);
+
+/* Replaces WeaverEngine::decode (weaver.rs:139-237) with the same semantics:
+ * host slices are copied into engine-owned device buffers that grow only on
+ * overflow (weaver.rs:241-311), one decode of one token runs with
+ * reference-literal math (no score scale, per-kv-head dictionary
+ * [kv_heads][dict_size][head_dim], bit 31 of refs masked), the call waits for
+ * the GPU and copies q_heads*head_dim f16 values to `out`.
+ * q_latent may be NULL (n_q_latent 0): it is then computed as q . D^T on the
+ * device.  Zero-length slices are allowed where the params need no data. */
+int aw_decode(aw_engine* engine,
+              const uint16_t* q_exact, size_t n_q_exact,
+              const uint16_t* q_latent, size_t n_q_latent,
+              const uint16_t* hot_pool, size_t n_hot_pool,
+              const aw_sparse_code* cold_pool, size_t n_cold_pool,
+              const uint32_t* loom_refs, size_t n_loom_refs,
+              const uint16_t* dictionary, size_t n_dictionary,
+              const aw_weaver_params* params,
+              uint16_t* out, size_t n_out);
+
+/* Device-resident batched / multi-query / multi-layer decode, asynchronous on
+ * `hip_stream` (a hipStream_t; NULL = the engine's own stream).  Extends the
+ * reference kernel (weaver_kernel.metal:118-240) with batch, queries, layers,
+ * causal drafts, score scale, shared dictionary and separate V.  Scratch comes
+ * from an engine-owned workspace that grows on demand (the growth allocates).
+ * Block refs and atom indices are checked on the device: a bad one is skipped
+ * and recorded; aw_engine_check_device_errors reports it. */
+int aw_decode_device(aw_engine* engine, const aw_decode_desc* desc, void* hip_stream);
+
+/* Wait for `hip_stream` and report AW_E_OOB if any kernel since the last check
+ * met an out-of-range block ref or atom index (then clears the record). */
+int aw_engine_check_device_errors(aw_engine* engine, void* hip_stream);
+
+/* Bit-exact SparseCode decode and atom gather, for testing the codec on the
+ * device: for code i and slot k, idx[4i+k] = indices[k], coef[4i+k] =
+ * (float)coeffs[k], atoms[(4i+k)*head_dim + j] = dict[indices[k]*head_dim + j]
+ * (raw bits).  Device pointers; the dictionary is one [dict_size][head_dim]
+ * table.  Indices >= dict_size yield atoms of 0xFFFF and are recorded like
+ * aw_decode_device.  Mirrors the gathers of weaver_kernel.metal:182-216. */
+int aw_debug_gather_codes(aw_engine* engine, const aw_sparse_code* codes, size_t n_codes,
+                          const uint16_t* dict, uint32_t dict_size, uint32_t head_dim,
+                          uint32_t* idx, float* coef, uint16_t* atoms, void* hip_stream);
+
+/* Per-stage kernel timing with HIP events recorded on the stream each kernel
+ * runs on.  While enabled, every launch is bracketed by a pair of events. */
+int aw_engine_set_profiling(aw_engine* engine, int enable);
+int aw_engine_stage_stats(aw_engine* engine, int stage, double* total_ms, uint64_t* launches);
+int aw_engine_reset_stage_stats(aw_engine* engine);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AETHER_WEAVER_H */

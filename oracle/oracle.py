@@ -1,0 +1,175 @@
+"""ctypes binding of the CPU oracle (oracle/weaver_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, as the checker (or the timed CPU port), never by
+the product package.  Functions take the host arrays produced by
+``aether_nexus_amd.workloads.host_arrays`` plus the workload geometry.
+"""
+from __future__ import annotations
+
+import ctypes
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+from aether_nexus_amd.types import AW_F_CAUSAL, DecodeDesc
+
+HERE = Path(__file__).resolve().parent
+LIB = HERE / "libweaver_oracle.so"
+SRC = HERE / "weaver_oracle.c"
+
+_lib = None
+
+
+def build() -> Path:
+    """Compile the oracle with gcc (no fast-math; fp contraction off)."""
+    subprocess.run(["make", "-s", "-C", str(HERE), "libweaver_oracle.so"], check=True)
+    return LIB
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB.is_file():
+            build()
+        l = ctypes.CDLL(str(LIB))
+        vp, u64 = ctypes.c_void_p, ctypes.c_uint64
+        l.or_h2f.restype = ctypes.c_float
+        l.or_h2f.argtypes = [ctypes.c_uint16]
+        l.or_f2h.restype = ctypes.c_uint16
+        l.or_f2h.argtypes = [ctypes.c_float]
+        l.or_h2f_array.argtypes = [vp, vp, ctypes.c_size_t]
+        l.or_f2h_array.argtypes = [vp, vp, ctypes.c_size_t]
+        l.or_decode_ref32.argtypes = [vp, ctypes.c_int]
+        l.or_decode_ref32_rows.argtypes = [vp, vp, u64, vp, ctypes.c_int]
+        l.or_decode_f64.argtypes = [vp, vp, u64, vp, ctypes.c_int]
+        l.or_qlatent_f64.argtypes = [vp, vp]
+        l.or_gather_codes.argtypes = [vp, u64, vp, ctypes.c_uint32, ctypes.c_uint32, vp, vp, vp]
+        for f in ("or_decode_ref32", "or_decode_ref32_rows", "or_decode_f64", "or_qlatent_f64", "or_gather_codes"):
+            getattr(l, f).restype = ctypes.c_int
+        _lib = l
+    return _lib
+
+
+class OracleError(RuntimeError):
+    pass
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data
+
+
+def host_desc(geom, arrs: dict, out: np.ndarray | None = None) -> tuple[DecodeDesc, list]:
+    """aw_decode_desc over host numpy arrays (kept alive by the returned list)."""
+    keep = []
+
+    def c(a, dt):
+        if a is None:
+            return None
+        a = np.ascontiguousarray(a, dtype=dt)
+        keep.append(a)
+        return a
+
+    d = DecodeDesc()
+    d.layers, d.batch, d.queries = geom.layers, geom.batch, geom.queries
+    d.q_heads, d.kv_heads, d.head_dim = geom.q_heads, geom.kv_heads, geom.head_dim
+    d.dict_size, d.dict_heads = geom.dict_size, geom.dict_heads
+    d.hot_count, d.cold_count = geom.hot_count, geom.cold_count
+    d.refs_stride = max(geom.refs_stride, 1)
+    d.flags = AW_F_CAUSAL if geom.causal else 0
+    d.scale = geom.scale
+    d.hot_blocks, d.cold_blocks = geom.hot_blocks, geom.cold_blocks
+    d.q = _p(c(arrs["q"], np.uint16))
+    d.q_latent = _p(c(arrs.get("q_latent"), np.uint16))
+    d.hot_k = _p(c(arrs.get("hot_k"), np.uint16))
+    d.hot_v = _p(c(arrs.get("hot_v"), np.uint16))
+    d.cold = _p(c(arrs.get("cold"), np.uint16))
+    d.refs = _p(c(arrs["refs"], np.uint32))
+    d.seq_hot = _p(c(arrs.get("seq_hot"), np.uint32))
+    d.seq_cold = _p(c(arrs.get("seq_cold"), np.uint32))
+    d.dict = _p(c(arrs.get("dictionary"), np.uint16))
+    if out is not None:
+        keep.append(out)
+        d.out = out.ctypes.data
+    return d, keep
+
+
+def n_rows(geom) -> int:
+    return geom.layers * geom.batch * geom.queries * geom.q_heads
+
+
+def decode_ref32(geom, arrs: dict, threads: int = 8) -> np.ndarray:
+    """fp32 restatement of weaver_kernel.metal -> f16 [L,B,Q,Hq,d] (as float16)."""
+    out = np.zeros(n_rows(geom) * geom.head_dim, dtype=np.uint16)
+    d, keep = host_desc(geom, arrs, out)
+    rc = lib().or_decode_ref32(ctypes.byref(d), threads)
+    if rc:
+        raise OracleError(f"or_decode_ref32 failed: {rc}")
+    return out.view(np.float16).reshape(geom.layers, geom.batch, geom.queries, geom.q_heads, geom.head_dim)
+
+
+def decode_ref32_rows(geom, arrs: dict, rows, threads: int = 8) -> np.ndarray:
+    rows = np.ascontiguousarray(rows, dtype=np.uint64)
+    out = np.zeros(rows.size * geom.head_dim, dtype=np.uint16)
+    d, keep = host_desc(geom, arrs)
+    rc = lib().or_decode_ref32_rows(ctypes.byref(d), rows.ctypes.data, rows.size, out.ctypes.data, threads)
+    if rc:
+        raise OracleError(f"or_decode_ref32_rows failed: {rc}")
+    return out.view(np.float16).reshape(rows.size, geom.head_dim)
+
+
+def decode_f64(geom, arrs: dict, rows=None, threads: int = 8) -> np.ndarray:
+    """fp64 dense brute force.  rows=None: all rows -> [L,B,Q,Hq,d]; else [n, d]
+    for row ids ((l*B + b)*Q + q)*Hq + h."""
+    d, keep = host_desc(geom, arrs)
+    if rows is None:
+        out = np.zeros(n_rows(geom) * geom.head_dim, dtype=np.float64)
+        rc = lib().or_decode_f64(ctypes.byref(d), None, 0, out.ctypes.data, threads)
+        shape = (geom.layers, geom.batch, geom.queries, geom.q_heads, geom.head_dim)
+    else:
+        rows = np.ascontiguousarray(rows, dtype=np.uint64)
+        out = np.zeros(rows.size * geom.head_dim, dtype=np.float64)
+        rc = lib().or_decode_f64(ctypes.byref(d), rows.ctypes.data, rows.size, out.ctypes.data, threads)
+        shape = (rows.size, geom.head_dim)
+    if rc:
+        raise OracleError(f"or_decode_f64 failed: {rc}")
+    return out.reshape(shape)
+
+
+def qlatent_f64(geom, arrs: dict) -> np.ndarray:
+    out = np.zeros(n_rows(geom) * geom.dict_size, dtype=np.float64)
+    d, keep = host_desc(geom, arrs)
+    rc = lib().or_qlatent_f64(ctypes.byref(d), out.ctypes.data)
+    if rc:
+        raise OracleError(f"or_qlatent_f64 failed: {rc}")
+    return out.reshape(geom.layers, geom.batch, geom.queries, geom.q_heads, geom.dict_size)
+
+
+def gather_codes(codes_words: np.ndarray, dictionary_bits: np.ndarray, dict_size: int, head_dim: int):
+    """(idx u32 [n*4], coef f32 [n*4], atoms u16 [n*4, head_dim]) — bit-exact decode."""
+    w = np.ascontiguousarray(codes_words, dtype=np.uint16).reshape(-1, 8)
+    dic = np.ascontiguousarray(dictionary_bits, dtype=np.uint16)
+    n = w.shape[0]
+    idx = np.zeros(n * 4, dtype=np.uint32)
+    coef = np.zeros(n * 4, dtype=np.float32)
+    atoms = np.zeros((n * 4, head_dim), dtype=np.uint16)
+    rc = lib().or_gather_codes(w.ctypes.data, n, dic.ctypes.data, dict_size, head_dim, idx.ctypes.data,
+                               coef.ctypes.data, atoms.ctypes.data)
+    if rc:
+        raise OracleError(f"or_gather_codes failed: {rc}")
+    return idx, coef, atoms
+
+
+def h2f(bits: np.ndarray) -> np.ndarray:
+    b = np.ascontiguousarray(bits, dtype=np.uint16)
+    out = np.zeros(b.shape, dtype=np.float32)
+    lib().or_h2f_array(b.ctypes.data, out.ctypes.data, b.size)
+    return out
+
+
+def f2h(vals: np.ndarray) -> np.ndarray:
+    v = np.ascontiguousarray(vals, dtype=np.float32)
+    out = np.zeros(v.shape, dtype=np.uint16)
+    lib().or_f2h_array(v.ctypes.data, out.ctypes.data, v.size)
+    return out

@@ -1,0 +1,127 @@
+"""GPU parity of the Weaver decode path against the CPU oracle.
+
+Every case runs through the C ABI (aw_decode / aw_decode_device) on cuda:0 and
+is compared with the fp64 brute force of oracle/weaver_oracle.c on the same
+seeded inputs: max-abs <= 2e-3 and rel-L2 <= 1e-3.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from aether_nexus_amd import workloads as W
+from aether_nexus_amd.types import SPARSE_CODE_DTYPE, WeaverParams
+from oracle import oracle
+from tests.helpers import assert_close, run_gpu
+
+pytestmark = pytest.mark.gpu
+
+
+def check(engine, stream, geom, seed=0, rows=None, what=""):
+    wl = W.generate(geom, seed=seed)
+    arrs = W.host_arrays(wl)
+    got = run_gpu(engine, wl, stream)
+    if rows is None:
+        ref = oracle.decode_f64(geom, arrs)
+        assert_close(got, ref, what or str(geom))
+    else:
+        ref = oracle.decode_f64(geom, arrs, rows=rows)
+        assert_close(got.reshape(-1, geom.head_dim)[rows], ref, what or str(geom))
+    return got
+
+
+# -- mirrors of the reference's own GPU tests (nexus-core/src/weaver.rs:333-420)
+
+def test_engine_creates_pipeline(engine):
+    """weaver.rs:335-356: engine creation, device name, max threads >= 32."""
+    assert engine.device_name()
+    assert engine.max_threads_per_threadgroup() >= 32
+
+
+def _reference_test_inputs():
+    q_heads, kv_heads, head_dim, dict_size, hot_count, cold_count = 32, 8, 128, 512, 2, 1
+    one = np.float16(1.0)
+    q_exact = np.full(q_heads * head_dim, one)
+    q_latent = np.full(q_heads * dict_size, one)
+    hot_pool = np.full(hot_count * 16 * kv_heads * head_dim, one)
+    # refs [0, 1, 2]: the cold ref names block 2, so the zero cold pool holds 3 blocks.
+    cold = np.zeros(3 * 16 * kv_heads, dtype=SPARSE_CODE_DTYPE)
+    refs = np.arange(hot_count + cold_count, dtype=np.uint32)
+    dictionary = np.full(kv_heads * dict_size * head_dim, one)
+    params = WeaverParams(q_heads=q_heads, kv_heads=kv_heads, head_dim=head_dim, block_size=16,
+                          gqa_group=q_heads // kv_heads, hot_count=hot_count, cold_count=cold_count,
+                          dict_size=dict_size, sparsity_k=4)
+    return q_exact, q_latent, hot_pool, cold, refs, dictionary, params
+
+
+def test_decode_produces_output_known_answer(engine):
+    """weaver.rs:359-420 inputs.  32 hot scores of 128 beat 16 zero cold scores
+    by e^128, so every output is exactly 1.0 (0x3C00)."""
+    out = engine.decode(*_reference_test_inputs())
+    assert out.data.shape == (32 * 128,)
+    assert np.any(out.data != 0)
+    assert np.all(out.data.view(np.uint16) == 0x3C00)
+
+
+def test_bench_inputs_known_answer(engine):
+    """bench.rs:113-133 inputs (0.01 everywhere, zero codes, refs 0..80).  The
+    cold refs 64..79 name blocks past the reference's 16-block cold pool; here
+    the zero pool holds 80 blocks.  Closed form: 1024 hot tokens of score
+    128*f16(0.01)^2 and 256 cold tokens of score 0 give 0.0080222 -> f16 0x201B."""
+    val = np.float16(0.01)
+    q_heads, kv_heads, head_dim, dict_size, hot, cold_n = 32, 8, 128, 512, 64, 16
+    params = WeaverParams(q_heads=q_heads, kv_heads=kv_heads, head_dim=head_dim, block_size=16, gqa_group=4,
+                          hot_count=hot, cold_count=cold_n, dict_size=dict_size, sparsity_k=4)
+    out = engine.decode(np.full(q_heads * head_dim, val), np.full(q_heads * dict_size, val),
+                        np.full(hot * 16 * kv_heads * head_dim, val), np.zeros(80 * 16 * kv_heads, SPARSE_CODE_DTYPE),
+                        np.arange(hot + cold_n, dtype=np.uint32), np.full(kv_heads * dict_size * head_dim, val), params)
+    v = float(val)
+    s = head_dim * v * v
+    expect = 1024 * np.exp(s) * v / (1024 * np.exp(s) + 256)
+    bits = out.data.view(np.uint16)
+    assert abs(expect - 0.0080222) < 1e-6
+    assert np.all(np.abs(out.data.astype(np.float64) - expect) < 1e-5)
+    assert set(np.unique(bits)).issubset({0x201B, 0x201C})  # within one f16 ulp of the tie point
+    assert np.mean(bits == 0x201B) > 0.5
+
+
+# -- the workloads, reference-literal and extended
+
+def test_tiny_shared_dict(engine, stream):
+    check(engine, stream, W.tiny(), seed=1, what="tiny shared dict")
+
+
+def test_tiny_per_head_dict(engine, stream):
+    check(engine, stream, W.tiny(dict_heads=8), seed=2, what="tiny per-kv-head dict")
+
+
+def test_tiny_reference_literal_host_api(engine):
+    """aw_decode with the reference's arguments: f16 q_latent given, per-kv-head
+    dictionary, scale 1, permuted refs with bit 31 set on some."""
+    geom = W.tiny(dict_heads=8, tag_bit31=True)
+    wl = W.generate(geom, seed=3)
+    a = W.host_arrays(wl)
+    ql = oracle.qlatent_f64(geom, a).astype(np.float16)
+    a["q_latent"] = ql.view(np.uint16)
+    ref = oracle.decode_f64(geom, a).reshape(-1)
+    params = WeaverParams(q_heads=8, kv_heads=8, head_dim=64, block_size=16, gqa_group=1,
+                          hot_count=geom.hot_count, cold_count=geom.cold_count, dict_size=512, sparsity_k=4)
+    out = engine.decode(a["q"], ql, a["hot_k"], a["cold"], a["refs"].reshape(-1), a["dictionary"], params)
+    assert_close(out.data, ref, "tiny reference-literal aw_decode")
+
+
+def test_hot_only(engine, stream):
+    check(engine, stream, W.hot_only(), seed=4, what="hot_only 32q/8kv d128 hot 4096")
+
+
+def test_hot_cold(engine, stream):
+    check(engine, stream, W.hot_cold(), seed=5, what="hot_cold hot 2048 cold 32768")
+
+
+def test_batched_reduced(engine, stream):
+    check(engine, stream, W.batched(batch=4, cold_count=512), seed=6, what="batched B4 zipf cold 8192")
+
+
+def test_spec_verify_reduced(engine, stream):
+    check(engine, stream, W.spec_verify(layers=2, batch=2, hot_count=16, cold_count=64), seed=7,
+          what="spec_verify L2 B2 Q8 causal")
