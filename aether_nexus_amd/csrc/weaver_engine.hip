@@ -74,10 +74,11 @@ struct Layout {
 
 bool supported_head_dim(uint32_t d) { return d == 64 || d == 128; }
 
-// Largest cold row chunk (1, 2 or 4) whose LDS tables fit.
+// Largest cold row chunk (1, 2 or 4) whose LDS tables fit (with at least one
+// 1024-token split's block refs).
 uint32_t pick_rc(uint32_t R, uint32_t A, size_t max_lds) {
     uint32_t rc = R >= 4 ? 4 : (R >= 2 ? 2 : 1);
-    while (rc > 1 && aw::cold_smem_bytes(A, (int)rc) > max_lds) rc /= 2;
+    while (rc > 1 && aw::cold_smem_bytes(A, (int)rc, 1024) > max_lds) rc /= 2;
     return rc;
 }
 
@@ -134,7 +135,7 @@ int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, Layout* L, char
     // Hot: ~8 waves per CU, >= 64 tokens per wave, splits <= kMaxSplits.
     if (d->hot_count > 0) {
         const uint64_t n_tok = (uint64_t)d->hot_count * kBlock;
-        uint64_t want = cdiv((uint64_t)n_cu * 8, n_lbg);
+        uint64_t want = cdiv((uint64_t)n_cu * 16, n_lbg);
         uint64_t cap = std::max<uint64_t>(1, cdiv(n_tok, 64));
         uint64_t S = std::max<uint64_t>(1, std::min<uint64_t>({want, cap, (uint64_t)aw::kMaxSplits}));
         uint64_t tps = align_up(cdiv(n_tok, S), 32);
@@ -144,18 +145,31 @@ int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, Layout* L, char
     // Cold: one work-group per CU at a time (LDS bound); >= 1024 tokens per split.
     if (d->cold_count > 0) {
         o.rc = pick_rc(R, A, max_lds);
-        if (aw::cold_smem_bytes(A, (int)o.rc) > max_lds) {
+        if (aw::cold_smem_bytes(A, (int)o.rc, 1024) > max_lds) {
             put_msg(msg, mlen, "dict_size %u needs %zu bytes of LDS, device allows %zu", A,
-                    aw::cold_smem_bytes(A, (int)o.rc), max_lds);
+                    aw::cold_smem_bytes(A, (int)o.rc, 1024), max_lds);
             return AW_E_UNSUPPORTED;
         }
         o.n_chunks = cdiv(R, o.rc);
         const uint64_t n_tok = (uint64_t)d->cold_count * kBlock;
         const uint64_t items = n_lbg * o.n_chunks;
         uint64_t want = cdiv((uint64_t)n_cu * 2, items);
-        uint64_t cap = std::max<uint64_t>(1, cdiv(n_tok, 1024));
+        // >= 1024 tokens per split, and bin partials (A*rc*4 bytes per split) at most
+        // twice the code bytes of the sequence.
+        uint64_t cap = std::max<uint64_t>(1, std::min<uint64_t>(cdiv(n_tok, 1024),
+                                                                (2 * n_tok * 16) / ((uint64_t)A * o.rc * 4)));
         uint64_t S = std::max<uint64_t>(1, std::min<uint64_t>({want, cap, (uint64_t)aw::kMaxSplits}));
         uint64_t tps = align_up(cdiv(n_tok, S), 16);
+        // The split's block refs live in LDS too: shorten splits until they fit.
+        while (tps > 1024 && aw::cold_smem_bytes(A, (int)o.rc, (uint32_t)tps) > max_lds) {
+            ++S;
+            tps = align_up(cdiv(n_tok, S), 16);
+        }
+        if (cdiv(n_tok, tps) > (uint64_t)aw::kMaxSplits) {
+            put_msg(msg, mlen, "cold pool of %llu tokens needs more than %d splits", (unsigned long long)n_tok,
+                    aw::kMaxSplits);
+            return AW_E_UNSUPPORTED;
+        }
         o.info.cold_tokens_per_split = (uint32_t)tps;
         o.info.cold_splits = cdiv(n_tok, tps);
         o.info.cold_row_chunk = o.rc;
@@ -163,11 +177,12 @@ int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, Layout* L, char
         const uint32_t dh = d->dict_heads;
         const uint32_t hg = dh == 1 ? d->kv_heads : 1;
         o.rows_per_group = d->batch * hg * R;
-        o.tiles_per_group = cdiv(o.rows_per_group, 16);
+        o.tiles_per_group = cdiv(o.rows_per_group, 64);
         o.n_groups = d->layers * dh;
+        // Enough work-groups to cover the CUs, >= 128 atoms per range.
         const uint64_t tiles = (uint64_t)o.tiles_per_group * o.n_groups;
         uint32_t n_ar = 1;
-        if (tiles < (uint64_t)n_cu / 2) n_ar = (uint32_t)std::min<uint64_t>(cdiv(n_cu, tiles), cdiv(A, 128));
+        if (tiles < (uint64_t)n_cu) n_ar = (uint32_t)std::min<uint64_t>(cdiv(n_cu, tiles), std::max(1u, A / 128));
         o.atoms_per_range = (uint32_t)align_up(cdiv(A, n_ar), 32);
         o.n_ar = cdiv(A, o.atoms_per_range);
     }
@@ -205,6 +220,8 @@ int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, Layout* L, char
 struct aw_engine {
     int device = 0;
     hipStream_t stream = nullptr;
+    hipStream_t side = nullptr;               // hot kernel, concurrent with q.D^T + cold
+    hipEvent_t ev_fork = nullptr, ev_join = nullptr;
     std::string name, last_error;
     uint64_t max_threads = 0;
     size_t max_lds = 0;
@@ -415,7 +432,7 @@ int launch_cold(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* ws
     (void)HD;
     const uint64_t grid = (uint64_t)cdiv(a.n_units, 8) * 8 * d->kv_heads;
     if (grid > 0x7FFFFFFFull) return fail(e, AW_E_UNSUPPORTED, "cold grid too large");
-    const size_t smem = aw::cold_smem_bytes(A, (int)o.rc);
+    const size_t smem = aw::cold_smem_bytes(A, (int)o.rc, a.tokens_per_split);
     StageTimer t(e, AW_STAGE_COLD, st);
     switch (o.rc) {
     case 4:
@@ -465,7 +482,7 @@ int launch_finish(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* 
     const uint64_t gx = (uint64_t)o.tiles_per_group * o.n_groups;
     if (gx > 0x7FFFFFFFull) return fail(e, AW_E_UNSUPPORTED, "finish grid too large");
     StageTimer t(e, AW_STAGE_FINISH, st);
-    hipLaunchKernelGGL((aw::finish_kernel<HD>), dim3((uint32_t)gx, o.n_ar), dim3(64 * aw::kFinishWaves), 0, st, a);
+    hipLaunchKernelGGL((aw::finish_kernel<HD>), dim3((uint32_t)gx, o.n_ar), dim3(256), 0, st, a);
     AW_HIP(e, hipGetLastError());
     return AW_OK;
 }
@@ -494,7 +511,7 @@ int launch_merge(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* w
     a.hot_splits = o.info.hot_splits;
     a.n_ar = o.n_ar;
     a.total_rows = (uint64_t)d->layers * d->batch * d->kv_heads * a.rows_r;
-    const uint64_t gx = cdiv(a.total_rows, 16);
+    const uint64_t gx = cdiv(a.total_rows, 4);
     if (gx > 0x7FFFFFFFull) return fail(e, AW_E_UNSUPPORTED, "merge grid too large");
     StageTimer t(e, AW_STAGE_MERGE, st);
     hipLaunchKernelGGL((aw::merge_kernel<HD>), dim3((uint32_t)gx), dim3(256), 0, st, a);
@@ -502,16 +519,29 @@ int launch_merge(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* w
     return AW_OK;
 }
 
+// Stage order on `st`: [q.D^T] -> cold -> finish [-> merge].  The hot kernel
+// (HBM-bound) runs on the engine's side stream concurrently with the cold
+// kernel (LDS-bound) and is joined before the finish.  With profiling on,
+// everything runs on `st` so each kernel's event-timed duration is its own.
 template <int HD>
 int run_pipeline(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* ws, hipStream_t st) {
     int rc = AW_OK;
     const bool cold = o.info.cold_splits > 0;
+    const bool hot = o.info.hot_splits > 0;
+    const bool fork = hot && cold && !e->profiling;
+    if (fork) {
+        AW_HIP(e, hipEventRecord(e->ev_fork, st));
+        AW_HIP(e, hipStreamWaitEvent(e->side, e->ev_fork, 0));
+        if ((rc = launch_hot<HD>(e, d, o, ws, e->side))) return rc;
+        AW_HIP(e, hipEventRecord(e->ev_join, e->side));
+    } else if (hot) {
+        if ((rc = launch_hot<HD>(e, d, o, ws, st))) return rc;
+    }
     if (cold && o.info.computes_q_latent)
         if ((rc = launch_project<HD>(e, d, o, (uint16_t*)(ws + o.off_ql), st))) return rc;
-    if (o.info.hot_splits)
-        if ((rc = launch_hot<HD>(e, d, o, ws, st))) return rc;
     if (cold) {
         if ((rc = launch_cold(e, d, o, ws, st))) return rc;
+        if (fork) AW_HIP(e, hipStreamWaitEvent(st, e->ev_join, 0));
         if ((rc = launch_finish<HD>(e, d, o, ws, st))) return rc;
         if (o.n_ar > 1)
             if ((rc = launch_merge<HD>(e, d, o, ws, st))) return rc;
@@ -715,6 +745,9 @@ int aw_engine_create(int device, aw_engine** out) {
     (void)hipFuncSetAttribute((const void*)aw::cold_kernel<1, kColdCPT>, hipFuncAttributeMaxDynamicSharedMemorySize,
                         (int)e->max_lds);
     if (hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking) != hipSuccess ||
+        hipStreamCreateWithFlags(&e->side, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&e->ev_fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&e->ev_join, hipEventDisableTiming) != hipSuccess ||
         hipMalloc((void**)&e->err, 256) != hipSuccess || hipMemset(e->err, 0, 256) != hipSuccess) {
         aw_engine_destroy(e);
         return AW_E_HIP;
@@ -732,6 +765,10 @@ void aw_engine_destroy(aw_engine* e) {
     for (DevBuf* b : {&e->q, &e->ql, &e->hot, &e->cold, &e->refs, &e->dict, &e->out, &e->ws})
         if (b->ptr) (void)hipFree(b->ptr);
     if (e->err) (void)hipFree(e->err);
+    if (e->side) (void)hipStreamSynchronize(e->side);
+    if (e->ev_fork) (void)hipEventDestroy(e->ev_fork);
+    if (e->ev_join) (void)hipEventDestroy(e->ev_join);
+    if (e->side) (void)hipStreamDestroy(e->side);
     if (e->stream) (void)hipStreamDestroy(e->stream);
     delete e;
 }

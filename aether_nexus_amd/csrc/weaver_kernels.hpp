@@ -46,7 +46,6 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kColdThreads = 512;
 constexpr int kFinishWaves = 4;
 constexpr int kMaxSplits = 64;
-constexpr float kColdSlack = 12.0f; // log2 headroom of a cold work-group's running reference
 
 // Error bits written to the engine's device error word.
 constexpr uint32_t kErrHotRef = 1u, kErrColdRef = 2u, kErrAtom = 4u;
@@ -434,17 +433,32 @@ __global__ __launch_bounds__(64) void hot_kernel(HotArgs a) {
 // ----------------------------------------------- cold pool, scores + bins
 //
 // Work item = (layer*batch+seq, chunk of RC query rows, split) x kv head g.
-// LDS: q_latent table [A][RC] f16, bins [A][RC] f32, reduction scratch.
-// Each thread scores CPT codes per tile (one 16-byte load each, next tile
-// prefetched).  The work-group keeps one reference maximum per row; weights
-// are 2^(s - ref) with s <= ref + kColdSlack, and the bins and partial sums are
-// rescaled only when a tile exceeds the reference by more than the slack.
-// The kv heads of one (sequence, chunk, split) are placed on one XCD (work
-// groups are dealt round-robin over the 8 XCDs), so the 128-byte lines that
-// interleave their 16-byte codes are fetched from HBM once per XCD L2.
+// LDS: q_latent table [A][RC] f16; per atom NP = ceil(RC/2) 64-bit bins,
+// each holding two rows' sums as 32-bit fixed point; the split's block refs.
+//
+// Integer bins: on gfx950 an LDS ds_add_f32 retires about one lane per 3
+// cycles per CU whatever the addresses, ds_add_u64 about one lane per 0.3
+// cycles (measured).  A row pair (v0, v1) is added as the 64-bit integer
+// v1*2^32 + v0 (v0 sign-extended); sums of such words are exact and decode back
+// to (sum v0, sum v1) while each row sum stays inside int32.
+//
+// Values are p*c*2^F with p = 2^(s - ref_r).  ref_r (integral, log2 units) and
+// F come from the split's first tile: ref_r = ceil(max score of the tile),
+// F sized so that the planned bound on sum |p*c| over the whole split stays
+// near 2^28.  The work-group then streams every tile with no further
+// synchronisation.  At the end a conservative bound, 4 * max|c| * sum_t sum_r p,
+// proves the bins could not have overflowed; when it cannot (scores far above
+// the first tile's, or coefficients far larger), the split is recomputed
+// exactly: a pass for the per-row maxima, a pass for the exact bound, a pass
+// for the bins.  Truncating float->int conversion keeps errors below one unit
+// of 2^-F per contribution, far under the output tolerance at these scales.
+//
+// The kv heads of one (sequence, chunk, split) run on one XCD (work-groups are
+// dealt round-robin over the 8 XCDs), so the 128-byte lines interleaving their
+// 16-byte codes come from HBM once per XCD L2.
 template <int RC, int CPT>
 __global__ __launch_bounds__(kColdThreads) void cold_kernel(ColdArgs a) {
-    constexpr int NT = kColdThreads, NW = NT / 64;
+    constexpr int NT = kColdThreads, NW = NT / 64, NP = (RC + 1) / 2, NRED = 2 * RC + 2;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t x = blockIdx.x % 8u, k = blockIdx.x / 8u;
@@ -476,213 +490,346 @@ __global__ __launch_bounds__(kColdThreads) void cold_kernel(ColdArgs a) {
     }
 
     const uint32_t qtab_bytes = (A * RC * 2 + 15) & ~15u;
+    const uint32_t n_blk = (t_end - t_begin + 15) / 16; // t_begin is a multiple of 16
     _Float16* qtab = (_Float16*)smem;
-    float* bins = (float*)(smem + qtab_bytes);
-    float* red = bins + (uint64_t)A * RC; // [2][NW][RC]
+    uint64_t* bins = (uint64_t*)(smem + qtab_bytes);       // [A][NP]
+    uint32_t* sref = (uint32_t*)(bins + (uint64_t)A * NP); // [n_blk] physical blocks, ~0 = invalid
+    float* red = (float*)(sref + ((n_blk + 3) & ~3u));    // [NW][NRED]
 
     // q_latent rows of this chunk into LDS; rows past R are zero.
-    for (uint32_t at = tid; at < A; at += NT) {
+    {
+        uint64_t rbase[RC];
+        bool rok[RC];
 #pragma unroll
         for (int rr = 0; rr < RC; ++rr) {
             const uint32_t r = c * RC + rr;
-            uint16_t bits = 0;
-            if (r < R)
-                bits = a.ql[(uint64_t)lb * a.s_lb + g * a.s_g + (r / a.gqa) * a.s_q + (r % a.gqa) * a.s_j +
-                            (uint64_t)at * a.s_a];
-            qtab[at * RC + rr] = __builtin_bit_cast(_Float16, bits);
+            rok[rr] = r < R;
+            rbase[rr] = rok[rr] ? (uint64_t)lb * a.s_lb + g * a.s_g + (uint64_t)(r / a.gqa) * a.s_q +
+                                      (uint64_t)(r % a.gqa) * a.s_j
+                                : 0;
+        }
+        for (uint32_t at = tid; at < A; at += NT)
+#pragma unroll
+            for (int rr = 0; rr < RC; ++rr)
+                qtab[at * RC + rr] =
+                    __builtin_bit_cast(_Float16, rok[rr] ? a.ql[rbase[rr] + (uint64_t)at * a.s_a] : (uint16_t)0);
+    }
+    // The split's block refs, resolved once, so code addresses come from LDS.
+    {
+        const uint32_t* refs = a.refs + (uint64_t)l * a.refs_layer + (uint64_t)(lb % a.batch) * a.refs_stride +
+                               a.hot_count + t_begin / 16;
+        for (uint32_t i = tid; i < n_blk; i += NT) {
+            uint32_t ref = refs[i] & kRefMask;
+            if (ref >= a.cold_blocks) {
+                flag_error(a.err, kErrColdRef);
+                ref = ~0u;
+            }
+            sref[i] = ref;
         }
     }
-    for (uint32_t i = tid; i < A * RC; i += NT) bins[i] = 0.0f;
-    __syncthreads();
 
-    const uint32_t* refs =
-        a.refs + (uint64_t)l * a.refs_layer + (uint64_t)(lb % a.batch) * a.refs_stride + a.hot_count;
     const uint4_t* cold = a.cold + (uint64_t)l * a.cold_layer;
+    const uint32_t tile_tokens = NT * CPT;
+    const uint32_t n_tiles = (t_end - t_begin + tile_tokens - 1) / tile_tokens;
+    const float sl = a.scale_log2;
 
     auto load_tile = [&](uint32_t t0, uint4_t (&buf)[CPT], bool (&ok)[CPT]) {
 #pragma unroll
         for (int kk = 0; kk < CPT; ++kk) {
             const uint32_t t = t0 + kk * NT + tid;
             bool v = t < t_end;
+            buf[kk] = (uint4_t)0u; // a token past the split or behind a bad ref scores as a zero code
             if (v) {
-                const uint32_t ref = refs[t >> 4] & kRefMask;
-                if (ref >= a.cold_blocks) {
-                    flag_error(a.err, kErrColdRef);
-                    v = false;
-                } else {
-                    buf[kk] = cold[((uint64_t)ref * kBlockTokens + (t & 15u)) * a.kv_heads + g];
-                }
+                const uint32_t ref = sref[(t - t_begin) >> 4];
+                v = ref != ~0u;
+                if (v) buf[kk] = cold[((uint64_t)ref * kBlockTokens + (t & 15u)) * a.kv_heads + g];
             }
             ok[kk] = v;
         }
     };
-
-    float mref[RC], lpart[RC];
+    // Unscaled score sums of one code for the RC rows: sum_k c_k * q_latent[idx_k][r].
+    auto score = [&](const uint4_t cw, float (&sc)[RC], uint32_t (&ia)[4], float (&cf)[4]) {
+        ia[0] = cw[0] & 0xFFFFu;
+        ia[1] = cw[0] >> 16;
+        ia[2] = cw[1] & 0xFFFFu;
+        ia[3] = cw[1] >> 16;
+        cf[0] = h2f_bits(cw[2] & 0xFFFFu);
+        cf[1] = h2f_bits(cw[2] >> 16);
+        cf[2] = h2f_bits(cw[3] & 0xFFFFu);
+        cf[3] = h2f_bits(cw[3] >> 16);
+        if (max(max(ia[0], ia[1]), max(ia[2], ia[3])) >= A) { // out-of-range atoms: skip those terms
+            flag_error(a.err, kErrAtom);
 #pragma unroll
-    for (int rr = 0; rr < RC; ++rr) {
-        mref[rr] = -INFINITY;
-        lpart[rr] = 0.0f;
-    }
-
-    uint4_t cur[CPT];
-    bool curv[CPT];
-    load_tile(t_begin, cur, curv);
-    int par = 0;
-    for (uint32_t t0 = t_begin; t0 < t_end; t0 += NT * CPT, par ^= 1) {
-        uint4_t nxt[CPT];
-        bool nxtv[CPT];
-        const bool more = t0 + NT * CPT < t_end;
-        if (more) load_tile(t0 + NT * CPT, nxt, nxtv);
-
-        // Decode codes and score them (metal:182-190).
-        float sc[CPT][RC];
-        uint32_t ia[CPT][4];
-        float cf[CPT][4];
-        float tmax[RC];
-#pragma unroll
-        for (int rr = 0; rr < RC; ++rr) tmax[rr] = -INFINITY;
-#pragma unroll
-        for (int kk = 0; kk < CPT; ++kk) {
-            const uint4_t cw = cur[kk];
-            ia[kk][0] = cw[0] & 0xFFFFu;
-            ia[kk][1] = cw[0] >> 16;
-            ia[kk][2] = cw[1] & 0xFFFFu;
-            ia[kk][3] = cw[1] >> 16;
-            cf[kk][0] = h2f_bits(cw[2] & 0xFFFFu);
-            cf[kk][1] = h2f_bits(cw[2] >> 16);
-            cf[kk][2] = h2f_bits(cw[3] & 0xFFFFu);
-            cf[kk][3] = h2f_bits(cw[3] >> 16);
-#pragma unroll
-            for (int rr = 0; rr < RC; ++rr) sc[kk][rr] = 0.0f;
-            if (curv[kk]) {
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    if (ia[kk][j] >= A) {
-                        flag_error(a.err, kErrAtom);
-                        ia[kk][j] = 0;
-                        cf[kk][j] = 0.0f;
-                    }
-                    const _Float16* qp = qtab + ia[kk][j] * RC;
-                    if constexpr (RC == 4) {
-                        const half4_t qv = *(const half4_t*)qp;
-#pragma unroll
-                        for (int rr = 0; rr < 4; ++rr) sc[kk][rr] += cf[kk][j] * (float)qv[rr];
-                    } else {
-#pragma unroll
-                        for (int rr = 0; rr < RC; ++rr) sc[kk][rr] += cf[kk][j] * (float)qp[rr];
-                    }
+            for (int j = 0; j < 4; ++j)
+                if (ia[j] >= A) {
+                    ia[j] = 0;
+                    cf[j] = 0.0f;
                 }
+        }
 #pragma unroll
-                for (int rr = 0; rr < RC; ++rr) {
-                    sc[kk][rr] *= a.scale_log2;
-                    tmax[rr] = fmaxf(tmax[rr], sc[kk][rr]);
-                }
+        for (int rr = 0; rr < RC; ++rr) sc[rr] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const _Float16* qp = qtab + ia[j] * RC;
+            if constexpr (RC == 4) {
+                const half4_t qv = *(const half4_t*)qp;
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) sc[rr] += cf[j] * (float)qv[rr];
+            } else {
+#pragma unroll
+                for (int rr = 0; rr < RC; ++rr) sc[rr] += cf[j] * (float)qp[rr];
             }
         }
-        // Work-group maximum of this tile.
+    };
+    auto cmax4 = [](const float (&cf)[4]) { return fmaxf(fmaxf(fabsf(cf[0]), fabsf(cf[1])), fmaxf(fabsf(cf[2]), fabsf(cf[3]))); };
+
+    // Work-group sums/maxima of up to NRED per-lane values (one barrier pair).
+    auto wg_reduce = [&](float (&v)[NRED], const bool (&is_max)[NRED]) {
+        __syncthreads(); // previous readers of `red` are done
 #pragma unroll
-        for (int rr = 0; rr < RC; ++rr) {
-            const float wm = wave_max(tmax[rr]);
-            if (lane == 0) red[(par * NW + wave) * RC + rr] = wm;
+        for (int i = 0; i < NRED; ++i) {
+            const float w = is_max[i] ? wave_max(v[i]) : wave_sum(v[i]);
+            if (lane == 0) red[wave * NRED + i] = w;
         }
         __syncthreads();
-        bool rescale = false;
-        float fac[RC];
 #pragma unroll
-        for (int rr = 0; rr < RC; ++rr) {
-            float tm = -INFINITY;
-#pragma unroll
-            for (int w = 0; w < NW; ++w) tm = fmaxf(tm, red[(par * NW + w) * RC + rr]);
-            fac[rr] = 1.0f;
-            if (tm != -INFINITY && (mref[rr] == -INFINITY || tm > mref[rr] + kColdSlack)) {
-                if (mref[rr] != -INFINITY) {
-                    fac[rr] = fast_exp2(mref[rr] - tm);
-                    rescale = true;
-                }
-                mref[rr] = tm;
-                lpart[rr] *= fac[rr];
-            }
+        for (int i = 0; i < NRED; ++i) {
+            float acc = is_max[i] ? -INFINITY : 0.0f;
+            for (int w = 0; w < NW; ++w) acc = is_max[i] ? fmaxf(acc, red[w * NRED + i]) : acc + red[w * NRED + i];
+            v[i] = acc;
         }
-        if (rescale) { // uniform across the work-group
-            for (uint32_t at = tid; at < A; at += NT)
+    };
+
+    float ref[RC];
+    int F = 0;
+    float lpart[RC], cmx = 0.0f;
+    uint4_t cur[CPT];
+    bool curv[CPT];
+    bool exact = false;
+    for (int attempt = 0; attempt < 2; ++attempt) {
+        for (uint32_t i = tid; i < A * NP; i += NT) bins[i] = 0ull;
+        __syncthreads();
+        load_tile(t_begin, cur, curv);
+        if (!exact) {
+            // Reference and scale from the first tile.
+            float v[NRED];
+            bool is_max[NRED];
 #pragma unroll
-                for (int rr = 0; rr < RC; ++rr) bins[at * RC + rr] *= fac[rr];
-            __syncthreads();
-        }
-        // Softmax weights into the per-atom bins.
-#pragma unroll
-        for (int kk = 0; kk < CPT; ++kk) {
-            if (!curv[kk]) continue;
-            float p[RC];
-#pragma unroll
-            for (int rr = 0; rr < RC; ++rr) {
-                p[rr] = fast_exp2(sc[kk][rr] - mref[rr]);
-                lpart[rr] += p[rr];
+            for (int i = 0; i < NRED; ++i) {
+                v[i] = i < RC ? -INFINITY : 0.0f;
+                is_max[i] = i < RC;
             }
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                float* bp = bins + ia[kk][j] * RC;
-#pragma unroll
-                for (int rr = 0; rr < RC; ++rr)
-                    __hip_atomic_fetch_add(bp + rr, p[rr] * cf[kk][j], __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_WORKGROUP);
-            }
-        }
-        if (more) {
+            float scs[CPT][RC];
 #pragma unroll
             for (int kk = 0; kk < CPT; ++kk) {
-                cur[kk] = nxt[kk];
-                curv[kk] = nxtv[kk];
+                uint32_t ia[4];
+                float cf[4];
+                score(cur[kk], scs[kk], ia, cf);
+                if (curv[kk]) {
+#pragma unroll
+                    for (int rr = 0; rr < RC; ++rr) v[rr] = fmaxf(v[rr], scs[kk][rr] * sl);
+                    v[2 * RC] = fmaxf(v[2 * RC], cmax4(cf)); // summed below: only a plan
+                }
+            }
+            wg_reduce(v, is_max);
+#pragma unroll
+            for (int rr = 0; rr < RC; ++rr) ref[rr] = v[rr] == -INFINITY ? 0.0f : ceilf(v[rr]);
+            float w[NRED];
+#pragma unroll
+            for (int i = 0; i < NRED; ++i) {
+                w[i] = 0.0f;
+                is_max[i] = false;
+            }
+#pragma unroll
+            for (int kk = 0; kk < CPT; ++kk)
+                if (curv[kk]) {
+                    float ps = 0.0f;
+#pragma unroll
+                    for (int rr = 0; rr < RC; ++rr) ps += fast_exp2(scs[kk][rr] * sl - ref[rr]);
+                    uint32_t ia[4];
+                    float cf[4], dummy[RC];
+                    score(cur[kk], dummy, ia, cf);
+                    w[0] += 4.0f * cmax4(cf) * ps;
+                }
+            wg_reduce(w, is_max);
+            const float plan = w[0] * (float)n_tiles; // bound on sum |p*c| over the split, if tiles are alike
+            F = plan > 0.0f ? min(100, max(-100, 28 - (ilogbf(plan) + 1))) : 0;
+        }
+        // Stream every tile into the bins.
+        const float Ff = (float)F;
+        float rf[RC];
+#pragma unroll
+        for (int rr = 0; rr < RC; ++rr) {
+            lpart[rr] = 0.0f;
+            rf[rr] = Ff - ref[rr];
+        }
+        cmx = 0.0f;
+        for (uint32_t t0 = t_begin; t0 < t_end; t0 += tile_tokens) {
+            uint4_t nxt[CPT];
+            bool nxtv[CPT];
+            const bool more = t0 + tile_tokens < t_end;
+            if (more) load_tile(t0 + tile_tokens, nxt, nxtv);
+#pragma unroll
+            for (int kk = 0; kk < CPT; ++kk) {
+                if (!curv[kk]) continue;
+                float sc[RC];
+                uint32_t ia[4];
+                float cf[4];
+                score(cur[kk], sc, ia, cf);
+                cmx = fmaxf(cmx, cmax4(cf));
+                float ps[RC]; // p * 2^F
+#pragma unroll
+                for (int rr = 0; rr < RC; ++rr) {
+                    ps[rr] = fast_exp2(fmaf(sc[rr], sl, rf[rr]));
+                    lpart[rr] += ps[rr];
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    uint64_t* bp = bins + ia[j] * NP;
+#pragma unroll
+                    for (int pp = 0; pp < NP; ++pp) {
+                        const int32_t v0 = (int32_t)(ps[2 * pp] * cf[j]);
+                        const int32_t v1 = (2 * pp + 1 < RC) ? (int32_t)(ps[min(2 * pp + 1, RC - 1)] * cf[j]) : 0;
+                        const uint64_t wv = ((uint64_t)(uint32_t)v1 << 32) + (uint64_t)(int64_t)v0;
+                        __hip_atomic_fetch_add(bp + pp, wv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                    }
+                }
+            }
+            if (more) {
+#pragma unroll
+                for (int kk = 0; kk < CPT; ++kk) {
+                    cur[kk] = nxt[kk];
+                    curv[kk] = nxtv[kk];
+                }
             }
         }
-    }
-    __syncthreads();
+        // Overflow proof: every |bin| <= sum over contributions |p*c|*2^F <= 4*max|c|*sum_r sum_t p*2^F.
+        float v[NRED];
+        bool is_max[NRED];
+#pragma unroll
+        for (int i = 0; i < NRED; ++i) {
+            v[i] = 0.0f;
+            is_max[i] = false;
+        }
+#pragma unroll
+        for (int rr = 0; rr < RC; ++rr) v[rr] = lpart[rr];
+        v[2 * RC] = cmx;
+        is_max[2 * RC] = true;
+        wg_reduce(v, is_max);
+        float psum = 0.0f;
+#pragma unroll
+        for (int rr = 0; rr < RC; ++rr) {
+            lpart[rr] = v[rr];
+            psum += v[rr];
+        }
+        const float bound = 4.0f * v[2 * RC] * psum; // already in units of 2^-F
+        if (exact || (bound < 2147483648.0f && bound == bound)) break;
 
-    // Bins out as rows [r][A]; track max |bin| per row for the f16 split of the finish.
+        // Exact path: per-row maxima, then the exact bound, then the bins.
+        exact = true;
+        float mx[RC];
+#pragma unroll
+        for (int rr = 0; rr < RC; ++rr) mx[rr] = -INFINITY;
+        for (uint32_t t0 = t_begin; t0 < t_end; t0 += tile_tokens) {
+            load_tile(t0, cur, curv);
+#pragma unroll
+            for (int kk = 0; kk < CPT; ++kk)
+                if (curv[kk]) {
+                    float sc[RC];
+                    uint32_t ia[4];
+                    float cf[4];
+                    score(cur[kk], sc, ia, cf);
+#pragma unroll
+                    for (int rr = 0; rr < RC; ++rr) mx[rr] = fmaxf(mx[rr], sc[rr] * sl);
+                }
+        }
+        float m2[NRED];
+        bool im2[NRED];
+#pragma unroll
+        for (int i = 0; i < NRED; ++i) {
+            m2[i] = i < RC ? mx[i] : 0.0f;
+            im2[i] = i < RC;
+        }
+        wg_reduce(m2, im2);
+#pragma unroll
+        for (int rr = 0; rr < RC; ++rr) ref[rr] = m2[rr] == -INFINITY ? 0.0f : ceilf(m2[rr]);
+        float eb = 0.0f; // exact sum over contributions of |p*c|, maximised over rows below
+        float ebr[RC];
+#pragma unroll
+        for (int rr = 0; rr < RC; ++rr) ebr[rr] = 0.0f;
+        for (uint32_t t0 = t_begin; t0 < t_end; t0 += tile_tokens) {
+            load_tile(t0, cur, curv);
+#pragma unroll
+            for (int kk = 0; kk < CPT; ++kk)
+                if (curv[kk]) {
+                    float sc[RC];
+                    uint32_t ia[4];
+                    float cf[4];
+                    score(cur[kk], sc, ia, cf);
+                    const float ca = fabsf(cf[0]) + fabsf(cf[1]) + fabsf(cf[2]) + fabsf(cf[3]);
+#pragma unroll
+                    for (int rr = 0; rr < RC; ++rr) ebr[rr] += fast_exp2(sc[rr] * sl - ref[rr]) * ca;
+                }
+        }
+#pragma unroll
+        for (int i = 0; i < NRED; ++i) {
+            m2[i] = i < RC ? ebr[i] : 0.0f;
+            im2[i] = false;
+        }
+        wg_reduce(m2, im2);
+#pragma unroll
+        for (int rr = 0; rr < RC; ++rr) eb = fmaxf(eb, m2[rr]);
+        F = eb > 0.0f ? min(100, max(-100, 29 - (ilogbf(eb) + 1))) : 0;
+        __syncthreads();
+    }
+
+    // Bins out as float rows [r][A]; track max |bin| per row for the f16 split of the finish.
+    const float inv = ldexpf(1.0f, -F);
     float amax[RC];
 #pragma unroll
     for (int rr = 0; rr < RC; ++rr) amax[rr] = 0.0f;
     for (uint32_t at = tid; at < A; at += NT) {
 #pragma unroll
-        for (int rr = 0; rr < RC; ++rr) {
-            const uint32_t r = c * RC + rr;
-            const float v = bins[at * RC + rr];
-            amax[rr] = fmaxf(amax[rr], fabsf(v));
-            if (r < R) a.part_w[(pbase + r) * A + at] = v;
-        }
-    }
-    // Reduce lpart (sum) and amax (max) over the work-group.
-    float* red2 = red + 2 * NW * RC; // [NW][2*RC]
+        for (int pp = 0; pp < NP; ++pp) {
+            const uint64_t wv = bins[at * NP + pp];
+            const int32_t v0 = (int32_t)(uint32_t)wv;
+            const int32_t v1 = (int32_t)((uint32_t)(wv >> 32) + (v0 < 0 ? 1u : 0u));
 #pragma unroll
-    for (int rr = 0; rr < RC; ++rr) {
-        const float ls = wave_sum(lpart[rr]);
-        const float am = wave_max(amax[rr]);
-        if (lane == 0) {
-            red2[wave * 2 * RC + rr] = ls;
-            red2[wave * 2 * RC + RC + rr] = am;
+            for (int h = 0; h < 2; ++h) {
+                const int rr = 2 * pp + h;
+                if (rr >= RC) continue;
+                const float v = (float)(h ? v1 : v0) * inv;
+                amax[rr] = fmaxf(amax[rr], fabsf(v));
+                const uint32_t r = c * RC + rr;
+                if (r < R) a.part_w[(pbase + r) * A + at] = v;
+            }
         }
     }
-    __syncthreads();
+    float v[NRED];
+    bool is_max[NRED];
+#pragma unroll
+    for (int i = 0; i < NRED; ++i) {
+        v[i] = i < RC ? amax[i] : 0.0f;
+        is_max[i] = true;
+    }
+    wg_reduce(v, is_max);
     if (tid < RC) {
         const uint32_t r = c * RC + tid;
         if (r < R) {
-            float ls = 0.0f, am = 0.0f;
-            for (int w = 0; w < NW; ++w) {
-                ls += red2[w * 2 * RC + tid];
-                am = fmaxf(am, red2[w * 2 * RC + RC + tid]);
-            }
-            a.part_m[pbase + r] = mref[tid];
-            a.part_l[pbase + r] = ls;
-            a.part_amax[pbase + r] = am;
+            a.part_m[pbase + r] = ref[tid];
+            a.part_l[pbase + r] = lpart[tid] * inv; // sum of p, back from units of 2^-F
+            a.part_amax[pbase + r] = v[tid];
         }
     }
 }
 
-// Shared-memory bytes of cold_kernel<RC> for a dictionary of A atoms.
-inline size_t cold_smem_bytes(uint32_t A, int RC) {
+// Shared-memory bytes of cold_kernel<RC> for a dictionary of A atoms and
+// splits of `tokens_per_split` tokens.
+inline size_t cold_smem_bytes(uint32_t A, int RC, uint32_t tokens_per_split) {
     const size_t qtab = ((size_t)A * RC * 2 + 15) & ~(size_t)15;
-    const int NW = kColdThreads / 64;
-    return qtab + (size_t)A * RC * 4 + (size_t)(2 * NW * RC + NW * 2 * RC) * 4;
+    const int NW = kColdThreads / 64, NP = (RC + 1) / 2;
+    const size_t n_blk = ((size_t)(tokens_per_split + 15) / 16 + 3) & ~(size_t)3;
+    return qtab + (size_t)A * NP * 8 + n_blk * 4 + (size_t)NW * (2 * RC + 2) * 4;
 }
 
 // ----------------------------------------------- per-row merge factors
@@ -749,27 +896,27 @@ __device__ inline float merge_value(float oh, float Mh, float Lh, float oc, floa
 
 // ------------------------------------------------------ bins . D (MFMA)
 //
-// Work-group = 16 rows sharing one dictionary x one atom range; 4 waves split
-// the range in chunks of 32 atoms.  O^T[dim][row] += D^T W^T with
+// Work-group = 64 rows sharing one dictionary (4 waves x 16 rows) x one atom
+// range.  All four waves walk the same 32-atom dictionary chunks, staged once
+// per work-group in LDS (double-buffered, the next chunk's loads in flight
+// during the current chunk's MFMAs).  Per wave: O^T[dim][row] += D^T W^T with
 //   B = W^T (lane: row li, atoms a0+4*lg+{0..3} and a0+16+4*lg+{0..3}: two
 //       16-byte loads per cold split, combined with the split factors),
 //       split into hi + lo f16 terms -> two MFMAs,
-//   A = D^T (lane: dim 16*nb+li, the same 8 atoms) gathered from a 32-atom
-//       dictionary chunk staged in LDS (pitch HD+4 halves).
+//   A = D^T (lane: dim 16*nb+li, the same 8 atoms) gathered from the LDS chunk
+//       (pitch HD+4 halves: the four atom rows 4*lg+e of one read fall on
+//       disjoint 8-bank groups).
 // With one atom range the log-sum-exp merge runs here too; otherwise the
 // partial cold outputs go to `ocp` for merge_kernel.
 template <int HD>
-__global__ __launch_bounds__(64 * kFinishWaves) void finish_kernel(FinishArgs a) {
-    constexpr int NB = HD / 16, P = HD + 4, NWF = kFinishWaves;
-    constexpr int DTILE = 32 * P;                           // halves per wave
-    constexpr int SMEM_D = NWF * DTILE * 2;                 // bytes
-    constexpr int SMEM_R = NWF * 16 * HD * 4;               // bytes
-    constexpr int SMEM = SMEM_D > SMEM_R ? SMEM_D : SMEM_R; // the two phases alias
-    __shared__ __attribute__((aligned(16))) unsigned char sbuf[SMEM];
-    __shared__ float s_cfac[16][kMaxSplits];
-    __shared__ float s_hfac[16][kMaxSplits];
-    __shared__ RowFactors s_rf[16];
-    __shared__ uint64_t s_row[16]; // lbg*R + r, or ~0 for padding rows
+__global__ __launch_bounds__(256) void finish_kernel(FinishArgs a) {
+    constexpr int NB = HD / 16, P = HD + 4, ROWS = 64;
+    constexpr int PIECES = 32 * HD / 8;    // 16-byte pieces per dictionary chunk
+    constexpr int PPT = PIECES / 256;      // pieces per thread (2 at HD=128, 1 at HD=64)
+    __shared__ __attribute__((aligned(16))) _Float16 sd[2][32 * P];
+    __shared__ float s_cfac[ROWS][kMaxSplits];
+    __shared__ RowFactors s_rf[ROWS];
+    __shared__ uint64_t s_row[ROWS]; // lbg*R + r, or ~0 for padding rows
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, li = lane & 15, lg = lane >> 4;
     const uint32_t group = blockIdx.x / a.tiles_per_group, tile = blockIdx.x % a.tiles_per_group;
     const uint32_t ar = blockIdx.y;
@@ -777,162 +924,187 @@ __global__ __launch_bounds__(64 * kFinishWaves) void finish_kernel(FinishArgs a)
     const uint32_t R = a.rows_r, A = a.dict_size;
     const uint32_t hg = a.dict_heads == 1 ? a.kv_heads : 1;
 
-    if (tid < 16) {
-        const uint32_t i = tile * 16 + tid;
+    if (tid < ROWS) {
+        const uint32_t i = tile * ROWS + tid;
         uint64_t rowid = ~0ull;
         if (i < a.rows_per_group) {
             const uint32_t b = i / (hg * R), rem = i % (hg * R);
             const uint32_t g = a.dict_heads == 1 ? rem / R : dg, r = rem % R;
             const uint64_t lbg = ((uint64_t)l * a.batch + b) * a.kv_heads + g;
             rowid = lbg * R + r;
-            const uint64_t cbase = lbg * a.cold_splits * R + r;
             RowFactors rf;
-            cold_row_factors(a.cold_m, a.cold_l, a.cold_amax, a.cold_splits, cbase, R, s_cfac[tid], rf.Mc, rf.Lc,
-                             rf.inv_scl);
+            cold_row_factors(a.cold_m, a.cold_l, a.cold_amax, a.cold_splits, lbg * a.cold_splits * R + r, R,
+                             s_cfac[tid], rf.Mc, rf.Lc, rf.inv_scl);
             rf.Mh = -INFINITY;
             rf.Lh = 0.0f;
-            if (a.hot_splits) {
-                const uint64_t hbase = lbg * a.hot_splits * R + r;
-                hot_row_factors(a.hot_m, a.hot_l, a.hot_splits, hbase, R, s_hfac[tid], rf.Mh, rf.Lh);
-            }
             s_rf[tid] = rf;
         }
         s_row[tid] = rowid;
     }
+
+    const uint16_t* dict = a.dict + (uint64_t)l * a.dict_layer + (uint64_t)dg * A * HD;
+    const uint32_t a_begin = ar * a.atoms_per_range;
+    const uint32_t a_end = min(a_begin + a.atoms_per_range, A);
+    const uint32_t n_ch = (a_end - a_begin + 31) / 32;
+
+    uint4_t dreg[PPT];
+    auto load_d = [&](uint32_t a0) {
+#pragma unroll
+        for (int q = 0; q < PPT; ++q) {
+            const int pc = tid + 256 * q, at = pc / (HD / 8), col = (pc % (HD / 8)) * 8;
+            dreg[q] = (a0 + at < a_end) ? *(const uint4_t*)(dict + (uint64_t)(a0 + at) * HD + col) : (uint4_t)0u;
+        }
+    };
+    auto store_d = [&](int buf) {
+#pragma unroll
+        for (int q = 0; q < PPT; ++q) {
+            const int pc = tid + 256 * q, at = pc / (HD / 8), col = (pc % (HD / 8)) * 8;
+            _Float16* dst = &sd[buf][at * P + col];
+            *(uint2_t*)dst = (uint2_t){dreg[q][0], dreg[q][1]};
+            *(uint2_t*)(dst + 4) = (uint2_t){dreg[q][2], dreg[q][3]};
+        }
+    };
+    if (n_ch) {
+        load_d(a_begin);
+        store_d(0);
+    }
     __syncthreads();
 
-    // This lane's B-operand row.
-    const uint64_t myrow = s_row[li];
+    const int myr = 16 * wave + li; // this lane's B-operand row
+    const uint64_t myrow = s_row[myr];
     const bool rowok = myrow != ~0ull;
     const uint64_t lbg_me = rowok ? myrow / R : 0, r_me = rowok ? myrow % R : 0;
-    const uint16_t* dict = a.dict + (uint64_t)l * a.dict_layer + (uint64_t)dg * A * HD;
-    _Float16* dtile = (_Float16*)sbuf + wave * DTILE;
+    const float* wbase = a.cold_w + ((lbg_me * a.cold_splits) * R + r_me) * A;
+    const uint64_t wsplit = (uint64_t)R * A;
 
     float4_t acc[NB];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) acc[nb] = (float4_t)0.0f;
 
-    const uint32_t a_begin = ar * a.atoms_per_range;
-    const uint32_t a_end = min(a_begin + a.atoms_per_range, A);
-    const uint32_t n_ch = (a_end - a_begin + 31) / 32;
-    const uint32_t iters = (n_ch + NWF - 1) / NWF;
-    for (uint32_t it = 0; it < iters; ++it) {
-        const uint32_t ch = it * NWF + wave;
+    // With one cold split (large batches) the next chunk's W values are
+    // prefetched with the next dictionary chunk.
+    const bool single = a.cold_splits == 1;
+    const float f0 = rowok ? s_cfac[myr][0] : 0.0f;
+    const bool wok = rowok && f0 != 0.0f; // an empty split wrote no bins: never read them
+    float4_t wn0 = (float4_t)0.0f, wn1 = (float4_t)0.0f;
+    auto load_w = [&](uint32_t a0) {
+        const uint32_t at0 = a0 + 4 * lg, at1 = a0 + 16 + 4 * lg;
+        wn0 = (wok && at0 < a_end) ? *(const float4_t*)(wbase + at0) : (float4_t)0.0f;
+        wn1 = (wok && at1 < a_end) ? *(const float4_t*)(wbase + at1) : (float4_t)0.0f;
+    };
+    if (single && n_ch) load_w(a_begin);
+
+    for (uint32_t ch = 0; ch < n_ch; ++ch) {
+        const int buf = ch & 1;
         const uint32_t a0 = a_begin + ch * 32;
-        const bool active = ch < n_ch;
-        __syncthreads();
-        if (active) {
-            // Dictionary chunk [32 atoms][HD] into this wave's LDS tile.
-            constexpr int PIECES = 32 * HD / 8;
-#pragma unroll
-            for (int pc = lane; pc < PIECES; pc += 64) {
-                const int at = pc / (HD / 8), col = (pc % (HD / 8)) * 8;
-                uint4_t v = (uint4_t)0u;
-                if (a0 + at < a_end) v = *(const uint4_t*)(dict + (uint64_t)(a0 + at) * HD + col);
-                _Float16* dst = dtile + at * P + col;
-                *(uint2_t*)dst = (uint2_t){v[0], v[1]};
-                *(uint2_t*)(dst + 4) = (uint2_t){v[2], v[3]};
-            }
+        const bool more = ch + 1 < n_ch;
+        const float4_t wc0 = wn0, wc1 = wn1;
+        if (more) {
+            load_d(a0 + 32);
+            if (single) load_w(a0 + 32);
         }
-        __syncthreads();
-        if (active) {
-            float w8[8];
+        float w8[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            w8[e] = f0 * wc0[e];
+            w8[4 + e] = f0 * wc1[e];
+        }
+        if (rowok && !single) {
 #pragma unroll
             for (int e = 0; e < 8; ++e) w8[e] = 0.0f;
-            if (rowok) {
-                for (uint32_t s = 0; s < a.cold_splits; ++s) {
-                    const float f = s_cfac[li][s];
-                    if (f == 0.0f) continue;
-                    const float* wrow = a.cold_w + ((lbg_me * a.cold_splits + s) * R + r_me) * A;
+            for (uint32_t s = 0; s < a.cold_splits; ++s) {
+                const float f = s_cfac[myr][s];
+                if (f == 0.0f) continue;
+                const float* wrow = wbase + s * wsplit;
 #pragma unroll
-                    for (int half = 0; half < 2; ++half) {
-                        const uint32_t at = a0 + 16 * half + 4 * lg;
-                        if (at < a_end) {
-                            const float4_t v = *(const float4_t*)(wrow + at);
+                for (int half = 0; half < 2; ++half) {
+                    const uint32_t at = a0 + 16 * half + 4 * lg;
+                    if (at < a_end) {
+                        const float4_t v = *(const float4_t*)(wrow + at);
 #pragma unroll
-                            for (int e = 0; e < 4; ++e) w8[4 * half + e] += f * v[e];
-                        }
+                        for (int e = 0; e < 4; ++e) w8[4 * half + e] += f * v[e];
                     }
                 }
             }
-            half8_t hi, lo;
+        }
+        half8_t hi, lo;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            hi[e] = (_Float16)w8[e];
+            lo[e] = (_Float16)(w8[e] - (float)hi[e]);
+        }
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+            half8_t dop;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                hi[e] = (_Float16)w8[e];
-                lo[e] = (_Float16)(w8[e] - (float)hi[e]);
+                const int row = e < 4 ? 4 * lg + e : 16 + 4 * lg + (e - 4);
+                dop[e] = sd[buf][row * P + 16 * nb + li];
             }
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb) {
-                half8_t dop;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const int row = e < 4 ? 4 * lg + e : 16 + 4 * lg + (e - 4);
-                    dop[e] = dtile[row * P + 16 * nb + li];
-                }
-                acc[nb] = mfma16x16x32(dop, hi, acc[nb]);
-                acc[nb] = mfma16x16x32(dop, lo, acc[nb]);
-            }
+            acc[nb] = mfma16x16x32(dop, hi, acc[nb]);
+            acc[nb] = mfma16x16x32(dop, lo, acc[nb]);
         }
+        if (more) store_d(buf ^ 1);
+        __syncthreads();
     }
-    __syncthreads();
-    // Cross-wave reduction: red[wave][row][dim].
-    float* red = (float*)sbuf;
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-        *(float4_t*)(red + (wave * 16 + li) * HD + 16 * nb + 4 * lg) = acc[nb];
-    __syncthreads();
 
-    constexpr int DPT = HD / 16; // dims per thread: 256 threads over 16 rows x HD
-    const int row = tid / 16, d0 = (tid % 16) * DPT;
-    const uint64_t rowid = s_row[row];
-    if (rowid == ~0ull) return;
-    const RowFactors rf = s_rf[row];
-    float oc[DPT];
-#pragma unroll
-    for (int e = 0; e < DPT; ++e) {
-        float v = 0.0f;
-#pragma unroll
-        for (int w = 0; w < NWF; ++w) v += red[(w * 16 + row) * HD + d0 + e];
-        oc[e] = v * rf.inv_scl;
-    }
+    if (!rowok) return;
+    // Lane holds O^T[dims 16*nb + 4*lg + e][row li of this wave].
+    const RowFactors rf = s_rf[myr];
+    const uint64_t rowid = myrow;
     if (a.n_ar > 1) {
-        float* dst = a.ocp + (rowid * a.n_ar + ar) * HD + d0;
+        float* dst = a.ocp + (rowid * a.n_ar + ar) * HD;
 #pragma unroll
-        for (int e = 0; e < DPT; ++e) dst[e] = oc[e];
+        for (int nb = 0; nb < NB; ++nb) *(float4_t*)(dst + 16 * nb + 4 * lg) = acc[nb] * rf.inv_scl;
         return;
     }
+    // Fused merge with the hot partials of this row.
     const uint64_t lbg = rowid / R, r = rowid % R;
-    float oh[DPT];
-#pragma unroll
-    for (int e = 0; e < DPT; ++e) oh[e] = 0.0f;
+    float Mh = -INFINITY, Lh = 0.0f;
     for (uint32_t s = 0; s < a.hot_splits; ++s) {
-        const float f = s_hfac[row][s];
-        if (f == 0.0f) continue;
-        const float* src = a.hot_o + ((lbg * a.hot_splits + s) * R + r) * HD + d0;
+        const uint64_t hb = (lbg * a.hot_splits + s) * R + r;
+        if (a.hot_l[hb] > 0.0f) Mh = fmaxf(Mh, a.hot_m[hb]);
+    }
+    float4_t oh[NB];
 #pragma unroll
-        for (int e = 0; e < DPT; ++e) oh[e] += f * src[e];
+    for (int nb = 0; nb < NB; ++nb) oh[nb] = (float4_t)0.0f;
+    for (uint32_t s = 0; s < a.hot_splits; ++s) {
+        const uint64_t hb = (lbg * a.hot_splits + s) * R + r;
+        const float hl = a.hot_l[hb];
+        if (!(hl > 0.0f)) continue;
+        const float f = fast_exp2(a.hot_m[hb] - Mh);
+        Lh += f * hl;
+        const float* src = a.hot_o + hb * HD;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) oh[nb] += f * *(const float4_t*)(src + 16 * nb + 4 * lg);
     }
     const uint64_t lb = lbg / a.kv_heads, g = lbg % a.kv_heads;
     const uint64_t q = r / a.gqa, h = g * a.gqa + r % a.gqa;
-    uint16_t* o = a.out + ((lb * a.queries + q) * a.q_heads + h) * HD + d0;
+    uint16_t* o = a.out + ((lb * a.queries + q) * a.q_heads + h) * HD;
 #pragma unroll
-    for (int e = 0; e < DPT; ++e)
-        o[e] = __builtin_bit_cast(uint16_t, (_Float16)merge_value(oh[e], rf.Mh, rf.Lh, oc[e], rf.Mc, rf.Lc));
+    for (int nb = 0; nb < NB; ++nb) {
+        half4_t v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            v[e] = (_Float16)merge_value(oh[nb][e], Mh, Lh, acc[nb][e] * rf.inv_scl, rf.Mc, rf.Lc);
+        *(half4_t*)(o + 16 * nb + 4 * lg) = v;
+    }
 }
 
 // --------------------------------------------------- log-sum-exp merge
 //
-// 16 rows (row id lbg*R + r) per 256-thread work-group; used when there is no
-// cold pool or when the cold output was split over several atom ranges.
+// One 64-thread group per row (row id lbg*R + r), four rows per work-group;
+// used when there is no cold pool or when the cold output was split over
+// several atom ranges.
 template <int HD>
 __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
-    __shared__ float s_hfac[16][kMaxSplits];
-    __shared__ RowFactors s_rf[16];
-    const int tid = threadIdx.x;
-    const uint64_t row0 = (uint64_t)blockIdx.x * 16;
+    constexpr int DPT = HD / 64;
+    __shared__ float s_hfac[4][kMaxSplits];
+    __shared__ RowFactors s_rf[4];
+    const int tid = threadIdx.x, row = tid / 64, lane = tid % 64;
+    const uint64_t rowid = (uint64_t)blockIdx.x * 4 + row;
     const uint32_t R = a.rows_r;
-    if (tid < 16) {
-        const uint64_t rowid = row0 + tid;
+    if (lane == 0) {
         RowFactors rf;
         rf.Mc = -INFINITY;
         rf.Lc = 0.0f;
@@ -945,18 +1117,16 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
                 cold_row_factors(a.cold_m, a.cold_l, a.cold_amax, a.cold_splits, lbg * a.cold_splits * R + r, R,
                                  nullptr, rf.Mc, rf.Lc, rf.inv_scl);
             if (a.hot_splits)
-                hot_row_factors(a.hot_m, a.hot_l, a.hot_splits, lbg * a.hot_splits * R + r, R, s_hfac[tid], rf.Mh,
+                hot_row_factors(a.hot_m, a.hot_l, a.hot_splits, lbg * a.hot_splits * R + r, R, s_hfac[row], rf.Mh,
                                 rf.Lh);
         }
-        s_rf[tid] = rf;
+        s_rf[row] = rf;
     }
     __syncthreads();
-    constexpr int DPT = HD / 16;
-    const int row = tid / 16, d0 = (tid % 16) * DPT;
-    const uint64_t rowid = row0 + row;
     if (rowid >= a.total_rows) return;
     const RowFactors rf = s_rf[row];
     const uint64_t lbg = rowid / R, r = rowid % R;
+    const int d0 = lane * DPT;
     float oc[DPT], oh[DPT];
 #pragma unroll
     for (int e = 0; e < DPT; ++e) {
@@ -971,10 +1141,9 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
         }
     for (uint32_t s = 0; s < a.hot_splits; ++s) {
         const float f = s_hfac[row][s];
-        if (f == 0.0f) continue;
         const float* src = a.hot_o + ((lbg * a.hot_splits + s) * R + r) * HD + d0;
 #pragma unroll
-        for (int e = 0; e < DPT; ++e) oh[e] += f * src[e];
+        for (int e = 0; e < DPT; ++e) oh[e] += f == 0.0f ? 0.0f : f * src[e];
     }
     const uint64_t lb = lbg / a.kv_heads, g = lbg % a.kv_heads;
     const uint64_t q = r / a.gqa, h = g * a.gqa + r % a.gqa;

@@ -125,3 +125,25 @@ def test_batched_reduced(engine, stream):
 def test_spec_verify_reduced(engine, stream):
     check(engine, stream, W.spec_verify(layers=2, batch=2, hot_count=16, cold_count=64), seed=7,
           what="spec_verify L2 B2 Q8 causal")
+
+
+def test_cold_only_large_coefficients(engine, stream):
+    """Peaked softmax over the cold pool: large coefficients push scores apart,
+    exercising the reference raises (bin shifts) and the fixed-point scale.
+    q_latent is passed in as f16 (as the reference takes it) so both sides score
+    with the same values; computing it on the device instead adds the f16
+    rounding of q_latent, which a softmax this peaked amplifies."""
+    import torch
+    geom = W.hot_cold(hot_count=0, cold_count=256, coef_std=6.0, q_std=2.0)
+    wl = W.generate(geom, seed=11)
+    a = W.host_arrays(wl)
+    ql = oracle.qlatent_f64(geom, a).astype(np.float16)
+    a["q_latent"] = ql.view(np.uint16)
+    wl.q_latent = torch.from_numpy(ql.view(np.int16).copy()).view(torch.float16)
+    got = run_gpu(engine, wl, stream)
+    assert_close(got, oracle.decode_f64(geom, a), "cold-only, coef std 6, f16 q_latent given")
+
+
+def test_cold_many_tiles_small_coefficients(engine, stream):
+    check(engine, stream, W.hot_cold(batch=2, hot_count=8, cold_count=2048, coef_std=0.05), seed=12,
+          what="hot+cold, coef std 0.05")
