@@ -194,7 +194,7 @@ int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, Layout* L, char
         off = align_up(off + bytes, kAlign);
         return at;
     };
-    if (o.info.computes_q_latent) o.off_ql = take(n_lbg * A * R * 2);
+    if (o.info.computes_q_latent) o.off_ql = take((uint64_t)d->layers * d->batch * d->queries * d->q_heads * A * 2);
     if (o.info.hot_splits) {
         const uint64_t n = n_lbg * o.info.hot_splits * R;
         o.off_hm = take(n * 4);
@@ -327,13 +327,10 @@ int launch_project(aw_engine* e, const aw_decode_desc* d, const Layout& o, uint1
     const dim3 block(64);
     const uint32_t gz = d->layers * d->dict_heads;
     if (rows <= 16) {
-        hipLaunchKernelGGL((aw::project_kernel<HD, 1, 1>), dim3(cdiv(d->dict_size, 16), cdiv(rows, 16), gz), block,
+        hipLaunchKernelGGL((aw::project_kernel<HD, 1, 4>), dim3(cdiv(d->dict_size, 64), cdiv(rows, 16), gz), block,
                            0, st, a);
     } else if (rows <= 32) {
-        hipLaunchKernelGGL((aw::project_kernel<HD, 2, 1>), dim3(cdiv(d->dict_size, 16), cdiv(rows, 32), gz), block,
-                           0, st, a);
-    } else if (rows <= 512) {
-        hipLaunchKernelGGL((aw::project_kernel<HD, 4, 2>), dim3(cdiv(d->dict_size, 32), cdiv(rows, 64), gz), block,
+        hipLaunchKernelGGL((aw::project_kernel<HD, 2, 2>), dim3(cdiv(d->dict_size, 32), cdiv(rows, 32), gz), block,
                            0, st, a);
     } else {
         hipLaunchKernelGGL((aw::project_kernel<HD, 4, 4>), dim3(cdiv(d->dict_size, 64), cdiv(rows, 64), gz), block,
@@ -385,6 +382,7 @@ int launch_hot(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* ws,
 }
 
 constexpr int kColdCPT = 4;
+constexpr int kColdPD = 2; // tiles of code loads in flight (1..4 measured alike)
 
 int launch_cold(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* ws, hipStream_t st) {
     aw::ColdArgs a{};
@@ -414,21 +412,13 @@ int launch_cold(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* ws
     a.cold_blocks = d->cold_blocks;
     a.cold_layer = d->cold_blocks * kBlock * d->kv_heads;
     a.refs_layer = (uint64_t)d->batch * d->refs_stride;
-    if (o.info.computes_q_latent) { // [lbg][A][R]
-        a.ql = (const uint16_t*)(ws + o.off_ql);
-        a.s_lb = (uint64_t)d->kv_heads * A * R;
-        a.s_g = (uint64_t)A * R;
-        a.s_q = G;
-        a.s_j = 1;
-        a.s_a = R;
-    } else { // caller's [L][B][Q][Hq][A]
-        a.ql = d->q_latent;
-        a.s_lb = (uint64_t)d->queries * d->q_heads * A;
-        a.s_g = (uint64_t)G * A;
-        a.s_q = (uint64_t)d->q_heads * A;
-        a.s_j = A;
-        a.s_a = 1;
-    }
+    // q_latent [L][B][Q][Hq][A], computed on the device or the caller's.
+    a.ql = o.info.computes_q_latent ? (const uint16_t*)(ws + o.off_ql) : d->q_latent;
+    a.s_lb = (uint64_t)d->queries * d->q_heads * A;
+    a.s_g = (uint64_t)G * A;
+    a.s_q = (uint64_t)d->q_heads * A;
+    a.s_j = A;
+    a.s_a = 1;
     (void)HD;
     const uint64_t grid = (uint64_t)cdiv(a.n_units, 8) * 8 * d->kv_heads;
     if (grid > 0x7FFFFFFFull) return fail(e, AW_E_UNSUPPORTED, "cold grid too large");
@@ -436,13 +426,13 @@ int launch_cold(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* ws
     StageTimer t(e, AW_STAGE_COLD, st);
     switch (o.rc) {
     case 4:
-        hipLaunchKernelGGL((aw::cold_kernel<4, kColdCPT>), dim3((uint32_t)grid), dim3(aw::kColdThreads), smem, st, a);
+        hipLaunchKernelGGL((aw::cold_kernel<4, kColdCPT, kColdPD>), dim3((uint32_t)grid), dim3(aw::kColdThreads), smem, st, a);
         break;
     case 2:
-        hipLaunchKernelGGL((aw::cold_kernel<2, kColdCPT>), dim3((uint32_t)grid), dim3(aw::kColdThreads), smem, st, a);
+        hipLaunchKernelGGL((aw::cold_kernel<2, kColdCPT, kColdPD>), dim3((uint32_t)grid), dim3(aw::kColdThreads), smem, st, a);
         break;
     default:
-        hipLaunchKernelGGL((aw::cold_kernel<1, kColdCPT>), dim3((uint32_t)grid), dim3(aw::kColdThreads), smem, st, a);
+        hipLaunchKernelGGL((aw::cold_kernel<1, kColdCPT, kColdPD>), dim3((uint32_t)grid), dim3(aw::kColdThreads), smem, st, a);
         break;
     }
     AW_HIP(e, hipGetLastError());
@@ -731,18 +721,18 @@ int aw_engine_create(int device, aw_engine** out) {
     e->n_cu = (uint32_t)prop.multiProcessorCount;
     int rc = AW_OK;
     if (!rc) rc = check_kernel(e, aw::hot_kernel<128, 1>, "hot_kernel");
-    if (!rc) rc = check_kernel(e, aw::cold_kernel<4, kColdCPT>, "cold_kernel");
+    if (!rc) rc = check_kernel(e, aw::cold_kernel<4, kColdCPT, kColdPD>, "cold_kernel");
     if (!rc) rc = check_kernel(e, aw::finish_kernel<128>, "finish_kernel");
     if (rc) {
         delete e;
         return rc;
     }
     // Let the cold kernel use the device's full LDS.
-    (void)hipFuncSetAttribute((const void*)aw::cold_kernel<4, kColdCPT>, hipFuncAttributeMaxDynamicSharedMemorySize,
+    (void)hipFuncSetAttribute((const void*)aw::cold_kernel<4, kColdCPT, kColdPD>, hipFuncAttributeMaxDynamicSharedMemorySize,
                         (int)e->max_lds);
-    (void)hipFuncSetAttribute((const void*)aw::cold_kernel<2, kColdCPT>, hipFuncAttributeMaxDynamicSharedMemorySize,
+    (void)hipFuncSetAttribute((const void*)aw::cold_kernel<2, kColdCPT, kColdPD>, hipFuncAttributeMaxDynamicSharedMemorySize,
                         (int)e->max_lds);
-    (void)hipFuncSetAttribute((const void*)aw::cold_kernel<1, kColdCPT>, hipFuncAttributeMaxDynamicSharedMemorySize,
+    (void)hipFuncSetAttribute((const void*)aw::cold_kernel<1, kColdCPT, kColdPD>, hipFuncAttributeMaxDynamicSharedMemorySize,
                         (int)e->max_lds);
     if (hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking) != hipSuccess ||
         hipStreamCreateWithFlags(&e->side, hipStreamNonBlocking) != hipSuccess ||

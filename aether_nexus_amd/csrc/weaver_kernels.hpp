@@ -61,15 +61,39 @@ __device__ inline float h2f_bits(uint32_t bits16) {
 __device__ inline void flag_error(uint32_t* err, uint32_t bit) {
     __hip_atomic_fetch_or(err, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ inline float wave_max(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m));
-    return v;
+// Wave-wide max / sum with DPP: quad permutes and row rotates reduce each
+// 16-lane row, row_bcast15 / row_bcast31 fold the rows into lane 63, which is
+// broadcast.  Every lane returns the result.
+template <bool MAX>
+__device__ inline float wave_reduce(float v) {
+    const int id = __builtin_bit_cast(int, MAX ? -INFINITY : 0.0f);
+#define AW_DPP_STEP(ctrl, rmask)                                                                               \
+    {                                                                                                          \
+        const float o = __builtin_bit_cast(                                                                    \
+            float, __builtin_amdgcn_update_dpp(id, __builtin_bit_cast(int, v), ctrl, rmask, 0xF, false));     \
+        v = MAX ? fmaxf(v, o) : v + o;                                                                         \
+    }
+    AW_DPP_STEP(0xB1, 0xF)  // quad_perm [1,0,3,2]
+    AW_DPP_STEP(0x4E, 0xF)  // quad_perm [2,3,0,1]
+    AW_DPP_STEP(0x124, 0xF) // row_ror:4
+    AW_DPP_STEP(0x128, 0xF) // row_ror:8
+    AW_DPP_STEP(0x142, 0xA) // row_bcast:15 into rows 1 and 3
+    AW_DPP_STEP(0x143, 0xC) // row_bcast:31 into rows 2 and 3
+#undef AW_DPP_STEP
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
-__device__ inline float wave_sum(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
-    return v;
+__device__ inline float wave_max(float v) { return wave_reduce<true>(v); }
+__device__ inline float wave_sum(float v) { return wave_reduce<false>(v); }
+
+// Log-sum-exp combination of one row's splits, one wave, lane = split
+// (S <= 64; lanes past S pass l = 0).  Empty splits (l == 0) get factor 0.
+// Returns the row maximum M, the combined sum L, and this lane's factor
+// 2^(m - M).
+__device__ inline void combine_splits(float m, float l, float& M, float& L, float& f) {
+    const bool ok = l > 0.0f;
+    M = wave_max(ok ? m : -INFINITY);
+    f = ok ? fast_exp2(m - M) : 0.0f;
+    L = wave_sum(f * l);
 }
 
 // ---------------------------------------------------------------- arguments
@@ -77,7 +101,7 @@ __device__ inline float wave_sum(float v) {
 struct ProjArgs {
     const uint16_t* q;    // [L][B][Q][Hq][HD]
     const uint16_t* dict; // [L][dict_heads][A][HD]
-    uint16_t* ql;         // [L*B*Hkv][A][R] f16
+    uint16_t* ql;         // [L][B][Q][Hq][A] f16
     uint32_t batch, queries, q_heads, kv_heads, gqa, rows_r;
     uint32_t dict_size, dict_heads;
     uint32_t rows_per_group; // B*Q*(dict_heads==1 ? Hq : G)
@@ -152,11 +176,15 @@ struct MergeArgs {
 
 // ------------------------------------------------------------ q . D^T (MFMA)
 //
-// One wave computes a (16*MR rows) x (16*NA atoms) tile with K = HD.
-// Operand layouts of v_mfma_f32_16x16x32_f16 (lane l, li = l%16, lg = l/16):
-//   A[i][k]: lane holds row li, k = 8*lg .. 8*lg+7   -> 16 contiguous bytes of a q row
-//   B[k][j]: lane holds col li, k = 8*lg .. 8*lg+7   -> 16 contiguous bytes of a D row
-//   C[i][j]: lane holds rows 4*lg .. 4*lg+3, col li
+// Computes q_latent^T = D q^T so that each lane ends up with four consecutive
+// atoms of one query row and stores them with one 8-byte write into
+// q_latent [L][B][Q][Hq][A] (the layout of the reference's q_latent buffer,
+// weaver_kernel.metal:111).  One wave computes (16*NA atoms) x (16*MR rows),
+// K = HD.  Operand layouts of v_mfma_f32_16x16x32_f16 (lane l, li = l%16,
+// lg = l/16):
+//   A[i][k]: lane holds row i = li, k = 8*lg .. 8*lg+7  -> 16 bytes of dictionary row (atom li)
+//   B[k][j]: lane holds col j = li, k = 8*lg .. 8*lg+7  -> 16 bytes of query row li
+//   C[i][j]: lane holds rows i = 4*lg .. 4*lg+3, col j = li -> 4 atoms of query row li
 // Rows of one group share one dictionary: group = (layer, dict head); inside a
 // group row i enumerates (b, q, head) with head over Hq (shared dictionary) or
 // over the G heads of kv head dg (per-kv-head dictionary).
@@ -166,74 +194,52 @@ __global__ __launch_bounds__(64) void project_kernel(ProjArgs a) {
     const int lane = threadIdx.x, li = lane & 15, lg = lane >> 4;
     const uint32_t group = blockIdx.z;
     const uint32_t l = group / a.dict_heads, dg = group % a.dict_heads;
-    const uint32_t h_per = a.dict_heads == 1 ? a.q_heads : a.gqa;
-    const uint32_t row0 = blockIdx.y * 16 * MR, atom0 = blockIdx.x * 16 * NA;
+    const uint32_t atom0 = blockIdx.x * 16 * NA, row0 = blockIdx.y * 16 * MR;
     const uint16_t* dict = a.dict + l * a.dict_layer + (uint64_t)dg * a.dict_size * HD;
+    const bool shared = a.dict_heads == 1;
 
-    half8_t aop[MR][KS];
+    // This lane's query rows (one per row block): global row index into q / q_latent.
+    uint64_t qrow[MR];
+    bool rok[MR];
 #pragma unroll
     for (int mr = 0; mr < MR; ++mr) {
         const uint32_t i = row0 + 16 * mr + li;
-        if (i < a.rows_per_group) {
-            const uint32_t b = i / (a.queries * h_per), rem = i % (a.queries * h_per);
-            const uint32_t q = rem / h_per, h = dg * a.gqa + rem % h_per;
-            const uint16_t* p = a.q + ((((uint64_t)l * a.batch + b) * a.queries + q) * a.q_heads + h) * HD;
-#pragma unroll
-            for (int j = 0; j < KS; ++j) aop[mr][j] = as_h8(*(const uint4_t*)(p + 32 * j + 8 * lg));
-        } else {
-#pragma unroll
-            for (int j = 0; j < KS; ++j) aop[mr][j] = (half8_t)(_Float16)0;
+        rok[mr] = i < a.rows_per_group;
+        if (shared) {
+            qrow[mr] = (uint64_t)l * a.rows_per_group + i; // rows of a layer are (b, q, h) in q's order
+        } else {                                           // (b, q, head hh of kv head dg)
+            const uint32_t bq = i / a.gqa, hh = i % a.gqa;
+            qrow[mr] = ((uint64_t)l * a.batch * a.queries + bq) * a.q_heads + dg * a.gqa + hh;
         }
     }
-    float4_t acc[MR][NA];
+    half8_t bop[MR][KS];
+#pragma unroll
+    for (int mr = 0; mr < MR; ++mr)
+#pragma unroll
+        for (int j = 0; j < KS; ++j)
+            bop[mr][j] = rok[mr] ? as_h8(*(const uint4_t*)(a.q + qrow[mr] * HD + 32 * j + 8 * lg))
+                                 : (half8_t)(_Float16)0;
 #pragma unroll
     for (int na = 0; na < NA; ++na) {
         const uint32_t at = atom0 + 16 * na + li;
-        half8_t bop[KS];
+        half8_t aop[KS];
 #pragma unroll
         for (int j = 0; j < KS; ++j)
-            bop[j] = at < a.dict_size ? as_h8(*(const uint4_t*)(dict + (uint64_t)at * HD + 32 * j + 8 * lg))
+            aop[j] = at < a.dict_size ? as_h8(*(const uint4_t*)(dict + (uint64_t)at * HD + 32 * j + 8 * lg))
                                       : (half8_t)(_Float16)0;
+        const uint32_t ao = atom0 + 16 * na + 4 * lg; // this lane's 4 output atoms
 #pragma unroll
         for (int mr = 0; mr < MR; ++mr) {
-            acc[mr][na] = (float4_t)0.0f;
+            float4_t acc = (float4_t)0.0f;
 #pragma unroll
-            for (int j = 0; j < KS; ++j) acc[mr][na] = mfma16x16x32(aop[mr][j], bop[j], acc[mr][na]);
-        }
-    }
-    // Store as f16 into ql[lbg][atom][r], r = q*G + (h % G).
-    const bool packed = (a.gqa % 4) == 0; // then C rows 4*lg..+3 are 4 consecutive r of one (b,q,g)
-#pragma unroll
-    for (int mr = 0; mr < MR; ++mr) {
-        const uint32_t ib = row0 + 16 * mr + 4 * lg;
-#pragma unroll
-        for (int na = 0; na < NA; ++na) {
-            const uint32_t at = atom0 + 16 * na + li;
-            if (at >= a.dict_size) continue;
-            if (packed) {
-                if (ib >= a.rows_per_group) continue;
-                const uint32_t b = ib / (a.queries * h_per), rem = ib % (a.queries * h_per);
-                const uint32_t q = rem / h_per, h = dg * a.gqa + rem % h_per;
-                const uint32_t g = h / a.gqa, r = q * a.gqa + h % a.gqa;
-                const uint64_t lbg = ((uint64_t)l * a.batch + b) * a.kv_heads + g;
+            for (int j = 0; j < KS; ++j) acc = mfma16x16x32(aop[j], bop[mr][j], acc);
+            if (rok[mr] && ao < a.dict_size) { // dict_size % 16 == 0: all four atoms are in range
                 half4_t v;
-                v[0] = (_Float16)acc[mr][na][0];
-                v[1] = (_Float16)acc[mr][na][1];
-                v[2] = (_Float16)acc[mr][na][2];
-                v[3] = (_Float16)acc[mr][na][3];
-                *(half4_t*)(a.ql + (lbg * a.dict_size + at) * a.rows_r + r) = v;
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const uint32_t i = ib + e;
-                    if (i >= a.rows_per_group) continue;
-                    const uint32_t b = i / (a.queries * h_per), rem = i % (a.queries * h_per);
-                    const uint32_t q = rem / h_per, h = dg * a.gqa + rem % h_per;
-                    const uint32_t g = h / a.gqa, r = q * a.gqa + h % a.gqa;
-                    const uint64_t lbg = ((uint64_t)l * a.batch + b) * a.kv_heads + g;
-                    a.ql[(lbg * a.dict_size + at) * a.rows_r + r] =
-                        __builtin_bit_cast(uint16_t, (_Float16)acc[mr][na][e]);
-                }
+                v[0] = (_Float16)acc[0];
+                v[1] = (_Float16)acc[1];
+                v[2] = (_Float16)acc[2];
+                v[3] = (_Float16)acc[3];
+                *(half4_t*)(a.ql + qrow[mr] * a.dict_size + ao) = v;
             }
         }
     }
@@ -450,13 +456,14 @@ __global__ __launch_bounds__(64) void hot_kernel(HotArgs a) {
 // proves the bins could not have overflowed; when it cannot (scores far above
 // the first tile's, or coefficients far larger), the split is recomputed
 // exactly: a pass for the per-row maxima, a pass for the exact bound, a pass
-// for the bins.  Truncating float->int conversion keeps errors below one unit
-// of 2^-F per contribution, far under the output tolerance at these scales.
+// for the bins.  Each contribution is rounded to the nearest unit of 2^-F
+// (half away from zero), so bin errors are unbiased, at most half a unit per
+// contribution.
 //
 // The kv heads of one (sequence, chunk, split) run on one XCD (work-groups are
 // dealt round-robin over the 8 XCDs), so the 128-byte lines interleaving their
 // 16-byte codes come from HBM once per XCD L2.
-template <int RC, int CPT>
+template <int RC, int CPT, int PD>
 __global__ __launch_bounds__(kColdThreads) void cold_kernel(ColdArgs a) {
     constexpr int NT = kColdThreads, NW = NT / 64, NP = (RC + 1) / 2, NRED = 2 * RC + 2;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -508,11 +515,36 @@ __global__ __launch_bounds__(kColdThreads) void cold_kernel(ColdArgs a) {
                                       (uint64_t)(r % a.gqa) * a.s_j
                                 : 0;
         }
-        for (uint32_t at = tid; at < A; at += NT)
+        // Atom-contiguous rows (s_a == 1, q_latent's layout): 16-byte loads of 8 atoms per
+        // row, interleaved into [A][RC] in registers.
+        if (a.s_a == 1 && (A % 8) == 0 && ((uintptr_t)a.ql & 15u) == 0) {
+            for (uint32_t a8 = tid; a8 < A / 8; a8 += NT) {
+                uint4_t w[RC];
 #pragma unroll
-            for (int rr = 0; rr < RC; ++rr)
-                qtab[at * RC + rr] =
-                    __builtin_bit_cast(_Float16, rok[rr] ? a.ql[rbase[rr] + (uint64_t)at * a.s_a] : (uint16_t)0);
+                for (int rr = 0; rr < RC; ++rr)
+                    w[rr] = rok[rr] ? *(const uint4_t*)(a.ql + rbase[rr] + (uint64_t)a8 * 8) : (uint4_t)0u;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    _Float16 hv[RC];
+#pragma unroll
+                    for (int rr = 0; rr < RC; ++rr)
+                        hv[rr] = __builtin_bit_cast(_Float16, (uint16_t)(w[rr][e / 2] >> (16 * (e % 2))));
+                    if constexpr (RC == 4) {
+                        half4_t v4 = {hv[0], hv[1], hv[2], hv[3]};
+                        *(half4_t*)(qtab + (a8 * 8 + e) * 4) = v4;
+                    } else {
+#pragma unroll
+                        for (int rr = 0; rr < RC; ++rr) qtab[(a8 * 8 + e) * RC + rr] = hv[rr];
+                    }
+                }
+            }
+        } else {
+            for (uint32_t at = tid; at < A; at += NT)
+#pragma unroll
+                for (int rr = 0; rr < RC; ++rr)
+                    qtab[at * RC + rr] =
+                        __builtin_bit_cast(_Float16, rok[rr] ? a.ql[rbase[rr] + (uint64_t)at * a.s_a] : (uint16_t)0);
+        }
     }
     // The split's block refs, resolved once, so code addresses come from LDS.
     {
@@ -655,7 +687,8 @@ __global__ __launch_bounds__(kColdThreads) void cold_kernel(ColdArgs a) {
             const float plan = w[0] * (float)n_tiles; // bound on sum |p*c| over the split, if tiles are alike
             F = plan > 0.0f ? min(100, max(-100, 28 - (ilogbf(plan) + 1))) : 0;
         }
-        // Stream every tile into the bins.
+        // Stream every tile into the bins; PD tiles of code loads stay in flight
+        // (a ring of registers, refilled as each slot is consumed).
         const float Ff = (float)F;
         float rf[RC];
 #pragma unroll
@@ -664,43 +697,52 @@ __global__ __launch_bounds__(kColdThreads) void cold_kernel(ColdArgs a) {
             rf[rr] = Ff - ref[rr];
         }
         cmx = 0.0f;
-        for (uint32_t t0 = t_begin; t0 < t_end; t0 += tile_tokens) {
-            uint4_t nxt[CPT];
-            bool nxtv[CPT];
-            const bool more = t0 + tile_tokens < t_end;
-            if (more) load_tile(t0 + tile_tokens, nxt, nxtv);
+        uint4_t ring[PD][CPT];
+        bool rv[PD][CPT];
 #pragma unroll
-            for (int kk = 0; kk < CPT; ++kk) {
-                if (!curv[kk]) continue;
-                float sc[RC];
-                uint32_t ia[4];
-                float cf[4];
-                score(cur[kk], sc, ia, cf);
-                cmx = fmaxf(cmx, cmax4(cf));
-                float ps[RC]; // p * 2^F
+        for (int kk = 0; kk < CPT; ++kk) {
+            ring[0][kk] = cur[kk];
+            rv[0][kk] = curv[kk];
+        }
 #pragma unroll
-                for (int rr = 0; rr < RC; ++rr) {
-                    ps[rr] = fast_exp2(fmaf(sc[rr], sl, rf[rr]));
-                    lpart[rr] += ps[rr];
-                }
+        for (int d = 1; d < PD; ++d) load_tile(t_begin + d * tile_tokens, ring[d], rv[d]);
+        for (uint32_t t0 = t_begin; t0 < t_end; t0 += PD * tile_tokens) {
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    uint64_t* bp = bins + ia[j] * NP;
-#pragma unroll
-                    for (int pp = 0; pp < NP; ++pp) {
-                        const int32_t v0 = (int32_t)(ps[2 * pp] * cf[j]);
-                        const int32_t v1 = (2 * pp + 1 < RC) ? (int32_t)(ps[min(2 * pp + 1, RC - 1)] * cf[j]) : 0;
-                        const uint64_t wv = ((uint64_t)(uint32_t)v1 << 32) + (uint64_t)(int64_t)v0;
-                        __hip_atomic_fetch_add(bp + pp, wv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-                    }
-                }
-            }
-            if (more) {
+            for (int d = 0; d < PD; ++d) {
 #pragma unroll
                 for (int kk = 0; kk < CPT; ++kk) {
-                    cur[kk] = nxt[kk];
-                    curv[kk] = nxtv[kk];
+                    if (!rv[d][kk]) continue;
+                    const uint4_t cw = ring[d][kk];
+                    float sc[RC];
+                    uint32_t ia[4];
+                    float cf[4];
+                    score(cw, sc, ia, cf);
+                    cmx = fmaxf(cmx, cmax4(cf));
+                    float ps[RC]; // p * 2^F
+#pragma unroll
+                    for (int rr = 0; rr < RC; ++rr) {
+                        ps[rr] = fast_exp2(fmaf(sc[rr], sl, rf[rr]));
+                        lpart[rr] += ps[rr];
+                    }
+                    // Round half away from zero (p > 0, so the sign is c's): the
+                    // +-0.5 rides in the FMA and the conversion truncates.
+                    const uint32_t cbits[4] = {cw[2] << 16, cw[2], cw[3] << 16, cw[3]};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        uint64_t* bp = bins + ia[j] * NP;
+                        const float hc = __builtin_bit_cast(float, (cbits[j] & 0x80000000u) | 0x3F000000u);
+#pragma unroll
+                        for (int pp = 0; pp < NP; ++pp) {
+                            const int32_t v0 = (int32_t)fmaf(ps[2 * pp], cf[j], hc);
+                            const int32_t v1 =
+                                (2 * pp + 1 < RC) ? (int32_t)fmaf(ps[min(2 * pp + 1, RC - 1)], cf[j], hc) : 0;
+                            const uint64_t wv = ((uint64_t)(uint32_t)v1 << 32) + (uint64_t)(int64_t)v0;
+                            __hip_atomic_fetch_add(bp + pp, wv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                        }
+                    }
                 }
+                // Refill this slot with the tile PD ahead.
+                load_tile(t0 + (d + PD) * tile_tokens, ring[d], rv[d]);
             }
         }
         // Overflow proof: every |bin| <= sum over contributions |p*c|*2^F <= 4*max|c|*sum_r sum_t p*2^F.
@@ -838,50 +880,19 @@ inline size_t cold_smem_bytes(uint32_t A, int RC, uint32_t tokens_per_split) {
 // pre-multiplied by 2^(m_s - Mc) / Lc * scl with scl a power of two that keeps
 // the largest combined bin below 2^14, so the hi/lo f16 split of each bin keeps
 // ~22 significant bits.  Hot splits combine to Mh, Lh with factors 2^(m_s - Mh).
+// Computed by one wave per row, lane = split.
 struct RowFactors {
     float Mc, Lc, inv_scl, Mh, Lh;
 };
 
-__device__ inline void cold_row_factors(const float* cm, const float* cl, const float* camax, uint32_t S,
-                                        uint64_t base, uint32_t R, float* fac_out, float& Mc, float& Lc,
-                                        float& inv_scl) {
-    Mc = -INFINITY;
-    for (uint32_t s = 0; s < S; ++s)
-        if (cl[base + (uint64_t)s * R] > 0.0f) Mc = fmaxf(Mc, cm[base + (uint64_t)s * R]);
-    Lc = 0.0f;
-    float bound = 0.0f;
-    for (uint32_t s = 0; s < S; ++s) {
-        const float l = cl[base + (uint64_t)s * R];
-        const float f = l > 0.0f ? fast_exp2(cm[base + (uint64_t)s * R] - Mc) : 0.0f;
-        Lc += f * l;
-        bound += f * camax[base + (uint64_t)s * R];
-    }
+__device__ inline float bin_scale(float bound, float Lc) {
     float scl = 1.0f;
     if (Lc > 0.0f && bound > 0.0f) {
         int e = ilogbf(bound / Lc) + 1;
         e = max(-100, min(100, e));
         scl = ldexpf(1.0f, 14 - e);
     }
-    inv_scl = 1.0f / scl;
-    if (fac_out)
-        for (uint32_t s = 0; s < S; ++s) {
-            const float l = cl[base + (uint64_t)s * R];
-            fac_out[s] = l > 0.0f ? fast_exp2(cm[base + (uint64_t)s * R] - Mc) / Lc * scl : 0.0f;
-        }
-}
-
-__device__ inline void hot_row_factors(const float* hm, const float* hl, uint32_t S, uint64_t base, uint32_t R,
-                                       float* fac_out, float& Mh, float& Lh) {
-    Mh = -INFINITY;
-    for (uint32_t s = 0; s < S; ++s)
-        if (hl[base + (uint64_t)s * R] > 0.0f) Mh = fmaxf(Mh, hm[base + (uint64_t)s * R]);
-    Lh = 0.0f;
-    for (uint32_t s = 0; s < S; ++s) {
-        const float l = hl[base + (uint64_t)s * R];
-        const float f = l > 0.0f ? fast_exp2(hm[base + (uint64_t)s * R] - Mh) : 0.0f;
-        Lh += f * l;
-        fac_out[s] = f;
-    }
+    return scl;
 }
 
 // out = (wh*Oh + wc*Lc*Oc) / (wh*Lh + wc*Lc); zero when nothing was visible.
@@ -911,10 +922,11 @@ __device__ inline float merge_value(float oh, float Mh, float Lh, float oc, floa
 template <int HD>
 __global__ __launch_bounds__(256) void finish_kernel(FinishArgs a) {
     constexpr int NB = HD / 16, P = HD + 4, ROWS = 64;
-    constexpr int PIECES = 32 * HD / 8;    // 16-byte pieces per dictionary chunk
-    constexpr int PPT = PIECES / 256;      // pieces per thread (2 at HD=128, 1 at HD=64)
+    constexpr int PIECES = 32 * HD / 8; // 16-byte pieces per dictionary chunk
+    constexpr int PPT = PIECES / 256;   // pieces per thread (2 at HD=128, 1 at HD=64)
     __shared__ __attribute__((aligned(16))) _Float16 sd[2][32 * P];
     __shared__ float s_cfac[ROWS][kMaxSplits];
+    __shared__ float s_hfac[ROWS][kMaxSplits];
     __shared__ RowFactors s_rf[ROWS];
     __shared__ uint64_t s_row[ROWS]; // lbg*R + r, or ~0 for padding rows
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, li = lane & 15, lg = lane >> 4;
@@ -923,23 +935,58 @@ __global__ __launch_bounds__(256) void finish_kernel(FinishArgs a) {
     const uint32_t l = group / a.dict_heads, dg = group % a.dict_heads;
     const uint32_t R = a.rows_r, A = a.dict_size;
     const uint32_t hg = a.dict_heads == 1 ? a.kv_heads : 1;
+    const bool fused = a.n_ar == 1 && a.hot_splits > 0;
 
-    if (tid < ROWS) {
-        const uint32_t i = tile * ROWS + tid;
-        uint64_t rowid = ~0ull;
-        if (i < a.rows_per_group) {
-            const uint32_t b = i / (hg * R), rem = i % (hg * R);
-            const uint32_t g = a.dict_heads == 1 ? rem / R : dg, r = rem % R;
-            const uint64_t lbg = ((uint64_t)l * a.batch + b) * a.kv_heads + g;
-            rowid = lbg * R + r;
+    // Split factors: wave w combines rows 16w..16w+15, lane = split; all loads first.
+    {
+        constexpr int RPW = ROWS / 4;
+        uint64_t rid[RPW];
+        float cm[RPW], cl[RPW], ca[RPW], hm[RPW], hl[RPW];
+#pragma unroll
+        for (int i = 0; i < RPW; ++i) {
+            const uint32_t row = tile * ROWS + wave * RPW + i;
+            rid[i] = ~0ull;
+            cm[i] = hm[i] = -INFINITY;
+            cl[i] = ca[i] = hl[i] = 0.0f;
+            if (row < a.rows_per_group) {
+                const uint32_t b = row / (hg * R), rem = row % (hg * R);
+                const uint32_t g = a.dict_heads == 1 ? rem / R : dg, r = rem % R;
+                const uint64_t lbg = ((uint64_t)l * a.batch + b) * a.kv_heads + g;
+                rid[i] = lbg * R + r;
+                if ((uint32_t)lane < a.cold_splits) {
+                    const uint64_t cb = (lbg * a.cold_splits + lane) * R + r;
+                    cm[i] = a.cold_m[cb];
+                    cl[i] = a.cold_l[cb];
+                    ca[i] = a.cold_amax[cb];
+                }
+                if (fused && (uint32_t)lane < a.hot_splits) {
+                    const uint64_t hb = (lbg * a.hot_splits + lane) * R + r;
+                    hm[i] = a.hot_m[hb];
+                    hl[i] = a.hot_l[hb];
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < RPW; ++i) {
+            const int row = wave * RPW + i;
             RowFactors rf;
-            cold_row_factors(a.cold_m, a.cold_l, a.cold_amax, a.cold_splits, lbg * a.cold_splits * R + r, R,
-                             s_cfac[tid], rf.Mc, rf.Lc, rf.inv_scl);
+            float f;
+            combine_splits(cm[i], cl[i], rf.Mc, rf.Lc, f);
+            const float scl = bin_scale(wave_sum(f * ca[i]), rf.Lc);
+            rf.inv_scl = 1.0f / scl;
+            if (lane < kMaxSplits) s_cfac[row][lane] = rf.Lc > 0.0f ? f / rf.Lc * scl : 0.0f;
             rf.Mh = -INFINITY;
             rf.Lh = 0.0f;
-            s_rf[tid] = rf;
+            if (fused) {
+                float fh;
+                combine_splits(hm[i], hl[i], rf.Mh, rf.Lh, fh);
+                if (lane < kMaxSplits) s_hfac[row][lane] = fh;
+            }
+            if (lane == 0) {
+                s_rf[row] = rf;
+                s_row[row] = rid[i];
+            }
         }
-        s_row[tid] = rowid;
     }
 
     const uint16_t* dict = a.dict + (uint64_t)l * a.dict_layer + (uint64_t)dg * A * HD;
@@ -1012,19 +1059,26 @@ __global__ __launch_bounds__(256) void finish_kernel(FinishArgs a) {
         if (rowok && !single) {
 #pragma unroll
             for (int e = 0; e < 8; ++e) w8[e] = 0.0f;
-            for (uint32_t s = 0; s < a.cold_splits; ++s) {
-                const float f = s_cfac[myr][s];
-                if (f == 0.0f) continue;
-                const float* wrow = wbase + s * wsplit;
+            const uint32_t at0 = a0 + 4 * lg, at1 = a0 + 16 + 4 * lg;
+            // Four splits' loads in flight at a time; empty splits are never read.
+            for (uint32_t s0 = 0; s0 < a.cold_splits; s0 += 4) {
+                float4_t v0[4], v1[4];
+                float fs[4];
 #pragma unroll
-                for (int half = 0; half < 2; ++half) {
-                    const uint32_t at = a0 + 16 * half + 4 * lg;
-                    if (at < a_end) {
-                        const float4_t v = *(const float4_t*)(wrow + at);
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) w8[4 * half + e] += f * v[e];
-                    }
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t sp = s0 + j;
+                    fs[j] = sp < a.cold_splits ? s_cfac[myr][sp] : 0.0f;
+                    const float* wrow = wbase + sp * wsplit;
+                    v0[j] = (fs[j] != 0.0f && at0 < a_end) ? *(const float4_t*)(wrow + at0) : (float4_t)0.0f;
+                    v1[j] = (fs[j] != 0.0f && at1 < a_end) ? *(const float4_t*)(wrow + at1) : (float4_t)0.0f;
                 }
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        w8[e] += fs[j] * v0[j][e];
+                        w8[4 + e] += fs[j] * v1[j][e];
+                    }
             }
         }
         half8_t hi, lo;
@@ -1052,7 +1106,7 @@ __global__ __launch_bounds__(256) void finish_kernel(FinishArgs a) {
     // Lane holds O^T[dims 16*nb + 4*lg + e][row li of this wave].
     const RowFactors rf = s_rf[myr];
     const uint64_t rowid = myrow;
-    if (a.n_ar > 1) {
+    if (!fused && a.n_ar > 1) {
         float* dst = a.ocp + (rowid * a.n_ar + ar) * HD;
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) *(float4_t*)(dst + 16 * nb + 4 * lg) = acc[nb] * rf.inv_scl;
@@ -1060,21 +1114,13 @@ __global__ __launch_bounds__(256) void finish_kernel(FinishArgs a) {
     }
     // Fused merge with the hot partials of this row.
     const uint64_t lbg = rowid / R, r = rowid % R;
-    float Mh = -INFINITY, Lh = 0.0f;
-    for (uint32_t s = 0; s < a.hot_splits; ++s) {
-        const uint64_t hb = (lbg * a.hot_splits + s) * R + r;
-        if (a.hot_l[hb] > 0.0f) Mh = fmaxf(Mh, a.hot_m[hb]);
-    }
     float4_t oh[NB];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) oh[nb] = (float4_t)0.0f;
     for (uint32_t s = 0; s < a.hot_splits; ++s) {
-        const uint64_t hb = (lbg * a.hot_splits + s) * R + r;
-        const float hl = a.hot_l[hb];
-        if (!(hl > 0.0f)) continue;
-        const float f = fast_exp2(a.hot_m[hb] - Mh);
-        Lh += f * hl;
-        const float* src = a.hot_o + hb * HD;
+        const float f = s_hfac[myr][s];
+        if (f == 0.0f) continue;
+        const float* src = a.hot_o + ((lbg * a.hot_splits + s) * R + r) * HD;
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) oh[nb] += f * *(const float4_t*)(src + 16 * nb + 4 * lg);
     }
@@ -1086,46 +1132,45 @@ __global__ __launch_bounds__(256) void finish_kernel(FinishArgs a) {
         half4_t v;
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-            v[e] = (_Float16)merge_value(oh[nb][e], Mh, Lh, acc[nb][e] * rf.inv_scl, rf.Mc, rf.Lc);
+            v[e] = (_Float16)merge_value(oh[nb][e], rf.Mh, rf.Lh, acc[nb][e] * rf.inv_scl, rf.Mc, rf.Lc);
         *(half4_t*)(o + 16 * nb + 4 * lg) = v;
     }
 }
 
 // --------------------------------------------------- log-sum-exp merge
 //
-// One 64-thread group per row (row id lbg*R + r), four rows per work-group;
-// used when there is no cold pool or when the cold output was split over
+// One wave per row (row id lbg*R + r), four rows per work-group: lanes first
+// combine the row's splits (lane = split), then each lane merges HD/64 dims.
+// Used when there is no cold pool or when the cold output was split over
 // several atom ranges.
 template <int HD>
 __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
     constexpr int DPT = HD / 64;
     __shared__ float s_hfac[4][kMaxSplits];
-    __shared__ RowFactors s_rf[4];
     const int tid = threadIdx.x, row = tid / 64, lane = tid % 64;
     const uint64_t rowid = (uint64_t)blockIdx.x * 4 + row;
+    if (rowid >= a.total_rows) return; // whole wave: no barrier follows
     const uint32_t R = a.rows_r;
-    if (lane == 0) {
-        RowFactors rf;
-        rf.Mc = -INFINITY;
-        rf.Lc = 0.0f;
-        rf.inv_scl = 1.0f;
-        rf.Mh = -INFINITY;
-        rf.Lh = 0.0f;
-        if (rowid < a.total_rows) {
-            const uint64_t lbg = rowid / R, r = rowid % R;
-            if (a.ocp)
-                cold_row_factors(a.cold_m, a.cold_l, a.cold_amax, a.cold_splits, lbg * a.cold_splits * R + r, R,
-                                 nullptr, rf.Mc, rf.Lc, rf.inv_scl);
-            if (a.hot_splits)
-                hot_row_factors(a.hot_m, a.hot_l, a.hot_splits, lbg * a.hot_splits * R + r, R, s_hfac[row], rf.Mh,
-                                rf.Lh);
-        }
-        s_rf[row] = rf;
-    }
-    __syncthreads();
-    if (rowid >= a.total_rows) return;
-    const RowFactors rf = s_rf[row];
     const uint64_t lbg = rowid / R, r = rowid % R;
+    float Mc = -INFINITY, Lc = 0.0f, Mh = -INFINITY, Lh = 0.0f;
+    {
+        float cm = -INFINITY, cl = 0.0f, hm = -INFINITY, hl = 0.0f;
+        if (a.ocp && (uint32_t)lane < a.cold_splits) {
+            const uint64_t cb = (lbg * a.cold_splits + lane) * R + r;
+            cm = a.cold_m[cb];
+            cl = a.cold_l[cb];
+        }
+        if ((uint32_t)lane < a.hot_splits) {
+            const uint64_t hb = (lbg * a.hot_splits + lane) * R + r;
+            hm = a.hot_m[hb];
+            hl = a.hot_l[hb];
+        }
+        float f;
+        combine_splits(cm, cl, Mc, Lc, f);
+        combine_splits(hm, hl, Mh, Lh, f);
+        if (lane < kMaxSplits) s_hfac[row][lane] = f;
+    }
+    __builtin_amdgcn_wave_barrier();
     const int d0 = lane * DPT;
     float oc[DPT], oh[DPT];
 #pragma unroll
@@ -1133,24 +1178,45 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
         oc[e] = 0.0f;
         oh[e] = 0.0f;
     }
-    if (a.ocp)
-        for (uint32_t ar = 0; ar < a.n_ar; ++ar) {
-            const float* src = a.ocp + (rowid * a.n_ar + ar) * HD + d0;
+    if (a.ocp) {
+        const float* src = a.ocp + rowid * a.n_ar * HD + d0;
+        uint32_t ar = 0;
+        for (; ar + 4 <= a.n_ar; ar += 4) {
+            float v[4][DPT];
 #pragma unroll
-            for (int e = 0; e < DPT; ++e) oc[e] += src[e];
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int e = 0; e < DPT; ++e) v[j][e] = src[(ar + j) * HD + e];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int e = 0; e < DPT; ++e) oc[e] += v[j][e];
         }
-    for (uint32_t s = 0; s < a.hot_splits; ++s) {
-        const float f = s_hfac[row][s];
-        const float* src = a.hot_o + ((lbg * a.hot_splits + s) * R + r) * HD + d0;
+        for (; ar < a.n_ar; ++ar)
 #pragma unroll
-        for (int e = 0; e < DPT; ++e) oh[e] += f == 0.0f ? 0.0f : f * src[e];
+            for (int e = 0; e < DPT; ++e) oc[e] += src[ar * HD + e];
+    }
+    const float* hsrc = a.hot_o + (lbg * a.hot_splits * R + r) * HD + d0;
+    for (uint32_t s0 = 0; s0 < a.hot_splits; s0 += 4) {
+        float v[4][DPT], fs[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t sp = s0 + j;
+            fs[j] = sp < a.hot_splits ? s_hfac[row][sp] : 0.0f;
+#pragma unroll
+            for (int e = 0; e < DPT; ++e) v[j][e] = fs[j] != 0.0f ? hsrc[(uint64_t)sp * R * HD + e] : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int e = 0; e < DPT; ++e) oh[e] += fs[j] * v[j][e];
     }
     const uint64_t lb = lbg / a.kv_heads, g = lbg % a.kv_heads;
     const uint64_t q = r / a.gqa, h = g * a.gqa + r % a.gqa;
     uint16_t* o = a.out + ((lb * a.queries + q) * a.q_heads + h) * HD + d0;
 #pragma unroll
     for (int e = 0; e < DPT; ++e)
-        o[e] = __builtin_bit_cast(uint16_t, (_Float16)merge_value(oh[e], rf.Mh, rf.Lh, oc[e], rf.Mc, rf.Lc));
+        o[e] = __builtin_bit_cast(uint16_t, (_Float16)merge_value(oh[e], Mh, Lh, oc[e], Mc, Lc));
 }
 
 // ------------------------------------------------ codec check (bit-exact)

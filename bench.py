@@ -53,6 +53,9 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--stage-sweep", action="store_true", help="per-kernel times at every batch size")
+    p.add_argument("--rocpd-summary", metavar="DB", help="print a per-kernel summary of a rocprofv3 database and exit")
+    p.add_argument("--kernel-filter", default="aw::", help="kernel-name filter for --rocpd-summary")
     return p.parse_args()
 
 
@@ -189,8 +192,46 @@ def reference_bench_config(engine, seed, steps):
                     "past its 16-block pool)"}
 
 
+def rocpd_summary(db: str, name_filter: str) -> str:
+    """Per-kernel summary of a rocprofv3 database (kernel trace and, when
+    present, counters averaged per dispatch), grouped by kernel and grid."""
+    import collections
+    import sqlite3
+    c = sqlite3.connect(db)
+    lines = []
+    dur = collections.defaultdict(list)
+    for name, d, gx, gy, wgx, vg, ag, lds in c.execute(
+            "select name, duration, grid_x, grid_y, workgroup_x, vgpr_count, accum_vgpr_count, lds_size from kernels"):
+        if name_filter in name:
+            dur[(name, gx, gy, wgx, vg, ag, lds)].append(d / 1e3)
+    lines.append("kernel | grid | wg | vgpr | agpr | lds | launches | avg_us | min_us | max_us")
+    for k, v in sorted(dur.items(), key=lambda x: -sum(x[1])):
+        lines.append(f"{k[0][:60]} | {k[1]}x{k[2]} | {k[3]} | {k[4]} | {k[5]} | {k[6]} | {len(v)} | "
+                     f"{sum(v) / len(v):.2f} | {min(v):.2f} | {max(v):.2f}")
+    try:
+        rows = list(c.execute("select kernel_name, grid_size, dispatch_id, counter_name, value from counters_collection"))
+    except sqlite3.Error:
+        rows = []
+    if rows:
+        per = collections.defaultdict(lambda: collections.defaultdict(float))
+        nd = collections.defaultdict(set)
+        for kn, gs, did, cn, v in rows:
+            if name_filter in kn:
+                per[(kn, gs)][cn] += v
+                nd[(kn, gs)].add(did)
+        lines.append("counters (average per dispatch)")
+        for key in per:
+            n = len(nd[key])
+            lines.append(f"{key[0][:60]} | grid {key[1]} | dispatches {n} | " +
+                         " ".join(f"{cn}={v / n:.0f}" for cn, v in sorted(per[key].items())))
+    return "\n".join(lines)
+
+
 def main():
     args = parse()
+    if args.rocpd_summary:
+        print(rocpd_summary(args.rocpd_summary, args.kernel_filter))
+        return 0
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               "(the Weaver path shards by sequence / kv head with no exchange; see the design notes)",
@@ -215,6 +256,9 @@ def main():
         row = {"batch": B, "ms_per_step": round(ms, 5), "tokens_per_s": round(B / (ms * 1e-3), 1),
                "alg_bytes_per_step": int(ab), "achieved_gbps": round(gbps, 1),
                "frac_of_peak": round(gbps / PEAK_HBM_GBPS, 4), "copies": geom.copies}
+        if args.stage_sweep:
+            row["stages_us"] = {k: (round(v * 1e3, 2) if v else None)
+                                for k, (v, n) in r.stage_times(max(args.steps, 10)).items()}
         log(json.dumps(row))
         sweep.append(row)
         if B == max(batches):
