@@ -829,14 +829,14 @@ int aw_decode(aw_engine* e, const uint16_t* q_exact, size_t n_q_exact, const uin
 int aw_decode_device(aw_engine* e, const aw_decode_desc* desc, void* stream) {
     if (!e) return AW_E_INVALID_ARG;
     AW_HIP(e, hipSetDevice(e->device));
-    hipStream_t st = stream ? (hipStream_t)stream : e->stream;
+    hipStream_t st = (hipStream_t)stream; // NULL is HIP's null stream
     return decode_device(e, desc, st);
 }
 
 int aw_engine_check_device_errors(aw_engine* e, void* stream) {
     if (!e) return AW_E_INVALID_ARG;
     AW_HIP(e, hipSetDevice(e->device));
-    hipStream_t st = stream ? (hipStream_t)stream : e->stream;
+    hipStream_t st = (hipStream_t)stream; // NULL is HIP's null stream
     uint32_t word = 0;
     AW_HIP(e, hipMemcpyAsync(&word, e->err, 4, hipMemcpyDeviceToHost, st));
     AW_HIP(e, hipStreamSynchronize(st));
@@ -857,7 +857,7 @@ int aw_debug_gather_codes(aw_engine* e, const aw_sparse_code* codes, size_t n, c
         return fail(e, AW_E_INVALID_ARG, "null pointer or zero size");
     if ((uintptr_t)codes & 15u) return fail(e, AW_E_ALIGN, "codes pointer is not 16-byte aligned");
     AW_HIP(e, hipSetDevice(e->device));
-    hipStream_t st = stream ? (hipStream_t)stream : e->stream;
+    hipStream_t st = (hipStream_t)stream; // NULL is HIP's null stream
     const uint64_t threads = (uint64_t)n * 4;
     hipLaunchKernelGGL(aw::gather_codes_kernel, dim3(cdiv(threads, 256)), dim3(256), 0, st,
                        (const aw::uint4_t*)codes, (uint64_t)n, dict, dict_size, head_dim, idx, coef, atoms, e->err);

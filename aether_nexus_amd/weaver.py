@@ -113,6 +113,19 @@ def _ptr(x) -> Optional[int]:
     return x.data_ptr()  # torch tensor on the device
 
 
+def _stream(stream: Optional[int]) -> Optional[int]:
+    """The hipStream_t to run on: the given handle, else torch's current stream
+    (so the work is ordered after the torch work that produced the inputs),
+    else HIP's null stream."""
+    if stream is not None:
+        return stream
+    import sys
+    torch = sys.modules.get("torch")
+    if torch is not None and torch.cuda.is_initialized():
+        return torch.cuda.current_stream().cuda_stream or None
+    return None
+
+
 class WeaverEngine:
     """gfx950 Weaver decode engine (reference: weaver.rs:31-56)."""
 
@@ -186,17 +199,17 @@ class WeaverEngine:
     # -- device API
     def decode_device(self, desc: DecodeDesc, stream: Optional[int] = None) -> None:
         """Enqueue one batched decode described by ``desc`` (device pointers)."""
-        rc = self._lib.aw_decode_device(self._h, ctypes.byref(desc), stream)
+        rc = self._lib.aw_decode_device(self._h, ctypes.byref(desc), _stream(stream))
         self._check(rc, "decode_device")
 
     def check_device_errors(self, stream: Optional[int] = None) -> None:
-        self._check(self._lib.aw_engine_check_device_errors(self._h, stream), "device check")
+        self._check(self._lib.aw_engine_check_device_errors(self._h, _stream(stream)), "device check")
 
     def gather_codes(self, codes, n_codes: int, dictionary, dict_size: int, head_dim: int, idx, coef, atoms,
                      stream: Optional[int] = None) -> None:
         """Bit-exact SparseCode decode + atom gather on the device (device pointers/tensors)."""
         rc = self._lib.aw_debug_gather_codes(self._h, _ptr(codes), n_codes, _ptr(dictionary), dict_size, head_dim,
-                                             _ptr(idx), _ptr(coef), _ptr(atoms), stream)
+                                             _ptr(idx), _ptr(coef), _ptr(atoms), _stream(stream))
         self._check(rc, "gather_codes")
 
     def set_profiling(self, enable: bool) -> None:

@@ -208,7 +208,7 @@ int aw_decode(aw_engine* engine,
               uint16_t* out, size_t n_out);
 
 /* Device-resident batched / multi-query / multi-layer decode, asynchronous on
- * `hip_stream` (a hipStream_t; NULL = the engine's own stream).  Extends the
+ * `hip_stream` (a hipStream_t; NULL is HIP's null stream).  Extends the
  * reference kernel (weaver_kernel.metal:118-240) with batch, queries, layers,
  * causal drafts, score scale, shared dictionary and separate V.  Scratch comes
  * from an engine-owned workspace that grows on demand (the growth allocates).

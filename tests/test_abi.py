@@ -1,0 +1,157 @@
+"""The C ABI without a GPU (CPU only): the library loads, exports every
+function include/aether_weaver.h declares, its structs match the ctypes
+mirrors, and the host-side validation and planning behave as documented.
+No compute entry point is called."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from aether_nexus_amd import _lib
+from aether_nexus_amd import workloads as W
+from aether_nexus_amd.types import (AW_E_ALIGN, AW_E_INVALID_ARG, AW_E_OOB, AW_E_UNSUPPORTED, SPARSE_CODE_DTYPE,
+                                    STRUCT_SIZES, DecodeDesc, PlanInfo, WeaverParams)
+from aether_nexus_amd.weaver import WeaverError, plan, validate_params
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "aether_weaver.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(aw_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_function():
+    lib = _lib.load()
+    names = declared_functions()
+    assert len(names) >= 17
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in the header but not exported"
+    assert set(names) == set(_lib.SIGNATURES), "ctypes signatures out of sync with the header"
+
+
+def test_struct_sizes_match():
+    lib = _lib.load()
+    sizes = (ctypes.c_size_t * 4)()
+    lib.aw_abi_struct_sizes(sizes)
+    assert tuple(sizes) == STRUCT_SIZES == (16, 48, ctypes.sizeof(DecodeDesc), ctypes.sizeof(PlanInfo))
+    assert lib.aw_abi_version() == 1
+    assert lib.aw_status_string(AW_E_OOB).decode().startswith("block ref")
+
+
+def params(**kw):
+    p = dict(q_heads=32, kv_heads=8, head_dim=128, block_size=16, gqa_group=4, hot_count=2, cold_count=1,
+             dict_size=512, sparsity_k=4)
+    p.update(kw)
+    return WeaverParams(**p)
+
+
+def good_args(p):
+    n_hot = max(p.hot_count, 1) * 16 * p.kv_heads * p.head_dim
+    cold = np.zeros(max(p.cold_count, 1) * 16 * p.kv_heads, SPARSE_CODE_DTYPE)
+    refs = np.arange(p.hot_count + p.cold_count, dtype=np.uint32)
+    refs[p.hot_count:] -= p.hot_count  # cold refs count from block 0 of the cold pool
+    return dict(n_q_exact=p.q_heads * p.head_dim, n_q_latent=p.q_heads * p.dict_size, n_hot_pool=n_hot,
+                cold_pool=cold, loom_refs=refs, n_dictionary=p.kv_heads * p.dict_size * p.head_dim,
+                n_out=p.q_heads * p.head_dim)
+
+
+def test_validate_accepts_reference_shapes():
+    p = params()
+    validate_params(p, **good_args(p))
+    p0 = params(hot_count=0, cold_count=0)
+    validate_params(p0, n_q_exact=4096, n_q_latent=0, n_hot_pool=0, cold_pool=None, loom_refs=None, n_dictionary=0,
+                    n_out=4096)
+
+
+@pytest.mark.parametrize("change,code", [
+    (dict(gqa_group=3), AW_E_INVALID_ARG),
+    (dict(block_size=32), AW_E_UNSUPPORTED),
+    (dict(sparsity_k=8), AW_E_UNSUPPORTED),
+    (dict(head_dim=96), AW_E_UNSUPPORTED),
+    (dict(dict_size=100), AW_E_UNSUPPORTED),
+])
+def test_validate_rejects_bad_params(change, code):
+    p = params(**change)
+    args = good_args(params())
+    with pytest.raises(WeaverError) as e:
+        validate_params(p, **args)
+    assert e.value.status == code
+
+
+def test_validate_rejects_short_buffers_and_bad_refs():
+    p = params()
+    args = good_args(p)
+    for k in ("n_q_exact", "n_q_latent", "n_dictionary", "n_out"):
+        bad = dict(args)
+        bad[k] = args[k] - 1
+        with pytest.raises(WeaverError) as e:
+            validate_params(p, **bad)
+        assert e.value.status == AW_E_INVALID_ARG, k
+    refs = args["loom_refs"].copy()
+    refs[0] = 2  # hot pool holds 2 blocks
+    with pytest.raises(WeaverError) as e:
+        validate_params(p, **{**args, "loom_refs": refs})
+    assert e.value.status == AW_E_OOB
+    refs = args["loom_refs"].copy()
+    refs[0] = 1 | (1 << 31)  # bit 31 is masked: still block 1
+    validate_params(p, **{**args, "loom_refs": refs})
+    cold = args["cold_pool"].copy()
+    cold["indices"][5, 2] = 512  # atom index == dict_size
+    with pytest.raises(WeaverError) as e:
+        validate_params(p, **{**args, "cold_pool": cold})
+    assert e.value.status == AW_E_OOB
+
+
+def test_validate_rejects_misaligned_codes():
+    lib = _lib.load()
+    p = params()
+    args = good_args(p)
+    buf = np.zeros(args["cold_pool"].nbytes + 32, np.uint8)
+    off = (-buf.ctypes.data) % 16 + 8  # 8 bytes past a 16-byte boundary
+    refs = args["loom_refs"]
+    msg = ctypes.create_string_buffer(256)
+    rc = lib.aw_validate_params(ctypes.byref(p), args["n_q_exact"], args["n_q_latent"], args["n_hot_pool"],
+                                buf.ctypes.data + off, args["cold_pool"].size, refs.ctypes.data, refs.size,
+                                args["n_dictionary"], args["n_out"], msg, 256)
+    assert rc == AW_E_ALIGN
+
+
+def test_plan_splits_and_workspace():
+    """aw_decode_plan: geometry checks and the split plan for the benchmark shapes."""
+    out = np.zeros(1, np.uint16)
+    g = W.hot_cold(batch=64)
+    d = W.make_desc if hasattr(W, "make_desc") else None
+    from aether_nexus_amd.weaver import make_desc
+    desc = make_desc(layers=1, batch=64, queries=1, q_heads=32, kv_heads=8, head_dim=128, dict_size=4096,
+                     dict_heads=1, hot_count=g.hot_count, cold_count=g.cold_count, refs_stride=g.refs_stride,
+                     hot_blocks=g.hot_blocks, cold_blocks=g.cold_blocks, q=1, out=1)
+    info = plan(desc)
+    assert info.rows_per_kv_head == 4
+    assert info.hot_splits >= 1 and info.hot_tokens_per_split % 32 == 0
+    assert info.hot_splits * info.hot_tokens_per_split >= g.hot_count * 16
+    assert info.cold_splits >= 1 and info.cold_splits * info.cold_tokens_per_split >= g.cold_count * 16
+    assert info.cold_row_chunk == 4 and info.computes_q_latent == 1
+    assert info.workspace_bytes > 0
+    del out, d
+    bad = make_desc(layers=1, batch=1, queries=20, q_heads=32, kv_heads=8, head_dim=128, dict_size=4096,
+                    dict_heads=1, hot_count=1, cold_count=0, refs_stride=1, hot_blocks=1, cold_blocks=0, q=1, out=1)
+    with pytest.raises(WeaverError) as e:  # 4 heads x 20 queries = 80 rows per kv head > 64
+        plan(bad)
+    assert e.value.status == AW_E_UNSUPPORTED
+
+
+def test_engine_create_without_gpu_fails_cleanly():
+    """No GPU in this container: creation reports an error instead of crashing."""
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    lib = _lib.load()
+    h = ctypes.c_void_p()
+    rc = lib.aw_engine_create(0, ctypes.byref(h))
+    assert rc != 0 and not h.value

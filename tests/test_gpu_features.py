@@ -1,0 +1,177 @@
+"""GPU parity of the device API's extensions and edge cases, through the C ABI
+(aw_decode_device, aw_debug_gather_codes), against the CPU oracle: golden
+vectors, bit-exact SparseCode decode and atom gather, ragged sequences,
+separate V, odd block counts, many query rows, out-of-range inputs reported
+by the device, and full-size shapes checked on sampled rows."""
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from aether_nexus_amd import workloads as W
+from aether_nexus_amd.types import AW_E_OOB
+from aether_nexus_amd.weaver import WeaverError
+from oracle import oracle
+from tests.helpers import assert_close, run_gpu
+
+pytestmark = pytest.mark.gpu
+FIX = Path(__file__).resolve().parent / "golden" / "tiny_seed1.npz"
+
+
+def t16(bits: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16).copy())
+
+
+@pytest.mark.parametrize("tag,geom", [("shared", W.tiny()), ("perhead", W.tiny(q_heads=4, kv_heads=2, dict_heads=2))])
+def test_golden_vectors(engine, stream, tag, geom):
+    z = np.load(FIX)
+    wl = W.Workload(geom, q=t16(z[f"{tag}_q"]).view(torch.float16), hot_k=t16(z[f"{tag}_hot_k"]).view(torch.float16),
+                    hot_v=None, cold=t16(z[f"{tag}_cold"]),
+                    refs=torch.from_numpy(z[f"{tag}_refs"].view(np.int32).copy()).unsqueeze(0),
+                    dictionary=t16(z[f"{tag}_dictionary"]).view(torch.float16))
+    assert_close(run_gpu(engine, wl, stream), z[f"{tag}_out_f64"], f"golden {tag}")
+
+
+def test_codec_gather_bit_exact(engine, stream):
+    """SparseCode decode and atom indexing on the device, bitwise against the CPU."""
+    n, A, D = 4096, 512, 64
+    gen = torch.Generator().manual_seed(3)
+    codes = W.make_codes(gen, (n,), A, 0.5, None, "cpu")
+    codes[0, :4] = torch.tensor([1, 42, 255, 511], dtype=torch.int16)  # types.rs:547-557 known answer
+    codes[0, 4:] = torch.tensor([0.5, -0.25, 1.0, 0.0], dtype=torch.float16).view(torch.int16)
+    dic = torch.randn((A, D), generator=gen).to(torch.float16)
+    idx = torch.empty(n * 4, dtype=torch.int32, device="cuda")
+    coef = torch.empty(n * 4, dtype=torch.float32, device="cuda")
+    atoms = torch.empty((n * 4, D), dtype=torch.int16, device="cuda")
+    cd, dd = codes.cuda(), dic.cuda()
+    engine.gather_codes(cd, n, dd, A, D, idx, coef, atoms, stream=stream)
+    engine.check_device_errors(stream)
+    ri, rc, ra = oracle.gather_codes(codes.numpy().view(np.uint16), dic.view(torch.int16).numpy().view(np.uint16), A, D)
+    np.testing.assert_array_equal(idx.cpu().numpy().view(np.uint32), ri)
+    np.testing.assert_array_equal(coef.cpu().numpy().view(np.uint32), rc.view(np.uint32))
+    np.testing.assert_array_equal(atoms.cpu().numpy().view(np.uint16), ra)
+    assert ri[:4].tolist() == [1, 42, 255, 511] and rc[:4].tolist() == [0.5, -0.25, 1.0, 0.0]
+
+
+def test_codec_out_of_range_index_is_reported(engine, stream):
+    """An atom index >= dict_size (forced from the host) is skipped and reported."""
+    n, A, D = 64, 512, 64
+    codes = torch.zeros((n, 8), dtype=torch.int16)
+    codes[7, 2] = A  # out of range
+    dic = torch.zeros((A, D), dtype=torch.float16)
+    idx = torch.empty(n * 4, dtype=torch.int32, device="cuda")
+    coef = torch.empty(n * 4, dtype=torch.float32, device="cuda")
+    atoms = torch.empty((n * 4, D), dtype=torch.int16, device="cuda")
+    engine.gather_codes(codes.cuda(), n, dic.cuda(), A, D, idx, coef, atoms, stream=stream)
+    with pytest.raises(WeaverError) as e:
+        engine.check_device_errors(stream)
+    assert e.value.status == AW_E_OOB
+    assert np.all(atoms.cpu().numpy()[7 * 4 + 2].view(np.uint16) == 0xFFFF)
+    engine.check_device_errors(stream)  # the record was cleared
+
+
+def test_ragged_sequences(engine, stream):
+    """Per-sequence hot/cold block counts, including empty pools."""
+    geom = W.hot_cold(batch=4, hot_count=6, cold_count=40, dict_size=1024)
+    wl = W.generate(geom, seed=21)
+    wl.seq_hot = torch.tensor([[6, 1, 0, 3]], dtype=torch.int32)
+    wl.seq_cold = torch.tensor([[0, 40, 7, 0]], dtype=torch.int32)
+    got = run_gpu(engine, wl, stream)
+    assert_close(got, oracle.decode_f64(geom, W.host_arrays(wl)), "ragged B4")
+
+
+def test_all_empty_sequence_gives_zero(engine, stream):
+    geom = W.hot_cold(batch=2, hot_count=2, cold_count=8, dict_size=512)
+    wl = W.generate(geom, seed=22)
+    wl.seq_hot = torch.tensor([[0, 2]], dtype=torch.int32)
+    wl.seq_cold = torch.tensor([[0, 8]], dtype=torch.int32)
+    got = run_gpu(engine, wl, stream)
+    assert np.all(got[0, 0] == 0)
+    assert_close(got, oracle.decode_f64(geom, W.host_arrays(wl)), "one empty sequence")
+
+
+def test_separate_v_pool(engine, stream):
+    geom = W.hot_cold(batch=2, hot_count=8, cold_count=64, separate_v=True)
+    wl = W.generate(geom, seed=23)
+    assert_close(run_gpu(engine, wl, stream), oracle.decode_f64(geom, W.host_arrays(wl)), "separate V")
+
+
+@pytest.mark.parametrize("hot_count", [1, 3, 5])
+def test_odd_block_counts(engine, stream, hot_count):
+    geom = W.hot_cold(hot_count=hot_count, cold_count=3, dict_size=256)
+    wl = W.generate(geom, seed=24 + hot_count)
+    assert_close(run_gpu(engine, wl, stream), oracle.decode_f64(geom, W.host_arrays(wl)), f"hot {hot_count} blocks")
+
+
+@pytest.mark.parametrize("queries,causal", [(5, False), (16, True), (2, True)])
+def test_many_query_rows(engine, stream, queries, causal):
+    """R = G*Q query rows per kv head up to 64 (several MFMA row tiles, several
+    cold row chunks)."""
+    geom = W.hot_cold(batch=2, queries=queries, causal=causal, hot_count=4, cold_count=32, dict_size=512)
+    wl = W.generate(geom, seed=30 + queries)
+    assert_close(run_gpu(engine, wl, stream), oracle.decode_f64(geom, W.host_arrays(wl)), f"Q={queries}")
+
+
+def test_head_dim_64_gqa(engine, stream):
+    geom = W.tiny(q_heads=16, kv_heads=4, hot_count=8, cold_count=24, queries=3, causal=True)
+    wl = W.generate(geom, seed=40)
+    assert_close(run_gpu(engine, wl, stream), oracle.decode_f64(geom, W.host_arrays(wl)), "d64 GQA 4")
+
+
+def test_out_of_range_refs_are_reported(engine, stream):
+    """A block ref past the pool (forced from the host) is skipped by the
+    kernels' bounds checks and reported as AW_E_OOB."""
+    geom = W.hot_cold(hot_count=2, cold_count=4, dict_size=256)
+    wl = W.generate(geom, seed=41)
+    wl.refs[0, 0, 0, 1] = geom.hot_blocks + 5
+    wl.refs[0, 0, 0, 3] = geom.cold_blocks + 7
+    dev = wl.to("cuda:0")
+    out = torch.empty(dev.out_shape(), dtype=torch.float16, device="cuda:0")
+    engine.decode_device(W.device_desc(dev, out), stream=stream)
+    with pytest.raises(WeaverError) as e:
+        engine.check_device_errors(stream)
+    assert e.value.status == AW_E_OOB
+    assert torch.isfinite(out.float()).all()
+
+
+def sampled_rows(geom, n, seed):
+    total = geom.layers * geom.batch * geom.queries * geom.q_heads
+    rng = np.random.default_rng(seed)
+    return np.unique(np.concatenate([[0, total - 1], rng.integers(0, total, n)])).astype(np.uint64)
+
+
+def full_size(engine, stream, geom, seed, n_rows, what):
+    wl = W.generate(geom, seed=seed, device="cuda:0")
+    out = torch.full(wl.out_shape(), float("nan"), dtype=torch.float16, device="cuda:0")
+    engine.decode_device(W.device_desc(wl, out), stream=stream)
+    engine.check_device_errors(stream)
+    got = out.view(-1, geom.head_dim)
+    bad = ~torch.isfinite(got.float()).all(dim=1)
+    if bad.any():
+        rows_bad = torch.nonzero(bad).flatten()
+        n_nan = int(torch.isnan(got.float()).sum())
+        pytest.fail(f"{what}: {int(bad.sum())} of {got.shape[0]} rows non-finite ({n_nan} NaN values), "
+                    f"first rows {rows_bad[:8].tolist()}, last {rows_bad[-4:].tolist()}")
+    rows = sampled_rows(geom, n_rows, seed)
+    ref = oracle.decode_f64(geom, W.host_arrays(wl), rows=rows, threads=16)
+    assert_close(got[torch.from_numpy(rows.astype(np.int64)).cuda()].cpu().numpy(), ref, what)
+
+
+def test_full_size_sweep_b64(engine, stream):
+    """hot 2048 + cold 32768 per kv head, B = 64: the benchmark shape."""
+    full_size(engine, stream, W.sweep(64), 50, 12, "sweep B64 (sampled rows)")
+
+
+def test_full_size_batched_zipf(engine, stream):
+    """B = 64, hot 1024 + cold 131072 SparseCodes per kv head, Zipf(1.1) atoms."""
+    full_size(engine, stream, W.batched(), 51, 8, "batched B64 Zipf (sampled rows)")
+
+
+def test_full_size_spec_verify(engine, stream):
+    """32 layers, B = 8, 8 causal drafts, hot 2048 + cold 65536 per kv head,
+    per-layer 4096 x 128 dictionary."""
+    full_size(engine, stream, W.spec_verify(), 52, 10, "spec-verify L32 (sampled rows)")
+    torch.cuda.empty_cache()
