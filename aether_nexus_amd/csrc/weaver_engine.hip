@@ -229,7 +229,7 @@ struct aw_engine {
     DevBuf q, ql, hot, cold, refs, dict, out; // aw_decode copies (weaver.rs:40-46)
     DevBuf ws;                                // per-request scratch
     uint32_t* err = nullptr;                  // device error word
-    bool profiling = false;
+    int profiling = 0; // AW_PROFILE_*
     struct Pending {
         int stage;
         hipEvent_t a, b;
@@ -511,14 +511,14 @@ int launch_merge(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* w
 
 // Stage order on `st`: [q.D^T] -> cold -> finish [-> merge].  The hot kernel
 // (HBM-bound) runs on the engine's side stream concurrently with the cold
-// kernel (LDS-bound) and is joined before the finish.  With profiling on,
-// everything runs on `st` so each kernel's event-timed duration is its own.
+// kernel (LDS-bound) and is joined before the finish.  AW_PROFILE_SERIAL puts
+// everything on `st` so each kernel's event-timed duration is its own.
 template <int HD>
 int run_pipeline(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* ws, hipStream_t st) {
     int rc = AW_OK;
     const bool cold = o.info.cold_splits > 0;
     const bool hot = o.info.hot_splits > 0;
-    const bool fork = hot && cold && !e->profiling;
+    const bool fork = hot && cold && e->profiling != AW_PROFILE_SERIAL;
     if (fork) {
         AW_HIP(e, hipEventRecord(e->ev_fork, st));
         AW_HIP(e, hipStreamWaitEvent(e->side, e->ev_fork, 0));
@@ -867,7 +867,8 @@ int aw_debug_gather_codes(aw_engine* e, const aw_sparse_code* codes, size_t n, c
 
 int aw_engine_set_profiling(aw_engine* e, int enable) {
     if (!e) return AW_E_INVALID_ARG;
-    e->profiling = enable != 0;
+    if (enable < AW_PROFILE_OFF || enable > AW_PROFILE_SERIAL) return fail(e, AW_E_INVALID_ARG, "profiling mode %d", enable);
+    e->profiling = enable;
     return AW_OK;
 }
 

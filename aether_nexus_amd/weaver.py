@@ -212,8 +212,10 @@ class WeaverEngine:
                                              _ptr(idx), _ptr(coef), _ptr(atoms), _stream(stream))
         self._check(rc, "gather_codes")
 
-    def set_profiling(self, enable: bool) -> None:
-        self._check(self._lib.aw_engine_set_profiling(self._h, int(bool(enable))), "set_profiling")
+    def set_profiling(self, mode) -> None:
+        """0/False: off; 1/True: event-time each kernel in the concurrent
+        pipeline; 2: event-time each kernel with the stages serialized."""
+        self._check(self._lib.aw_engine_set_profiling(self._h, int(mode)), "set_profiling")
 
     def reset_stage_stats(self) -> None:
         self._check(self._lib.aw_engine_reset_stage_stats(self._h), "reset_stage_stats")

@@ -56,6 +56,11 @@ def parse():
     p.add_argument("--stage-sweep", action="store_true", help="per-kernel times at every batch size")
     p.add_argument("--rocpd-summary", metavar="DB", help="print a per-kernel summary of a rocprofv3 database and exit")
     p.add_argument("--kernel-filter", default="aw::", help="kernel-name filter for --rocpd-summary")
+    p.add_argument("--copy-calibration", type=int, metavar="MIB", default=0,
+                   help="first run a plain device copy of MIB MiB (counter calibration)")
+    p.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DB", "WRITE_DB"),
+                   help="print HBM traffic per launch from a FETCH_SIZE and a WRITE_SIZE rocprofv3 database and exit")
+    p.add_argument("--traffic-command", default="", help="command line recorded in --traffic-summary output")
     return p.parse_args()
 
 
@@ -112,19 +117,23 @@ class Runner:
             torch.cuda.synchronize()
         return a.elapsed_time(b) / steps  # ms per step
 
-    def stage_times(self, steps):
-        """Average duration per kernel stage (HIP events around each launch)."""
+    def stage_times(self, steps, mode=1):
+        """Average duration per kernel stage: HIP events bracket each launch on
+        the stream it runs on.  mode 1 keeps the concurrent pipeline of the timed
+        steps (launched from the host, same rotation); mode 2 serializes it."""
         torch = self.torch
         eng = self.engine
         eng.reset_stage_stats()
-        eng.set_profiling(True)
+        eng.set_profiling(mode)
         try:
-            for i in range(steps):
-                eng.decode_device(self.descs[i % len(self.descs)], stream=self.stream.cuda_stream)
-            torch.cuda.synchronize()
+            with torch.cuda.stream(self.stream):
+                torch.cuda.synchronize()
+                for i in range(steps):
+                    eng.decode_device(self.descs[i % len(self.descs)], stream=self.stream.cuda_stream)
+                torch.cuda.synchronize()
             st = eng.stage_stats()
         finally:
-            eng.set_profiling(False)
+            eng.set_profiling(0)
         return {k: (ms / n if n else None, n) for k, (ms, n) in st.items()}
 
 
@@ -227,10 +236,111 @@ def rocpd_summary(db: str, name_filter: str) -> str:
     return "\n".join(lines)
 
 
+TRAFFIC_FILE = ROOT / "profiles" / "traffic_b64.txt"
+
+
+def sources_digest() -> str:
+    """sha256 over the HIP sources, so a traffic profile is only used for the
+    kernels it was measured on."""
+    import hashlib
+    h = hashlib.sha256()
+    for f in sorted((ROOT / "aether_nexus_amd" / "csrc").glob("*")):
+        if f.suffix in (".hip", ".hpp", ".h"):
+            h.update(f.name.encode())
+            h.update(f.read_bytes())
+    return h.hexdigest()[:16]
+
+
+def copy_calibration(mib: int, reps: int = 10):
+    """A plain elementwise copy of known size (torch's bitwise_not over int32:
+    reads and writes `mib` MiB once), for scaling the FETCH_SIZE / WRITE_SIZE
+    counters to bytes."""
+    import torch
+    n = (mib << 20) // 4
+    src = torch.empty(n, dtype=torch.int32, device="cuda:0").fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        torch.bitwise_not(src, out=dst)
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    log(f"copy calibration: {reps} x {4 * n} bytes, {8 * n * reps / el / 1e9:.0f} GB/s read+write")
+    del src, dst
+    torch.cuda.empty_cache()
+
+
+def _counters(db: str) -> dict:
+    """(kernel name, grid) -> {counter: average per dispatch} of a rocprofv3 database."""
+    import collections
+    import sqlite3
+    c = sqlite3.connect(db)
+    per = collections.defaultdict(lambda: collections.defaultdict(float))
+    nd = collections.defaultdict(set)
+    for kn, gs, did, cn, v in c.execute(
+            "select kernel_name, grid_size, dispatch_id, counter_name, value from counters_collection"):
+        per[(kn, gs)][cn] += v
+        nd[(kn, gs)].add(did)
+    return {k: {cn: v / len(nd[k]) for cn, v in d.items()} for k, d in per.items()}
+
+
+def traffic_summary(fetch_db: str, write_db: str, copy_mib: int, command: str) -> str:
+    """HBM bytes per launch of each aw:: kernel (largest grid = the B = 64 launch)
+    from a FETCH_SIZE and a WRITE_SIZE pass, each scaled by what the counter
+    reads for the calibration copy of `copy_mib` MiB in the same pass."""
+    copy_bytes = copy_mib << 20
+    f, w = _counters(fetch_db), _counters(write_db)
+
+    def copy_kib(d, cn):
+        cands = [(k, v[cn]) for k, v in d.items() if "bitwise_not" in k[0] and cn in v]
+        if not cands:
+            raise SystemExit(f"no bitwise_not calibration kernel with {cn} in the database")
+        return max(cands, key=lambda kv: kv[0][1])  # the largest grid: the calibration copy
+    (ck_f, cf), (ck_w, cw) = copy_kib(f, "FETCH_SIZE"), copy_kib(w, "WRITE_SIZE")
+    ff, fw = copy_bytes / (cf * 1024), copy_bytes / (cw * 1024)
+    lines = ["# HBM traffic per launch, hot 2048 + cold 32768 per kv head, B = 64 (32q/8kv, d128, 4096 atoms)",
+             f"# command: {command}",
+             f"# sources: {sources_digest()}",
+             f"copy_bytes {copy_bytes} kernel {ck_f[0][:48]!r} fetch_kib {cf:.0f} write_kib {cw:.0f}",
+             f"factor_fetch {ff:.4f} factor_write {fw:.4f}"]
+    best = {}
+    for (kn, gs), v in f.items():
+        if "aw::" in kn and "FETCH_SIZE" in v:
+            short = kn.split("(")[0].split("::")[-1].split("<")[0]
+            if short not in best or gs > best[short][1]:
+                best[short] = (kn, gs)
+    for short, key in sorted(best.items()):
+        fk = f[key]["FETCH_SIZE"]
+        wk = w.get(key, {}).get("WRITE_SIZE", float("nan"))
+        tb = fk * 1024 * ff + wk * 1024 * fw
+        lines.append(f"kernel {short} grid {key[1]} fetch_kib {fk:.0f} write_kib {wk:.0f} traffic_bytes {tb:.0f}")
+    return "\n".join(lines)
+
+
+def read_traffic(kernel: str):
+    """Traffic bytes per launch of `kernel` from the committed profile, or
+    (None, reason) when absent or measured on other sources."""
+    if not TRAFFIC_FILE.exists():
+        return None, "no traffic profile"
+    txt = TRAFFIC_FILE.read_text().splitlines()
+    digest = next((ln.split()[-1] for ln in txt if ln.startswith("# sources:")), None)
+    if digest != sources_digest():
+        return None, "traffic profile measured on other kernel sources"
+    for ln in txt:
+        p = ln.split()
+        if len(p) >= 10 and p[0] == "kernel" and p[1] == kernel:
+            return int(float(p[p.index("traffic_bytes") + 1])), None
+    return None, f"{kernel} missing from traffic profile"
+
+
 def main():
     args = parse()
     if args.rocpd_summary:
         print(rocpd_summary(args.rocpd_summary, args.kernel_filter))
+        return 0
+    if args.traffic_summary:
+        print(traffic_summary(args.traffic_summary[0], args.traffic_summary[1], args.copy_calibration or 256,
+                              args.traffic_command))
         return 0
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -244,6 +354,8 @@ def main():
     batches = [int(x) for x in args.batches.split(",") if x]
     engine = WeaverEngine()
     log(f"device: {engine.device_name()}")
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
     sweep = []
     head = None
     for B in batches:
@@ -268,16 +380,23 @@ def main():
             torch.cuda.empty_cache()
 
     geom, r, row = head
-    stages = r.stage_times(max(args.steps, 20))
+    # Per-kernel durations over the same steps, launched from the host with
+    # events around each kernel on its own stream (pipeline unchanged).
+    stages = r.stage_times(args.steps, mode=1)
+    serial = r.stage_times(args.steps, mode=2)
     kb_per_launch = kernel_bytes(geom)
     # Dominant of the two bandwidth-bound kernels.
     dom = max(("hot", "cold"), key=lambda k: stages[k][0] or 0.0)
     dur_ms = stages[dom][0]
     achieved = kb_per_launch[dom] / (dur_ms * 1e-3) / 1e9
+    traffic, why = read_traffic(f"{dom}_kernel")
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-                "frac": round(achieved / PEAK_HBM_GBPS, 4), "traffic": None, "kernel": f"{dom}_kernel",
+                "frac": round(achieved / PEAK_HBM_GBPS, 4), "traffic": traffic, "kernel": f"{dom}_kernel",
                 "alg_bytes_per_launch": int(kb_per_launch[dom]), "avg_launch_us": round(dur_ms * 1e3, 2)}
+    if why:
+        roofline["traffic_note"] = why
     stages_us = {k: (round(v * 1e3, 2) if v else None) for k, (v, n) in stages.items()}
+    serial_us = {k: (round(v * 1e3, 2) if v else None) for k, (v, n) in serial.items()}
     ref_cfg = reference_bench_config(engine, args.seed, 200)
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds, args.seed)
 
@@ -304,6 +423,7 @@ def main():
         "frac_of_peak": row["frac_of_peak"],
         "sweep": sweep,
         "stages_us": stages_us,
+        "stages_serial_us": serial_us,
         "roofline": roofline,
         "cpu_baseline": cpu,
         "reference_bench_config": ref_cfg,

@@ -231,8 +231,15 @@ int aw_debug_gather_codes(aw_engine* engine, const aw_sparse_code* codes, size_t
                           uint32_t* idx, float* coef, uint16_t* atoms, void* hip_stream);
 
 /* Per-stage kernel timing with HIP events recorded on the stream each kernel
- * runs on.  While enabled, every launch is bracketed by a pair of events. */
-int aw_engine_set_profiling(aw_engine* engine, int enable);
+ * runs on: every launch is bracketed by a pair of events.  AW_PROFILE_ON keeps
+ * the pipeline as it runs unprofiled (the hot kernel on the engine's side
+ * stream, concurrent with q.D^T and the cold kernel); AW_PROFILE_SERIAL runs
+ * every stage on the caller's stream, one after another.  No reference
+ * counterpart (the reference times whole calls, bench.rs:149-168). */
+#define AW_PROFILE_OFF 0
+#define AW_PROFILE_ON 1
+#define AW_PROFILE_SERIAL 2
+int aw_engine_set_profiling(aw_engine* engine, int mode);
 int aw_engine_stage_stats(aw_engine* engine, int stage, double* total_ms, uint64_t* launches);
 int aw_engine_reset_stage_stats(aw_engine* engine);
 
