@@ -68,7 +68,7 @@ struct Layout {
     uint32_t n_ar = 1;     // atom ranges of the finish
     uint32_t atoms_per_range = 0;
     uint32_t tiles_per_group = 0, rows_per_group = 0, n_groups = 0;
-    size_t off_ql = 0, off_hm = 0, off_hl = 0, off_ho = 0;
+    size_t off_ql = 0, off_dt = 0, off_hm = 0, off_hl = 0, off_ho = 0;
     size_t off_cm = 0, off_cl = 0, off_ca = 0, off_cw = 0, off_ocp = 0;
 };
 
@@ -138,6 +138,13 @@ int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, Layout* L, char
         uint64_t want = cdiv((uint64_t)n_cu * 16, n_lbg);
         uint64_t cap = std::max<uint64_t>(1, cdiv(n_tok, 64));
         uint64_t S = std::max<uint64_t>(1, std::min<uint64_t>({want, cap, (uint64_t)aw::kMaxSplits}));
+        // A split holds at most 64 blocks (its refs live in one register of the wave).
+        S = std::max<uint64_t>(S, cdiv(n_tok, 64 * kBlock));
+        if (S > (uint64_t)aw::kMaxSplits) {
+            put_msg(msg, mlen, "hot pool of %llu tokens needs more than %d splits of 1024 tokens",
+                    (unsigned long long)n_tok, aw::kMaxSplits);
+            return AW_E_UNSUPPORTED;
+        }
         uint64_t tps = align_up(cdiv(n_tok, S), 32);
         o.info.hot_tokens_per_split = (uint32_t)tps;
         o.info.hot_splits = cdiv(n_tok, tps);
@@ -195,6 +202,7 @@ int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, Layout* L, char
         return at;
     };
     if (o.info.computes_q_latent) o.off_ql = take((uint64_t)d->layers * d->batch * d->queries * d->q_heads * A * 2);
+    if (d->cold_count > 0) o.off_dt = take((uint64_t)d->layers * d->dict_heads * A * HD * 2);
     if (o.info.hot_splits) {
         const uint64_t n = n_lbg * o.info.hot_splits * R;
         o.off_hm = take(n * 4);
@@ -307,11 +315,12 @@ struct StageTimer {
 };
 
 template <int HD>
-int launch_project(aw_engine* e, const aw_decode_desc* d, const Layout& o, uint16_t* ql, hipStream_t st) {
+int launch_project(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* ws, hipStream_t st) {
     aw::ProjArgs a{};
     a.q = d->q;
     a.dict = d->dict;
-    a.ql = ql;
+    a.ql = o.info.computes_q_latent ? (uint16_t*)(ws + o.off_ql) : nullptr;
+    a.dt = (uint16_t*)(ws + o.off_dt);
     a.batch = d->batch;
     a.queries = d->queries;
     a.q_heads = d->q_heads;
@@ -322,7 +331,8 @@ int launch_project(aw_engine* e, const aw_decode_desc* d, const Layout& o, uint1
     a.dict_heads = d->dict_heads;
     a.rows_per_group = d->batch * d->queries * (d->dict_heads == 1 ? d->q_heads : a.gqa);
     a.dict_layer = (uint64_t)d->dict_heads * d->dict_size * HD;
-    const uint32_t rows = a.rows_per_group;
+    // Without q_latent to compute, one row block per atom block only writes D^T.
+    const uint32_t rows = a.ql ? a.rows_per_group : 1;
     StageTimer t(e, AW_STAGE_PROJECT, st);
     const dim3 block(64);
     const uint32_t gz = d->layers * d->dict_heads;
@@ -371,12 +381,16 @@ int launch_hot(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* ws,
     if (grid > 0x7FFFFFFFull) return fail(e, AW_E_UNSUPPORTED, "hot grid too large");
     StageTimer t(e, AW_STAGE_HOT, st);
     const uint32_t R = a.rows_r;
-    if (R <= 16)
-        hipLaunchKernelGGL((aw::hot_kernel<HD, 1>), dim3((uint32_t)grid), dim3(64), 0, st, a);
-    else if (R <= 32)
-        hipLaunchKernelGGL((aw::hot_kernel<HD, 2>), dim3((uint32_t)grid), dim3(64), 0, st, a);
-    else
-        hipLaunchKernelGGL((aw::hot_kernel<HD, 4>), dim3((uint32_t)grid), dim3(64), 0, st, a);
+#define AW_LAUNCH_HOT(RTV, SV) hipLaunchKernelGGL((aw::hot_kernel<HD, RTV, SV>), dim3((uint32_t)grid), dim3(64), 0, st, a)
+    const bool sepv = a.hot_v != nullptr;
+    if (R <= 16) {
+        if (sepv) AW_LAUNCH_HOT(1, true); else AW_LAUNCH_HOT(1, false);
+    } else if (R <= 32) {
+        if (sepv) AW_LAUNCH_HOT(2, true); else AW_LAUNCH_HOT(2, false);
+    } else {
+        if (sepv) AW_LAUNCH_HOT(4, true); else AW_LAUNCH_HOT(4, false);
+    }
+#undef AW_LAUNCH_HOT
     AW_HIP(e, hipGetLastError());
     return AW_OK;
 }
@@ -424,17 +438,22 @@ int launch_cold(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* ws
     if (grid > 0x7FFFFFFFull) return fail(e, AW_E_UNSUPPORTED, "cold grid too large");
     const size_t smem = aw::cold_smem_bytes(A, (int)o.rc, a.tokens_per_split);
     StageTimer t(e, AW_STAGE_COLD, st);
+    const bool pow2 = (A & (A - 1u)) == 0u;
+#define AW_LAUNCH_COLD(RCV, P2)                                                                                    \
+    hipLaunchKernelGGL((aw::cold_kernel<RCV, kColdCPT, kColdPD, P2>), dim3((uint32_t)grid), dim3(aw::kColdThreads), \
+                       smem, st, a)
     switch (o.rc) {
     case 4:
-        hipLaunchKernelGGL((aw::cold_kernel<4, kColdCPT, kColdPD>), dim3((uint32_t)grid), dim3(aw::kColdThreads), smem, st, a);
+        if (pow2) AW_LAUNCH_COLD(4, true); else AW_LAUNCH_COLD(4, false);
         break;
     case 2:
-        hipLaunchKernelGGL((aw::cold_kernel<2, kColdCPT, kColdPD>), dim3((uint32_t)grid), dim3(aw::kColdThreads), smem, st, a);
+        if (pow2) AW_LAUNCH_COLD(2, true); else AW_LAUNCH_COLD(2, false);
         break;
     default:
-        hipLaunchKernelGGL((aw::cold_kernel<1, kColdCPT, kColdPD>), dim3((uint32_t)grid), dim3(aw::kColdThreads), smem, st, a);
+        if (pow2) AW_LAUNCH_COLD(1, true); else AW_LAUNCH_COLD(1, false);
         break;
     }
+#undef AW_LAUNCH_COLD
     AW_HIP(e, hipGetLastError());
     return AW_OK;
 }
@@ -442,7 +461,7 @@ int launch_cold(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* ws
 template <int HD>
 int launch_finish(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* ws, hipStream_t st) {
     aw::FinishArgs a{};
-    a.dict = d->dict;
+    a.dt = (const uint16_t*)(ws + o.off_dt);
     a.cold_m = (const float*)(ws + o.off_cm);
     a.cold_l = (const float*)(ws + o.off_cl);
     a.cold_w = (const float*)(ws + o.off_cw);
@@ -472,7 +491,10 @@ int launch_finish(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* 
     const uint64_t gx = (uint64_t)o.tiles_per_group * o.n_groups;
     if (gx > 0x7FFFFFFFull) return fail(e, AW_E_UNSUPPORTED, "finish grid too large");
     StageTimer t(e, AW_STAGE_FINISH, st);
-    hipLaunchKernelGGL((aw::finish_kernel<HD>), dim3((uint32_t)gx, o.n_ar), dim3(256), 0, st, a);
+    if (a.cold_splits == 1)
+        hipLaunchKernelGGL((aw::finish_kernel<HD, true>), dim3((uint32_t)gx, o.n_ar), dim3(256), 0, st, a);
+    else
+        hipLaunchKernelGGL((aw::finish_kernel<HD, false>), dim3((uint32_t)gx, o.n_ar), dim3(256), 0, st, a);
     AW_HIP(e, hipGetLastError());
     return AW_OK;
 }
@@ -527,8 +549,8 @@ int run_pipeline(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* w
     } else if (hot) {
         if ((rc = launch_hot<HD>(e, d, o, ws, st))) return rc;
     }
-    if (cold && o.info.computes_q_latent)
-        if ((rc = launch_project<HD>(e, d, o, (uint16_t*)(ws + o.off_ql), st))) return rc;
+    if (cold)
+        if ((rc = launch_project<HD>(e, d, o, ws, st))) return rc;
     if (cold) {
         if ((rc = launch_cold(e, d, o, ws, st))) return rc;
         if (fork) AW_HIP(e, hipStreamWaitEvent(st, e->ev_join, 0));
@@ -550,6 +572,10 @@ int decode_device(aw_engine* e, const aw_decode_desc* d, hipStream_t st) {
     if (d->hot_count && (!d->hot_k || !d->refs)) return fail(e, AW_E_INVALID_ARG, "hot_k and refs are required");
     if (d->cold_count && (!d->cold || !d->refs || !d->dict))
         return fail(e, AW_E_INVALID_ARG, "cold, refs and dict are required");
+    if (d->cold_count && d->cold_blocks == 0)
+        return fail(e, AW_E_INVALID_ARG, "cold_count > 0 needs cold_blocks > 0");
+    if (d->hot_count && d->hot_blocks == 0)
+        return fail(e, AW_E_INVALID_ARG, "hot_count > 0 needs hot_blocks > 0");
     if (d->cold_count && ((uintptr_t)d->cold & 15u))
         return fail(e, AW_E_ALIGN, "cold pool pointer is not 16-byte aligned");
     if ((rc = ensure(e->ws, o.info.workspace_bytes, e->last_error))) return rc;
@@ -720,20 +746,24 @@ int aw_engine_create(int device, aw_engine** out) {
     e->max_lds = prop.sharedMemPerBlock;
     e->n_cu = (uint32_t)prop.multiProcessorCount;
     int rc = AW_OK;
-    if (!rc) rc = check_kernel(e, aw::hot_kernel<128, 1>, "hot_kernel");
-    if (!rc) rc = check_kernel(e, aw::cold_kernel<4, kColdCPT, kColdPD>, "cold_kernel");
-    if (!rc) rc = check_kernel(e, aw::finish_kernel<128>, "finish_kernel");
+    if (!rc) rc = check_kernel(e, aw::hot_kernel<128, 1, false>, "hot_kernel");
+    if (!rc) rc = check_kernel(e, aw::cold_kernel<4, kColdCPT, kColdPD, true>, "cold_kernel");
+    if (!rc) rc = check_kernel(e, aw::finish_kernel<128, true>, "finish_kernel");
     if (rc) {
         delete e;
         return rc;
     }
     // Let the cold kernel use the device's full LDS.
-    (void)hipFuncSetAttribute((const void*)aw::cold_kernel<4, kColdCPT, kColdPD>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                        (int)e->max_lds);
-    (void)hipFuncSetAttribute((const void*)aw::cold_kernel<2, kColdCPT, kColdPD>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                        (int)e->max_lds);
-    (void)hipFuncSetAttribute((const void*)aw::cold_kernel<1, kColdCPT, kColdPD>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                        (int)e->max_lds);
+    {
+        const void* fns[] = {(const void*)aw::cold_kernel<4, kColdCPT, kColdPD, true>,
+                             (const void*)aw::cold_kernel<4, kColdCPT, kColdPD, false>,
+                             (const void*)aw::cold_kernel<2, kColdCPT, kColdPD, true>,
+                             (const void*)aw::cold_kernel<2, kColdCPT, kColdPD, false>,
+                             (const void*)aw::cold_kernel<1, kColdCPT, kColdPD, true>,
+                             (const void*)aw::cold_kernel<1, kColdCPT, kColdPD, false>};
+        for (const void* f : fns)
+            (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)e->max_lds);
+    }
     if (hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking) != hipSuccess ||
         hipStreamCreateWithFlags(&e->side, hipStreamNonBlocking) != hipSuccess ||
         hipEventCreateWithFlags(&e->ev_fork, hipEventDisableTiming) != hipSuccess ||

@@ -55,6 +55,9 @@ __device__ inline float4_t mfma16x16x32(half8_t a, half8_t b, float4_t c) {
 }
 __device__ inline half8_t as_h8(uint4_t v) { return __builtin_bit_cast(half8_t, v); }
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+// e with 2^(e-1) <= x < 2^e for finite x > 0 (v_frexp_exp_i32_f32), and x * 2^e (v_ldexp_f32).
+__device__ inline int exp_of(float x) { return __builtin_amdgcn_frexp_expf(x); }
+__device__ inline float pow2f(int e) { return __builtin_amdgcn_ldexpf(1.0f, e); }
 __device__ inline float h2f_bits(uint32_t bits16) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
 }
@@ -101,7 +104,8 @@ __device__ inline void combine_splits(float m, float l, float& M, float& L, floa
 struct ProjArgs {
     const uint16_t* q;    // [L][B][Q][Hq][HD]
     const uint16_t* dict; // [L][dict_heads][A][HD]
-    uint16_t* ql;         // [L][B][Q][Hq][A] f16
+    uint16_t* ql;         // [L][B][Q][Hq][A] f16, or null: transpose only
+    uint16_t* dt;         // [L][dict_heads][HD][A] f16: D^T for the finish
     uint32_t batch, queries, q_heads, kv_heads, gqa, rows_r;
     uint32_t dict_size, dict_heads;
     uint32_t rows_per_group; // B*Q*(dict_heads==1 ? Hq : G)
@@ -144,7 +148,7 @@ struct ColdArgs {
 };
 
 struct FinishArgs {
-    const uint16_t* dict;
+    const uint16_t* dt; // D^T [L][dict_heads][HD][A]
     const float* cold_m;
     const float* cold_l;
     const float* cold_w;
@@ -188,23 +192,33 @@ struct MergeArgs {
 // Rows of one group share one dictionary: group = (layer, dict head); inside a
 // group row i enumerates (b, q, head) with head over Hq (shared dictionary) or
 // over the G heads of kv head dg (per-kv-head dictionary).
+//
+// The waves of the first row block also write their 16*NA atoms of D^T
+// ([HD][A], through LDS): the finish contracts over atoms, and MFMA operands
+// want the contracted index contiguous in each lane.
 template <int HD, int MR, int NA>
 __global__ __launch_bounds__(64) void project_kernel(ProjArgs a) {
-    constexpr int KS = HD / 32;
+    constexpr int KS = HD / 32, TP = HD + 8; // LDS pitch of the transpose, halves
+    __shared__ __attribute__((aligned(16))) _Float16 st[16 * NA * TP];
     const int lane = threadIdx.x, li = lane & 15, lg = lane >> 4;
     const uint32_t group = blockIdx.z;
     const uint32_t l = group / a.dict_heads, dg = group % a.dict_heads;
     const uint32_t atom0 = blockIdx.x * 16 * NA, row0 = blockIdx.y * 16 * MR;
-    const uint16_t* dict = a.dict + l * a.dict_layer + (uint64_t)dg * a.dict_size * HD;
+    const uint64_t dgoff = l * a.dict_layer + (uint64_t)dg * a.dict_size * HD;
+    const uint16_t* dict = a.dict + dgoff;
     const bool shared = a.dict_heads == 1;
+    const bool transpose = blockIdx.y == 0;
 
     // This lane's query rows (one per row block): global row index into q / q_latent.
+    // All loads are issued up front and unconditionally (clamped rows / atoms);
+    // rows and atoms out of range are zeroed after.
     uint64_t qrow[MR];
     bool rok[MR];
 #pragma unroll
     for (int mr = 0; mr < MR; ++mr) {
-        const uint32_t i = row0 + 16 * mr + li;
-        rok[mr] = i < a.rows_per_group;
+        const uint32_t i0 = row0 + 16 * mr + li;
+        rok[mr] = a.ql != nullptr && i0 < a.rows_per_group;
+        const uint32_t i = a.rows_per_group ? min(i0, a.rows_per_group - 1u) : 0u;
         if (shared) {
             qrow[mr] = (uint64_t)l * a.rows_per_group + i; // rows of a layer are (b, q, h) in q's order
         } else {                                           // (b, q, head hh of kv head dg)
@@ -212,27 +226,42 @@ __global__ __launch_bounds__(64) void project_kernel(ProjArgs a) {
             qrow[mr] = ((uint64_t)l * a.batch * a.queries + bq) * a.q_heads + dg * a.gqa + hh;
         }
     }
-    half8_t bop[MR][KS];
-#pragma unroll
-    for (int mr = 0; mr < MR; ++mr)
-#pragma unroll
-        for (int j = 0; j < KS; ++j)
-            bop[mr][j] = rok[mr] ? as_h8(*(const uint4_t*)(a.q + qrow[mr] * HD + 32 * j + 8 * lg))
-                                 : (half8_t)(_Float16)0;
+    half8_t bop[MR][KS], aop[NA][KS];
 #pragma unroll
     for (int na = 0; na < NA; ++na) {
-        const uint32_t at = atom0 + 16 * na + li;
-        half8_t aop[KS];
+        const uint32_t at = min(atom0 + 16 * na + li, a.dict_size - 1u);
 #pragma unroll
-        for (int j = 0; j < KS; ++j)
-            aop[j] = at < a.dict_size ? as_h8(*(const uint4_t*)(dict + (uint64_t)at * HD + 32 * j + 8 * lg))
-                                      : (half8_t)(_Float16)0;
+        for (int j = 0; j < KS; ++j) aop[na][j] = as_h8(*(const uint4_t*)(dict + (uint64_t)at * HD + 32 * j + 8 * lg));
+    }
+    if (a.ql != nullptr) {
+#pragma unroll
+        for (int mr = 0; mr < MR; ++mr)
+#pragma unroll
+            for (int j = 0; j < KS; ++j) bop[mr][j] = as_h8(*(const uint4_t*)(a.q + qrow[mr] * HD + 32 * j + 8 * lg));
+    }
+#pragma unroll
+    for (int na = 0; na < NA; ++na)
+        if (atom0 + 16 * na + li >= a.dict_size)
+#pragma unroll
+            for (int j = 0; j < KS; ++j) aop[na][j] = (half8_t)(_Float16)0;
+#pragma unroll
+    for (int na = 0; na < NA; ++na) {
+        if (transpose) {
+#pragma unroll
+            for (int j = 0; j < KS; ++j) {
+                const uint4_t w = __builtin_bit_cast(uint4_t, aop[na][j]);
+                _Float16* dst = st + (16 * na + li) * TP + 32 * j + 8 * lg;
+                *(uint2_t*)dst = (uint2_t){w[0], w[1]};
+                *(uint2_t*)(dst + 4) = (uint2_t){w[2], w[3]};
+            }
+        }
+        if (a.ql == nullptr) continue;
         const uint32_t ao = atom0 + 16 * na + 4 * lg; // this lane's 4 output atoms
 #pragma unroll
         for (int mr = 0; mr < MR; ++mr) {
             float4_t acc = (float4_t)0.0f;
 #pragma unroll
-            for (int j = 0; j < KS; ++j) acc = mfma16x16x32(aop[j], bop[mr][j], acc);
+            for (int j = 0; j < KS; ++j) acc = mfma16x16x32(aop[na][j], bop[mr][j], acc);
             if (rok[mr] && ao < a.dict_size) { // dict_size % 16 == 0: all four atoms are in range
                 half4_t v;
                 v[0] = (_Float16)acc[0];
@@ -241,6 +270,24 @@ __global__ __launch_bounds__(64) void project_kernel(ProjArgs a) {
                 v[3] = (_Float16)acc[3];
                 *(half4_t*)(a.ql + qrow[mr] * a.dict_size + ao) = v;
             }
+        }
+    }
+    if (transpose) {
+        // D^T pieces of 8 atoms: piece p = (dim p / (2*NA), atom group p % (2*NA)).
+        __syncthreads();
+        constexpr int GROUPS = 2 * NA, PIECES = HD * GROUPS;
+        uint16_t* dt = a.dt + dgoff;
+        for (int p = lane; p < PIECES; p += 64) {
+            const int d = p / GROUPS, ag = p % GROUPS;
+            const uint32_t at = atom0 + 8 * ag;
+            if (at >= a.dict_size) continue;
+            uint16_t h[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) h[e] = __builtin_bit_cast(uint16_t, st[(8 * ag + e) * TP + d]);
+            uint4_t v;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = (uint32_t)h[2 * e] | ((uint32_t)h[2 * e + 1] << 16);
+            *(uint4_t*)(dt + (uint64_t)d * a.dict_size + at) = v;
         }
     }
 }
@@ -258,7 +305,13 @@ __global__ __launch_bounds__(64) void project_kernel(ProjArgs a) {
 //      gathered from the chunk staged in LDS.
 // LDS pitch HD+4 halves (66 words at HD=128) puts the four token rows 4*lg+e'
 // of one read on disjoint 8-bank groups.
-template <int HD, int RT>
+//
+// A split holds at most 64 blocks; their refs are staged in LDS once.  Every
+// global load of the loop is
+// unconditional (a bad ref reads block 0 and the chunk's registers are zeroed
+// before use), so the next chunk's loads really stay in flight while the
+// current chunk is computed.
+template <int HD, int RT, bool SEPV>
 __global__ __launch_bounds__(64) void hot_kernel(HotArgs a) {
     constexpr int KS = HD / 32, NB = HD / 16, P = HD + 4;
     __shared__ __attribute__((aligned(16))) _Float16 lds[32 * P];
@@ -272,22 +325,27 @@ __global__ __launch_bounds__(64) void hot_kernel(HotArgs a) {
     const uint32_t t_end = min(t_begin + a.tokens_per_split, n_tok);
     const uint32_t R = a.rows_r;
 
+    // Block refs of this split (tokens_per_split <= 64 blocks), staged in LDS:
+    // the loop reads them with LDS loads, which never wait behind the K loads.
+    __shared__ uint32_t s_refs[64];
+    const uint32_t blk0 = t_begin / kBlockTokens;
+    const uint32_t n_blk = t_end > t_begin ? (t_end - t_begin + kBlockTokens - 1) / kBlockTokens : 0u;
+    {
+        const uint32_t* refs = a.refs + (uint64_t)l * a.refs_layer + (uint64_t)(lb % a.batch) * a.refs_stride;
+        s_refs[lane] = refs[blk0 + min((uint32_t)lane, n_blk ? n_blk - 1u : 0u)] & kRefMask;
+        __syncthreads();
+    }
+
     half8_t qop[RT][KS];
     int lim[RT];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-        const uint32_t r = 16 * rt + li;
-        if (r < R) {
-            const uint32_t q = r / a.gqa, h = g * a.gqa + r % a.gqa;
-            const uint16_t* p = a.q + (((uint64_t)lb * a.queries + q) * a.q_heads + h) * HD;
+        const uint32_t r = min(16u * rt + li, R - 1u);
+        const uint32_t q = r / a.gqa, h = g * a.gqa + r % a.gqa;
+        const uint16_t* p = a.q + (((uint64_t)lb * a.queries + q) * a.q_heads + h) * HD;
 #pragma unroll
-            for (int j = 0; j < KS; ++j) qop[rt][j] = as_h8(*(const uint4_t*)(p + 32 * j + 8 * lg));
-            lim[rt] = a.causal ? (int)n_tok - (int)a.queries + 1 + (int)q : (int)n_tok;
-        } else {
-#pragma unroll
-            for (int j = 0; j < KS; ++j) qop[rt][j] = (half8_t)(_Float16)0;
-            lim[rt] = 0;
-        }
+        for (int j = 0; j < KS; ++j) qop[rt][j] = as_h8(*(const uint4_t*)(p + 32 * j + 8 * lg));
+        lim[rt] = 16u * rt + li < R ? (a.causal ? (int)n_tok - (int)a.queries + 1 + (int)q : (int)n_tok) : 0;
     }
 
     float m_run[RT], l_run[RT];
@@ -301,35 +359,53 @@ __global__ __launch_bounds__(64) void hot_kernel(HotArgs a) {
     }
 
     const uint16_t* kbase = a.hot_k + (uint64_t)l * a.hot_layer;
-    const uint16_t* vbase = a.hot_v ? a.hot_v + (uint64_t)l * a.hot_layer : nullptr;
-    const uint32_t* refs = a.refs + (uint64_t)l * a.refs_layer + (uint64_t)(lb % a.batch) * a.refs_stride;
+    const uint16_t* vbase = SEPV ? a.hot_v + (uint64_t)l * a.hot_layer : nullptr;
+    bool bad = false;
 
-    // Resolve the two blocks of chunk c0 and load this lane's K pieces.
-    auto load_chunk = [&](uint32_t c0, uint4_t (&kr)[2][KS], uint64_t (&rowoff)[2], bool (&ok)[2]) {
+    // The two blocks of chunk c0: this lane's K (and V) pieces, and whether each block is usable.
+    auto load_chunk = [&](uint32_t c0, uint4_t (&kr)[2][KS], uint4_t (&vr)[2][KS], bool (&ok)[2]) {
 #pragma unroll
         for (int tb = 0; tb < 2; ++tb) {
+            const uint32_t bi = (c0 - t_begin) / kBlockTokens + tb;
             const bool in = c0 + 16 * tb < t_end;
-            const uint32_t ref = in ? (refs[c0 / 16 + tb] & kRefMask) : 0u;
+            const uint32_t ref = s_refs[min(bi, 63u)];
             ok[tb] = in && ref < a.hot_blocks;
-            if (in && !ok[tb]) flag_error(a.err, kErrHotRef);
-            rowoff[tb] = (((uint64_t)ref * kBlockTokens + li) * a.kv_heads + g) * HD + 8 * lg;
+            bad |= in && !ok[tb];
+            const uint32_t pr = ok[tb] ? ref : 0u;
+            const uint64_t rowoff = (((uint64_t)pr * kBlockTokens + li) * a.kv_heads + g) * HD + 8 * lg;
 #pragma unroll
-            for (int j = 0; j < KS; ++j)
-                kr[tb][j] = ok[tb] ? *(const uint4_t*)(kbase + rowoff[tb] + 32 * j) : (uint4_t)0u;
+            for (int j = 0; j < KS; ++j) kr[tb][j] = *(const uint4_t*)(kbase + rowoff + 32 * j);
+            if constexpr (SEPV) {
+#pragma unroll
+                for (int j = 0; j < KS; ++j) vr[tb][j] = *(const uint4_t*)(vbase + rowoff + 32 * j);
+            }
         }
     };
 
-    uint4_t kcur[2][KS];
-    uint64_t offcur[2];
-    bool okcur[2];
-    if (t_begin < t_end) load_chunk(t_begin, kcur, offcur, okcur);
+    // Two chunk buffers used in turn (no register copies between iterations, so
+    // the wait for a chunk's loads sits right before its first use).
+    uint4_t kb[2][2][KS], vb[2][2][KS];
+    bool okb[2][2] = {{false, false}, {false, false}};
+    const uint32_t last = t_end > t_begin ? t_begin + ((t_end - t_begin - 1) / 32) * 32 : t_begin;
+    if (t_begin < t_end) load_chunk(t_begin, kb[0], vb[0], okb[0]);
+    // Rows past R: zero query (their lim is 0, so their output is never written).
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+        if (16u * rt + li >= R)
+#pragma unroll
+            for (int j = 0; j < KS; ++j) qop[rt][j] = (half8_t)(_Float16)0;
 
-    for (uint32_t c0 = t_begin; c0 < t_end; c0 += 32) {
-        uint4_t knext[2][KS];
-        uint64_t offnext[2];
-        bool oknext[2];
-        const bool more = c0 + 32 < t_end;
-        if (more) load_chunk(c0 + 32, knext, offnext, oknext);
+    auto process = [&](uint32_t c0, uint4_t (&kcur)[2][KS], uint4_t (&vcur)[2][KS], const bool (&okcur)[2]) {
+        // Unusable blocks (past the split or a bad ref) become zeros.
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb)
+            if (!okcur[tb]) {
+#pragma unroll
+                for (int j = 0; j < KS; ++j) {
+                    kcur[tb][j] = (uint4_t)0u;
+                    vcur[tb][j] = (uint4_t)0u;
+                }
+            }
 
         // S^T = K Q^T
         float4_t sacc[RT][2];
@@ -349,8 +425,7 @@ __global__ __launch_bounds__(64) void hot_kernel(HotArgs a) {
         for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
             for (int j = 0; j < KS; ++j) {
-                uint4_t v = kcur[tb][j];
-                if (vbase) v = okcur[tb] ? *(const uint4_t*)(vbase + offcur[tb] + 32 * j) : (uint4_t)0u;
+                const uint4_t v = SEPV ? vcur[tb][j] : kcur[tb][j];
                 _Float16* dst = lds + (16 * tb + li) * P + 32 * j + 8 * lg;
                 *(uint2_t*)dst = (uint2_t){v[0], v[1]};
                 *(uint2_t*)(dst + 4) = (uint2_t){v[2], v[3]};
@@ -406,17 +481,16 @@ __global__ __launch_bounds__(64) void hot_kernel(HotArgs a) {
 #pragma unroll
             for (int rt = 0; rt < RT; ++rt) oacc[rt][nb] = mfma16x16x32(vop, pop[rt], oacc[rt][nb]);
         }
+    };
 
-        if (more) {
-#pragma unroll
-            for (int tb = 0; tb < 2; ++tb) {
-                offcur[tb] = offnext[tb];
-                okcur[tb] = oknext[tb];
-#pragma unroll
-                for (int j = 0; j < KS; ++j) kcur[tb][j] = knext[tb][j];
-            }
-        }
+    for (uint32_t c0 = t_begin; c0 < t_end; c0 += 64) {
+        load_chunk(min(c0 + 32, last), kb[1], vb[1], okb[1]); // the last chunk reloads itself
+        process(c0, kb[0], vb[0], okb[0]);
+        if (c0 + 32 >= t_end) break;
+        load_chunk(min(c0 + 64, last), kb[0], vb[0], okb[0]);
+        process(c0 + 32, kb[1], vb[1], okb[1]);
     }
+    if (bad) flag_error(a.err, kErrHotRef);
 
     const uint64_t pbase = ((uint64_t)lbg * a.splits + s) * R;
 #pragma unroll
@@ -448,24 +522,38 @@ __global__ __launch_bounds__(64) void hot_kernel(HotArgs a) {
 // v1*2^32 + v0 (v0 sign-extended); sums of such words are exact and decode back
 // to (sum v0, sum v1) while each row sum stays inside int32.
 //
-// Values are p*c*2^F with p = 2^(s - ref_r).  ref_r (integral, log2 units) and
-// F come from the split's first tile: ref_r = ceil(max score of the tile),
-// F sized so that the planned bound on sum |p*c| over the whole split stays
-// near 2^28.  The work-group then streams every tile with no further
-// synchronisation.  At the end a conservative bound, 4 * max|c| * sum_t sum_r p,
-// proves the bins could not have overflowed; when it cannot (scores far above
-// the first tile's, or coefficients far larger), the split is recomputed
-// exactly: a pass for the per-row maxima, a pass for the exact bound, a pass
-// for the bins.  Each contribution is rounded to the nearest unit of 2^-F
-// (half away from zero), so bin errors are unbiased, at most half a unit per
-// contribution.
+// Each contribution p*c*2^F is rounded to the nearest integer (ties to even)
+// by one FMA with 1.5*2^23: for |x| < 2^22 the sum's bit pattern is
+// 0x4B400000 + round(x).  The two patterns of a row pair, read as one 64-bit
+// word, minus 0x4B4000004B400000 give exactly v1*2^32 + v0.
+//
+// p = 2^(s - ref_r).  ref_r (integral, log2 units) and F come from the split's
+// first tile: ref_r = ceil(max score of the tile); F keeps the planned bound on
+// sum |p*c| over the whole split near 2^28 and the tile's largest contribution
+// below 2^18.  The work-group then streams every tile with no further
+// synchronisation.  At the end two conservative bounds, 4 * max|c| *
+// sum_t sum_r p < 2^31 and max p * max|c| < 2^22, prove the bins exact; when
+// they fail (scores far above the first tile's, coefficients far larger), the
+// split is recomputed exactly: a pass for the per-row maxima, a pass for the
+// exact bound, a pass for the bins.
+//
+// Every global load of the streaming loop is unconditional (out-of-range and
+// bad-ref tokens read an all-zero code and get p = 0 by a select), so the
+// compiler can count loads in flight and the PD-deep ring really prefetches.
 //
 // The kv heads of one (sequence, chunk, split) run on one XCD (work-groups are
 // dealt round-robin over the 8 XCDs), so the 128-byte lines interleaving their
 // 16-byte codes come from HBM once per XCD L2.
-template <int RC, int CPT, int PD>
+// All-zero code read by tokens outside the split or behind a bad ref; global
+// (not constant) memory, so every code load stays a global load.
+__device__ __attribute__((aligned(16))) uint4_t g_zero_code = {0u, 0u, 0u, 0u};
+
+constexpr float kMagic = 12582912.0f;                 // 1.5 * 2^23
+constexpr uint64_t kMagic2 = 0x4B4000004B400000ull;   // two magic patterns
+
+template <int RC, int CPT, int PD, bool POW2>
 __global__ __launch_bounds__(kColdThreads) void cold_kernel(ColdArgs a) {
-    constexpr int NT = kColdThreads, NW = NT / 64, NP = (RC + 1) / 2, NRED = 2 * RC + 2;
+    constexpr int NT = kColdThreads, NW = NT / 64, NP = (RC + 1) / 2, NRED = RC + 2; // row values, max|c|, max p
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t x = blockIdx.x % 8u, k = blockIdx.x / 8u;
@@ -521,8 +609,10 @@ __global__ __launch_bounds__(kColdThreads) void cold_kernel(ColdArgs a) {
             for (uint32_t a8 = tid; a8 < A / 8; a8 += NT) {
                 uint4_t w[RC];
 #pragma unroll
+                for (int rr = 0; rr < RC; ++rr) w[rr] = *(const uint4_t*)(a.ql + rbase[rr] + (uint64_t)a8 * 8);
+#pragma unroll
                 for (int rr = 0; rr < RC; ++rr)
-                    w[rr] = rok[rr] ? *(const uint4_t*)(a.ql + rbase[rr] + (uint64_t)a8 * 8) : (uint4_t)0u;
+                    if (!rok[rr]) w[rr] = (uint4_t)0u;
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     _Float16 hv[RC];
@@ -559,61 +649,85 @@ __global__ __launch_bounds__(kColdThreads) void cold_kernel(ColdArgs a) {
             sref[i] = ref;
         }
     }
+    __syncthreads(); // qtab and sref complete
 
     const uint4_t* cold = a.cold + (uint64_t)l * a.cold_layer;
     const uint32_t tile_tokens = NT * CPT;
     const uint32_t n_tiles = (t_end - t_begin + tile_tokens - 1) / tile_tokens;
     const float sl = a.scale_log2;
 
-    auto load_tile = [&](uint32_t t0, uint4_t (&buf)[CPT], bool (&ok)[CPT]) {
+    // Code of token t for this kv head; tokens past the split or behind a bad ref
+    // read the zero code and are reported invalid.  The load itself is
+    // unconditional.  Split in two so the ring can read a tile's refs from LDS
+    // ahead of the atomics it issues, and load the codes after them.
+    auto tile_refs = [&](uint32_t t0, uint32_t (&rb)[CPT]) {
 #pragma unroll
         for (int kk = 0; kk < CPT; ++kk) {
             const uint32_t t = t0 + kk * NT + tid;
-            bool v = t < t_end;
-            buf[kk] = (uint4_t)0u; // a token past the split or behind a bad ref scores as a zero code
-            if (v) {
-                const uint32_t ref = sref[(t - t_begin) >> 4];
-                v = ref != ~0u;
-                if (v) buf[kk] = cold[((uint64_t)ref * kBlockTokens + (t & 15u)) * a.kv_heads + g];
-            }
-            ok[kk] = v;
+            rb[kk] = t < t_end ? sref[(t - t_begin) >> 4] : ~0u;
         }
     };
-    // Unscaled score sums of one code for the RC rows: sum_k c_k * q_latent[idx_k][r].
-    auto score = [&](const uint4_t cw, float (&sc)[RC], uint32_t (&ia)[4], float (&cf)[4]) {
-        ia[0] = cw[0] & 0xFFFFu;
-        ia[1] = cw[0] >> 16;
-        ia[2] = cw[1] & 0xFFFFu;
-        ia[3] = cw[1] >> 16;
-        cf[0] = h2f_bits(cw[2] & 0xFFFFu);
-        cf[1] = h2f_bits(cw[2] >> 16);
-        cf[2] = h2f_bits(cw[3] & 0xFFFFu);
-        cf[3] = h2f_bits(cw[3] >> 16);
-        if (max(max(ia[0], ia[1]), max(ia[2], ia[3])) >= A) { // out-of-range atoms: skip those terms
-            flag_error(a.err, kErrAtom);
+    auto tile_codes = [&](uint32_t t0, const uint32_t (&rb)[CPT], uint4_t (&buf)[CPT], bool (&ok)[CPT]) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                if (ia[j] >= A) {
-                    ia[j] = 0;
-                    cf[j] = 0.0f;
-                }
+        for (int kk = 0; kk < CPT; ++kk) {
+            const uint32_t t = t0 + kk * NT + tid;
+            ok[kk] = rb[kk] != ~0u;
+            const uint4_t* p =
+                ok[kk] ? cold + ((uint64_t)rb[kk] * kBlockTokens + (t & 15u)) * a.kv_heads + g : &g_zero_code;
+            buf[kk] = *p;
         }
+    };
+    auto load_tile = [&](uint32_t t0, uint4_t (&buf)[CPT], bool (&ok)[CPT]) {
+        uint32_t rb[CPT];
+        tile_refs(t0, rb);
+        tile_codes(t0, rb, buf, ok);
+    };
+    // Atom indices of a code word, always inside the tables: a power-of-two
+    // dictionary masks them (any bit outside the mask is recorded in `oob`),
+    // others are clamped (recorded when clamping changed them).
+    auto atoms = [&](const uint4_t cw, uint32_t (&ia)[4], uint32_t& oob) {
+        if constexpr (POW2) {
+            ia[0] = cw[0] & (A - 1u);
+            ia[1] = (cw[0] >> 16) & (A - 1u);
+            ia[2] = cw[1] & (A - 1u);
+            ia[3] = (cw[1] >> 16) & (A - 1u);
+            oob |= cw[0] | cw[1];
+        } else {
+            const uint32_t r0 = cw[0] & 0xFFFFu, r1 = cw[0] >> 16, r2 = cw[1] & 0xFFFFu, r3 = cw[1] >> 16;
+            oob = max(oob, max(max(r0, r1), max(r2, r3)));
+            ia[0] = min(r0, A - 1u);
+            ia[1] = min(r1, A - 1u);
+            ia[2] = min(r2, A - 1u);
+            ia[3] = min(r3, A - 1u);
+        }
+    };
+    auto coef = [](const uint4_t cw, int j) -> _Float16 {
+        return __builtin_bit_cast(_Float16, (uint16_t)(cw[2 + j / 2] >> (16 * (j % 2))));
+    };
+    // Unscaled score sums of one code for the RC rows: sum_k c_k * q_latent[idx_k][r].
+    auto score = [&](const uint4_t cw, const uint32_t (&ia)[4], float (&sc)[RC]) {
 #pragma unroll
         for (int rr = 0; rr < RC; ++rr) sc[rr] = 0.0f;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
+            const float cj = (float)coef(cw, j);
             const _Float16* qp = qtab + ia[j] * RC;
             if constexpr (RC == 4) {
                 const half4_t qv = *(const half4_t*)qp;
 #pragma unroll
-                for (int rr = 0; rr < 4; ++rr) sc[rr] += cf[j] * (float)qv[rr];
+                for (int rr = 0; rr < 4; ++rr) sc[rr] = fmaf(cj, (float)qv[rr], sc[rr]);
             } else {
 #pragma unroll
-                for (int rr = 0; rr < RC; ++rr) sc[rr] += cf[j] * (float)qp[rr];
+                for (int rr = 0; rr < RC; ++rr) sc[rr] = fmaf(cj, (float)qp[rr], sc[rr]);
             }
         }
     };
-    auto cmax4 = [](const float (&cf)[4]) { return fmaxf(fmaxf(fabsf(cf[0]), fabsf(cf[1])), fmaxf(fabsf(cf[2]), fabsf(cf[3]))); };
+    // max |c| of a code, as packed f16 magnitudes (monotone as integers).
+    auto cmax_bits = [](const uint4_t cw) -> uint32_t {
+        const uint32_t m0 = cw[2] & 0x7FFF7FFFu, m1 = cw[3] & 0x7FFF7FFFu;
+        const uint32_t lo = max(m0 & 0xFFFFu, m1 & 0xFFFFu), hi = max(m0 >> 16, m1 >> 16);
+        return max(lo, hi);
+    };
 
     // Work-group sums/maxima of up to NRED per-lane values (one barrier pair).
     auto wg_reduce = [&](float (&v)[NRED], const bool (&is_max)[NRED]) {
@@ -634,38 +748,42 @@ __global__ __launch_bounds__(kColdThreads) void cold_kernel(ColdArgs a) {
 
     float ref[RC];
     int F = 0;
-    float lpart[RC], cmx = 0.0f;
+    float lpart[RC];
+    float cmx = 0.0f, pmx = 0.0f;
+    uint32_t oob = 0;
     uint4_t cur[CPT];
     bool curv[CPT];
     bool exact = false;
     for (int attempt = 0; attempt < 2; ++attempt) {
         for (uint32_t i = tid; i < A * NP; i += NT) bins[i] = 0ull;
-        __syncthreads();
         load_tile(t_begin, cur, curv);
+        __syncthreads(); // bins zeroed before any thread adds
         if (!exact) {
-            // Reference and scale from the first tile.
+            // Reference and scale from the first tile (invalid tokens masked).
             float v[NRED];
             bool is_max[NRED];
 #pragma unroll
             for (int i = 0; i < NRED; ++i) {
                 v[i] = i < RC ? -INFINITY : 0.0f;
-                is_max[i] = i < RC;
+                is_max[i] = true;
             }
             float scs[CPT][RC];
 #pragma unroll
             for (int kk = 0; kk < CPT; ++kk) {
                 uint32_t ia[4];
-                float cf[4];
-                score(cur[kk], scs[kk], ia, cf);
+                uint32_t dummy = 0;
+                atoms(cur[kk], ia, dummy);
+                score(cur[kk], ia, scs[kk]);
                 if (curv[kk]) {
 #pragma unroll
                     for (int rr = 0; rr < RC; ++rr) v[rr] = fmaxf(v[rr], scs[kk][rr] * sl);
-                    v[2 * RC] = fmaxf(v[2 * RC], cmax4(cf)); // summed below: only a plan
+                    v[RC] = fmaxf(v[RC], (float)__builtin_bit_cast(_Float16, (uint16_t)cmax_bits(cur[kk])));
                 }
             }
             wg_reduce(v, is_max);
 #pragma unroll
             for (int rr = 0; rr < RC; ++rr) ref[rr] = v[rr] == -INFINITY ? 0.0f : ceilf(v[rr]);
+            const float cmax0 = v[RC];
             float w[NRED];
 #pragma unroll
             for (int i = 0; i < NRED; ++i) {
@@ -678,14 +796,13 @@ __global__ __launch_bounds__(kColdThreads) void cold_kernel(ColdArgs a) {
                     float ps = 0.0f;
 #pragma unroll
                     for (int rr = 0; rr < RC; ++rr) ps += fast_exp2(scs[kk][rr] * sl - ref[rr]);
-                    uint32_t ia[4];
-                    float cf[4], dummy[RC];
-                    score(cur[kk], dummy, ia, cf);
-                    w[0] += 4.0f * cmax4(cf) * ps;
+                    w[0] += 4.0f * (float)__builtin_bit_cast(_Float16, (uint16_t)cmax_bits(cur[kk])) * ps;
                 }
             wg_reduce(w, is_max);
             const float plan = w[0] * (float)n_tiles; // bound on sum |p*c| over the split, if tiles are alike
-            F = plan > 0.0f ? min(100, max(-100, 28 - (ilogbf(plan) + 1))) : 0;
+            int Fs = plan > 0.0f ? 28 - exp_of(plan) : 100;
+            int Fm = cmax0 > 0.0f ? 18 - exp_of(cmax0) : 100; // p <= 1 in the first tile
+            F = min(100, max(-100, min(Fs, Fm)));
         }
         // Stream every tile into the bins; PD tiles of code loads stay in flight
         // (a ring of registers, refilled as each slot is consumed).
@@ -696,7 +813,8 @@ __global__ __launch_bounds__(kColdThreads) void cold_kernel(ColdArgs a) {
             lpart[rr] = 0.0f;
             rf[rr] = Ff - ref[rr];
         }
-        cmx = 0.0f;
+        uint32_t cmx_bits = 0;
+        pmx = 0.0f;
         uint4_t ring[PD][CPT];
         bool rv[PD][CPT];
 #pragma unroll
@@ -709,43 +827,48 @@ __global__ __launch_bounds__(kColdThreads) void cold_kernel(ColdArgs a) {
         for (uint32_t t0 = t_begin; t0 < t_end; t0 += PD * tile_tokens) {
 #pragma unroll
             for (int d = 0; d < PD; ++d) {
+                uint32_t rnext[CPT]; // refs of the tile PD ahead, read before this slot's atomics
+                tile_refs(t0 + (d + PD) * tile_tokens, rnext);
 #pragma unroll
                 for (int kk = 0; kk < CPT; ++kk) {
-                    if (!rv[d][kk]) continue;
                     const uint4_t cw = ring[d][kk];
-                    float sc[RC];
                     uint32_t ia[4];
-                    float cf[4];
-                    score(cw, sc, ia, cf);
-                    cmx = fmaxf(cmx, cmax4(cf));
-                    float ps[RC]; // p * 2^F
+                    atoms(cw, ia, oob);
+                    float sc[RC];
+                    score(cw, ia, sc);
+                    cmx_bits = max(cmx_bits, cmax_bits(cw));
+                    float ps[RC]; // p * 2^F, zero for invalid tokens
 #pragma unroll
                     for (int rr = 0; rr < RC; ++rr) {
-                        ps[rr] = fast_exp2(fmaf(sc[rr], sl, rf[rr]));
+                        const float p = fast_exp2(fmaf(sc[rr], sl, rf[rr]));
+                        ps[rr] = rv[d][kk] ? p : 0.0f;
                         lpart[rr] += ps[rr];
                     }
-                    // Round half away from zero (p > 0, so the sign is c's): the
-                    // +-0.5 rides in the FMA and the conversion truncates.
-                    const uint32_t cbits[4] = {cw[2] << 16, cw[2], cw[3] << 16, cw[3]};
+                    if constexpr (RC == 4) pmx = fmaxf(pmx, fmaxf(fmaxf(ps[0], ps[1]), fmaxf(ps[2], ps[3])));
+                    else if constexpr (RC == 2) pmx = fmaxf(pmx, fmaxf(ps[0], ps[1]));
+                    else pmx = fmaxf(pmx, ps[0]);
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
                         uint64_t* bp = bins + ia[j] * NP;
-                        const float hc = __builtin_bit_cast(float, (cbits[j] & 0x80000000u) | 0x3F000000u);
+                        const float cj = (float)coef(cw, j);
 #pragma unroll
                         for (int pp = 0; pp < NP; ++pp) {
-                            const int32_t v0 = (int32_t)fmaf(ps[2 * pp], cf[j], hc);
-                            const int32_t v1 =
-                                (2 * pp + 1 < RC) ? (int32_t)fmaf(ps[min(2 * pp + 1, RC - 1)], cf[j], hc) : 0;
-                            const uint64_t wv = ((uint64_t)(uint32_t)v1 << 32) + (uint64_t)(int64_t)v0;
+                            const uint32_t b0 = __builtin_bit_cast(uint32_t, fmaf(ps[2 * pp], cj, kMagic));
+                            const uint32_t b1 = (2 * pp + 1 < RC)
+                                                    ? __builtin_bit_cast(uint32_t, fmaf(ps[min(2 * pp + 1, RC - 1)], cj, kMagic))
+                                                    : 0x4B400000u;
+                            const uint64_t wv = (((uint64_t)b1 << 32) | b0) - kMagic2;
                             __hip_atomic_fetch_add(bp + pp, wv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
                         }
                     }
                 }
                 // Refill this slot with the tile PD ahead.
-                load_tile(t0 + (d + PD) * tile_tokens, ring[d], rv[d]);
+                tile_codes(t0 + (d + PD) * tile_tokens, rnext, ring[d], rv[d]);
             }
         }
-        // Overflow proof: every |bin| <= sum over contributions |p*c|*2^F <= 4*max|c|*sum_r sum_t p*2^F.
+        cmx = (float)__builtin_bit_cast(_Float16, (uint16_t)cmx_bits);
+        // Overflow proof: every |bin| <= sum over contributions |p*c|*2^F <= 4*max|c|*sum_r sum_t p*2^F,
+        // and every contribution |p*c|*2^F <= max p*2^F * max|c| stays inside the rounding trick.
         float v[NRED];
         bool is_max[NRED];
 #pragma unroll
@@ -755,8 +878,10 @@ __global__ __launch_bounds__(kColdThreads) void cold_kernel(ColdArgs a) {
         }
 #pragma unroll
         for (int rr = 0; rr < RC; ++rr) v[rr] = lpart[rr];
-        v[2 * RC] = cmx;
-        is_max[2 * RC] = true;
+        v[RC] = cmx;
+        is_max[RC] = true;
+        v[RC + 1] = pmx;
+        is_max[RC + 1] = true;
         wg_reduce(v, is_max);
         float psum = 0.0f;
 #pragma unroll
@@ -764,12 +889,14 @@ __global__ __launch_bounds__(kColdThreads) void cold_kernel(ColdArgs a) {
             lpart[rr] = v[rr];
             psum += v[rr];
         }
-        const float bound = 4.0f * v[2 * RC] * psum; // already in units of 2^-F
-        if (exact || (bound < 2147483648.0f && bound == bound)) break;
+        const float bound = 4.0f * v[RC] * psum; // already in units of 2^-F
+        const float cbound = v[RC + 1] * v[RC];
+        if (exact || (bound < 2147483648.0f && cbound < 4194304.0f)) break;
 
         // Exact path: per-row maxima, then the exact bound, then the bins.
         exact = true;
         float mx[RC];
+        float cm2 = 0.0f;
 #pragma unroll
         for (int rr = 0; rr < RC; ++rr) mx[rr] = -INFINITY;
         for (uint32_t t0 = t_begin; t0 < t_end; t0 += tile_tokens) {
@@ -777,10 +904,11 @@ __global__ __launch_bounds__(kColdThreads) void cold_kernel(ColdArgs a) {
 #pragma unroll
             for (int kk = 0; kk < CPT; ++kk)
                 if (curv[kk]) {
-                    float sc[RC];
                     uint32_t ia[4];
-                    float cf[4];
-                    score(cur[kk], sc, ia, cf);
+                    uint32_t dummy = 0;
+                    atoms(cur[kk], ia, dummy);
+                    float sc[RC];
+                    score(cur[kk], ia, sc);
 #pragma unroll
                     for (int rr = 0; rr < RC; ++rr) mx[rr] = fmaxf(mx[rr], sc[rr] * sl);
                 }
@@ -795,7 +923,6 @@ __global__ __launch_bounds__(kColdThreads) void cold_kernel(ColdArgs a) {
         wg_reduce(m2, im2);
 #pragma unroll
         for (int rr = 0; rr < RC; ++rr) ref[rr] = m2[rr] == -INFINITY ? 0.0f : ceilf(m2[rr]);
-        float eb = 0.0f; // exact sum over contributions of |p*c|, maximised over rows below
         float ebr[RC];
 #pragma unroll
         for (int rr = 0; rr < RC; ++rr) ebr[rr] = 0.0f;
@@ -804,11 +931,15 @@ __global__ __launch_bounds__(kColdThreads) void cold_kernel(ColdArgs a) {
 #pragma unroll
             for (int kk = 0; kk < CPT; ++kk)
                 if (curv[kk]) {
-                    float sc[RC];
                     uint32_t ia[4];
-                    float cf[4];
-                    score(cur[kk], sc, ia, cf);
-                    const float ca = fabsf(cf[0]) + fabsf(cf[1]) + fabsf(cf[2]) + fabsf(cf[3]);
+                    uint32_t dummy = 0;
+                    atoms(cur[kk], ia, dummy);
+                    float sc[RC];
+                    score(cur[kk], ia, sc);
+                    float ca = 0.0f;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) ca += fabsf((float)coef(cur[kk], j));
+                    cm2 = fmaxf(cm2, (float)__builtin_bit_cast(_Float16, (uint16_t)cmax_bits(cur[kk])));
 #pragma unroll
                     for (int rr = 0; rr < RC; ++rr) ebr[rr] += fast_exp2(sc[rr] * sl - ref[rr]) * ca;
                 }
@@ -818,15 +949,27 @@ __global__ __launch_bounds__(kColdThreads) void cold_kernel(ColdArgs a) {
             m2[i] = i < RC ? ebr[i] : 0.0f;
             im2[i] = false;
         }
+        m2[RC] = cm2;
+        im2[RC] = true;
         wg_reduce(m2, im2);
+        float eb = 0.0f; // exact sum over contributions of |p*c|, maximised over rows
 #pragma unroll
         for (int rr = 0; rr < RC; ++rr) eb = fmaxf(eb, m2[rr]);
-        F = eb > 0.0f ? min(100, max(-100, 29 - (ilogbf(eb) + 1))) : 0;
+        // p <= 1 now: contributions are at most max|c| * 2^F.
+        const int Fs = eb > 0.0f ? 29 - exp_of(eb) : 100;
+        const int Fm = m2[RC] > 0.0f ? 21 - exp_of(m2[RC]) : 100;
+        F = min(100, max(-100, min(Fs, Fm)));
         __syncthreads();
     }
-
+    // Atom indices outside the dictionary: recorded (their terms went to a clamped atom).
+    {
+        bool bad;
+        if constexpr (POW2) bad = (oob & ~((A - 1u) | ((A - 1u) << 16))) != 0u;
+        else bad = oob >= A;
+        if (bad) flag_error(a.err, kErrAtom);
+    }
     // Bins out as float rows [r][A]; track max |bin| per row for the f16 split of the finish.
-    const float inv = ldexpf(1.0f, -F);
+    const float inv = pow2f(-F);
     float amax[RC];
 #pragma unroll
     for (int rr = 0; rr < RC; ++rr) amax[rr] = 0.0f;
@@ -871,7 +1014,7 @@ inline size_t cold_smem_bytes(uint32_t A, int RC, uint32_t tokens_per_split) {
     const size_t qtab = ((size_t)A * RC * 2 + 15) & ~(size_t)15;
     const int NW = kColdThreads / 64, NP = (RC + 1) / 2;
     const size_t n_blk = ((size_t)(tokens_per_split + 15) / 16 + 3) & ~(size_t)3;
-    return qtab + (size_t)A * NP * 8 + n_blk * 4 + (size_t)NW * (2 * RC + 2) * 4;
+    return qtab + (size_t)A * NP * 8 + n_blk * 4 + (size_t)NW * (RC + 2) * 4;
 }
 
 // ----------------------------------------------- per-row merge factors
@@ -888,11 +1031,27 @@ struct RowFactors {
 __device__ inline float bin_scale(float bound, float Lc) {
     float scl = 1.0f;
     if (Lc > 0.0f && bound > 0.0f) {
-        int e = ilogbf(bound / Lc) + 1;
-        e = max(-100, min(100, e));
-        scl = ldexpf(1.0f, 14 - e);
+        const int e = max(-100, min(100, exp_of(bound / Lc)));
+        scl = pow2f(14 - e);
     }
     return scl;
+}
+
+// Segmented wave reductions over groups of `lpr` lanes (a power of two <= 64).
+template <bool MAX>
+__device__ inline float seg_reduce(float v, uint32_t lpr) {
+    for (uint32_t o = lpr >> 1; o > 0; o >>= 1) {
+        const float w = __shfl_xor(v, (int)o);
+        v = MAX ? fmaxf(v, w) : v + w;
+    }
+    return v;
+}
+// combine_splits over a segment of lanes (lane = split).
+__device__ inline void combine_seg(float m, float l, uint32_t lpr, float& M, float& L, float& f) {
+    const bool ok = l > 0.0f;
+    M = seg_reduce<true>(ok ? m : -INFINITY, lpr);
+    f = ok ? fast_exp2(m - M) : 0.0f;
+    L = seg_reduce<false>(f * l, lpr);
 }
 
 // out = (wh*Oh + wc*Lc*Oc) / (wh*Lh + wc*Lc); zero when nothing was visible.
@@ -908,23 +1067,20 @@ __device__ inline float merge_value(float oh, float Mh, float Lh, float oc, floa
 // ------------------------------------------------------ bins . D (MFMA)
 //
 // Work-group = 64 rows sharing one dictionary (4 waves x 16 rows) x one atom
-// range.  All four waves walk the same 32-atom dictionary chunks, staged once
-// per work-group in LDS (double-buffered, the next chunk's loads in flight
-// during the current chunk's MFMAs).  Per wave: O^T[dim][row] += D^T W^T with
-//   B = W^T (lane: row li, atoms a0+4*lg+{0..3} and a0+16+4*lg+{0..3}: two
-//       16-byte loads per cold split, combined with the split factors),
-//       split into hi + lo f16 terms -> two MFMAs,
-//   A = D^T (lane: dim 16*nb+li, the same 8 atoms) gathered from the LDS chunk
-//       (pitch HD+4 halves: the four atom rows 4*lg+e of one read fall on
-//       disjoint 8-bank groups).
-// With one atom range the log-sum-exp merge runs here too; otherwise the
-// partial cold outputs go to `ocp` for merge_kernel.
-template <int HD>
+// range.  Per wave: O^T[dim][row] += D^T W^T over 32-atom chunks,
+//   A = D^T (lane: dim 16*nb+li, atoms a0+8*lg .. +7: one 16-byte load from
+//       D^T [HD][A], which the projection wrote; L2-resident, shared by the
+//       four waves through L1),
+//   B = W^T (lane: row li, the same 8 atoms: two 16-byte loads per cold split,
+//       combined with the split factors), split into hi + lo f16 terms -> two
+//       MFMAs per dim block.
+// No LDS staging and no barriers in the loop: the waves stream independently,
+// with the W and D^T loads two chunks ahead (SINGLE: one cold split;
+// otherwise the splits' W are combined per chunk).  With one atom range the log-sum-exp merge runs here too;
+// otherwise the partial cold outputs go to `ocp` for merge_kernel.
+template <int HD, bool SINGLE>
 __global__ __launch_bounds__(256) void finish_kernel(FinishArgs a) {
-    constexpr int NB = HD / 16, P = HD + 4, ROWS = 64;
-    constexpr int PIECES = 32 * HD / 8; // 16-byte pieces per dictionary chunk
-    constexpr int PPT = PIECES / 256;   // pieces per thread (2 at HD=128, 1 at HD=64)
-    __shared__ __attribute__((aligned(16))) _Float16 sd[2][32 * P];
+    constexpr int NB = HD / 16, ROWS = 64;
     __shared__ float s_cfac[ROWS][kMaxSplits];
     __shared__ float s_hfac[ROWS][kMaxSplits];
     __shared__ RowFactors s_rf[ROWS];
@@ -934,88 +1090,70 @@ __global__ __launch_bounds__(256) void finish_kernel(FinishArgs a) {
     const uint32_t ar = blockIdx.y;
     const uint32_t l = group / a.dict_heads, dg = group % a.dict_heads;
     const uint32_t R = a.rows_r, A = a.dict_size;
-    const uint32_t hg = a.dict_heads == 1 ? a.kv_heads : 1;
     const bool fused = a.n_ar == 1 && a.hot_splits > 0;
 
-    // Split factors: wave w combines rows 16w..16w+15, lane = split; all loads first.
+    // Split factors: wave w combines its rows 16w..16w+15.  Lanes form segments of
+    // lpr = pow2 >= splits lanes (lane in segment = split), one row per segment,
+    // 64/lpr rows per pass; all loads of a pass are unconditional (clamped).
     {
-        constexpr int RPW = ROWS / 4;
-        uint64_t rid[RPW];
-        float cm[RPW], cl[RPW], ca[RPW], hm[RPW], hl[RPW];
-#pragma unroll
-        for (int i = 0; i < RPW; ++i) {
-            const uint32_t row = tile * ROWS + wave * RPW + i;
-            rid[i] = ~0ull;
-            cm[i] = hm[i] = -INFINITY;
-            cl[i] = ca[i] = hl[i] = 0.0f;
-            if (row < a.rows_per_group) {
-                const uint32_t b = row / (hg * R), rem = row % (hg * R);
-                const uint32_t g = a.dict_heads == 1 ? rem / R : dg, r = rem % R;
-                const uint64_t lbg = ((uint64_t)l * a.batch + b) * a.kv_heads + g;
-                rid[i] = lbg * R + r;
-                if ((uint32_t)lane < a.cold_splits) {
-                    const uint64_t cb = (lbg * a.cold_splits + lane) * R + r;
-                    cm[i] = a.cold_m[cb];
-                    cl[i] = a.cold_l[cb];
-                    ca[i] = a.cold_amax[cb];
-                }
-                if (fused && (uint32_t)lane < a.hot_splits) {
-                    const uint64_t hb = (lbg * a.hot_splits + lane) * R + r;
-                    hm[i] = a.hot_m[hb];
-                    hl[i] = a.hot_l[hb];
-                }
+        const uint32_t sneed = max(a.cold_splits, fused ? a.hot_splits : 1u);
+        const uint32_t lpr = sneed <= 1 ? 1u : 1u << (32 - __builtin_clz(sneed - 1u));
+        const uint32_t seg = (uint32_t)lane / lpr, sp = (uint32_t)lane % lpr;
+        const uint32_t per_pass = 64u / lpr;
+        const float* hmp = fused ? a.hot_m : a.cold_m; // any valid array when the hot side is absent
+        const float* hlp = fused ? a.hot_l : a.cold_l;
+        for (uint32_t i0 = 0; i0 < 16u; i0 += per_pass) {
+            const uint32_t i = i0 + seg;                   // row of this wave handled by this segment
+            const uint32_t row_raw = tile * ROWS + wave * 16 + i;
+            const bool rv = i < 16u && row_raw < a.rows_per_group;
+            const uint32_t row = min(row_raw, a.rows_per_group - 1u);
+            uint64_t lbg;
+            uint32_t r;
+            if (a.dict_heads == 1) { // row = (b*Hkv + g)*R + r
+                lbg = (uint64_t)l * a.batch * a.kv_heads + row / R;
+                r = row % R;
+            } else { // row = b*R + r of kv head dg
+                lbg = ((uint64_t)l * a.batch + row / R) * a.kv_heads + dg;
+                r = row % R;
             }
-        }
-#pragma unroll
-        for (int i = 0; i < RPW; ++i) {
-            const int row = wave * RPW + i;
+            const uint32_t cs = min(sp, a.cold_splits - 1u);
+            const uint64_t cb = (lbg * a.cold_splits + cs) * R + r;
+            float cm = a.cold_m[cb], cl = a.cold_l[cb], ca = a.cold_amax[cb];
+            const uint32_t hs = min(sp, a.hot_splits > 0 ? a.hot_splits - 1u : 0u);
+            const uint64_t hb = fused ? (lbg * a.hot_splits + hs) * R + r : cb;
+            float hm = hmp[hb], hl = hlp[hb];
+            const bool cv = rv && sp < a.cold_splits, hv = rv && fused && sp < a.hot_splits;
+            cm = cv ? cm : -INFINITY;
+            cl = cv ? cl : 0.0f;
+            ca = cv ? ca : 0.0f;
+            hm = hv ? hm : -INFINITY;
+            hl = hv ? hl : 0.0f;
             RowFactors rf;
             float f;
-            combine_splits(cm[i], cl[i], rf.Mc, rf.Lc, f);
-            const float scl = bin_scale(wave_sum(f * ca[i]), rf.Lc);
+            combine_seg(cm, cl, lpr, rf.Mc, rf.Lc, f);
+            const float scl = bin_scale(seg_reduce<false>(f * ca, lpr), rf.Lc);
             rf.inv_scl = 1.0f / scl;
-            if (lane < kMaxSplits) s_cfac[row][lane] = rf.Lc > 0.0f ? f / rf.Lc * scl : 0.0f;
+            const uint32_t srow = wave * 16 + min(i, 15u);
+            if (i < 16u) s_cfac[srow][sp] = rf.Lc > 0.0f ? f / rf.Lc * scl : 0.0f;
             rf.Mh = -INFINITY;
             rf.Lh = 0.0f;
             if (fused) {
                 float fh;
-                combine_splits(hm[i], hl[i], rf.Mh, rf.Lh, fh);
-                if (lane < kMaxSplits) s_hfac[row][lane] = fh;
+                combine_seg(hm, hl, lpr, rf.Mh, rf.Lh, fh);
+                if (i < 16u) s_hfac[srow][sp] = fh;
             }
-            if (lane == 0) {
-                s_rf[row] = rf;
-                s_row[row] = rid[i];
+            if (i < 16u && sp == 0) {
+                s_rf[srow] = rf;
+                s_row[srow] = rv ? lbg * R + r : ~0ull;
             }
         }
     }
+    __syncthreads(); // each wave reads back only its own rows; one barrier orders the LDS traffic
 
-    const uint16_t* dict = a.dict + (uint64_t)l * a.dict_layer + (uint64_t)dg * A * HD;
+    const uint16_t* dt = a.dt + (uint64_t)l * a.dict_layer + (uint64_t)dg * HD * A;
     const uint32_t a_begin = ar * a.atoms_per_range;
     const uint32_t a_end = min(a_begin + a.atoms_per_range, A);
     const uint32_t n_ch = (a_end - a_begin + 31) / 32;
-
-    uint4_t dreg[PPT];
-    auto load_d = [&](uint32_t a0) {
-#pragma unroll
-        for (int q = 0; q < PPT; ++q) {
-            const int pc = tid + 256 * q, at = pc / (HD / 8), col = (pc % (HD / 8)) * 8;
-            dreg[q] = (a0 + at < a_end) ? *(const uint4_t*)(dict + (uint64_t)(a0 + at) * HD + col) : (uint4_t)0u;
-        }
-    };
-    auto store_d = [&](int buf) {
-#pragma unroll
-        for (int q = 0; q < PPT; ++q) {
-            const int pc = tid + 256 * q, at = pc / (HD / 8), col = (pc % (HD / 8)) * 8;
-            _Float16* dst = &sd[buf][at * P + col];
-            *(uint2_t*)dst = (uint2_t){dreg[q][0], dreg[q][1]};
-            *(uint2_t*)(dst + 4) = (uint2_t){dreg[q][2], dreg[q][3]};
-        }
-    };
-    if (n_ch) {
-        load_d(a_begin);
-        store_d(0);
-    }
-    __syncthreads();
 
     const int myr = 16 * wave + li; // this lane's B-operand row
     const uint64_t myrow = s_row[myr];
@@ -1023,83 +1161,97 @@ __global__ __launch_bounds__(256) void finish_kernel(FinishArgs a) {
     const uint64_t lbg_me = rowok ? myrow / R : 0, r_me = rowok ? myrow % R : 0;
     const float* wbase = a.cold_w + ((lbg_me * a.cold_splits) * R + r_me) * A;
     const uint64_t wsplit = (uint64_t)R * A;
+    const float f0 = rowok ? s_cfac[myr][0] : 0.0f;
+    const bool wok = rowok && f0 != 0.0f; // an empty split wrote no bins: never read them
 
+    // D^T operand of chunk a0: 8 dim blocks x 16 bytes (atoms a0+8*lg .. +7, all in or all out:
+    // dict_size % 16 == 0).  Loads are unconditional (clamped to the last 8 atoms); atoms past the
+    // range are zeroed where the chunk is used.
+    auto load_d = [&](uint32_t a0, uint4_t (&dop)[NB]) {
+        const uint32_t at = min(a0 + 8 * lg, A - 8u);
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) dop[nb] = *(const uint4_t*)(dt + (uint64_t)(16 * nb + li) * A + at);
+    };
+    // Single-split W of chunk a0: this lane's row, atoms a0+8*lg .. +7 (clamped; masked at use).
+    auto load_w = [&](uint32_t a0, float4_t& w0, float4_t& w1) {
+        const uint32_t at = min(a0 + 8 * lg, A - 8u);
+        w0 = *(const float4_t*)(wbase + at);
+        w1 = *(const float4_t*)(wbase + at + 4);
+    };
     float4_t acc[NB];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) acc[nb] = (float4_t)0.0f;
 
-    // With one cold split (large batches) the next chunk's W values are
-    // prefetched with the next dictionary chunk.
-    const bool single = a.cold_splits == 1;
-    const float f0 = rowok ? s_cfac[myr][0] : 0.0f;
-    const bool wok = rowok && f0 != 0.0f; // an empty split wrote no bins: never read them
-    float4_t wn0 = (float4_t)0.0f, wn1 = (float4_t)0.0f;
-    auto load_w = [&](uint32_t a0) {
-        const uint32_t at0 = a0 + 4 * lg, at1 = a0 + 16 + 4 * lg;
-        wn0 = (wok && at0 < a_end) ? *(const float4_t*)(wbase + at0) : (float4_t)0.0f;
-        wn1 = (wok && at1 < a_end) ? *(const float4_t*)(wbase + at1) : (float4_t)0.0f;
-    };
-    if (single && n_ch) load_w(a_begin);
+    // Rings of PF = 2 chunks for D^T and W: chunk c lives in slot c % 2 and the
+    // slot is refilled with chunk c + 2 right after use (no register copies).
+    constexpr int PF = 2;
+    uint4_t dr[PF][NB];
+    float4_t wr0[PF], wr1[PF];
+#pragma unroll
+    for (int p = 0; p < PF; ++p) {
+        load_d(a_begin + 32 * p, dr[p]);
+        if constexpr (SINGLE) load_w(a_begin + 32 * p, wr0[p], wr1[p]);
+    }
 
-    for (uint32_t ch = 0; ch < n_ch; ++ch) {
-        const int buf = ch & 1;
-        const uint32_t a0 = a_begin + ch * 32;
-        const bool more = ch + 1 < n_ch;
-        const float4_t wc0 = wn0, wc1 = wn1;
-        if (more) {
-            load_d(a0 + 32);
-            if (single) load_w(a0 + 32);
-        }
-        float w8[8];
+    for (uint32_t ch = 0; ch < n_ch; ch += PF) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            w8[e] = f0 * wc0[e];
-            w8[4 + e] = f0 * wc1[e];
-        }
-        if (rowok && !single) {
+        for (int p = 0; p < PF; ++p) {
+            const uint32_t c = ch + p;
+            if (c >= n_ch) break;
+            const uint32_t a0 = a_begin + 32 * c;
+            const bool in = a0 + 8 * lg < a_end; // this lane's 8 atoms are in the range
+            float w8[8];
+            if constexpr (SINGLE) {
+                const bool use = wok && in; // empty splits wrote no bins: never use them
 #pragma unroll
-            for (int e = 0; e < 8; ++e) w8[e] = 0.0f;
-            const uint32_t at0 = a0 + 4 * lg, at1 = a0 + 16 + 4 * lg;
-            // Four splits' loads in flight at a time; empty splits are never read.
-            for (uint32_t s0 = 0; s0 < a.cold_splits; s0 += 4) {
-                float4_t v0[4], v1[4];
-                float fs[4];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const uint32_t sp = s0 + j;
-                    fs[j] = sp < a.cold_splits ? s_cfac[myr][sp] : 0.0f;
-                    const float* wrow = wbase + sp * wsplit;
-                    v0[j] = (fs[j] != 0.0f && at0 < a_end) ? *(const float4_t*)(wrow + at0) : (float4_t)0.0f;
-                    v1[j] = (fs[j] != 0.0f && at1 < a_end) ? *(const float4_t*)(wrow + at1) : (float4_t)0.0f;
+                for (int e = 0; e < 4; ++e) {
+                    w8[e] = use ? f0 * wr0[p][e] : 0.0f;
+                    w8[4 + e] = use ? f0 * wr1[p][e] : 0.0f;
                 }
+                load_w(a0 + 32 * PF, wr0[p], wr1[p]); // refill this slot PF chunks ahead (clamped)
+            } else {
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
+                for (int e = 0; e < 8; ++e) w8[e] = 0.0f;
+                const uint32_t at = min(a0 + 8 * lg, A - 8u);
+                // Four splits' loads in flight at a time (clamped split index); splits with
+                // factor 0 (empty) are masked at use.
+                for (uint32_t s0 = 0; s0 < a.cold_splits; s0 += 4) {
+                    float4_t v0[4], v1[4];
+                    float fs[4];
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        w8[e] += fs[j] * v0[j][e];
-                        w8[4 + e] += fs[j] * v1[j][e];
+                    for (int j = 0; j < 4; ++j) {
+                        const uint32_t sp = min(s0 + j, a.cold_splits - 1u);
+                        const float* wrow = wbase + sp * wsplit + at;
+                        v0[j] = *(const float4_t*)wrow;
+                        v1[j] = *(const float4_t*)(wrow + 4);
+                        fs[j] = rowok && in && s0 + j < a.cold_splits ? s_cfac[myr][s0 + j] : 0.0f;
                     }
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            w8[e] += fs[j] != 0.0f ? fs[j] * v0[j][e] : 0.0f;
+                            w8[4 + e] += fs[j] != 0.0f ? fs[j] * v1[j][e] : 0.0f;
+                        }
+                }
             }
-        }
-        half8_t hi, lo;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            hi[e] = (_Float16)w8[e];
-            lo[e] = (_Float16)(w8[e] - (float)hi[e]);
-        }
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-            half8_t dop;
+            half8_t hi, lo;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const int row = e < 4 ? 4 * lg + e : 16 + 4 * lg + (e - 4);
-                dop[e] = sd[buf][row * P + 16 * nb + li];
+                hi[e] = (_Float16)w8[e];
+                lo[e] = (_Float16)(w8[e] - (float)hi[e]);
             }
-            acc[nb] = mfma16x16x32(dop, hi, acc[nb]);
-            acc[nb] = mfma16x16x32(dop, lo, acc[nb]);
+            if (a0 + 32 > a_end) { // partial chunk (uniform): zero the D^T atoms past the range
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb) dr[p][nb] = in ? dr[p][nb] : (uint4_t)0u;
+            }
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                acc[nb] = mfma16x16x32(as_h8(dr[p][nb]), hi, acc[nb]);
+                acc[nb] = mfma16x16x32(as_h8(dr[p][nb]), lo, acc[nb]);
+            }
+            load_d(a0 + 32 * PF, dr[p]); // refill (clamped past the range)
         }
-        if (more) store_d(buf ^ 1);
-        __syncthreads();
     }
 
     if (!rowok) return;
@@ -1153,63 +1305,71 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
     const uint32_t R = a.rows_r;
     const uint64_t lbg = rowid / R, r = rowid % R;
     float Mc = -INFINITY, Lc = 0.0f, Mh = -INFINITY, Lh = 0.0f;
+    // Every load below is unconditional (clamped indices; absent arrays read the zero
+    // code) and masked at use, so they are all in flight together.
+    const bool has_c = a.ocp != nullptr, has_h = a.hot_splits > 0;
+    const float* zero = (const float*)&g_zero_code;
+    const uint32_t cs = has_c ? min((uint32_t)lane, a.cold_splits - 1u) : 0u;
+    const uint32_t hs = has_h ? min((uint32_t)lane, a.hot_splits - 1u) : 0u;
+    const uint64_t cb = has_c ? (lbg * a.cold_splits + cs) * R + r : 0;
+    const uint64_t hb = has_h ? (lbg * a.hot_splits + hs) * R + r : 0;
+    float cm = (has_c ? a.cold_m : zero)[cb];
+    float cl = (has_c ? a.cold_l : zero)[cb];
+    float hm = (has_h ? a.hot_m : zero)[hb];
+    float hl = (has_h ? a.hot_l : zero)[hb];
+    const int d0 = lane * DPT;
+    float oc[DPT], oh[DPT];
+    const float* csrc = has_c ? a.ocp + rowid * a.n_ar * HD + d0 : zero;
+    const uint32_t n_ar = has_c ? a.n_ar : 1u;
+#pragma unroll
+    for (int e = 0; e < DPT; ++e) {
+        oc[e] = 0.0f;
+        oh[e] = 0.0f;
+    }
     {
-        float cm = -INFINITY, cl = 0.0f, hm = -INFINITY, hl = 0.0f;
-        if (a.ocp && (uint32_t)lane < a.cold_splits) {
-            const uint64_t cb = (lbg * a.cold_splits + lane) * R + r;
-            cm = a.cold_m[cb];
-            cl = a.cold_l[cb];
+        constexpr int U = 8; // atom ranges summed per batch of loads
+        for (uint32_t ar = 0; ar < n_ar; ar += U) {
+            float v[U][DPT];
+#pragma unroll
+            for (int j = 0; j < U; ++j) {
+                const uint32_t aj = has_c ? min(ar + j, n_ar - 1u) : 0u;
+#pragma unroll
+                for (int e = 0; e < DPT; ++e) v[j][e] = csrc[has_c ? aj * HD + e : 0];
+            }
+#pragma unroll
+            for (int j = 0; j < U; ++j)
+#pragma unroll
+                for (int e = 0; e < DPT; ++e) oc[e] += (has_c && ar + j < n_ar) ? v[j][e] : 0.0f;
         }
-        if ((uint32_t)lane < a.hot_splits) {
-            const uint64_t hb = (lbg * a.hot_splits + lane) * R + r;
-            hm = a.hot_m[hb];
-            hl = a.hot_l[hb];
-        }
+    }
+    {
+        const bool cv = has_c && (uint32_t)lane < a.cold_splits;
+        const bool hv = has_h && (uint32_t)lane < a.hot_splits;
+        cm = cv ? cm : -INFINITY;
+        cl = cv ? cl : 0.0f;
+        hm = hv ? hm : -INFINITY;
+        hl = hv ? hl : 0.0f;
         float f;
         combine_splits(cm, cl, Mc, Lc, f);
         combine_splits(hm, hl, Mh, Lh, f);
         if (lane < kMaxSplits) s_hfac[row][lane] = f;
     }
     __builtin_amdgcn_wave_barrier();
-    const int d0 = lane * DPT;
-    float oc[DPT], oh[DPT];
-#pragma unroll
-    for (int e = 0; e < DPT; ++e) {
-        oc[e] = 0.0f;
-        oh[e] = 0.0f;
-    }
-    if (a.ocp) {
-        const float* src = a.ocp + rowid * a.n_ar * HD + d0;
-        uint32_t ar = 0;
-        for (; ar + 4 <= a.n_ar; ar += 4) {
-            float v[4][DPT];
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-#pragma unroll
-                for (int e = 0; e < DPT; ++e) v[j][e] = src[(ar + j) * HD + e];
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-#pragma unroll
-                for (int e = 0; e < DPT; ++e) oc[e] += v[j][e];
-        }
-        for (; ar < a.n_ar; ++ar)
-#pragma unroll
-            for (int e = 0; e < DPT; ++e) oc[e] += src[ar * HD + e];
-    }
-    const float* hsrc = a.hot_o + (lbg * a.hot_splits * R + r) * HD + d0;
+    const float* hsrc = has_h ? a.hot_o + (lbg * a.hot_splits * R + r) * HD + d0 : zero;
     for (uint32_t s0 = 0; s0 < a.hot_splits; s0 += 4) {
         float v[4][DPT], fs[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const uint32_t sp = s0 + j;
-            fs[j] = sp < a.hot_splits ? s_hfac[row][sp] : 0.0f;
+            const uint32_t sp = min(s0 + j, a.hot_splits - 1u);
 #pragma unroll
-            for (int e = 0; e < DPT; ++e) v[j][e] = fs[j] != 0.0f ? hsrc[(uint64_t)sp * R * HD + e] : 0.0f;
+            for (int e = 0; e < DPT; ++e) v[j][e] = hsrc[(uint64_t)sp * R * HD + e];
         }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) fs[j] = s0 + j < a.hot_splits ? s_hfac[row][s0 + j] : 0.0f;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
-            for (int e = 0; e < DPT; ++e) oh[e] += fs[j] * v[j][e];
+            for (int e = 0; e < DPT; ++e) oh[e] += fs[j] != 0.0f ? fs[j] * v[j][e] : 0.0f;
     }
     const uint64_t lb = lbg / a.kv_heads, g = lbg % a.kv_heads;
     const uint64_t q = r / a.gqa, h = g * a.gqa + r % a.gqa;
