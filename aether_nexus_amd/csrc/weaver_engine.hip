@@ -74,6 +74,12 @@ struct Layout {
 
 bool supported_head_dim(uint32_t d) { return d == 64 || d == 128; }
 
+// Row pitches of D^T (halves) and of the cold bins W (floats): one 128-byte line
+// of padding, so rows whose natural stride is a power of two (8 or 16 KiB at
+// 4096 atoms) spread over the L2 channels instead of landing on one.
+uint32_t dt_pitch(uint32_t A) { return A + 64; }
+uint32_t w_pitch(uint32_t A) { return A + 32; }
+
 // Largest cold row chunk (1, 2 or 4) whose LDS tables fit (with at least one
 // 1024-token split's block refs).
 uint32_t pick_rc(uint32_t R, uint32_t A, size_t max_lds) {
@@ -184,12 +190,12 @@ int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, Layout* L, char
         const uint32_t dh = d->dict_heads;
         const uint32_t hg = dh == 1 ? d->kv_heads : 1;
         o.rows_per_group = d->batch * hg * R;
-        o.tiles_per_group = cdiv(o.rows_per_group, 64);
+        o.tiles_per_group = cdiv(o.rows_per_group, (uint32_t)aw::kFinishRows);
         o.n_groups = d->layers * dh;
-        // Enough work-groups to cover the CUs, >= 128 atoms per range.
+        // About one 8-wave work-group per CU, >= 128 atoms per range.
         const uint64_t tiles = (uint64_t)o.tiles_per_group * o.n_groups;
         uint32_t n_ar = 1;
-        if (tiles < (uint64_t)n_cu) n_ar = (uint32_t)std::min<uint64_t>(cdiv(n_cu, tiles), std::max(1u, A / 128));
+        if (tiles < (uint64_t)n_cu) n_ar = (uint32_t)std::min<uint64_t>(cdiv((uint64_t)n_cu, tiles), std::max(1u, A / 128));
         o.atoms_per_range = (uint32_t)align_up(cdiv(A, n_ar), 32);
         o.n_ar = cdiv(A, o.atoms_per_range);
     }
@@ -202,7 +208,7 @@ int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, Layout* L, char
         return at;
     };
     if (o.info.computes_q_latent) o.off_ql = take((uint64_t)d->layers * d->batch * d->queries * d->q_heads * A * 2);
-    if (d->cold_count > 0) o.off_dt = take((uint64_t)d->layers * d->dict_heads * A * HD * 2);
+    if (d->cold_count > 0) o.off_dt = take((uint64_t)d->layers * d->dict_heads * dt_pitch(A) * HD * 2);
     if (o.info.hot_splits) {
         const uint64_t n = n_lbg * o.info.hot_splits * R;
         o.off_hm = take(n * 4);
@@ -214,7 +220,7 @@ int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, Layout* L, char
         o.off_cm = take(n * 4);
         o.off_cl = take(n * 4);
         o.off_ca = take(n * 4);
-        o.off_cw = take(n * A * 4);
+        o.off_cw = take(n * w_pitch(A) * 4);
         if (o.n_ar > 1) o.off_ocp = take(n_lbg * R * o.n_ar * HD * 4);
     }
     o.info.workspace_bytes = off;
@@ -321,6 +327,7 @@ int launch_project(aw_engine* e, const aw_decode_desc* d, const Layout& o, char*
     a.dict = d->dict;
     a.ql = o.info.computes_q_latent ? (uint16_t*)(ws + o.off_ql) : nullptr;
     a.dt = (uint16_t*)(ws + o.off_dt);
+    a.dt_pitch = dt_pitch(d->dict_size);
     a.batch = d->batch;
     a.queries = d->queries;
     a.q_heads = d->q_heads;
@@ -409,6 +416,7 @@ int launch_cold(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* ws
     a.part_l = (float*)(ws + o.off_cl);
     a.part_amax = (float*)(ws + o.off_ca);
     a.part_w = (float*)(ws + o.off_cw);
+    a.w_pitch = w_pitch(d->dict_size);
     a.err = e->err;
     a.batch = d->batch;
     a.kv_heads = d->kv_heads;
@@ -462,6 +470,8 @@ template <int HD>
 int launch_finish(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* ws, hipStream_t st) {
     aw::FinishArgs a{};
     a.dt = (const uint16_t*)(ws + o.off_dt);
+    a.dt_pitch = dt_pitch(d->dict_size);
+    a.w_pitch = w_pitch(d->dict_size);
     a.cold_m = (const float*)(ws + o.off_cm);
     a.cold_l = (const float*)(ws + o.off_cl);
     a.cold_w = (const float*)(ws + o.off_cw);
@@ -491,10 +501,16 @@ int launch_finish(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* 
     const uint64_t gx = (uint64_t)o.tiles_per_group * o.n_groups;
     if (gx > 0x7FFFFFFFull) return fail(e, AW_E_UNSUPPORTED, "finish grid too large");
     StageTimer t(e, AW_STAGE_FINISH, st);
+    const bool fused = o.n_ar == 1 && a.hot_splits > 0;
+    const uint32_t sneed = std::max(a.cold_splits, fused ? a.hot_splits : 1u);
+    uint32_t sf = 1;
+    while (sf < sneed) sf *= 2;
+    const size_t smem = aw::finish_smem_bytes(HD, sf);
+    const dim3 block(aw::kFinishWaves * 64);
     if (a.cold_splits == 1)
-        hipLaunchKernelGGL((aw::finish_kernel<HD, true>), dim3((uint32_t)gx, o.n_ar), dim3(256), 0, st, a);
+        hipLaunchKernelGGL((aw::finish_kernel<HD, true>), dim3((uint32_t)gx, o.n_ar), block, smem, st, a);
     else
-        hipLaunchKernelGGL((aw::finish_kernel<HD, false>), dim3((uint32_t)gx, o.n_ar), dim3(256), 0, st, a);
+        hipLaunchKernelGGL((aw::finish_kernel<HD, false>), dim3((uint32_t)gx, o.n_ar), block, smem, st, a);
     AW_HIP(e, hipGetLastError());
     return AW_OK;
 }
@@ -540,7 +556,7 @@ int run_pipeline(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* w
     int rc = AW_OK;
     const bool cold = o.info.cold_splits > 0;
     const bool hot = o.info.hot_splits > 0;
-    const bool fork = hot && cold && e->profiling != AW_PROFILE_SERIAL;
+    const bool fork = false; // measured: the hot kernel fills the GPU first, so a side stream bought no overlap
     if (fork) {
         AW_HIP(e, hipEventRecord(e->ev_fork, st));
         AW_HIP(e, hipStreamWaitEvent(e->side, e->ev_fork, 0));
@@ -762,6 +778,10 @@ int aw_engine_create(int device, aw_engine** out) {
                              (const void*)aw::cold_kernel<1, kColdCPT, kColdPD, true>,
                              (const void*)aw::cold_kernel<1, kColdCPT, kColdPD, false>};
         for (const void* f : fns)
+            (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)e->max_lds);
+        const void* fin[] = {(const void*)aw::finish_kernel<128, true>, (const void*)aw::finish_kernel<128, false>,
+                             (const void*)aw::finish_kernel<64, true>, (const void*)aw::finish_kernel<64, false>};
+        for (const void* f : fin)
             (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)e->max_lds);
     }
     if (hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking) != hipSuccess ||

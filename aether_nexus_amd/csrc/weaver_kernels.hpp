@@ -44,7 +44,6 @@ constexpr uint32_t kBlockTokens = 16;      // tokens per block (ModelDims::BLOCK
 constexpr uint32_t kRefMask = 0x7FFFFFFFu; // weaver_kernel.metal:145,174
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kColdThreads = 512;
-constexpr int kFinishWaves = 4;
 constexpr int kMaxSplits = 64;
 
 // Error bits written to the engine's device error word.
@@ -105,7 +104,8 @@ struct ProjArgs {
     const uint16_t* q;    // [L][B][Q][Hq][HD]
     const uint16_t* dict; // [L][dict_heads][A][HD]
     uint16_t* ql;         // [L][B][Q][Hq][A] f16, or null: transpose only
-    uint16_t* dt;         // [L][dict_heads][HD][A] f16: D^T for the finish
+    uint16_t* dt;         // [L][dict_heads][HD][dt_pitch] f16: D^T for the finish
+    uint32_t dt_pitch;    // A + padding: rows of D^T do not alias one L2 channel
     uint32_t batch, queries, q_heads, kv_heads, gqa, rows_r;
     uint32_t dict_size, dict_heads;
     uint32_t rows_per_group; // B*Q*(dict_heads==1 ? Hq : G)
@@ -135,7 +135,8 @@ struct ColdArgs {
     const uint32_t* seq_cold;
     float* part_m; // [lbg][S][R]
     float* part_l;
-    float* part_w;   // [lbg][S][R][A]
+    float* part_w;   // [lbg][S][R][w_pitch]
+    uint32_t w_pitch; // A + padding (rows 16 KiB apart would share L2 channels)
     float* part_amax; // [lbg][S][R]: max_a |bin[a]|
     uint32_t* err;
     uint32_t batch, kv_heads, gqa, rows_r;
@@ -148,7 +149,8 @@ struct ColdArgs {
 };
 
 struct FinishArgs {
-    const uint16_t* dt; // D^T [L][dict_heads][HD][A]
+    const uint16_t* dt; // D^T [L][dict_heads][HD][dt_pitch]
+    uint32_t dt_pitch, w_pitch;
     const float* cold_m;
     const float* cold_l;
     const float* cold_w;
@@ -276,7 +278,7 @@ __global__ __launch_bounds__(64) void project_kernel(ProjArgs a) {
         // D^T pieces of 8 atoms: piece p = (dim p / (2*NA), atom group p % (2*NA)).
         __syncthreads();
         constexpr int GROUPS = 2 * NA, PIECES = HD * GROUPS;
-        uint16_t* dt = a.dt + dgoff;
+        uint16_t* dt = a.dt + (uint64_t)group * HD * a.dt_pitch;
         for (int p = lane; p < PIECES; p += 64) {
             const int d = p / GROUPS, ag = p % GROUPS;
             const uint32_t at = atom0 + 8 * ag;
@@ -287,7 +289,7 @@ __global__ __launch_bounds__(64) void project_kernel(ProjArgs a) {
             uint4_t v;
 #pragma unroll
             for (int e = 0; e < 4; ++e) v[e] = (uint32_t)h[2 * e] | ((uint32_t)h[2 * e + 1] << 16);
-            *(uint4_t*)(dt + (uint64_t)d * a.dict_size + at) = v;
+            *(uint4_t*)(dt + (uint64_t)d * a.dt_pitch + at) = v;
         }
     }
 }
@@ -312,7 +314,7 @@ __global__ __launch_bounds__(64) void project_kernel(ProjArgs a) {
 // before use), so the next chunk's loads really stay in flight while the
 // current chunk is computed.
 template <int HD, int RT, bool SEPV>
-__global__ __launch_bounds__(64) void hot_kernel(HotArgs a) {
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu((RT == 1 && !SEPV) ? 3 : 1))) void hot_kernel(HotArgs a) {
     constexpr int KS = HD / 32, NB = HD / 16, P = HD + 4;
     __shared__ __attribute__((aligned(16))) _Float16 lds[32 * P];
     const int lane = threadIdx.x, li = lane & 15, lg = lane >> 4;
@@ -986,7 +988,7 @@ __global__ __launch_bounds__(kColdThreads) void cold_kernel(ColdArgs a) {
                 const float v = (float)(h ? v1 : v0) * inv;
                 amax[rr] = fmaxf(amax[rr], fabsf(v));
                 const uint32_t r = c * RC + rr;
-                if (r < R) a.part_w[(pbase + r) * A + at] = v;
+                if (r < R) a.part_w[(pbase + r) * a.w_pitch + at] = v;
             }
         }
     }
@@ -1023,11 +1025,7 @@ inline size_t cold_smem_bytes(uint32_t A, int RC, uint32_t tokens_per_split) {
 // pre-multiplied by 2^(m_s - Mc) / Lc * scl with scl a power of two that keeps
 // the largest combined bin below 2^14, so the hi/lo f16 split of each bin keeps
 // ~22 significant bits.  Hot splits combine to Mh, Lh with factors 2^(m_s - Mh).
-// Computed by one wave per row, lane = split.
-struct RowFactors {
-    float Mc, Lc, inv_scl, Mh, Lh;
-};
-
+// Computed by lanes = splits (a wave per row, or segments of a wave).
 __device__ inline float bin_scale(float bound, float Lc) {
     float scl = 1.0f;
     if (Lc > 0.0f && bound > 0.0f) {
@@ -1066,56 +1064,66 @@ __device__ inline float merge_value(float oh, float Mh, float Lh, float oc, floa
 
 // ------------------------------------------------------ bins . D (MFMA)
 //
-// Work-group = 64 rows sharing one dictionary (4 waves x 16 rows) x one atom
-// range.  Per wave: O^T[dim][row] += D^T W^T over 32-atom chunks,
-//   A = D^T (lane: dim 16*nb+li, atoms a0+8*lg .. +7: one 16-byte load from
-//       D^T [HD][A], which the projection wrote; L2-resident, shared by the
-//       four waves through L1),
+// Work-group = 128 rows sharing one dictionary (8 waves x 16 rows) x one atom
+// range.  The D^T chunk of 32 atoms x HD dims (written by the projection as
+// [HD][A]) is staged once per work-group in LDS and shared by the 8 waves, so
+// D^T is read from L2 once per 128 rows.  Per wave: O^T[dim][row] += D^T W^T,
+//   A = D^T (lane: dim 16*nb+li, atoms 8*lg .. +7: one 16-byte LDS read),
 //   B = W^T (lane: row li, the same 8 atoms: two 16-byte loads per cold split,
 //       combined with the split factors), split into hi + lo f16 terms -> two
 //       MFMAs per dim block.
-// No LDS staging and no barriers in the loop: the waves stream independently,
-// with the W and D^T loads two chunks ahead (SINGLE: one cold split;
-// otherwise the splits' W are combined per chunk).  With one atom range the log-sum-exp merge runs here too;
-// otherwise the partial cold outputs go to `ocp` for merge_kernel.
+// D^T pieces are prefetched two chunks ahead in registers and the LDS chunk is
+// double-buffered (one barrier per chunk); the W loads (the HBM stream) run two
+// chunks ahead in a register ring (SINGLE: one cold split; otherwise the
+// splits' W are combined per chunk).  Each wave finishes its own rows: with one
+// atom range the log-sum-exp merge runs here, otherwise the partial cold
+// outputs go to `ocp` for merge_kernel.
+constexpr int kFinishWaves = 8;
+constexpr int kFinishRows = 16 * kFinishWaves;
+constexpr int kFinishPitch = 40; // halves per staged D^T row (32 atoms + 8)
+
+// Dynamic LDS of finish_kernel: D^T double buffer, per-row split factors for
+// `sf` splits (cold and, when fused, hot), row factors and row ids.
+inline size_t finish_smem_bytes(int HD, uint32_t sf) {
+    return (size_t)2 * HD * kFinishPitch * 2 + (size_t)2 * kFinishRows * sf * 4 + (size_t)kFinishRows * 8 +
+           (size_t)kFinishRows * 5 * 4;
+}
+
 template <int HD, bool SINGLE>
-__global__ __launch_bounds__(256) void finish_kernel(FinishArgs a) {
-    constexpr int NB = HD / 16, ROWS = 64;
-    __shared__ float s_cfac[ROWS][kMaxSplits];
-    __shared__ float s_hfac[ROWS][kMaxSplits];
-    __shared__ RowFactors s_rf[ROWS];
-    __shared__ uint64_t s_row[ROWS]; // lbg*R + r, or ~0 for padding rows
+__global__ __launch_bounds__(kFinishWaves * 64) void finish_kernel(FinishArgs a) {
+    constexpr int NB = HD / 16, DP = kFinishPitch, PIECES = HD * 4; // 16-byte pieces per chunk
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, li = lane & 15, lg = lane >> 4;
     const uint32_t group = blockIdx.x / a.tiles_per_group, tile = blockIdx.x % a.tiles_per_group;
     const uint32_t ar = blockIdx.y;
     const uint32_t l = group / a.dict_heads, dg = group % a.dict_heads;
     const uint32_t R = a.rows_r, A = a.dict_size;
     const bool fused = a.n_ar == 1 && a.hot_splits > 0;
+    const uint32_t sneed = max(a.cold_splits, fused ? a.hot_splits : 1u);
+    const uint32_t lpr = sneed <= 1 ? 1u : 1u << (32 - __builtin_clz(sneed - 1u)); // factors per row
+    _Float16* sd = (_Float16*)smem;                                   // [2][HD][DP]
+    float* s_cfac = (float*)(smem + (size_t)2 * HD * DP * 2);         // [ROWS][lpr]
+    float* s_hfac = s_cfac + (size_t)kFinishRows * lpr;               // [ROWS][lpr]
+    uint64_t* s_row = (uint64_t*)(s_hfac + (size_t)kFinishRows * lpr); // [ROWS]
+    float* s_rf = (float*)(s_row + kFinishRows);                      // [ROWS][5]: Mc, Lc, inv_scl, Mh, Lh
 
-    // Split factors: wave w combines its rows 16w..16w+15.  Lanes form segments of
-    // lpr = pow2 >= splits lanes (lane in segment = split), one row per segment,
-    // 64/lpr rows per pass; all loads of a pass are unconditional (clamped).
+    // Split factors of this wave's 16 rows: lanes form segments of lpr lanes (lane
+    // in segment = split), one row per segment, 64/lpr rows per pass; all loads of
+    // a pass are unconditional (clamped).
     {
-        const uint32_t sneed = max(a.cold_splits, fused ? a.hot_splits : 1u);
-        const uint32_t lpr = sneed <= 1 ? 1u : 1u << (32 - __builtin_clz(sneed - 1u));
         const uint32_t seg = (uint32_t)lane / lpr, sp = (uint32_t)lane % lpr;
         const uint32_t per_pass = 64u / lpr;
         const float* hmp = fused ? a.hot_m : a.cold_m; // any valid array when the hot side is absent
         const float* hlp = fused ? a.hot_l : a.cold_l;
         for (uint32_t i0 = 0; i0 < 16u; i0 += per_pass) {
-            const uint32_t i = i0 + seg;                   // row of this wave handled by this segment
-            const uint32_t row_raw = tile * ROWS + wave * 16 + i;
+            const uint32_t i = i0 + seg; // row of this wave handled by this segment
+            const uint32_t row_raw = tile * kFinishRows + wave * 16 + i;
             const bool rv = i < 16u && row_raw < a.rows_per_group;
             const uint32_t row = min(row_raw, a.rows_per_group - 1u);
             uint64_t lbg;
-            uint32_t r;
-            if (a.dict_heads == 1) { // row = (b*Hkv + g)*R + r
-                lbg = (uint64_t)l * a.batch * a.kv_heads + row / R;
-                r = row % R;
-            } else { // row = b*R + r of kv head dg
-                lbg = ((uint64_t)l * a.batch + row / R) * a.kv_heads + dg;
-                r = row % R;
-            }
+            if (a.dict_heads == 1) lbg = (uint64_t)l * a.batch * a.kv_heads + row / R; // row = (b*Hkv + g)*R + r
+            else lbg = ((uint64_t)l * a.batch + row / R) * a.kv_heads + dg;            // row = b*R + r
+            const uint32_t r = row % R;
             const uint32_t cs = min(sp, a.cold_splits - 1u);
             const uint64_t cb = (lbg * a.cold_splits + cs) * R + r;
             float cm = a.cold_m[cb], cl = a.cold_l[cb], ca = a.cold_amax[cb];
@@ -1128,76 +1136,91 @@ __global__ __launch_bounds__(256) void finish_kernel(FinishArgs a) {
             ca = cv ? ca : 0.0f;
             hm = hv ? hm : -INFINITY;
             hl = hv ? hl : 0.0f;
-            RowFactors rf;
-            float f;
-            combine_seg(cm, cl, lpr, rf.Mc, rf.Lc, f);
-            const float scl = bin_scale(seg_reduce<false>(f * ca, lpr), rf.Lc);
-            rf.inv_scl = 1.0f / scl;
+            float Mc, Lc, f;
+            combine_seg(cm, cl, lpr, Mc, Lc, f);
+            const float scl = bin_scale(seg_reduce<false>(f * ca, lpr), Lc);
+            float Mh = -INFINITY, Lh = 0.0f, fh = 0.0f;
+            if (fused) combine_seg(hm, hl, lpr, Mh, Lh, fh);
             const uint32_t srow = wave * 16 + min(i, 15u);
-            if (i < 16u) s_cfac[srow][sp] = rf.Lc > 0.0f ? f / rf.Lc * scl : 0.0f;
-            rf.Mh = -INFINITY;
-            rf.Lh = 0.0f;
-            if (fused) {
-                float fh;
-                combine_seg(hm, hl, lpr, rf.Mh, rf.Lh, fh);
-                if (i < 16u) s_hfac[srow][sp] = fh;
-            }
-            if (i < 16u && sp == 0) {
-                s_rf[srow] = rf;
-                s_row[srow] = rv ? lbg * R + r : ~0ull;
+            if (i < 16u) {
+                s_cfac[srow * lpr + sp] = Lc > 0.0f ? f / Lc * scl : 0.0f;
+                s_hfac[srow * lpr + sp] = fh;
+                if (sp == 0) {
+                    s_row[srow] = rv ? lbg * R + r : ~0ull;
+                    float* rf = s_rf + srow * 5;
+                    rf[0] = Mc;
+                    rf[1] = Lc;
+                    rf[2] = 1.0f / scl;
+                    rf[3] = Mh;
+                    rf[4] = Lh;
+                }
             }
         }
     }
-    __syncthreads(); // each wave reads back only its own rows; one barrier orders the LDS traffic
+    __builtin_amdgcn_wave_barrier();
 
-    const uint16_t* dt = a.dt + (uint64_t)l * a.dict_layer + (uint64_t)dg * HD * A;
+    const uint16_t* dt = a.dt + (uint64_t)group * HD * a.dt_pitch;
     const uint32_t a_begin = ar * a.atoms_per_range;
     const uint32_t a_end = min(a_begin + a.atoms_per_range, A);
     const uint32_t n_ch = (a_end - a_begin + 31) / 32;
 
-    const int myr = 16 * wave + li; // this lane's B-operand row
+    const int myr = wave * 16 + li; // this lane's B-operand row
     const uint64_t myrow = s_row[myr];
     const bool rowok = myrow != ~0ull;
     const uint64_t lbg_me = rowok ? myrow / R : 0, r_me = rowok ? myrow % R : 0;
-    const float* wbase = a.cold_w + ((lbg_me * a.cold_splits) * R + r_me) * A;
-    const uint64_t wsplit = (uint64_t)R * A;
-    const float f0 = rowok ? s_cfac[myr][0] : 0.0f;
+    const float* wbase = a.cold_w + ((lbg_me * a.cold_splits) * R + r_me) * a.w_pitch;
+    const uint64_t wsplit = (uint64_t)R * a.w_pitch;
+    const float f0 = rowok ? s_cfac[myr * lpr] : 0.0f;
     const bool wok = rowok && f0 != 0.0f; // an empty split wrote no bins: never read them
 
-    // D^T operand of chunk a0: 8 dim blocks x 16 bytes (atoms a0+8*lg .. +7, all in or all out:
-    // dict_size % 16 == 0).  Loads are unconditional (clamped to the last 8 atoms); atoms past the
-    // range are zeroed where the chunk is used.
-    auto load_d = [&](uint32_t a0, uint4_t (&dop)[NB]) {
-        const uint32_t at = min(a0 + 8 * lg, A - 8u);
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) dop[nb] = *(const uint4_t*)(dt + (uint64_t)(16 * nb + li) * A + at);
+    // This thread's 16-byte piece of a D^T chunk: dim p/4, atoms 8*(p%4) .. +7 (clamped).
+    auto load_piece = [&](uint32_t c, int p) -> uint4_t {
+        const uint32_t at = min(a_begin + 32 * c + 8 * (p & 3), A - 8u);
+        return *(const uint4_t*)(dt + (uint64_t)(p >> 2) * a.dt_pitch + at);
     };
-    // Single-split W of chunk a0: this lane's row, atoms a0+8*lg .. +7 (clamped; masked at use).
-    auto load_w = [&](uint32_t a0, float4_t& w0, float4_t& w1) {
-        const uint32_t at = min(a0 + 8 * lg, A - 8u);
+    auto store_piece = [&](int buf, int p, uint4_t v) {
+        _Float16* dst = sd + ((size_t)buf * HD + (p >> 2)) * DP + 8 * (p & 3);
+        *(uint4_t*)dst = v;
+    };
+    // Single-split W of chunk c: this lane's row, atoms 8*lg .. +7 (clamped; masked at use).
+    auto load_w = [&](uint32_t c, float4_t& w0, float4_t& w1) {
+        const uint32_t at = min(a_begin + 32 * c + 8 * lg, A - 8u);
         w0 = *(const float4_t*)(wbase + at);
         w1 = *(const float4_t*)(wbase + at + 4);
     };
+
+    constexpr int PPT = (PIECES + kFinishWaves * 64 - 1) / (kFinishWaves * 64); // pieces per thread (1)
+    uint4_t pre[2][PPT];
+#pragma unroll
+    for (int q = 0; q < PPT; ++q) {
+        const int p = tid + q * kFinishWaves * 64;
+        if (p < PIECES) {
+            store_piece(0, p, load_piece(0, p));
+            pre[1][q] = load_piece(1, p);
+        }
+    }
+    float4_t wr0[2], wr1[2];
+    if constexpr (SINGLE) {
+        load_w(0, wr0[0], wr1[0]);
+        load_w(1, wr0[1], wr1[1]);
+    }
+    __syncthreads();
+
     float4_t acc[NB];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) acc[nb] = (float4_t)0.0f;
 
-    // Rings of PF = 2 chunks for D^T and W: chunk c lives in slot c % 2 and the
-    // slot is refilled with chunk c + 2 right after use (no register copies).
-    constexpr int PF = 2;
-    uint4_t dr[PF][NB];
-    float4_t wr0[PF], wr1[PF];
+    for (uint32_t ch = 0; ch < n_ch; ch += 2) {
 #pragma unroll
-    for (int p = 0; p < PF; ++p) {
-        load_d(a_begin + 32 * p, dr[p]);
-        if constexpr (SINGLE) load_w(a_begin + 32 * p, wr0[p], wr1[p]);
-    }
-
-    for (uint32_t ch = 0; ch < n_ch; ch += PF) {
-#pragma unroll
-        for (int p = 0; p < PF; ++p) {
-            const uint32_t c = ch + p;
+        for (int s = 0; s < 2; ++s) { // chunk c = ch + s uses LDS buffer s and register slots s
+            const uint32_t c = ch + s;
             if (c >= n_ch) break;
+            // Prefetch the D^T pieces of chunk c + 2 (slot s held chunk c, already in LDS).
+#pragma unroll
+            for (int q = 0; q < PPT; ++q) {
+                const int p = tid + q * kFinishWaves * 64;
+                if (p < PIECES) pre[s][q] = load_piece(c + 2, p);
+            }
             const uint32_t a0 = a_begin + 32 * c;
             const bool in = a0 + 8 * lg < a_end; // this lane's 8 atoms are in the range
             float w8[8];
@@ -1205,10 +1228,10 @@ __global__ __launch_bounds__(256) void finish_kernel(FinishArgs a) {
                 const bool use = wok && in; // empty splits wrote no bins: never use them
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    w8[e] = use ? f0 * wr0[p][e] : 0.0f;
-                    w8[4 + e] = use ? f0 * wr1[p][e] : 0.0f;
+                    w8[e] = use ? f0 * wr0[s][e] : 0.0f;
+                    w8[4 + e] = use ? f0 * wr1[s][e] : 0.0f;
                 }
-                load_w(a0 + 32 * PF, wr0[p], wr1[p]); // refill this slot PF chunks ahead (clamped)
+                load_w(c + 2, wr0[s], wr1[s]); // refill this slot two chunks ahead (clamped)
             } else {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) w8[e] = 0.0f;
@@ -1224,7 +1247,7 @@ __global__ __launch_bounds__(256) void finish_kernel(FinishArgs a) {
                         const float* wrow = wbase + sp * wsplit + at;
                         v0[j] = *(const float4_t*)wrow;
                         v1[j] = *(const float4_t*)(wrow + 4);
-                        fs[j] = rowok && in && s0 + j < a.cold_splits ? s_cfac[myr][s0 + j] : 0.0f;
+                        fs[j] = rowok && in && s0 + j < a.cold_splits ? s_cfac[myr * lpr + s0 + j] : 0.0f;
                     }
 #pragma unroll
                     for (int j = 0; j < 4; ++j)
@@ -1241,27 +1264,34 @@ __global__ __launch_bounds__(256) void finish_kernel(FinishArgs a) {
                 hi[e] = (_Float16)w8[e];
                 lo[e] = (_Float16)(w8[e] - (float)hi[e]);
             }
-            if (a0 + 32 > a_end) { // partial chunk (uniform): zero the D^T atoms past the range
-#pragma unroll
-                for (int nb = 0; nb < NB; ++nb) dr[p][nb] = in ? dr[p][nb] : (uint4_t)0u;
-            }
+            const bool partial = a0 + 32 > a_end; // uniform: atoms past the range get a zero operand
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) {
-                acc[nb] = mfma16x16x32(as_h8(dr[p][nb]), hi, acc[nb]);
-                acc[nb] = mfma16x16x32(as_h8(dr[p][nb]), lo, acc[nb]);
+                uint4_t dv = *(const uint4_t*)(sd + ((size_t)s * HD + 16 * nb + li) * DP + 8 * lg);
+                if (partial && !in) dv = (uint4_t)0u;
+                acc[nb] = mfma16x16x32(as_h8(dv), hi, acc[nb]);
+                acc[nb] = mfma16x16x32(as_h8(dv), lo, acc[nb]);
             }
-            load_d(a0 + 32 * PF, dr[p]); // refill (clamped past the range)
+            // Chunk c + 1's pieces (slot s ^ 1) into the other LDS buffer: its last readers
+            // (chunk c - 1) passed the previous barrier.
+#pragma unroll
+            for (int q = 0; q < PPT; ++q) {
+                const int p = tid + q * kFinishWaves * 64;
+                if (p < PIECES) store_piece(s ^ 1, p, pre[s ^ 1][q]);
+            }
+            __syncthreads();
         }
     }
 
     if (!rowok) return;
     // Lane holds O^T[dims 16*nb + 4*lg + e][row li of this wave].
-    const RowFactors rf = s_rf[myr];
+    const float* rf = s_rf + myr * 5;
+    const float Mc = rf[0], Lc = rf[1], inv_scl = rf[2], Mh = rf[3], Lh = rf[4];
     const uint64_t rowid = myrow;
     if (!fused && a.n_ar > 1) {
         float* dst = a.ocp + (rowid * a.n_ar + ar) * HD;
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) *(float4_t*)(dst + 16 * nb + 4 * lg) = acc[nb] * rf.inv_scl;
+        for (int nb = 0; nb < NB; ++nb) *(float4_t*)(dst + 16 * nb + 4 * lg) = acc[nb] * inv_scl;
         return;
     }
     // Fused merge with the hot partials of this row.
@@ -1270,7 +1300,7 @@ __global__ __launch_bounds__(256) void finish_kernel(FinishArgs a) {
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) oh[nb] = (float4_t)0.0f;
     for (uint32_t s = 0; s < a.hot_splits; ++s) {
-        const float f = s_hfac[myr][s];
+        const float f = s_hfac[myr * lpr + s];
         if (f == 0.0f) continue;
         const float* src = a.hot_o + ((lbg * a.hot_splits + s) * R + r) * HD;
 #pragma unroll
@@ -1284,7 +1314,7 @@ __global__ __launch_bounds__(256) void finish_kernel(FinishArgs a) {
         half4_t v;
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-            v[e] = (_Float16)merge_value(oh[nb][e], rf.Mh, rf.Lh, acc[nb][e] * rf.inv_scl, rf.Mc, rf.Lc);
+            v[e] = (_Float16)merge_value(oh[nb][e], Mh, Lh, acc[nb][e] * inv_scl, Mc, Lc);
         *(half4_t*)(o + 16 * nb + 4 * lg) = v;
     }
 }
