@@ -88,7 +88,9 @@ uint32_t pick_rc(uint32_t R, uint32_t A, size_t max_lds) {
     return rc;
 }
 
-int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, Layout* L, char* msg, size_t mlen) {
+// hot_waves_per_cu[rt]: resident hot waves per CU for RT = 1, 2, 4 row tiles (0, 1, 2).
+int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, const uint32_t hot_waves_per_cu[3], Layout* L,
+         char* msg, size_t mlen) {
     if (!d) {
         put_msg(msg, mlen, "null descriptor");
         return AW_E_INVALID_ARG;
@@ -138,10 +140,14 @@ int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, Layout* L, char
     o.info.rows_per_kv_head = R;
     o.info.computes_q_latent = (d->cold_count > 0 && d->q_latent == nullptr) ? 1u : 0u;
 
-    // Hot: ~8 waves per CU, >= 64 tokens per wave, splits <= kMaxSplits.
+    // Hot: one round of waves filling the resident capacity, >= 64 tokens per wave,
+    // splits <= kMaxSplits.
     if (d->hot_count > 0) {
         const uint64_t n_tok = (uint64_t)d->hot_count * kBlock;
-        uint64_t want = cdiv((uint64_t)n_cu * 16, n_lbg);
+        // Beside the cold kernel (one 8-wave work-group per CU) one hot wave per SIMD fits.
+        uint32_t wpc = hot_waves_per_cu[R <= 16 ? 0 : (R <= 32 ? 1 : 2)];
+        if (d->cold_count > 0) wpc = std::min(wpc, 4u);
+        uint64_t want = cdiv((uint64_t)n_cu * std::max(1u, wpc), n_lbg);
         uint64_t cap = std::max<uint64_t>(1, cdiv(n_tok, 64));
         uint64_t S = std::max<uint64_t>(1, std::min<uint64_t>({want, cap, (uint64_t)aw::kMaxSplits}));
         // A split holds at most 64 blocks (its refs live in one register of the wave).
@@ -240,6 +246,7 @@ struct aw_engine {
     uint64_t max_threads = 0;
     size_t max_lds = 0;
     uint32_t n_cu = 0;
+    uint32_t hot_wpc[3] = {12, 4, 4}; // resident hot waves per CU (RT = 1, 2, 4)
     DevBuf q, ql, hot, cold, refs, dict, out; // aw_decode copies (weaver.rs:40-46)
     DevBuf ws;                                // per-request scratch
     uint32_t* err = nullptr;                  // device error word
@@ -283,7 +290,7 @@ hipEvent_t take_event(aw_engine* e) {
         return ev;
     }
     hipEvent_t ev = nullptr;
-    if (hipEventCreate(&ev) != hipSuccess) return nullptr;
+    if (hipEventCreateWithFlags(&ev, hipEventReleaseToDevice) != hipSuccess) return nullptr;
     return ev;
 }
 
@@ -442,11 +449,24 @@ int launch_cold(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* ws
     a.s_j = A;
     a.s_a = 1;
     (void)HD;
-    const uint64_t grid = (uint64_t)cdiv(a.n_units, 8) * 8 * d->kv_heads;
-    if (grid > 0x7FFFFFFFull) return fail(e, AW_E_UNSUPPORTED, "cold grid too large");
+    const uint64_t n_wg = (uint64_t)cdiv(a.n_units, 8) * 8 * d->kv_heads;
+    if (n_wg > 0x7FFFFFFFull) return fail(e, AW_E_UNSUPPORTED, "cold grid too large");
+    a.n_wg = (uint32_t)n_wg;
     const size_t smem = aw::cold_smem_bytes(A, (int)o.rc, a.tokens_per_split);
-    StageTimer t(e, AW_STAGE_COLD, st);
     const bool pow2 = (A & (A - 1u)) == 0u;
+    // One resident round of work-groups (a multiple of 8: each keeps its XCD).
+    const void* fn = o.rc == 4 ? (pow2 ? (const void*)aw::cold_kernel<4, kColdCPT, kColdPD, true>
+                                       : (const void*)aw::cold_kernel<4, kColdCPT, kColdPD, false>)
+                   : o.rc == 2 ? (pow2 ? (const void*)aw::cold_kernel<2, kColdCPT, kColdPD, true>
+                                       : (const void*)aw::cold_kernel<2, kColdCPT, kColdPD, false>)
+                               : (pow2 ? (const void*)aw::cold_kernel<1, kColdCPT, kColdPD, true>
+                                       : (const void*)aw::cold_kernel<1, kColdCPT, kColdPD, false>);
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, aw::kColdThreads, smem) != hipSuccess || per_cu < 1)
+        per_cu = 1;
+    const uint64_t resident = std::max<uint64_t>(8, ((uint64_t)e->n_cu * per_cu) / 8 * 8);
+    const uint64_t grid = std::min<uint64_t>(n_wg, resident);
+    StageTimer t(e, AW_STAGE_COLD, st);
 #define AW_LAUNCH_COLD(RCV, P2)                                                                                    \
     hipLaunchKernelGGL((aw::cold_kernel<RCV, kColdCPT, kColdPD, P2>), dim3((uint32_t)grid), dim3(aw::kColdThreads), \
                        smem, st, a)
@@ -548,32 +568,36 @@ int launch_merge(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* w
 }
 
 // Stage order on `st`: [q.D^T] -> cold -> finish [-> merge].  The hot kernel
-// (HBM-bound) runs on the engine's side stream concurrently with the cold
-// kernel (LDS-bound) and is joined before the finish.  AW_PROFILE_SERIAL puts
-// everything on `st` so each kernel's event-timed duration is its own.
+// (HBM-bound) runs on the engine's side stream, forked after q.D^T, so it starts
+// together with the cold kernel (L1/LDS-bound, one resident work-group per CU)
+// and fills the resources the cold work-groups leave free.  It is joined only
+// where its partials are read: before the merge, or before the finish when the
+// finish merges.  AW_PROFILE_SERIAL puts everything on `st`, one kernel at a time.
 template <int HD>
 int run_pipeline(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* ws, hipStream_t st) {
     int rc = AW_OK;
     const bool cold = o.info.cold_splits > 0;
     const bool hot = o.info.hot_splits > 0;
-    const bool fork = false; // measured: the hot kernel fills the GPU first, so a side stream bought no overlap
+    const bool fork = hot && cold && e->profiling != AW_PROFILE_SERIAL;
+    if (!cold) {
+        if (hot && (rc = launch_hot<HD>(e, d, o, ws, st))) return rc;
+        return launch_merge<HD>(e, d, o, ws, st);
+    }
+    if (hot && !fork)
+        if ((rc = launch_hot<HD>(e, d, o, ws, st))) return rc;
+    if ((rc = launch_project<HD>(e, d, o, ws, st))) return rc;
     if (fork) {
         AW_HIP(e, hipEventRecord(e->ev_fork, st));
         AW_HIP(e, hipStreamWaitEvent(e->side, e->ev_fork, 0));
         if ((rc = launch_hot<HD>(e, d, o, ws, e->side))) return rc;
         AW_HIP(e, hipEventRecord(e->ev_join, e->side));
-    } else if (hot) {
-        if ((rc = launch_hot<HD>(e, d, o, ws, st))) return rc;
     }
-    if (cold)
-        if ((rc = launch_project<HD>(e, d, o, ws, st))) return rc;
-    if (cold) {
-        if ((rc = launch_cold(e, d, o, ws, st))) return rc;
+    if ((rc = launch_cold(e, d, o, ws, st))) return rc;
+    const bool merge = o.n_ar > 1; // otherwise the finish merges
+    if (fork && !merge) AW_HIP(e, hipStreamWaitEvent(st, e->ev_join, 0));
+    if ((rc = launch_finish<HD>(e, d, o, ws, st))) return rc;
+    if (merge) {
         if (fork) AW_HIP(e, hipStreamWaitEvent(st, e->ev_join, 0));
-        if ((rc = launch_finish<HD>(e, d, o, ws, st))) return rc;
-        if (o.n_ar > 1)
-            if ((rc = launch_merge<HD>(e, d, o, ws, st))) return rc;
-    } else {
         if ((rc = launch_merge<HD>(e, d, o, ws, st))) return rc;
     }
     return AW_OK;
@@ -582,7 +606,7 @@ int run_pipeline(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* w
 int decode_device(aw_engine* e, const aw_decode_desc* d, hipStream_t st) {
     Layout o;
     char msg[256] = {0};
-    int rc = plan(d, e->max_lds, e->n_cu, &o, msg, sizeof msg);
+    int rc = plan(d, e->max_lds, e->n_cu, e->hot_wpc, &o, msg, sizeof msg);
     if (rc) return fail(e, rc, "%s", msg);
     if (!d->out || !d->q) return fail(e, AW_E_INVALID_ARG, "q and out are required");
     if (d->hot_count && (!d->hot_k || !d->refs)) return fail(e, AW_E_INVALID_ARG, "hot_k and refs are required");
@@ -735,7 +759,8 @@ int aw_validate_params(const aw_weaver_params* p, size_t n_q_exact, size_t n_q_l
 int aw_decode_plan(const aw_decode_desc* desc, aw_decode_plan_info* info, char* msg, size_t mlen) {
     Layout o;
     // Host-side planning assumes the MI355X limits: 160 KiB LDS per work-group, 256 CUs.
-    int rc = plan(desc, 160 * 1024, 256, &o, msg, mlen);
+    const uint32_t wpc[3] = {12, 4, 4}; // gfx950 residency of the hot kernel variants
+    int rc = plan(desc, 160 * 1024, 256, wpc, &o, msg, mlen);
     if (rc == AW_OK && info) *info = o.info;
     return rc;
 }
@@ -769,6 +794,16 @@ int aw_engine_create(int device, aw_engine** out) {
         delete e;
         return rc;
     }
+    // Resident hot waves per CU, from the compiled kernels' resource use (K == V variants).
+    {
+        const void* hk[3] = {(const void*)aw::hot_kernel<128, 1, false>, (const void*)aw::hot_kernel<128, 2, false>,
+                             (const void*)aw::hot_kernel<128, 4, false>};
+        for (int i = 0; i < 3; ++i) {
+            int nb = 0;
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, hk[i], 64, 0) == hipSuccess && nb > 0)
+                e->hot_wpc[i] = (uint32_t)nb;
+        }
+    }
     // Let the cold kernel use the device's full LDS.
     {
         const void* fns[] = {(const void*)aw::cold_kernel<4, kColdCPT, kColdPD, true>,
@@ -786,8 +821,10 @@ int aw_engine_create(int device, aw_engine** out) {
     }
     if (hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking) != hipSuccess ||
         hipStreamCreateWithFlags(&e->side, hipStreamNonBlocking) != hipSuccess ||
-        hipEventCreateWithFlags(&e->ev_fork, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&e->ev_join, hipEventDisableTiming) != hipSuccess ||
+        // Fork/join order two streams of this device: a device-scope release is enough,
+        // no system-scope cache writeback.
+        hipEventCreateWithFlags(&e->ev_fork, hipEventDisableTiming | hipEventDisableSystemFence) != hipSuccess ||
+        hipEventCreateWithFlags(&e->ev_join, hipEventDisableTiming | hipEventDisableSystemFence) != hipSuccess ||
         hipMalloc((void**)&e->err, 256) != hipSuccess || hipMemset(e->err, 0, 256) != hipSuccess) {
         aw_engine_destroy(e);
         return AW_E_HIP;

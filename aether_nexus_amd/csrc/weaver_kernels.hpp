@@ -142,6 +142,7 @@ struct ColdArgs {
     uint32_t batch, kv_heads, gqa, rows_r;
     uint32_t hot_count, cold_count, refs_stride, dict_size;
     uint32_t splits, tokens_per_split, n_chunks, n_units;
+    uint32_t n_wg; // work items (8 XCD slots x kv heads x unit groups)
     float scale_log2;
     uint64_t cold_blocks, cold_layer, refs_layer;
     // q_latent element (lb, g, q, j, a) = ql[lb*s_lb + g*s_g + q*s_q + j*s_j + a*s_a]
@@ -553,12 +554,14 @@ __device__ __attribute__((aligned(16))) uint4_t g_zero_code = {0u, 0u, 0u, 0u};
 constexpr float kMagic = 12582912.0f;                 // 1.5 * 2^23
 constexpr uint64_t kMagic2 = 0x4B4000004B400000ull;   // two magic patterns
 
+// One work item `wg` (its index in the full grid of work items; the kernel below
+// walks them persistently, one work-group per CU slot).
 template <int RC, int CPT, int PD, bool POW2>
-__global__ __launch_bounds__(kColdThreads) void cold_kernel(ColdArgs a) {
+__device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
     constexpr int NT = kColdThreads, NW = NT / 64, NP = (RC + 1) / 2, NRED = RC + 2; // row values, max|c|, max p
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t x = blockIdx.x % 8u, k = blockIdx.x / 8u;
+    const uint32_t x = wg % 8u, k = wg / 8u;
     const uint32_t g = k % a.kv_heads;
     const uint32_t u = (k / a.kv_heads) * 8u + x;
     if (u >= a.n_units) return;
@@ -1007,6 +1010,17 @@ __global__ __launch_bounds__(kColdThreads) void cold_kernel(ColdArgs a) {
             a.part_l[pbase + r] = lpart[tid] * inv; // sum of p, back from units of 2^-F
             a.part_amax[pbase + r] = v[tid];
         }
+    }
+}
+
+// Persistent: work-group i takes work items i, i + gridDim.x, ... (gridDim.x a
+// multiple of 8, so each keeps its XCD), so the grid is one resident round and
+// the hot kernel can run beside it in the resources it leaves free.
+template <int RC, int CPT, int PD, bool POW2>
+__global__ __launch_bounds__(kColdThreads) void cold_kernel(ColdArgs a) {
+    for (uint32_t wg = blockIdx.x; wg < a.n_wg; wg += gridDim.x) {
+        cold_unit<RC, CPT, PD, POW2>(a, wg);
+        __syncthreads(); // the next item rewrites the LDS tables
     }
 }
 
