@@ -556,11 +556,20 @@ constexpr uint64_t kMagic2 = 0x4B4000004B400000ull;   // two magic patterns
 
 // One work item `wg` (its index in the full grid of work items; the kernel below
 // walks them persistently, one work-group per CU slot).
+//
+// Tokens are dealt to waves in wave tiles of 64*CPT consecutive tokens: wave w
+// takes tiles w, w + NW, w + 2*NW, ... (so the first NW tiles, the planning
+// sample, cover the split's first NT*CPT tokens).  The assignment is static, so
+// every float sum runs in the same order on every call.
 template <int RC, int CPT, int PD, bool POW2>
 __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
-    constexpr int NT = kColdThreads, NW = NT / 64, NP = (RC + 1) / 2, NRED = RC + 2; // row values, max|c|, max p
+    constexpr int NT = kColdThreads, NW = NT / 64, NP = (RC + 1) / 2;
+    constexpr int NB = RC + 2;      // values of the end-of-split reductions
+    constexpr int NR = 2 * RC + 2;  // LDS slots per wave: the plan's (max, sum) pairs and max|c|
+    constexpr uint32_t WT = 64u * CPT; // tokens of one wave tile
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6); // uniform, so tile branches stay scalar
     const uint32_t x = wg % 8u, k = wg / 8u;
     const uint32_t g = k % a.kv_heads;
     const uint32_t u = (k / a.kv_heads) * 8u + x;
@@ -591,101 +600,42 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
 
     const uint32_t qtab_bytes = (A * RC * 2 + 15) & ~15u;
     const uint32_t n_blk = (t_end - t_begin + 15) / 16; // t_begin is a multiple of 16
+    const uint32_t n_wt = (t_end - t_begin + WT - 1) / WT;
     _Float16* qtab = (_Float16*)smem;
     uint64_t* bins = (uint64_t*)(smem + qtab_bytes);       // [A][NP]
     uint32_t* sref = (uint32_t*)(bins + (uint64_t)A * NP); // [n_blk] physical blocks, ~0 = invalid
-    float* red = (float*)(sref + ((n_blk + 3) & ~3u));    // [NW][NRED]
-
-    // q_latent rows of this chunk into LDS; rows past R are zero.
-    {
-        uint64_t rbase[RC];
-        bool rok[RC];
-#pragma unroll
-        for (int rr = 0; rr < RC; ++rr) {
-            const uint32_t r = c * RC + rr;
-            rok[rr] = r < R;
-            rbase[rr] = rok[rr] ? (uint64_t)lb * a.s_lb + g * a.s_g + (uint64_t)(r / a.gqa) * a.s_q +
-                                      (uint64_t)(r % a.gqa) * a.s_j
-                                : 0;
-        }
-        // Atom-contiguous rows (s_a == 1, q_latent's layout): 16-byte loads of 8 atoms per
-        // row, interleaved into [A][RC] in registers.
-        if (a.s_a == 1 && (A % 8) == 0 && ((uintptr_t)a.ql & 15u) == 0) {
-            for (uint32_t a8 = tid; a8 < A / 8; a8 += NT) {
-                uint4_t w[RC];
-#pragma unroll
-                for (int rr = 0; rr < RC; ++rr) w[rr] = *(const uint4_t*)(a.ql + rbase[rr] + (uint64_t)a8 * 8);
-#pragma unroll
-                for (int rr = 0; rr < RC; ++rr)
-                    if (!rok[rr]) w[rr] = (uint4_t)0u;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    _Float16 hv[RC];
-#pragma unroll
-                    for (int rr = 0; rr < RC; ++rr)
-                        hv[rr] = __builtin_bit_cast(_Float16, (uint16_t)(w[rr][e / 2] >> (16 * (e % 2))));
-                    if constexpr (RC == 4) {
-                        half4_t v4 = {hv[0], hv[1], hv[2], hv[3]};
-                        *(half4_t*)(qtab + (a8 * 8 + e) * 4) = v4;
-                    } else {
-#pragma unroll
-                        for (int rr = 0; rr < RC; ++rr) qtab[(a8 * 8 + e) * RC + rr] = hv[rr];
-                    }
-                }
-            }
-        } else {
-            for (uint32_t at = tid; at < A; at += NT)
-#pragma unroll
-                for (int rr = 0; rr < RC; ++rr)
-                    qtab[at * RC + rr] =
-                        __builtin_bit_cast(_Float16, rok[rr] ? a.ql[rbase[rr] + (uint64_t)at * a.s_a] : (uint16_t)0);
-        }
-    }
-    // The split's block refs, resolved once, so code addresses come from LDS.
-    {
-        const uint32_t* refs = a.refs + (uint64_t)l * a.refs_layer + (uint64_t)(lb % a.batch) * a.refs_stride +
-                               a.hot_count + t_begin / 16;
-        for (uint32_t i = tid; i < n_blk; i += NT) {
-            uint32_t ref = refs[i] & kRefMask;
-            if (ref >= a.cold_blocks) {
-                flag_error(a.err, kErrColdRef);
-                ref = ~0u;
-            }
-            sref[i] = ref;
-        }
-    }
-    __syncthreads(); // qtab and sref complete
+    float* red = (float*)(sref + ((n_blk + 3) & ~3u));    // [NW][NR]
 
     const uint4_t* cold = a.cold + (uint64_t)l * a.cold_layer;
-    const uint32_t tile_tokens = NT * CPT;
-    const uint32_t n_tiles = (t_end - t_begin + tile_tokens - 1) / tile_tokens;
+    const uint32_t* grefs = a.refs + (uint64_t)l * a.refs_layer + (uint64_t)(lb % a.batch) * a.refs_stride +
+                            a.hot_count + t_begin / 16;
     const float sl = a.scale_log2;
 
-    // Code of token t for this kv head; tokens past the split or behind a bad ref
-    // read the zero code and are reported invalid.  The load itself is
-    // unconditional.  Split in two so the ring can read a tile's refs from LDS
-    // ahead of the atomics it issues, and load the codes after them.
-    auto tile_refs = [&](uint32_t t0, uint32_t (&rb)[CPT]) {
+    // Token of lane `lane`, slot kk of wave tile `tile`.
+    auto tok = [&](uint32_t tile, int kk) { return t_begin + tile * WT + (uint32_t)kk * 64u + (uint32_t)lane; };
+    // Refs of a wave tile from LDS (~0 past the split or behind a bad ref).
+    auto tile_refs = [&](uint32_t tile, uint32_t (&rb)[CPT]) {
 #pragma unroll
         for (int kk = 0; kk < CPT; ++kk) {
-            const uint32_t t = t0 + kk * NT + tid;
+            const uint32_t t = tok(tile, kk);
             rb[kk] = t < t_end ? sref[(t - t_begin) >> 4] : ~0u;
         }
     };
-    auto tile_codes = [&](uint32_t t0, const uint32_t (&rb)[CPT], uint4_t (&buf)[CPT], bool (&ok)[CPT]) {
+    // Codes of a wave tile for this kv head; invalid tokens read the zero code.
+    // The load itself is unconditional.
+    auto tile_codes = [&](uint32_t tile, const uint32_t (&rb)[CPT], uint4_t (&buf)[CPT], bool (&ok)[CPT]) {
 #pragma unroll
         for (int kk = 0; kk < CPT; ++kk) {
-            const uint32_t t = t0 + kk * NT + tid;
             ok[kk] = rb[kk] != ~0u;
-            const uint4_t* p =
-                ok[kk] ? cold + ((uint64_t)rb[kk] * kBlockTokens + (t & 15u)) * a.kv_heads + g : &g_zero_code;
+            const uint4_t* p = ok[kk] ? cold + ((uint64_t)rb[kk] * kBlockTokens + (tok(tile, kk) & 15u)) * a.kv_heads + g
+                                      : &g_zero_code;
             buf[kk] = *p;
         }
     };
-    auto load_tile = [&](uint32_t t0, uint4_t (&buf)[CPT], bool (&ok)[CPT]) {
+    auto load_tile = [&](uint32_t tile, uint4_t (&buf)[CPT], bool (&ok)[CPT]) {
         uint32_t rb[CPT];
-        tile_refs(t0, rb);
-        tile_codes(t0, rb, buf, ok);
+        tile_refs(tile, rb);
+        tile_codes(tile, rb, buf, ok);
     };
     // Atom indices of a code word, always inside the tables: a power-of-two
     // dictionary masks them (any bit outside the mask is recorded in `oob`),
@@ -733,84 +683,205 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
         const uint32_t lo = max(m0 & 0xFFFFu, m1 & 0xFFFFu), hi = max(m0 >> 16, m1 >> 16);
         return max(lo, hi);
     };
+    auto cmax_f = [&](const uint4_t cw) { return (float)__builtin_bit_cast(_Float16, (uint16_t)cmax_bits(cw)); };
 
-    // Work-group sums/maxima of up to NRED per-lane values (one barrier pair).
-    auto wg_reduce = [&](float (&v)[NRED], const bool (&is_max)[NRED]) {
+    // Work-group sums/maxima of NB per-lane values (one barrier pair).
+    auto wg_reduce = [&](float (&v)[NB], const bool (&is_max)[NB]) {
         __syncthreads(); // previous readers of `red` are done
 #pragma unroll
-        for (int i = 0; i < NRED; ++i) {
+        for (int i = 0; i < NB; ++i) {
             const float w = is_max[i] ? wave_max(v[i]) : wave_sum(v[i]);
-            if (lane == 0) red[wave * NRED + i] = w;
+            if (lane == 0) red[wave * NR + i] = w;
         }
         __syncthreads();
 #pragma unroll
-        for (int i = 0; i < NRED; ++i) {
+        for (int i = 0; i < NB; ++i) {
             float acc = is_max[i] ? -INFINITY : 0.0f;
-            for (int w = 0; w < NW; ++w) acc = is_max[i] ? fmaxf(acc, red[w * NRED + i]) : acc + red[w * NRED + i];
+            for (int w = 0; w < NW; ++w) acc = is_max[i] ? fmaxf(acc, red[w * NR + i]) : acc + red[w * NR + i];
             v[i] = acc;
         }
     };
 
-    float ref[RC];
-    int F = 0;
-    float lpart[RC];
-    float cmx = 0.0f, pmx = 0.0f;
-    uint32_t oob = 0;
-    uint4_t cur[CPT];
-    bool curv[CPT];
-    bool exact = false;
-    for (int attempt = 0; attempt < 2; ++attempt) {
-        for (uint32_t i = tid; i < A * NP; i += NT) bins[i] = 0ull;
-        load_tile(t_begin, cur, curv);
-        __syncthreads(); // bins zeroed before any thread adds
-        if (!exact) {
-            // Reference and scale from the first tile (invalid tokens masked).
-            float v[NRED];
-            bool is_max[NRED];
+    // Set-up loads, oldest first, so that waiting for one never waits for the
+    // code loads behind it: the first SR block refs and the first q_latent chunk
+    // of each thread, then the refs of the ring's first tiles, then their codes.
+    constexpr int SR = 4; // block refs per thread loaded up front (splits of <= 64*NT blocks)
+    uint32_t srg[SR];
 #pragma unroll
-            for (int i = 0; i < NRED; ++i) {
-                v[i] = i < RC ? -INFINITY : 0.0f;
-                is_max[i] = true;
+    for (int j = 0; j < SR; ++j) srg[j] = grefs[min(tid + (uint32_t)j * NT, n_blk - 1)];
+    uint64_t rbase[RC];
+    bool rok[RC];
+#pragma unroll
+    for (int rr = 0; rr < RC; ++rr) {
+        const uint32_t r = c * RC + rr;
+        rok[rr] = r < R;
+        rbase[rr] = rok[rr] ? (uint64_t)lb * a.s_lb + g * a.s_g + (uint64_t)(r / a.gqa) * a.s_q +
+                                  (uint64_t)(r % a.gqa) * a.s_j
+                            : 0;
+    }
+    // Atom-contiguous rows (s_a == 1, q_latent's layout) load as 16-byte pieces of
+    // 8 atoms per row, interleaved into [A][RC] in registers.
+    const bool qvec = a.s_a == 1 && (A % 8) == 0 && ((uintptr_t)a.ql & 15u) == 0;
+    uint4_t qw[RC];
+    if (qvec) {
+#pragma unroll
+        for (int rr = 0; rr < RC; ++rr) qw[rr] = *(const uint4_t*)(a.ql + rbase[rr] + (uint64_t)min((uint32_t)tid, A / 8 - 1) * 8);
+    }
+    auto put_q = [&](uint32_t a8, uint4_t (&w)[RC]) {
+#pragma unroll
+        for (int rr = 0; rr < RC; ++rr)
+            if (!rok[rr]) w[rr] = (uint4_t)0u;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            _Float16 hv[RC];
+#pragma unroll
+            for (int rr = 0; rr < RC; ++rr) hv[rr] = __builtin_bit_cast(_Float16, (uint16_t)(w[rr][e / 2] >> (16 * (e % 2))));
+            if constexpr (RC == 4) {
+                half4_t v4 = {hv[0], hv[1], hv[2], hv[3]};
+                *(half4_t*)(qtab + (a8 * 8 + e) * 4) = v4;
+            } else {
+#pragma unroll
+                for (int rr = 0; rr < RC; ++rr) qtab[(a8 * 8 + e) * RC + rr] = hv[rr];
             }
-            float scs[CPT][RC];
+        }
+    };
+
+    // Ring of PD wave tiles of codes in flight per wave; slot d holds tile tl[d].
+    uint4_t ring[PD][CPT];
+    bool rv[PD][CPT];
+    uint32_t tl[PD];
+    {
+        uint32_t rg[PD][CPT];
+#pragma unroll
+        for (int d = 0; d < PD; ++d) {
+            tl[d] = (uint32_t)(wave + d * NW);
+#pragma unroll
+            for (int kk = 0; kk < CPT; ++kk) rg[d][kk] = grefs[min((tok(tl[d], kk) - t_begin) >> 4, n_blk - 1)];
+        }
+#pragma unroll
+        for (int d = 0; d < PD; ++d) {
+            uint32_t rb[CPT];
 #pragma unroll
             for (int kk = 0; kk < CPT; ++kk) {
-                uint32_t ia[4];
-                uint32_t dummy = 0;
-                atoms(cur[kk], ia, dummy);
-                score(cur[kk], ia, scs[kk]);
-                if (curv[kk]) {
-#pragma unroll
-                    for (int rr = 0; rr < RC; ++rr) v[rr] = fmaxf(v[rr], scs[kk][rr] * sl);
-                    v[RC] = fmaxf(v[RC], (float)__builtin_bit_cast(_Float16, (uint16_t)cmax_bits(cur[kk])));
-                }
+                const uint32_t ref = rg[d][kk] & kRefMask;
+                rb[kk] = (tok(tl[d], kk) < t_end && ref < a.cold_blocks) ? ref : ~0u;
             }
-            wg_reduce(v, is_max);
-#pragma unroll
-            for (int rr = 0; rr < RC; ++rr) ref[rr] = v[rr] == -INFINITY ? 0.0f : ceilf(v[rr]);
-            const float cmax0 = v[RC];
-            float w[NRED];
-#pragma unroll
-            for (int i = 0; i < NRED; ++i) {
-                w[i] = 0.0f;
-                is_max[i] = false;
-            }
-#pragma unroll
-            for (int kk = 0; kk < CPT; ++kk)
-                if (curv[kk]) {
-                    float ps = 0.0f;
-#pragma unroll
-                    for (int rr = 0; rr < RC; ++rr) ps += fast_exp2(scs[kk][rr] * sl - ref[rr]);
-                    w[0] += 4.0f * (float)__builtin_bit_cast(_Float16, (uint16_t)cmax_bits(cur[kk])) * ps;
-                }
-            wg_reduce(w, is_max);
-            const float plan = w[0] * (float)n_tiles; // bound on sum |p*c| over the split, if tiles are alike
-            int Fs = plan > 0.0f ? 28 - exp_of(plan) : 100;
-            int Fm = cmax0 > 0.0f ? 18 - exp_of(cmax0) : 100; // p <= 1 in the first tile
-            F = min(100, max(-100, min(Fs, Fm)));
+            tile_codes(tl[d], rb, ring[d], rv[d]);
         }
-        // Stream every tile into the bins; PD tiles of code loads stay in flight
-        // (a ring of registers, refilled as each slot is consumed).
+    }
+    // Tables into LDS: q_latent rows of this chunk (rows past R are zero) and the
+    // split's block refs, resolved once so code addresses come from LDS.
+    if (qvec) {
+        if ((uint32_t)tid < A / 8) put_q(tid, qw);
+        for (uint32_t a8 = tid + NT; a8 < A / 8; a8 += NT) {
+            uint4_t w[RC];
+#pragma unroll
+            for (int rr = 0; rr < RC; ++rr) w[rr] = *(const uint4_t*)(a.ql + rbase[rr] + (uint64_t)a8 * 8);
+            put_q(a8, w);
+        }
+    } else {
+        for (uint32_t at = tid; at < A; at += NT)
+#pragma unroll
+            for (int rr = 0; rr < RC; ++rr)
+                qtab[at * RC + rr] =
+                    __builtin_bit_cast(_Float16, rok[rr] ? a.ql[rbase[rr] + (uint64_t)at * a.s_a] : (uint16_t)0);
+    }
+    auto put_ref = [&](uint32_t i, uint32_t ref) {
+        ref &= kRefMask;
+        if (ref >= a.cold_blocks) {
+            flag_error(a.err, kErrColdRef);
+            ref = ~0u;
+        }
+        sref[i] = ref;
+    };
+#pragma unroll
+    for (int j = 0; j < SR; ++j)
+        if (tid + (uint32_t)j * NT < n_blk) put_ref(tid + j * NT, srg[j]);
+    for (uint32_t i = tid + SR * NT; i < n_blk; i += NT) put_ref(i, grefs[i]);
+    for (uint32_t i = tid; i < A * NP; i += NT) bins[i] = 0ull;
+    __syncthreads(); // qtab, sref and bins ready
+
+    // Plan from the first NW tiles (the ring's slot 0 of every wave): per row the
+    // pair (max scaled score m, sum over tokens of 4*max|c|*2^(s - m)), combined
+    // over lanes and waves like log-sum-exp partials, plus max |c|.
+    float ref[RC];
+    int F = 0;
+    {
+        const uint32_t n_tiles = (t_end - t_begin + NT * CPT - 1) / (NT * CPT); // plan tiles of NT*CPT tokens
+        float scs[CPT][RC], cm[CPT];
+        float m[RC], w[RC], cmw = 0.0f;
+#pragma unroll
+        for (int rr = 0; rr < RC; ++rr) m[rr] = -INFINITY;
+#pragma unroll
+        for (int kk = 0; kk < CPT; ++kk) {
+            uint32_t ia[4];
+            uint32_t dummy = 0;
+            atoms(ring[0][kk], ia, dummy);
+            score(ring[0][kk], ia, scs[kk]);
+            cm[kk] = rv[0][kk] ? cmax_f(ring[0][kk]) : 0.0f;
+            cmw = fmaxf(cmw, cm[kk]);
+#pragma unroll
+            for (int rr = 0; rr < RC; ++rr) {
+                scs[kk][rr] *= sl;
+                if (rv[0][kk]) m[rr] = fmaxf(m[rr], scs[kk][rr]);
+            }
+        }
+#pragma unroll
+        for (int rr = 0; rr < RC; ++rr) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int kk = 0; kk < CPT; ++kk) acc += cm[kk] * fast_exp2(scs[kk][rr] - (rv[0][kk] ? m[rr] : scs[kk][rr]));
+            // Onto the wave's maximum.
+            const float mw = wave_max(m[rr]);
+            w[rr] = wave_sum(m[rr] == -INFINITY ? 0.0f : 4.0f * acc * fast_exp2(m[rr] - mw));
+            m[rr] = mw;
+        }
+        cmw = wave_max(cmw);
+        if (lane == 0) {
+#pragma unroll
+            for (int rr = 0; rr < RC; ++rr) {
+                red[wave * NR + 2 * rr] = m[rr];
+                red[wave * NR + 2 * rr + 1] = w[rr];
+            }
+            red[wave * NR + 2 * RC] = cmw;
+        }
+        __syncthreads();
+        float plan = 0.0f, cmax0 = 0.0f;
+#pragma unroll
+        for (int rr = 0; rr < RC; ++rr) {
+            float M = -INFINITY;
+            for (int v = 0; v < NW; ++v) M = fmaxf(M, red[v * NR + 2 * rr]);
+            ref[rr] = M == -INFINITY ? 0.0f : ceilf(M);
+            float L = 0.0f;
+            for (int v = 0; v < NW; ++v) {
+                const float mv = red[v * NR + 2 * rr];
+                L += mv == -INFINITY ? 0.0f : red[v * NR + 2 * rr + 1] * fast_exp2(mv - ref[rr]);
+            }
+            plan += L;
+        }
+        for (int v = 0; v < NW; ++v) cmax0 = fmaxf(cmax0, red[v * NR + 2 * RC]);
+        plan *= (float)n_tiles; // bound on sum |p*c| over the split, if tiles are alike
+        const int Fs = plan > 0.0f ? 28 - exp_of(plan) : 100;
+        const int Fm = cmax0 > 0.0f ? 18 - exp_of(cmax0) : 100; // p <= 1 in the first tile
+        F = min(100, max(-100, min(Fs, Fm)));
+    }
+
+    float lpart[RC];
+    uint32_t oob = 0;
+    bool exact = false;
+    for (int attempt = 0; attempt < 2; ++attempt) {
+        if (attempt) {
+            for (uint32_t i = tid; i < A * NP; i += NT) bins[i] = 0ull;
+#pragma unroll
+            for (int d = 0; d < PD; ++d) {
+                tl[d] = (uint32_t)(wave + d * NW);
+                load_tile(tl[d], ring[d], rv[d]);
+            }
+            __syncthreads(); // bins zeroed before any wave adds
+        }
+        // Stream the split into the bins.  Each slot, once consumed, is refilled
+        // with the wave's tile PD*NW further on; slot 0 always holds the wave's
+        // earliest tile, so once it is past the end the wave is done.
         const float Ff = (float)F;
         float rf[RC];
 #pragma unroll
@@ -819,65 +890,59 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
             rf[rr] = Ff - ref[rr];
         }
         uint32_t cmx_bits = 0;
-        pmx = 0.0f;
-        uint4_t ring[PD][CPT];
-        bool rv[PD][CPT];
-#pragma unroll
-        for (int kk = 0; kk < CPT; ++kk) {
-            ring[0][kk] = cur[kk];
-            rv[0][kk] = curv[kk];
-        }
-#pragma unroll
-        for (int d = 1; d < PD; ++d) load_tile(t_begin + d * tile_tokens, ring[d], rv[d]);
-        for (uint32_t t0 = t_begin; t0 < t_end; t0 += PD * tile_tokens) {
+        float pmx = 0.0f;
+        while (tl[0] < n_wt) {
 #pragma unroll
             for (int d = 0; d < PD; ++d) {
-                uint32_t rnext[CPT]; // refs of the tile PD ahead, read before this slot's atomics
-                tile_refs(t0 + (d + PD) * tile_tokens, rnext);
+                const uint32_t nt = tl[d] + (uint32_t)(PD * NW);
+                uint32_t rnext[CPT]; // refs of the slot's next tile, read before this slot's atomics
+                tile_refs(nt, rnext);
+                if (tl[d] < n_wt) { // uniform; no global loads inside
 #pragma unroll
-                for (int kk = 0; kk < CPT; ++kk) {
-                    const uint4_t cw = ring[d][kk];
-                    uint32_t ia[4];
-                    atoms(cw, ia, oob);
-                    float sc[RC];
-                    score(cw, ia, sc);
-                    cmx_bits = max(cmx_bits, cmax_bits(cw));
-                    float ps[RC]; // p * 2^F, zero for invalid tokens
+                    for (int kk = 0; kk < CPT; ++kk) {
+                        const uint4_t cw = ring[d][kk];
+                        uint32_t ia[4];
+                        atoms(cw, ia, oob);
+                        float sc[RC];
+                        score(cw, ia, sc);
+                        cmx_bits = max(cmx_bits, cmax_bits(cw));
+                        float ps[RC]; // p * 2^F, zero for invalid tokens
 #pragma unroll
-                    for (int rr = 0; rr < RC; ++rr) {
-                        const float p = fast_exp2(fmaf(sc[rr], sl, rf[rr]));
-                        ps[rr] = rv[d][kk] ? p : 0.0f;
-                        lpart[rr] += ps[rr];
-                    }
-                    if constexpr (RC == 4) pmx = fmaxf(pmx, fmaxf(fmaxf(ps[0], ps[1]), fmaxf(ps[2], ps[3])));
-                    else if constexpr (RC == 2) pmx = fmaxf(pmx, fmaxf(ps[0], ps[1]));
-                    else pmx = fmaxf(pmx, ps[0]);
+                        for (int rr = 0; rr < RC; ++rr) {
+                            const float p = fast_exp2(fmaf(sc[rr], sl, rf[rr]));
+                            ps[rr] = rv[d][kk] ? p : 0.0f;
+                            lpart[rr] += ps[rr];
+                        }
+                        if constexpr (RC == 4) pmx = fmaxf(pmx, fmaxf(fmaxf(ps[0], ps[1]), fmaxf(ps[2], ps[3])));
+                        else if constexpr (RC == 2) pmx = fmaxf(pmx, fmaxf(ps[0], ps[1]));
+                        else pmx = fmaxf(pmx, ps[0]);
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        uint64_t* bp = bins + ia[j] * NP;
-                        const float cj = (float)coef(cw, j);
+                        for (int j = 0; j < 4; ++j) {
+                            uint64_t* bp = bins + ia[j] * NP;
+                            const float cj = (float)coef(cw, j);
 #pragma unroll
-                        for (int pp = 0; pp < NP; ++pp) {
-                            const uint32_t b0 = __builtin_bit_cast(uint32_t, fmaf(ps[2 * pp], cj, kMagic));
-                            const uint32_t b1 = (2 * pp + 1 < RC)
-                                                    ? __builtin_bit_cast(uint32_t, fmaf(ps[min(2 * pp + 1, RC - 1)], cj, kMagic))
-                                                    : 0x4B400000u;
-                            const uint64_t wv = (((uint64_t)b1 << 32) | b0) - kMagic2;
-                            __hip_atomic_fetch_add(bp + pp, wv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                            for (int pp = 0; pp < NP; ++pp) {
+                                const uint32_t b0 = __builtin_bit_cast(uint32_t, fmaf(ps[2 * pp], cj, kMagic));
+                                const uint32_t b1 =
+                                    (2 * pp + 1 < RC) ? __builtin_bit_cast(uint32_t, fmaf(ps[min(2 * pp + 1, RC - 1)], cj, kMagic))
+                                                      : 0x4B400000u;
+                                const uint64_t wv = (((uint64_t)b1 << 32) | b0) - kMagic2;
+                                __hip_atomic_fetch_add(bp + pp, wv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                            }
                         }
                     }
                 }
-                // Refill this slot with the tile PD ahead.
-                tile_codes(t0 + (d + PD) * tile_tokens, rnext, ring[d], rv[d]);
+                tile_codes(nt, rnext, ring[d], rv[d]); // unconditional: past the end they read the zero code
+                tl[d] = nt;
             }
         }
-        cmx = (float)__builtin_bit_cast(_Float16, (uint16_t)cmx_bits);
+        const float cmx = (float)__builtin_bit_cast(_Float16, (uint16_t)cmx_bits);
         // Overflow proof: every |bin| <= sum over contributions |p*c|*2^F <= 4*max|c|*sum_r sum_t p*2^F,
         // and every contribution |p*c|*2^F <= max p*2^F * max|c| stays inside the rounding trick.
-        float v[NRED];
-        bool is_max[NRED];
+        float v[NB];
+        bool is_max[NB];
 #pragma unroll
-        for (int i = 0; i < NRED; ++i) {
+        for (int i = 0; i < NB; ++i) {
             v[i] = 0.0f;
             is_max[i] = false;
         }
@@ -904,8 +969,10 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
         float cm2 = 0.0f;
 #pragma unroll
         for (int rr = 0; rr < RC; ++rr) mx[rr] = -INFINITY;
-        for (uint32_t t0 = t_begin; t0 < t_end; t0 += tile_tokens) {
-            load_tile(t0, cur, curv);
+        for (uint32_t tile = wave; tile < n_wt; tile += NW) {
+            uint4_t cur[CPT];
+            bool curv[CPT];
+            load_tile(tile, cur, curv);
 #pragma unroll
             for (int kk = 0; kk < CPT; ++kk)
                 if (curv[kk]) {
@@ -918,10 +985,10 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
                     for (int rr = 0; rr < RC; ++rr) mx[rr] = fmaxf(mx[rr], sc[rr] * sl);
                 }
         }
-        float m2[NRED];
-        bool im2[NRED];
+        float m2[NB];
+        bool im2[NB];
 #pragma unroll
-        for (int i = 0; i < NRED; ++i) {
+        for (int i = 0; i < NB; ++i) {
             m2[i] = i < RC ? mx[i] : 0.0f;
             im2[i] = i < RC;
         }
@@ -931,8 +998,10 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
         float ebr[RC];
 #pragma unroll
         for (int rr = 0; rr < RC; ++rr) ebr[rr] = 0.0f;
-        for (uint32_t t0 = t_begin; t0 < t_end; t0 += tile_tokens) {
-            load_tile(t0, cur, curv);
+        for (uint32_t tile = wave; tile < n_wt; tile += NW) {
+            uint4_t cur[CPT];
+            bool curv[CPT];
+            load_tile(tile, cur, curv);
 #pragma unroll
             for (int kk = 0; kk < CPT; ++kk)
                 if (curv[kk]) {
@@ -944,13 +1013,13 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
                     float ca = 0.0f;
 #pragma unroll
                     for (int j = 0; j < 4; ++j) ca += fabsf((float)coef(cur[kk], j));
-                    cm2 = fmaxf(cm2, (float)__builtin_bit_cast(_Float16, (uint16_t)cmax_bits(cur[kk])));
+                    cm2 = fmaxf(cm2, cmax_f(cur[kk]));
 #pragma unroll
                     for (int rr = 0; rr < RC; ++rr) ebr[rr] += fast_exp2(sc[rr] * sl - ref[rr]) * ca;
                 }
         }
 #pragma unroll
-        for (int i = 0; i < NRED; ++i) {
+        for (int i = 0; i < NB; ++i) {
             m2[i] = i < RC ? ebr[i] : 0.0f;
             im2[i] = false;
         }
@@ -964,7 +1033,7 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
         const int Fs = eb > 0.0f ? 29 - exp_of(eb) : 100;
         const int Fm = m2[RC] > 0.0f ? 21 - exp_of(m2[RC]) : 100;
         F = min(100, max(-100, min(Fs, Fm)));
-        __syncthreads();
+        __syncthreads(); // every wave is done with the bins
     }
     // Atom indices outside the dictionary: recorded (their terms went to a clamped atom).
     {
@@ -995,10 +1064,10 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
             }
         }
     }
-    float v[NRED];
-    bool is_max[NRED];
+    float v[NB];
+    bool is_max[NB];
 #pragma unroll
-    for (int i = 0; i < NRED; ++i) {
+    for (int i = 0; i < NB; ++i) {
         v[i] = i < RC ? amax[i] : 0.0f;
         is_max[i] = true;
     }
@@ -1030,7 +1099,7 @@ inline size_t cold_smem_bytes(uint32_t A, int RC, uint32_t tokens_per_split) {
     const size_t qtab = ((size_t)A * RC * 2 + 15) & ~(size_t)15;
     const int NW = kColdThreads / 64, NP = (RC + 1) / 2;
     const size_t n_blk = ((size_t)(tokens_per_split + 15) / 16 + 3) & ~(size_t)3;
-    return qtab + (size_t)A * NP * 8 + n_blk * 4 + (size_t)NW * (RC + 2) * 4;
+    return qtab + (size_t)A * NP * 8 + n_blk * 4 + (size_t)NW * (2 * RC + 2) * 4;
 }
 
 // ----------------------------------------------- per-row merge factors

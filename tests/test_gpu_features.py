@@ -160,6 +160,24 @@ def full_size(engine, stream, geom, seed, n_rows, what):
     assert_close(got[torch.from_numpy(rows.astype(np.int64)).cuda()].cpu().numpy(), ref, what)
 
 
+def test_repeat_calls_bit_identical(engine, stream):
+    """The same inputs give the same output bits on every call (fixed
+    reduction orders; integer bins), also after other decodes ran in between."""
+    geom = W.sweep(16)
+    wl = W.generate(geom, seed=53, device="cuda:0")
+    outs = []
+    for i in range(3):
+        if i == 2:  # a different shape in between reuses the workspace
+            other = W.generate(W.hot_cold(hot_count=3, cold_count=40), seed=54, device="cuda:0")
+            o2 = torch.empty(other.out_shape(), dtype=torch.float16, device="cuda:0")
+            engine.decode_device(W.device_desc(other, o2), stream=stream)
+        out = torch.empty(wl.out_shape(), dtype=torch.float16, device="cuda:0")
+        engine.decode_device(W.device_desc(wl, out), stream=stream)
+        engine.check_device_errors(stream)
+        outs.append(out.view(torch.int16).cpu())
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+
+
 def test_full_size_sweep_b64(engine, stream):
     """hot 2048 + cold 32768 per kv head, B = 64: the benchmark shape."""
     full_size(engine, stream, W.sweep(64), 50, 12, "sweep B64 (sampled rows)")
