@@ -347,19 +347,24 @@ int launch_project(aw_engine* e, const aw_decode_desc* d, const Layout& o, char*
     a.dict_layer = (uint64_t)d->dict_heads * d->dict_size * HD;
     // Without q_latent to compute, one row block per atom block only writes D^T.
     const uint32_t rows = a.ql ? a.rows_per_group : 1;
-    StageTimer t(e, AW_STAGE_PROJECT, st);
-    const dim3 block(64);
     const uint32_t gz = d->layers * d->dict_heads;
-    if (rows <= 16) {
-        hipLaunchKernelGGL((aw::project_kernel<HD, 1, 4>), dim3(cdiv(d->dict_size, 64), cdiv(rows, 16), gz), block,
-                           0, st, a);
-    } else if (rows <= 32) {
-        hipLaunchKernelGGL((aw::project_kernel<HD, 2, 2>), dim3(cdiv(d->dict_size, 32), cdiv(rows, 32), gz), block,
-                           0, st, a);
-    } else {
-        hipLaunchKernelGGL((aw::project_kernel<HD, 4, 4>), dim3(cdiv(d->dict_size, 64), cdiv(rows, 64), gz), block,
-                           0, st, a);
-    }
+    const uint32_t A = d->dict_size;
+    StageTimer t(e, AW_STAGE_PROJECT, st);
+    const dim3 block(aw::kProjThreads);
+    // Tiles as large as keep >= one work-group per CU: fewer re-reads of D and q.
+    auto wgs = [&](uint32_t tr, uint32_t ta) { return (uint64_t)cdiv(A, ta) * cdiv(rows, tr) * gz; };
+#define AW_LAUNCH_PROJ(TR, TA, WR)                                                                              \
+    hipLaunchKernelGGL((aw::project_kernel<HD, TR, TA, WR>), dim3(cdiv(A, TA), cdiv(rows, TR), gz), block,      \
+                       aw::project_smem_bytes(HD, TR, TA), st, a)
+    if (rows <= 32)
+        AW_LAUNCH_PROJ(32, 64, 2);
+    else if (wgs(128, 256) >= e->n_cu)
+        AW_LAUNCH_PROJ(128, 256, 2);
+    else if (wgs(128, 128) >= e->n_cu)
+        AW_LAUNCH_PROJ(128, 128, 4);
+    else
+        AW_LAUNCH_PROJ(128, 64, 8);
+#undef AW_LAUNCH_PROJ
     AW_HIP(e, hipGetLastError());
     return AW_OK;
 }
@@ -807,7 +812,7 @@ int aw_engine_create(int device, aw_engine** out) {
                 e->hot_wpc[i] = (uint32_t)nb;
         }
     }
-    // Let the cold kernel use the device's full LDS.
+    // Let the cold, finish and projection kernels use the device's full LDS.
     {
         const void* fns[] = {(const void*)aw::cold_kernel<4, kColdCPT, kColdPD, true>,
                              (const void*)aw::cold_kernel<4, kColdCPT, kColdPD, false>,
@@ -820,6 +825,12 @@ int aw_engine_create(int device, aw_engine** out) {
         const void* fin[] = {(const void*)aw::finish_kernel<128, true>, (const void*)aw::finish_kernel<128, false>,
                              (const void*)aw::finish_kernel<64, true>, (const void*)aw::finish_kernel<64, false>};
         for (const void* f : fin)
+            (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)e->max_lds);
+        const void* proj[] = {(const void*)aw::project_kernel<128, 32, 64, 2>, (const void*)aw::project_kernel<128, 128, 256, 2>,
+                              (const void*)aw::project_kernel<128, 128, 128, 4>, (const void*)aw::project_kernel<128, 128, 64, 8>,
+                              (const void*)aw::project_kernel<64, 32, 64, 2>, (const void*)aw::project_kernel<64, 128, 256, 2>,
+                              (const void*)aw::project_kernel<64, 128, 128, 4>, (const void*)aw::project_kernel<64, 128, 64, 8>};
+        for (const void* f : proj)
             (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)e->max_lds);
     }
     if (hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking) != hipSuccess ||

@@ -183,114 +183,140 @@ struct MergeArgs {
 
 // ------------------------------------------------------------ q . D^T (MFMA)
 //
-// Computes q_latent^T = D q^T so that each lane ends up with four consecutive
-// atoms of one query row and stores them with one 8-byte write into
+// q_latent[row][atom] = q[row] . D[atom] over K = HD, written f16 into
 // q_latent [L][B][Q][Hq][A] (the layout of the reference's q_latent buffer,
-// weaver_kernel.metal:111).  One wave computes (16*NA atoms) x (16*MR rows),
-// K = HD.  Operand layouts of v_mfma_f32_16x16x32_f16 (lane l, li = l%16,
-// lg = l/16):
-//   A[i][k]: lane holds row i = li, k = 8*lg .. 8*lg+7  -> 16 bytes of dictionary row (atom li)
-//   B[k][j]: lane holds col j = li, k = 8*lg .. 8*lg+7  -> 16 bytes of query row li
-//   C[i][j]: lane holds rows i = 4*lg .. 4*lg+3, col j = li -> 4 atoms of query row li
-// Rows of one group share one dictionary: group = (layer, dict head); inside a
-// group row i enumerates (b, q, head) with head over Hq (shared dictionary) or
-// over the G heads of kv head dg (per-kv-head dictionary).
+// weaver_kernel.metal:111).  Rows of one group share one dictionary: group =
+// (layer, dict head); inside a group row i enumerates (b, q, head) with head
+// over Hq (shared dictionary) or over the G heads of kv head dg (per-kv-head
+// dictionary).
 //
-// The waves of the first row block also write their 16*NA atoms of D^T
-// ([HD][A], through LDS): the finish contracts over atoms, and MFMA operands
-// want the contracted index contiguous in each lane.
-template <int HD, int MR, int NA>
-__global__ __launch_bounds__(64) void project_kernel(ProjArgs a) {
-    constexpr int KS = HD / 32, TP = HD + 8; // LDS pitch of the transpose, halves
-    __shared__ __attribute__((aligned(16))) _Float16 st[16 * NA * TP];
-    const int lane = threadIdx.x, li = lane & 15, lg = lane >> 4;
+// Work-group = TR rows x TA atoms, 8 waves.  The q rows and dictionary atoms
+// of the tile are staged once in LDS (16-byte coalesced loads, all issued
+// before any is stored), so the dictionary is read from L2 once per TR rows and
+// q once per TA atoms.  Waves form a WR x WA grid; each computes MT x NT tiles
+// of 16 x 16 with v_mfma_f32_16x16x32_f16 (lane l, li = l%16, lg = l/16):
+//   A[i][k]: atom li of the tile, k = 8*lg .. 8*lg+7  (one 16-byte LDS read)
+//   B[k][j]: row li of the tile, the same k               (one 16-byte LDS read)
+//   C[i][j]: atoms 4*lg .. 4*lg+3, row li.
+// The f16 results go through LDS (the staging area, free once every wave has
+// its operands) so q_latent is written in 16-byte pieces of whole rows.
+// Every work-group also writes D^T ([HD][dt_pitch], f16) for its atoms and a
+// share of the dims (the row blocks split HD) from the staged tile: the finish
+// contracts over atoms, and MFMA operands want the contracted index contiguous
+// in each lane.
+constexpr int kProjThreads = 512;
+constexpr int kProjPitch(int HD) { return HD + 8; } // halves per staged row: 16 rows of a read hit distinct banks
+
+// Staged q and dictionary tiles, reused afterwards for the f16 output tile.
+inline size_t project_smem_bytes(int HD, int TR, int TA) {
+    const size_t in = (size_t)(TR + TA) * kProjPitch(HD) * 2, out = (size_t)TR * (TA + 8) * 2;
+    return in > out ? in : out;
+}
+
+template <int HD, int TR, int TA, int WR>
+__global__ __launch_bounds__(kProjThreads) void project_kernel(ProjArgs a) {
+    constexpr int NW = kProjThreads / 64, P = kProjPitch(HD), KS = HD / 32, PR = HD / 8; // 16-byte pieces per row
+    constexpr int WA = NW / WR;
+    constexpr int MT = TR / WR / 16, NT = TA / WA / 16;
+    static_assert(MT >= 1 && NT >= 1 && MT * WR * 16 == TR && NT * WA * 16 == TA, "tile shape");
+    constexpr int PIECES = (TR + TA) * PR, PT = (PIECES + kProjThreads - 1) / kProjThreads;
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    _Float16* sq = (_Float16*)smem; // [TR][P] query rows
+    _Float16* sd = sq + TR * P;     // [TA][P] dictionary atoms
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, li = lane & 15, lg = lane >> 4;
     const uint32_t group = blockIdx.z;
     const uint32_t l = group / a.dict_heads, dg = group % a.dict_heads;
-    const uint32_t atom0 = blockIdx.x * 16 * NA, row0 = blockIdx.y * 16 * MR;
-    const uint64_t dgoff = l * a.dict_layer + (uint64_t)dg * a.dict_size * HD;
-    const uint16_t* dict = a.dict + dgoff;
+    const uint32_t atom0 = blockIdx.x * TA, row0 = blockIdx.y * TR;
+    const uint32_t A = a.dict_size;
+    const uint16_t* dict = a.dict + l * a.dict_layer + (uint64_t)dg * A * HD;
     const bool shared = a.dict_heads == 1;
-    const bool transpose = blockIdx.y == 0;
+    // Global q / q_latent row of group row i (clamped into the group).
+    auto qrow_of = [&](uint32_t i) -> uint64_t {
+        i = min(i, a.rows_per_group - 1u);
+        if (shared) return (uint64_t)l * a.rows_per_group + i; // rows of a layer are (b, q, h) in q's order
+        const uint32_t bq = i / a.gqa, hh = i % a.gqa;         // (b, q, head hh of kv head dg)
+        return ((uint64_t)l * a.batch * a.queries + bq) * a.q_heads + dg * a.gqa + hh;
+    };
 
-    // This lane's query rows (one per row block): global row index into q / q_latent.
-    // All loads are issued up front and unconditionally (clamped rows / atoms);
-    // rows and atoms out of range are zeroed after.
-    uint64_t qrow[MR];
-    bool rok[MR];
+    // Stage the tile: every load first (clamped rows and atoms), then every store.
+    {
+        uint4_t v[PT];
 #pragma unroll
-    for (int mr = 0; mr < MR; ++mr) {
-        const uint32_t i0 = row0 + 16 * mr + li;
-        rok[mr] = a.ql != nullptr && i0 < a.rows_per_group;
-        const uint32_t i = a.rows_per_group ? min(i0, a.rows_per_group - 1u) : 0u;
-        if (shared) {
-            qrow[mr] = (uint64_t)l * a.rows_per_group + i; // rows of a layer are (b, q, h) in q's order
-        } else {                                           // (b, q, head hh of kv head dg)
-            const uint32_t bq = i / a.gqa, hh = i % a.gqa;
-            qrow[mr] = ((uint64_t)l * a.batch * a.queries + bq) * a.q_heads + dg * a.gqa + hh;
+        for (int k = 0; k < PT; ++k) {
+            const int p = min(tid + k * kProjThreads, PIECES - 1);
+            const int r = p / PR, c = p % PR;
+            const uint16_t* src = r < TR ? a.q + qrow_of(row0 + r) * HD : dict + (uint64_t)min(atom0 + (uint32_t)(r - TR), A - 1u) * HD;
+            v[k] = *(const uint4_t*)(src + 8 * c);
+        }
+#pragma unroll
+        for (int k = 0; k < PT; ++k) {
+            const int p = tid + k * kProjThreads;
+            if (p < PIECES) *(uint4_t*)(sq + (p / PR) * P + 8 * (p % PR)) = v[k]; // sd follows sq
         }
     }
-    half8_t bop[MR][KS], aop[NA][KS];
+    __syncthreads();
+
+    const int wr = wave / WA, wa = wave % WA;
+    float4_t acc[MT][NT];
+    if (a.ql != nullptr) {
+        half8_t aop[NT][KS];
 #pragma unroll
-    for (int na = 0; na < NA; ++na) {
-        const uint32_t at = min(atom0 + 16 * na + li, a.dict_size - 1u);
+        for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-        for (int j = 0; j < KS; ++j) aop[na][j] = as_h8(*(const uint4_t*)(dict + (uint64_t)at * HD + 32 * j + 8 * lg));
+            for (int j = 0; j < KS; ++j)
+                aop[nt][j] = *(const half8_t*)(sd + (wa * (TA / WA) + nt * 16 + li) * P + 32 * j + 8 * lg);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            half8_t bop[KS];
+#pragma unroll
+            for (int j = 0; j < KS; ++j) bop[j] = *(const half8_t*)(sq + (wr * (TR / WR) + mt * 16 + li) * P + 32 * j + 8 * lg);
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                acc[mt][nt] = (float4_t)0.0f;
+#pragma unroll
+                for (int j = 0; j < KS; ++j) acc[mt][nt] = mfma16x16x32(aop[nt][j], bop[j], acc[mt][nt]);
+            }
+        }
+    }
+    {
+        // D^T of the tile's atoms, the dims split over the row blocks: pieces of 8
+        // atoms, piece p = (atom group p / nd, dim d0 + p % nd).
+        const uint32_t nrb = gridDim.y, y = blockIdx.y;
+        const int d0 = (int)((y * (uint32_t)HD) / nrb), nd = (int)(((y + 1) * (uint32_t)HD) / nrb) - d0;
+        const int TP = nd * (TA / 8);
+        uint16_t* dt = a.dt + (uint64_t)group * HD * a.dt_pitch;
+        for (int p = tid; p < TP; p += kProjThreads) {
+            const int d = d0 + p % nd, ag = p / nd;
+            const uint32_t at = atom0 + 8 * ag;
+            if (at >= A) continue;
+            uint32_t w[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                w[e] = (uint32_t)__builtin_bit_cast(uint16_t, sd[(8 * ag + 2 * e) * P + d]) |
+                       ((uint32_t)__builtin_bit_cast(uint16_t, sd[(8 * ag + 2 * e + 1) * P + d]) << 16);
+            *(uint4_t*)(dt + (uint64_t)d * a.dt_pitch + at) = (uint4_t){w[0], w[1], w[2], w[3]};
+        }
     }
     if (a.ql != nullptr) {
+        constexpr int OP = TA + 8; // halves per staged output row
+        __syncthreads(); // every wave is done with the staged q and dictionary
+        _Float16* so = sq;
 #pragma unroll
-        for (int mr = 0; mr < MR; ++mr)
+        for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-            for (int j = 0; j < KS; ++j) bop[mr][j] = as_h8(*(const uint4_t*)(a.q + qrow[mr] * HD + 32 * j + 8 * lg));
-    }
+            for (int nt = 0; nt < NT; ++nt) {
+                half4_t h;
 #pragma unroll
-    for (int na = 0; na < NA; ++na)
-        if (atom0 + 16 * na + li >= a.dict_size)
-#pragma unroll
-            for (int j = 0; j < KS; ++j) aop[na][j] = (half8_t)(_Float16)0;
-#pragma unroll
-    for (int na = 0; na < NA; ++na) {
-        if (transpose) {
-#pragma unroll
-            for (int j = 0; j < KS; ++j) {
-                const uint4_t w = __builtin_bit_cast(uint4_t, aop[na][j]);
-                _Float16* dst = st + (16 * na + li) * TP + 32 * j + 8 * lg;
-                *(uint2_t*)dst = (uint2_t){w[0], w[1]};
-                *(uint2_t*)(dst + 4) = (uint2_t){w[2], w[3]};
+                for (int e = 0; e < 4; ++e) h[e] = (_Float16)acc[mt][nt][e];
+                *(half4_t*)(so + (wr * (TR / WR) + mt * 16 + li) * OP + wa * (TA / WA) + nt * 16 + 4 * lg) = h;
             }
-        }
-        if (a.ql == nullptr) continue;
-        const uint32_t ao = atom0 + 16 * na + 4 * lg; // this lane's 4 output atoms
-#pragma unroll
-        for (int mr = 0; mr < MR; ++mr) {
-            float4_t acc = (float4_t)0.0f;
-#pragma unroll
-            for (int j = 0; j < KS; ++j) acc = mfma16x16x32(aop[na][j], bop[mr][j], acc);
-            if (rok[mr] && ao < a.dict_size) { // dict_size % 16 == 0: all four atoms are in range
-                half4_t v;
-                v[0] = (_Float16)acc[0];
-                v[1] = (_Float16)acc[1];
-                v[2] = (_Float16)acc[2];
-                v[3] = (_Float16)acc[3];
-                *(half4_t*)(a.ql + qrow[mr] * a.dict_size + ao) = v;
-            }
-        }
-    }
-    if (transpose) {
-        // D^T pieces of 8 atoms: piece p = (dim p / (2*NA), atom group p % (2*NA)).
         __syncthreads();
-        constexpr int GROUPS = 2 * NA, PIECES = HD * GROUPS;
-        uint16_t* dt = a.dt + (uint64_t)group * HD * a.dt_pitch;
-        for (int p = lane; p < PIECES; p += 64) {
-            const int d = p / GROUPS, ag = p % GROUPS;
-            const uint32_t at = atom0 + 8 * ag;
-            if (at >= a.dict_size) continue;
-            uint16_t h[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) h[e] = __builtin_bit_cast(uint16_t, st[(8 * ag + e) * TP + d]);
-            uint4_t v;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = (uint32_t)h[2 * e] | ((uint32_t)h[2 * e + 1] << 16);
-            *(uint4_t*)(dt + (uint64_t)d * a.dt_pitch + at) = v;
+        constexpr int OPR = TA / 8, OPIECES = TR * OPR; // 16-byte pieces per row / tile
+        for (int p = tid; p < OPIECES; p += kProjThreads) {
+            const int r = p / OPR, c = p % OPR;
+            const uint32_t i = row0 + r, ao = atom0 + 8 * c;
+            if (i < a.rows_per_group && ao < A)
+                *(uint4_t*)(a.ql + qrow_of(i) * A + ao) = *(const uint4_t*)(so + r * OP + 8 * c);
         }
     }
 }
