@@ -32,6 +32,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace aw {
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
@@ -1174,33 +1176,37 @@ __device__ inline float merge_value(float oh, float Mh, float Lh, float oc, floa
 // ------------------------------------------------------ bins . D (MFMA)
 //
 // Work-group = 128 rows sharing one dictionary (8 waves x 16 rows) x one atom
-// range.  The D^T chunk of 32 atoms x HD dims (written by the projection as
-// [HD][A]) is staged once per work-group in LDS and shared by the 8 waves, so
-// D^T is read from L2 once per 128 rows.  Per wave: O^T[dim][row] += D^T W^T,
+// range, walked in super-chunks of 64 atoms.  A super-chunk's D^T (64 atoms x
+// HD dims, written by the projection as [HD][A]) is staged once in LDS and
+// shared by the 8 waves, so D^T is read from L2 once per 128 rows.  Per wave:
+// O^T[dim][row] += D^T W^T in sub-chunks of 32 atoms,
 //   A = D^T (lane: dim 16*nb+li, atoms 8*lg .. +7: one 16-byte LDS read),
-//   B = W^T (lane: row li, the same 8 atoms: two 16-byte loads per cold split,
-//       combined with the split factors), split into hi + lo f16 terms -> two
-//       MFMAs per dim block.
-// D^T pieces are prefetched two chunks ahead in registers and the LDS chunk is
-// double-buffered (one barrier per chunk); the W loads (the HBM stream) run two
-// chunks ahead in a register ring (SINGLE: one cold split; otherwise the
-// splits' W are combined per chunk).  Each wave finishes its own rows: with one
-// atom range the log-sum-exp merge runs here, otherwise the partial cold
-// outputs go to `ocp` for merge_kernel.
+//   B = W^T (lane: row li, the same 8 atoms), split into hi + lo f16 terms ->
+//       two MFMAs per dim block.
+// Pipelining, one barrier per super-chunk: the bins W of super-chunk s+1 load
+// into the second of two register sets while s is computed (SINGLE: one cold
+// split; with several splits each super-chunk's splits are loaded and combined
+// at its start), and the D^T pieces of s+1, loaded one super-chunk ahead into
+// registers, go to the other LDS buffer after s's MFMAs.  The first loads are
+// issued before the per-row split factors are worked out.  Each wave finishes
+// its own rows: with one atom range the log-sum-exp merge runs here, otherwise
+// the partial cold outputs go to `ocp` for merge_kernel.
 constexpr int kFinishWaves = 8;
 constexpr int kFinishRows = 16 * kFinishWaves;
-constexpr int kFinishPitch = 40; // halves per staged D^T row (32 atoms + 8)
+constexpr int kFinishSC = 64;                  // atoms per super-chunk
+constexpr int kFinishPitch = kFinishSC + 8;    // halves per staged D^T row
 
 // Dynamic LDS of finish_kernel: D^T double buffer, per-row split factors for
-// `sf` splits (cold and, when fused, hot), row factors and row ids.
+// `sf` splits (cold and, when fused, hot), row factors.
 inline size_t finish_smem_bytes(int HD, uint32_t sf) {
-    return (size_t)2 * HD * kFinishPitch * 2 + (size_t)2 * kFinishRows * sf * 4 + (size_t)kFinishRows * 8 +
-           (size_t)kFinishRows * 5 * 4;
+    return (size_t)2 * HD * kFinishPitch * 2 + (size_t)2 * kFinishRows * sf * 4 + (size_t)kFinishRows * 5 * 4;
 }
 
 template <int HD, bool SINGLE>
 __global__ __launch_bounds__(kFinishWaves * 64) void finish_kernel(FinishArgs a) {
-    constexpr int NB = HD / 16, DP = kFinishPitch, PIECES = HD * 4; // 16-byte pieces per chunk
+    constexpr int NB = HD / 16, DP = kFinishPitch, NS = kFinishSC / 32; // sub-chunks per super-chunk
+    constexpr int GP = kFinishSC / 8, PIECES = HD * GP, PPT = PIECES / (kFinishWaves * 64); // 16-byte D^T pieces
+    static_assert(PIECES % (kFinishWaves * 64) == 0, "D^T pieces per thread");
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, li = lane & 15, lg = lane >> 4;
     const uint32_t group = blockIdx.x / a.tiles_per_group, tile = blockIdx.x % a.tiles_per_group;
@@ -1210,11 +1216,71 @@ __global__ __launch_bounds__(kFinishWaves * 64) void finish_kernel(FinishArgs a)
     const bool fused = a.n_ar == 1 && a.hot_splits > 0;
     const uint32_t sneed = max(a.cold_splits, fused ? a.hot_splits : 1u);
     const uint32_t lpr = sneed <= 1 ? 1u : 1u << (32 - __builtin_clz(sneed - 1u)); // factors per row
-    _Float16* sd = (_Float16*)smem;                                   // [2][HD][DP]
-    float* s_cfac = (float*)(smem + (size_t)2 * HD * DP * 2);         // [ROWS][lpr]
-    float* s_hfac = s_cfac + (size_t)kFinishRows * lpr;               // [ROWS][lpr]
-    uint64_t* s_row = (uint64_t*)(s_hfac + (size_t)kFinishRows * lpr); // [ROWS]
-    float* s_rf = (float*)(s_row + kFinishRows);                      // [ROWS][5]: Mc, Lc, inv_scl, Mh, Lh
+    _Float16* sd = (_Float16*)smem;                           // [2][HD][DP]
+    float* s_cfac = (float*)(smem + (size_t)2 * HD * DP * 2); // [ROWS][lpr]
+    float* s_hfac = s_cfac + (size_t)kFinishRows * lpr;       // [ROWS][lpr]
+    float* s_rf = s_hfac + (size_t)kFinishRows * lpr;         // [ROWS][5]: Mc, Lc, inv_scl, Mh, Lh
+
+    // Row (lbg, r) of group row `row` (clamped into the group).
+    auto row_id = [&](uint32_t row, uint64_t& lbg, uint32_t& r) {
+        row = min(row, a.rows_per_group - 1u);
+        if (a.dict_heads == 1) lbg = (uint64_t)l * a.batch * a.kv_heads + row / R; // row = (b*Hkv + g)*R + r
+        else lbg = ((uint64_t)l * a.batch + row / R) * a.kv_heads + dg;            // row = b*R + r
+        r = row % R;
+    };
+    // This lane's B-operand row.
+    const uint32_t my_raw = tile * kFinishRows + wave * 16 + li;
+    const bool rowok = my_raw < a.rows_per_group;
+    uint64_t lbg_me;
+    uint32_t r_me;
+    row_id(my_raw, lbg_me, r_me);
+    const int myr = wave * 16 + li;
+    const float* wbase = a.cold_w + ((lbg_me * a.cold_splits) * R + r_me) * a.w_pitch;
+    const uint64_t wsplit = (uint64_t)R * a.w_pitch;
+
+    const uint16_t* dt = a.dt + (uint64_t)group * HD * a.dt_pitch;
+    const uint32_t a_begin = ar * a.atoms_per_range;
+    const uint32_t a_end = min(a_begin + a.atoms_per_range, A);
+    const uint32_t n_sc = (a_end - a_begin + kFinishSC - 1) / kFinishSC;
+
+    // Loads past the range (the prefetch beyond the last super-chunk, the tail of a
+    // partial one) are clamped to its last 8 atoms: lines already read, never the
+    // next range's bins.
+    const uint32_t a_last = a_end - 8u;
+    // D^T pieces of super-chunk s: piece p = (dim p / GP, atoms 8*(p%GP) .. +7).
+    auto load_dt = [&](uint32_t s, uint4_t (&v)[PPT]) {
+#pragma unroll
+        for (int q = 0; q < PPT; ++q) {
+            const int p = tid + q * kFinishWaves * 64;
+            const uint32_t at = min(a_begin + kFinishSC * s + 8 * (p % GP), a_last);
+            v[q] = *(const uint4_t*)(dt + (uint64_t)(p / GP) * a.dt_pitch + at);
+        }
+    };
+    auto store_dt = [&](int buf, const uint4_t (&v)[PPT]) {
+#pragma unroll
+        for (int q = 0; q < PPT; ++q) {
+            const int p = tid + q * kFinishWaves * 64;
+            *(uint4_t*)(sd + ((size_t)buf * HD + p / GP) * DP + 8 * (p % GP)) = v[q];
+        }
+    };
+    // Single-split W of super-chunk s: this lane's row, atoms 32*k + 8*lg .. +7 of each sub-chunk k.
+    auto load_w = [&](uint32_t s, float4_t (&w)[2 * NS]) {
+#pragma unroll
+        for (int k = 0; k < NS; ++k) {
+            const uint32_t at = min(a_begin + kFinishSC * s + 32 * k + 8 * lg, a_last);
+            w[2 * k] = *(const float4_t*)(wbase + at);
+            w[2 * k + 1] = *(const float4_t*)(wbase + at + 4);
+        }
+    };
+
+    // First loads, oldest first: D^T of super-chunk 0, its W (SINGLE), then D^T of 1 and W of 1.
+    uint4_t dpre[PPT];
+    float4_t wA[2 * NS], wB[2 * NS];
+    load_dt(0, dpre);
+    if constexpr (SINGLE) load_w(0, wA);
+    uint4_t d1[PPT];
+    load_dt(1, d1);
+    if constexpr (SINGLE) load_w(1, wB);
 
     // Split factors of this wave's 16 rows: lanes form segments of lpr lanes (lane
     // in segment = split), one row per segment, 64/lpr rows per pass; all loads of
@@ -1228,11 +1294,9 @@ __global__ __launch_bounds__(kFinishWaves * 64) void finish_kernel(FinishArgs a)
             const uint32_t i = i0 + seg; // row of this wave handled by this segment
             const uint32_t row_raw = tile * kFinishRows + wave * 16 + i;
             const bool rv = i < 16u && row_raw < a.rows_per_group;
-            const uint32_t row = min(row_raw, a.rows_per_group - 1u);
             uint64_t lbg;
-            if (a.dict_heads == 1) lbg = (uint64_t)l * a.batch * a.kv_heads + row / R; // row = (b*Hkv + g)*R + r
-            else lbg = ((uint64_t)l * a.batch + row / R) * a.kv_heads + dg;            // row = b*R + r
-            const uint32_t r = row % R;
+            uint32_t r;
+            row_id(row_raw, lbg, r);
             const uint32_t cs = min(sp, a.cold_splits - 1u);
             const uint64_t cb = (lbg * a.cold_splits + cs) * R + r;
             float cm = a.cold_m[cb], cl = a.cold_l[cb], ca = a.cold_amax[cb];
@@ -1255,7 +1319,6 @@ __global__ __launch_bounds__(kFinishWaves * 64) void finish_kernel(FinishArgs a)
                 s_cfac[srow * lpr + sp] = Lc > 0.0f ? f / Lc * scl : 0.0f;
                 s_hfac[srow * lpr + sp] = fh;
                 if (sp == 0) {
-                    s_row[srow] = rv ? lbg * R + r : ~0ull;
                     float* rf = s_rf + srow * 5;
                     rf[0] = Mc;
                     rf[1] = Lc;
@@ -1266,137 +1329,122 @@ __global__ __launch_bounds__(kFinishWaves * 64) void finish_kernel(FinishArgs a)
             }
         }
     }
-    __builtin_amdgcn_wave_barrier();
+    store_dt(0, dpre);
+    __syncthreads(); // factors and D^T of super-chunk 0 visible
 
-    const uint16_t* dt = a.dt + (uint64_t)group * HD * a.dt_pitch;
-    const uint32_t a_begin = ar * a.atoms_per_range;
-    const uint32_t a_end = min(a_begin + a.atoms_per_range, A);
-    const uint32_t n_ch = (a_end - a_begin + 31) / 32;
-
-    const int myr = wave * 16 + li; // this lane's B-operand row
-    const uint64_t myrow = s_row[myr];
-    const bool rowok = myrow != ~0ull;
-    const uint64_t lbg_me = rowok ? myrow / R : 0, r_me = rowok ? myrow % R : 0;
-    const float* wbase = a.cold_w + ((lbg_me * a.cold_splits) * R + r_me) * a.w_pitch;
-    const uint64_t wsplit = (uint64_t)R * a.w_pitch;
     const float f0 = rowok ? s_cfac[myr * lpr] : 0.0f;
     const bool wok = rowok && f0 != 0.0f; // an empty split wrote no bins: never read them
-
-    // This thread's 16-byte piece of a D^T chunk: dim p/4, atoms 8*(p%4) .. +7 (clamped).
-    auto load_piece = [&](uint32_t c, int p) -> uint4_t {
-        const uint32_t at = min(a_begin + 32 * c + 8 * (p & 3), A - 8u);
-        return *(const uint4_t*)(dt + (uint64_t)(p >> 2) * a.dt_pitch + at);
-    };
-    auto store_piece = [&](int buf, int p, uint4_t v) {
-        _Float16* dst = sd + ((size_t)buf * HD + (p >> 2)) * DP + 8 * (p & 3);
-        *(uint4_t*)dst = v;
-    };
-    // Single-split W of chunk c: this lane's row, atoms 8*lg .. +7 (clamped; masked at use).
-    auto load_w = [&](uint32_t c, float4_t& w0, float4_t& w1) {
-        const uint32_t at = min(a_begin + 32 * c + 8 * lg, A - 8u);
-        w0 = *(const float4_t*)(wbase + at);
-        w1 = *(const float4_t*)(wbase + at + 4);
-    };
-
-    constexpr int PPT = (PIECES + kFinishWaves * 64 - 1) / (kFinishWaves * 64); // pieces per thread (1)
-    uint4_t pre[2][PPT];
-#pragma unroll
-    for (int q = 0; q < PPT; ++q) {
-        const int p = tid + q * kFinishWaves * 64;
-        if (p < PIECES) {
-            store_piece(0, p, load_piece(0, p));
-            pre[1][q] = load_piece(1, p);
-        }
-    }
-    float4_t wr0[2], wr1[2];
-    if constexpr (SINGLE) {
-        load_w(0, wr0[0], wr1[0]);
-        load_w(1, wr0[1], wr1[1]);
-    }
-    __syncthreads();
-
     float4_t acc[NB];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) acc[nb] = (float4_t)0.0f;
 
-    for (uint32_t ch = 0; ch < n_ch; ch += 2) {
-#pragma unroll
-        for (int s = 0; s < 2; ++s) { // chunk c = ch + s uses LDS buffer s and register slots s
-            const uint32_t c = ch + s;
-            if (c >= n_ch) break;
-            // Prefetch the D^T pieces of chunk c + 2 (slot s held chunk c, already in LDS).
-#pragma unroll
-            for (int q = 0; q < PPT; ++q) {
-                const int p = tid + q * kFinishWaves * 64;
-                if (p < PIECES) pre[s][q] = load_piece(c + 2, p);
-            }
-            const uint32_t a0 = a_begin + 32 * c;
-            const bool in = a0 + 8 * lg < a_end; // this lane's 8 atoms are in the range
-            float w8[8];
-            if constexpr (SINGLE) {
-                const bool use = wok && in; // empty splits wrote no bins: never use them
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    w8[e] = use ? f0 * wr0[s][e] : 0.0f;
-                    w8[4 + e] = use ? f0 * wr1[s][e] : 0.0f;
-                }
-                load_w(c + 2, wr0[s], wr1[s]); // refill this slot two chunks ahead (clamped)
-            } else {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) w8[e] = 0.0f;
-                const uint32_t at = min(a0 + 8 * lg, A - 8u);
-                // Four splits' loads in flight at a time (clamped split index); splits with
-                // factor 0 (empty) are masked at use.
-                for (uint32_t s0 = 0; s0 < a.cold_splits; s0 += 4) {
-                    float4_t v0[4], v1[4];
-                    float fs[4];
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const uint32_t sp = min(s0 + j, a.cold_splits - 1u);
-                        const float* wrow = wbase + sp * wsplit + at;
-                        v0[j] = *(const float4_t*)wrow;
-                        v1[j] = *(const float4_t*)(wrow + 4);
-                        fs[j] = rowok && in && s0 + j < a.cold_splits ? s_cfac[myr * lpr + s0 + j] : 0.0f;
-                    }
-#pragma unroll
-                    for (int j = 0; j < 4; ++j)
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            w8[e] += fs[j] != 0.0f ? fs[j] * v0[j][e] : 0.0f;
-                            w8[4 + e] += fs[j] != 0.0f ? fs[j] * v1[j][e] : 0.0f;
-                        }
-                }
-            }
-            half8_t hi, lo;
+    // One super-chunk: MFMAs from LDS buffer s&1 and W (SINGLE: registers w, then refilled
+    // with super-chunk s+2); D^T of s+1 (registers dn) into the other buffer, then the
+    // loads of D^T s+2 into dn; one barrier.
+    auto step = [&](uint32_t s, float4_t (&w)[2 * NS], uint4_t (&dn)[PPT], auto last) {
+        const int buf = (int)(s & 1u);
+        const uint32_t a0 = a_begin + kFinishSC * s;
+        // B operands of the NS sub-chunks, hi + lo f16 terms; atoms past the range
+        // (and rows without bins) are zero.
+        half8_t his[NS], los[NS];
+        auto split = [&](int k, const float (&x8)[8], bool rows_ok) {
+            const bool in = a0 + 32 * k + 8 * lg < a_end && rows_ok; // this lane's 8 atoms count
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                hi[e] = (_Float16)w8[e];
-                lo[e] = (_Float16)(w8[e] - (float)hi[e]);
+                const float x = in ? x8[e] : 0.0f;
+                his[k][e] = (_Float16)x;
+                los[k][e] = (_Float16)(x - (float)his[k][e]);
             }
-            const bool partial = a0 + 32 > a_end; // uniform: atoms past the range get a zero operand
+        };
+        if constexpr (SINGLE) {
+#pragma unroll
+            for (int k = 0; k < NS; ++k) {
+                float x8[8];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    x8[e] = f0 * w[2 * k][e];
+                    x8[4 + e] = f0 * w[2 * k + 1][e];
+                }
+                split(k, x8, wok);
+            }
+            // Refill two super-chunks ahead (clamped), below every read of w: loads
+            // hoisted above them would need fresh registers and a copy, which waits.
+            __builtin_amdgcn_sched_barrier(0);
+            load_w(s + 2, w);
+        } else {
+            float w8s[NS][8];
+#pragma unroll
+            for (int k = 0; k < NS; ++k)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) w8s[k][e] = 0.0f;
+            // Four splits' loads in flight at a time (clamped split index); splits with
+            // factor 0 (empty) are masked at use.
+            for (uint32_t s0 = 0; s0 < a.cold_splits; s0 += 4) {
+                float fs[4];
+                float4_t v[4][2 * NS];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t sp = min(s0 + j, a.cold_splits - 1u);
+                    const float* wrow = wbase + sp * wsplit;
+#pragma unroll
+                    for (int k = 0; k < NS; ++k) {
+                        const uint32_t at = min(a0 + 32 * k + 8 * lg, a_last);
+                        v[j][2 * k] = *(const float4_t*)(wrow + at);
+                        v[j][2 * k + 1] = *(const float4_t*)(wrow + at + 4);
+                    }
+                    fs[j] = rowok && s0 + j < a.cold_splits ? s_cfac[myr * lpr + s0 + j] : 0.0f;
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int k = 0; k < NS; ++k)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            w8s[k][e] += fs[j] != 0.0f ? fs[j] * v[j][2 * k][e] : 0.0f;
+                            w8s[k][4 + e] += fs[j] != 0.0f ? fs[j] * v[j][2 * k + 1][e] : 0.0f;
+                        }
+            }
+#pragma unroll
+            for (int k = 0; k < NS; ++k) split(k, w8s[k], rowok);
+        }
+        // Sub-chunks past the range run with zero operands: no branch here, so nothing
+        // above sinks below the refill.
+#pragma unroll
+        for (int k = 0; k < NS; ++k) {
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) {
-                uint4_t dv = *(const uint4_t*)(sd + ((size_t)s * HD + 16 * nb + li) * DP + 8 * lg);
-                if (partial && !in) dv = (uint4_t)0u;
-                acc[nb] = mfma16x16x32(as_h8(dv), hi, acc[nb]);
-                acc[nb] = mfma16x16x32(as_h8(dv), lo, acc[nb]);
+                const uint4_t dv = *(const uint4_t*)(sd + ((size_t)buf * HD + 16 * nb + li) * DP + 32 * k + 8 * lg);
+                acc[nb] = mfma16x16x32(as_h8(dv), his[k], acc[nb]);
+                acc[nb] = mfma16x16x32(as_h8(dv), los[k], acc[nb]);
             }
-            // Chunk c + 1's pieces (slot s ^ 1) into the other LDS buffer: its last readers
-            // (chunk c - 1) passed the previous barrier.
-#pragma unroll
-            for (int q = 0; q < PPT; ++q) {
-                const int p = tid + q * kFinishWaves * 64;
-                if (p < PIECES) store_piece(s ^ 1, p, pre[s ^ 1][q]);
-            }
+        }
+        if constexpr (!decltype(last)::value) {
+            // D^T of s+1 into the other buffer: its last readers (s-1) passed the previous barrier.
+            store_dt(buf ^ 1, dn);
+            load_dt(s + 2, dn);
             __syncthreads();
         }
+    };
+    // The last super-chunk stores and prefetches nothing, so it waits for nothing.
+    using more_t = std::integral_constant<bool, false>;
+    using last_t = std::integral_constant<bool, true>;
+    uint32_t s = 0;
+    for (; s + 2 < n_sc; s += 2) {
+        step(s, wA, d1, more_t{});
+        step(s + 1, wB, d1, more_t{});
+    }
+    if (s + 1 < n_sc) {
+        step(s, wA, d1, more_t{});
+        step(s + 1, wB, d1, last_t{});
+    } else {
+        step(s, wA, d1, last_t{});
     }
 
     if (!rowok) return;
     // Lane holds O^T[dims 16*nb + 4*lg + e][row li of this wave].
     const float* rf = s_rf + myr * 5;
     const float Mc = rf[0], Lc = rf[1], inv_scl = rf[2], Mh = rf[3], Lh = rf[4];
-    const uint64_t rowid = myrow;
+    const uint64_t rowid = lbg_me * R + r_me;
     if (!fused && a.n_ar > 1) {
         float* dst = a.ocp + (rowid * a.n_ar + ar) * HD;
 #pragma unroll
@@ -1404,7 +1452,7 @@ __global__ __launch_bounds__(kFinishWaves * 64) void finish_kernel(FinishArgs a)
         return;
     }
     // Fused merge with the hot partials of this row.
-    const uint64_t lbg = rowid / R, r = rowid % R;
+    const uint64_t lbg = lbg_me, r = r_me;
     float4_t oh[NB];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) oh[nb] = (float4_t)0.0f;
