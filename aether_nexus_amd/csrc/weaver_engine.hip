@@ -119,6 +119,10 @@ int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, const uint32_t 
         put_msg(msg, mlen, "refs_stride %u < hot_count + cold_count", d->refs_stride);
         return AW_E_INVALID_ARG;
     }
+    if (d->flags & ~(AW_F_CAUSAL | AW_F_COLD_HEAD_BLOCKED)) {
+        put_msg(msg, mlen, "unknown flags 0x%x", d->flags & ~(AW_F_CAUSAL | AW_F_COLD_HEAD_BLOCKED));
+        return AW_E_INVALID_ARG;
+    }
     if (!(d->scale == d->scale) || std::isinf(d->scale)) {
         put_msg(msg, mlen, "scale must be finite");
         return AW_E_INVALID_ARG;
@@ -445,6 +449,9 @@ int launch_cold(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* ws
     a.scale_log2 = d->scale * aw::kLog2e;
     a.cold_blocks = d->cold_blocks;
     a.cold_layer = d->cold_blocks * kBlock * d->kv_heads;
+    const bool head_blocked = (d->flags & AW_F_COLD_HEAD_BLOCKED) != 0;
+    a.s_tok = head_blocked ? 1u : d->kv_heads;
+    a.s_head = head_blocked ? kBlock : 1u;
     a.refs_layer = (uint64_t)d->batch * d->refs_stride;
     // q_latent [L][B][Q][Hq][A], computed on the device or the caller's.
     a.ql = o.info.computes_q_latent ? (const uint16_t*)(ws + o.off_ql) : d->q_latent;

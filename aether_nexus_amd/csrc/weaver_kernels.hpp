@@ -143,6 +143,7 @@ struct ColdArgs {
     uint32_t* err;
     uint32_t batch, kv_heads, gqa, rows_r;
     uint32_t hot_count, cold_count, refs_stride, dict_size;
+    uint32_t s_tok, s_head; // code (block b, token j, kv head g) = cold[b*16*kv_heads + j*s_tok + g*s_head]
     uint32_t splits, tokens_per_split, n_chunks, n_units;
     uint32_t n_wg; // work items (8 XCD slots x kv heads x unit groups)
     float scale_log2;
@@ -635,6 +636,7 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
     float* red = (float*)(sref + ((n_blk + 3) & ~3u));    // [NW][NR]
 
     const uint4_t* cold = a.cold + (uint64_t)l * a.cold_layer;
+    const uint64_t blk_codes = (uint64_t)kBlockTokens * a.kv_heads;
     const uint32_t* grefs = a.refs + (uint64_t)l * a.refs_layer + (uint64_t)(lb % a.batch) * a.refs_stride +
                             a.hot_count + t_begin / 16;
     const float sl = a.scale_log2;
@@ -655,7 +657,7 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
 #pragma unroll
         for (int kk = 0; kk < CPT; ++kk) {
             ok[kk] = rb[kk] != ~0u;
-            const uint4_t* p = ok[kk] ? cold + ((uint64_t)rb[kk] * kBlockTokens + (tok(tile, kk) & 15u)) * a.kv_heads + g
+            const uint4_t* p = ok[kk] ? cold + (uint64_t)rb[kk] * blk_codes + (tok(tile, kk) & 15u) * a.s_tok + g * a.s_head
                                       : &g_zero_code;
             buf[kk] = *p;
         }

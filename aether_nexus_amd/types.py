@@ -171,6 +171,7 @@ class LoomDescriptor:
 # --------------------------------------------------- device request (C ABI)
 
 AW_F_CAUSAL = 1
+AW_F_COLD_HEAD_BLOCKED = 2
 
 AW_OK = 0
 AW_E_INVALID_ARG = -1

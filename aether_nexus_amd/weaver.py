@@ -19,8 +19,8 @@ from typing import Any, Optional
 import numpy as np
 
 from . import _lib
-from .types import (AW_F_CAUSAL, SPARSE_CODE_DTYPE, STAGES, STRUCT_SIZES, DecodeDesc, PlanInfo,
-                    WeaverParams)
+from .types import (AW_F_CAUSAL, AW_F_COLD_HEAD_BLOCKED, SPARSE_CODE_DTYPE, STAGES, STRUCT_SIZES, DecodeDesc,
+                    PlanInfo, WeaverParams)
 
 
 class WeaverError(RuntimeError):
@@ -236,14 +236,16 @@ def make_desc(*, layers: int, batch: int, queries: int, q_heads: int, kv_heads: 
               dict_size: int, dict_heads: int, hot_count: int, cold_count: int, refs_stride: int,
               hot_blocks: int, cold_blocks: int, q, out, hot_k=None, hot_v=None, cold=None, refs=None,
               dictionary=None, q_latent=None, seq_hot=None, seq_cold=None, scale: float = 1.0,
-              causal: bool = False) -> DecodeDesc:
-    """Build an ``aw_decode_desc`` from device tensors (or raw device pointers)."""
+              causal: bool = False, cold_head_blocked: bool = False) -> DecodeDesc:
+    """Build an ``aw_decode_desc`` from device tensors (or raw device pointers).
+    ``cold_head_blocked``: the cold pool is [L][blocks][kv_heads][16] instead of
+    the reference's [L][blocks][16][kv_heads]."""
     d = DecodeDesc()
     d.layers, d.batch, d.queries = layers, batch, queries
     d.q_heads, d.kv_heads, d.head_dim = q_heads, kv_heads, head_dim
     d.dict_size, d.dict_heads = dict_size, dict_heads
     d.hot_count, d.cold_count, d.refs_stride = hot_count, cold_count, refs_stride
-    d.flags = AW_F_CAUSAL if causal else 0
+    d.flags = (AW_F_CAUSAL if causal else 0) | (AW_F_COLD_HEAD_BLOCKED if cold_head_blocked else 0)
     d.scale = scale
     d.hot_blocks, d.cold_blocks = hot_blocks, cold_blocks
     d.q, d.q_latent, d.hot_k, d.hot_v = _ptr(q), _ptr(q_latent), _ptr(hot_k), _ptr(hot_v)

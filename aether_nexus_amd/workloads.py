@@ -245,13 +245,23 @@ def host_arrays(wl: Workload, copy: int = 0) -> dict:
     return out
 
 
-def device_desc(wl: Workload, out: torch.Tensor, copy: int = 0):
-    """``aw_decode_desc`` for a workload whose tensors live on the GPU."""
+def head_blocked(cold: torch.Tensor) -> torch.Tensor:
+    """The cold pool [L][blocks][16][kv_heads][8] reordered to
+    [L][blocks][kv_heads][16][8] (AW_F_COLD_HEAD_BLOCKED)."""
+    return cold.permute(0, 1, 3, 2, 4).contiguous()
+
+
+def device_desc(wl: Workload, out: torch.Tensor, copy: int = 0, cold_head_blocked: Optional[torch.Tensor] = None):
+    """``aw_decode_desc`` for a workload whose tensors live on the GPU.
+    ``cold_head_blocked``: the workload's cold pool reordered by head_blocked();
+    the descriptor then points at it and sets AW_F_COLD_HEAD_BLOCKED."""
     from .weaver import make_desc
     g = wl.geom
     return make_desc(layers=g.layers, batch=g.batch, queries=g.queries, q_heads=g.q_heads, kv_heads=g.kv_heads,
                      head_dim=g.head_dim, dict_size=g.dict_size, dict_heads=g.dict_heads, hot_count=g.hot_count,
                      cold_count=g.cold_count, refs_stride=max(g.refs_stride, 1), hot_blocks=g.hot_blocks,
-                     cold_blocks=g.cold_blocks, q=wl.q, out=out, hot_k=wl.hot_k, hot_v=wl.hot_v, cold=wl.cold,
+                     cold_blocks=g.cold_blocks, q=wl.q, out=out, hot_k=wl.hot_k, hot_v=wl.hot_v,
+                     cold=wl.cold if cold_head_blocked is None else cold_head_blocked,
                      refs=wl.refs[copy], dictionary=wl.dictionary, q_latent=wl.q_latent, seq_hot=wl.seq_hot,
-                     seq_cold=wl.seq_cold, scale=g.scale, causal=g.causal)
+                     seq_cold=wl.seq_cold, scale=g.scale, causal=g.causal,
+                     cold_head_blocked=cold_head_blocked is not None)

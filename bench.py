@@ -72,15 +72,18 @@ def copies_for(geom) -> int:
 class Runner:
     """One workload resident on the GPU, its descriptors and (optionally) graphs."""
 
-    def __init__(self, engine, geom, seed, use_graph):
+    def __init__(self, engine, geom, seed, use_graph, wl=None, cold_head_blocked=False):
         import torch
         from aether_nexus_amd import workloads as W
         self.torch = torch
         self.engine = engine
         self.geom = geom
-        self.wl = W.generate(geom, seed=seed, device="cuda:0")
+        self.wl = wl if wl is not None else W.generate(geom, seed=seed, device="cuda:0")
         self.out = torch.empty(self.wl.out_shape(), dtype=torch.float16, device="cuda:0")
-        self.descs = [W.device_desc(self.wl, self.out, copy=c) for c in range(geom.copies)]
+        # Optionally the same codes in the head-blocked pool layout (AW_F_COLD_HEAD_BLOCKED).
+        self.cold_hb = W.head_blocked(self.wl.cold) if cold_head_blocked else None
+        self.descs = [W.device_desc(self.wl, self.out, copy=c, cold_head_blocked=self.cold_hb)
+                      for c in range(geom.copies)]
         self.stream = torch.cuda.Stream()
         self.graphs = None
         sh = self.stream.cuda_stream
@@ -397,6 +400,21 @@ def main():
         roofline["traffic_note"] = why
     stages_us = {k: (round(v * 1e3, 2) if v else None) for k, (v, n) in stages.items()}
     serial_us = {k: (round(v * 1e3, 2) if v else None) for k, (v, n) in serial.items()}
+    # The same workload with the cold pool in the head-blocked layout: a pool
+    # order a device-side producer can write, whose codes of one kv head fill
+    # whole 64-byte sectors (not the drop-in layout; reported beside it).
+    rh = Runner(engine, geom, args.seed, not args.no_graph, wl=r.wl, cold_head_blocked=True)
+    ms_hb = rh.time_steps(args.steps, args.warmup)
+    same = bool(torch.equal(rh.out.view(torch.int16), r.out.view(torch.int16)))
+    gb_hb = geom.algorithmic_bytes()["total"] / (ms_hb * 1e-3) / 1e9
+    head_blocked = {"ms_per_step": round(ms_hb, 5), "tokens_per_s": round(geom.batch / (ms_hb * 1e-3), 1),
+                    "achieved_gbps": round(gb_hb, 1), "frac_of_peak": round(gb_hb / PEAK_HBM_GBPS, 4),
+                    "output_bit_identical": same,
+                    "stages_us": {k: (round(v * 1e3, 2) if v else None)
+                                  for k, (v, n) in rh.stage_times(args.steps, mode=1).items()}}
+    log(json.dumps({"cold_head_blocked_layout": head_blocked}))
+    del rh
+    torch.cuda.empty_cache()
     ref_cfg = reference_bench_config(engine, args.seed, 200)
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds, args.seed)
 
@@ -425,6 +443,7 @@ def main():
         "stages_us": stages_us,
         "stages_serial_us": serial_us,
         "roofline": roofline,
+        "cold_head_blocked_layout": head_blocked,
         "cpu_baseline": cpu,
         "reference_bench_config": ref_cfg,
     }

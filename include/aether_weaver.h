@@ -78,6 +78,15 @@ typedef struct aw_weaver_params {
 #define AW_F_CAUSAL 1u /* query j of Q sees hot tokens p < n_hot_tokens - Q + 1 + j
                           (the rule of nexus-core/src/ops.metal:549); cold tokens are
                           all older than the drafts and always visible */
+#define AW_F_COLD_HEAD_BLOCKED 2u /* cold pool laid out [L][cold_blocks][kv_heads][16]:
+                          each kv head's 16 codes of a block contiguous (256 bytes).
+                          No reference counterpart: the reference pool is
+                          [blocks][16][kv_heads] (fabric.rs:124-186), where one kv
+                          head's code is 16 bytes of every 128-byte token line, so a
+                          cold work-group reads a 64-byte sector per code.  For
+                          producers that can write it (an encoder on the device),
+                          the head-blocked order reads whole sectors; the results
+                          are identical bit for bit. */
 
 /* One decode call over L layers x B sequences x Q query tokens.  All pointers
  * are DEVICE pointers.  Element layouts (f16 = raw binary16 bits):
@@ -87,7 +96,8 @@ typedef struct aw_weaver_params {
  *            reference's q_latent buffer, weaver_kernel.metal:111)
  *   hot_k    [L][hot_blocks][16][kv_heads][head_dim]
  *   hot_v    same as hot_k, or NULL: V is the K row (reference, metal:162-166)
- *   cold     [L][cold_blocks][16][kv_heads]   (16-byte aligned)
+ *   cold     [L][cold_blocks][16][kv_heads]   (16-byte aligned; with
+ *            AW_F_COLD_HEAD_BLOCKED [L][cold_blocks][kv_heads][16])
  *   refs     [L][B][refs_stride]: hot refs [0, hot_count), cold refs
  *            [hot_count, hot_count + cold_count) of each sequence
  *   seq_hot, seq_cold  optional [L][B] per-sequence block counts

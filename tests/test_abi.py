@@ -146,6 +146,26 @@ def test_plan_splits_and_workspace():
     assert e.value.status == AW_E_UNSUPPORTED
 
 
+def test_plan_flags():
+    """The head-blocked cold layout plans like the reference layout; unknown flag bits are rejected."""
+    from aether_nexus_amd.types import AW_E_INVALID_ARG, AW_F_CAUSAL, AW_F_COLD_HEAD_BLOCKED
+    from aether_nexus_amd.weaver import make_desc
+    g = W.hot_cold(batch=64)
+    kw = dict(layers=1, batch=64, queries=1, q_heads=32, kv_heads=8, head_dim=128, dict_size=4096, dict_heads=1,
+              hot_count=g.hot_count, cold_count=g.cold_count, refs_stride=g.refs_stride, hot_blocks=g.hot_blocks,
+              cold_blocks=g.cold_blocks, q=1, out=1)
+    ref = plan(make_desc(**kw))
+    hb = plan(make_desc(**kw, cold_head_blocked=True))
+    assert (hb.cold_splits, hb.cold_tokens_per_split, hb.workspace_bytes) == \
+        (ref.cold_splits, ref.cold_tokens_per_split, ref.workspace_bytes)
+    assert AW_F_COLD_HEAD_BLOCKED == 2 and AW_F_CAUSAL == 1
+    bad = make_desc(**kw)
+    bad.flags = 4
+    with pytest.raises(WeaverError) as e:
+        plan(bad)
+    assert e.value.status == AW_E_INVALID_ARG
+
+
 def test_engine_create_without_gpu_fails_cleanly():
     """No GPU in this container: creation reports an error instead of crashing."""
     import torch

@@ -160,6 +160,21 @@ def full_size(engine, stream, geom, seed, n_rows, what):
     assert_close(got[torch.from_numpy(rows.astype(np.int64)).cuda()].cpu().numpy(), ref, what)
 
 
+@pytest.mark.parametrize("geom", [W.sweep(8), W.hot_cold(hot_count=3, cold_count=40, dict_size=256, batch=3),
+                                  W.tiny(q_heads=4, kv_heads=2, dict_heads=2)], ids=["sweep_b8", "ragged", "perhead"])
+def test_cold_head_blocked_layout_bit_identical(engine, stream, geom):
+    """AW_F_COLD_HEAD_BLOCKED: the same codes laid out [blocks][kv_heads][16] give
+    the same output bits as the reference layout [blocks][16][kv_heads]."""
+    wl = W.generate(geom, seed=55, device="cuda:0")
+    ref = torch.empty(wl.out_shape(), dtype=torch.float16, device="cuda:0")
+    engine.decode_device(W.device_desc(wl, ref), stream=stream)
+    hb = W.head_blocked(wl.cold)
+    out = torch.empty(wl.out_shape(), dtype=torch.float16, device="cuda:0")
+    engine.decode_device(W.device_desc(wl, out, cold_head_blocked=hb), stream=stream)
+    engine.check_device_errors(stream)
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+
+
 def test_repeat_calls_bit_identical(engine, stream):
     """The same inputs give the same output bits on every call (fixed
     reduction orders; integer bins), also after other decodes ran in between."""
