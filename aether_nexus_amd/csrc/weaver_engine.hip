@@ -418,8 +418,11 @@ int launch_hot(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* ws,
     return AW_OK;
 }
 
-constexpr int kColdCPT = 4;
-constexpr int kColdPD = 2; // tiles of code loads in flight (1..4 measured alike)
+// Codes per lane per wave tile, and wave tiles of code loads in flight.  2 x 4
+// measured faster than 4 x 2, 4 x 3, 4 x 4 and 8 x 2 at B = 64; deeper rings hold
+// more VGPRs, which crowd out the hot waves running beside the cold kernel.
+constexpr int kColdCPT = 2;
+constexpr int kColdPD = 4;
 
 int launch_cold(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* ws, hipStream_t st) {
     aw::ColdArgs a{};
