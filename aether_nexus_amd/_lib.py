@@ -41,6 +41,9 @@ SIGNATURES = {
     "aw_engine_set_profiling": (_c_int, [_vp, _c_int]),
     "aw_engine_stage_stats": (_c_int, [_vp, _c_int, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_u64)]),
     "aw_engine_reset_stage_stats": (_c_int, [_vp]),
+    "aw_abi_encode_desc_size": (_sz, []),
+    "aw_encode_device": (_c_int, [_vp, _vp, _vp]),
+    "aw_encode": (_c_int, [_vp, _vp, _sz, _vp, _sz, _u32, _u32, _u32, _u32, _vp, _sz, _vp, _sz, _vp]),
 }
 
 _cache: dict[str, ctypes.CDLL] = {}

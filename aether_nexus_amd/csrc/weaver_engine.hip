@@ -665,6 +665,8 @@ void aw_abi_struct_sizes(size_t sizes[4]) {
     sizes[3] = sizeof(aw_decode_plan_info);
 }
 
+size_t aw_abi_encode_desc_size(void) { return sizeof(aw_encode_desc); }
+
 const char* aw_status_string(int status) {
     switch (status) {
     case AW_OK: return "ok";
@@ -974,6 +976,139 @@ int aw_debug_gather_codes(aw_engine* e, const aw_sparse_code* codes, size_t n, c
                        (const aw::uint4_t*)codes, (uint64_t)n, dict, dict_size, head_dim, idx, coef, atoms, e->err);
     AW_HIP(e, hipGetLastError());
     return AW_OK;
+}
+
+namespace {
+
+// Geometry checks of an encoder request (numeric fields only).
+int encode_check(const aw_encode_desc* d, char* msg, size_t mlen) {
+    if (d->kv_heads == 0 || !supported_head_dim(d->head_dim)) {
+        put_msg(msg, mlen, "kv_heads %u must be >= 1 and head_dim %u 64 or 128", d->kv_heads, d->head_dim);
+        return AW_E_UNSUPPORTED;
+    }
+    if (d->dict_size == 0 || d->dict_size > 65536 || d->dict_size % 16) {
+        put_msg(msg, mlen, "dict_size %u must be a multiple of 16 in [16, 65536]", d->dict_size);
+        return AW_E_UNSUPPORTED;
+    }
+    if (d->dict_heads != 1 && d->dict_heads != d->kv_heads) {
+        put_msg(msg, mlen, "dict_heads must be 1 (shared) or kv_heads");
+        return AW_E_INVALID_ARG;
+    }
+    if (d->flags & ~AW_F_COLD_HEAD_BLOCKED) {
+        put_msg(msg, mlen, "unknown encoder flags 0x%x", d->flags & ~AW_F_COLD_HEAD_BLOCKED);
+        return AW_E_INVALID_ARG;
+    }
+    if (d->n_blocks >= (1u << 27)) {
+        put_msg(msg, mlen, "n_blocks %u too large", d->n_blocks);
+        return AW_E_UNSUPPORTED;
+    }
+    return AW_OK;
+}
+
+int encode_device(aw_engine* e, const aw_encode_desc* d, hipStream_t st) {
+    char msg[256] = {0};
+    int rc = encode_check(d, msg, sizeof msg);
+    if (rc) return fail(e, rc, "%s", msg);
+    if (!d->n_blocks) return AW_OK;
+    if (!d->hot || !d->dict || !d->src_blocks || !d->cold || !d->hot_blocks || !d->cold_blocks)
+        return fail(e, AW_E_INVALID_ARG, "hot, dict, src_blocks and cold are required, with hot_blocks and cold_blocks > 0");
+    if ((uintptr_t)d->cold & 15u) return fail(e, AW_E_ALIGN, "cold pool pointer is not 16-byte aligned");
+    if (((uintptr_t)d->hot | (uintptr_t)d->dict) & 15u)
+        return fail(e, AW_E_ALIGN, "hot pool and dictionary pointers must be 16-byte aligned");
+    AW_HIP(e, hipSetDevice(e->device));
+    aw::EncodeArgs a{};
+    a.hot = d->hot;
+    a.dict = d->dict;
+    a.src = d->src_blocks;
+    a.dst = d->dst_blocks;
+    a.cold = (aw::uint4_t*)d->cold;
+    a.entropy = d->entropy;
+    a.err = e->err;
+    a.kv_heads = d->kv_heads;
+    a.dict_size = d->dict_size;
+    a.dict_heads = d->dict_heads;
+    a.n_blocks = d->n_blocks;
+    const bool head_blocked = (d->flags & AW_F_COLD_HEAD_BLOCKED) != 0;
+    a.s_tok = head_blocked ? 1u : d->kv_heads;
+    a.s_head = head_blocked ? kBlock : 1u;
+    a.hot_blocks = d->hot_blocks;
+    a.cold_blocks = d->cold_blocks;
+    const dim3 grid(cdiv((uint64_t)d->n_blocks * kBlock, aw::kEncThreads), d->kv_heads);
+    if (d->head_dim == 64)
+        hipLaunchKernelGGL(aw::encode_kernel<64>, grid, dim3(aw::kEncThreads), 0, st, a);
+    else
+        hipLaunchKernelGGL(aw::encode_kernel<128>, grid, dim3(aw::kEncThreads), 0, st, a);
+    AW_HIP(e, hipGetLastError());
+    if (d->entropy) {
+        hipLaunchKernelGGL(aw::entropy_kernel, dim3(cdiv(d->n_blocks, 64)), dim3(64), 0, st, a, d->head_dim);
+        AW_HIP(e, hipGetLastError());
+    }
+    return AW_OK;
+}
+
+} // namespace
+
+int aw_encode_device(aw_engine* e, const aw_encode_desc* desc, void* stream) {
+    if (!e || !desc) return AW_E_INVALID_ARG;
+    return encode_device(e, desc, (hipStream_t)stream); // NULL is HIP's null stream
+}
+
+int aw_encode(aw_engine* e, const uint16_t* hot, size_t n_hot, const uint16_t* dict, size_t n_dict,
+              uint32_t kv_heads, uint32_t head_dim, uint32_t dict_size, uint32_t dict_heads, const uint32_t* blocks,
+              size_t n_blocks, aw_sparse_code* cold, size_t n_cold, float* entropy) {
+    if (!e) return AW_E_INVALID_ARG;
+    aw_encode_desc d{};
+    d.kv_heads = kv_heads;
+    d.head_dim = head_dim;
+    d.dict_size = dict_size;
+    d.dict_heads = dict_heads;
+    d.n_blocks = (uint32_t)std::min<size_t>(n_blocks, 0xFFFFFFFFu);
+    char msg[256] = {0};
+    int rc = encode_check(&d, msg, sizeof msg);
+    if (rc) return fail(e, rc, "%s", msg);
+    if (n_blocks != d.n_blocks) return fail(e, AW_E_UNSUPPORTED, "too many blocks");
+    if (!n_blocks) return AW_OK;
+    const size_t per_block = (size_t)kBlock * kv_heads * head_dim, codes_per_block = (size_t)kBlock * kv_heads;
+    if (!hot || !dict || !blocks || !cold) return fail(e, AW_E_INVALID_ARG, "hot, dict, blocks and cold are required");
+    if (n_hot < per_block || n_hot % per_block)
+        return fail(e, AW_E_INVALID_ARG, "hot slice of %zu values is not a whole number of %zu-value blocks", n_hot, per_block);
+    if (n_dict != (size_t)dict_heads * dict_size * head_dim)
+        return fail(e, AW_E_INVALID_ARG, "dictionary slice of %zu values, expected %zu", n_dict,
+                    (size_t)dict_heads * dict_size * head_dim);
+    if (n_cold < codes_per_block || n_cold % codes_per_block)
+        return fail(e, AW_E_INVALID_ARG, "cold slice of %zu codes is not a whole number of %zu-code blocks", n_cold,
+                    codes_per_block);
+    const uint64_t hot_blocks = n_hot / per_block, cold_blocks = n_cold / codes_per_block;
+    for (size_t i = 0; i < n_blocks; ++i) {
+        const uint32_t b = blocks[i] & 0x7FFFFFFFu;
+        if (b >= hot_blocks || b >= cold_blocks)
+            return fail(e, AW_E_OOB, "block %u (entry %zu) outside the hot pool (%llu blocks) or cold pool (%llu blocks)",
+                        b, i, (unsigned long long)hot_blocks, (unsigned long long)cold_blocks);
+    }
+    AW_HIP(e, hipSetDevice(e->device));
+    auto fill = [&](DevBuf& b, const void* src, size_t bytes) -> int {
+        int r = ensure(b, bytes, e->last_error);
+        if (r) return r;
+        AW_HIP(e, hipMemcpyAsync(b.ptr, src, bytes, hipMemcpyHostToDevice, e->stream));
+        return AW_OK;
+    };
+    if ((rc = fill(e->hot, hot, n_hot * 2))) return rc;
+    if ((rc = fill(e->dict, dict, n_dict * 2))) return rc;
+    if ((rc = fill(e->refs, blocks, n_blocks * 4))) return rc;
+    if ((rc = fill(e->cold, cold, n_cold * sizeof(aw_sparse_code)))) return rc;
+    if (entropy && (rc = ensure(e->out, n_blocks * 4, e->last_error))) return rc;
+    d.hot = (const uint16_t*)e->hot.ptr;
+    d.dict = (const uint16_t*)e->dict.ptr;
+    d.src_blocks = (const uint32_t*)e->refs.ptr;
+    d.cold = (aw_sparse_code*)e->cold.ptr;
+    d.entropy = entropy ? (float*)e->out.ptr : nullptr;
+    d.hot_blocks = hot_blocks;
+    d.cold_blocks = cold_blocks;
+    if ((rc = encode_device(e, &d, e->stream))) return rc;
+    AW_HIP(e, hipMemcpyAsync(cold, e->cold.ptr, n_cold * sizeof(aw_sparse_code), hipMemcpyDeviceToHost, e->stream));
+    if (entropy) AW_HIP(e, hipMemcpyAsync(entropy, e->out.ptr, n_blocks * 4, hipMemcpyDeviceToHost, e->stream));
+    AW_HIP(e, hipStreamSynchronize(e->stream));
+    return aw_engine_check_device_errors(e, e->stream);
 }
 
 int aw_engine_set_profiling(aw_engine* e, int enable) {

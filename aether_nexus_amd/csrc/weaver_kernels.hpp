@@ -1586,4 +1586,153 @@ __global__ void gather_codes_kernel(const uint4_t* codes, uint64_t n, const uint
     for (uint32_t j = 0; j < HD; ++j) atoms[t * HD + j] = at < A ? dict[(uint64_t)at * HD + j] : (uint16_t)0xFFFFu;
 }
 
+// --------------------------------------------- SparseCode encoder (distiller)
+//
+// Replaces Distiller::distill_block (distiller.rs:171-246).  Lane = one token of
+// one kv head: it keeps the token's HD values in registers and walks every atom
+// of the head's dictionary in index order, each dot product summed in head-dim
+// order from -0.0 with one FMA per term (f16 x f16 products are exact in f32, so
+// the FMA rounds exactly like the reference's product-then-add,
+// distiller.rs:212-216).  A wave holds 64 tokens of one kv head, so it reads one
+// dictionary row at a time: 16-atom chunks are staged in LDS by the work-group
+// (double-buffered, the next chunk's loads in flight while the current one is
+// used) and read back as broadcasts.  The running top 4 keeps (score desc,
+// atom asc): an atom enters only with a strictly larger score, and atoms come in
+// index order, so equal scores keep the lower index first (the reference test at
+// distiller.rs:299-307 expects 0,1,2,3 for equal scores).  NaN and -inf never
+// enter; an unfilled slot keeps the zero code's index 0 and coefficient 0.
+struct EncodeArgs {
+    const uint16_t* hot;  // [hot_blocks][16][kv_heads][HD]
+    const uint16_t* dict; // [dict_heads][A][HD]
+    const uint32_t* src;  // hot block per encoded block
+    const uint32_t* dst;  // cold block per encoded block, or null: the source index
+    uint4_t* cold;        // code (block, token, head) = cold[block*16*kv_heads + token*s_tok + head*s_head]
+    float* entropy;       // [n_blocks] or null
+    uint32_t* err;
+    uint32_t kv_heads, dict_size, dict_heads, n_blocks;
+    uint32_t s_tok, s_head;
+    uint64_t hot_blocks, cold_blocks;
+};
+constexpr int kEncThreads = 256;
+constexpr int kEncAtoms = 16; // atoms per staged dictionary chunk (dict_size % 16 == 0)
+
+template <int HD>
+__global__ __launch_bounds__(kEncThreads) void encode_kernel(EncodeArgs a) {
+    constexpr int PR = HD / 8, NPC = kEncAtoms * PR; // 16-byte pieces per row / per chunk
+    __shared__ __attribute__((aligned(16))) uint4_t sd[2][NPC];
+    const int tid = threadIdx.x;
+    const uint32_t g = blockIdx.y;
+    const uint32_t n_tok = a.n_blocks * kBlockTokens;
+    const uint32_t T = blockIdx.x * kEncThreads + tid; // token of the request
+    const bool live = T < n_tok;
+    const uint32_t Tc = live ? T : n_tok - 1u;
+    const uint32_t bi = Tc / kBlockTokens, tt = Tc % kBlockTokens;
+    const uint32_t b = a.src[bi] & kRefMask;
+    const uint32_t c = a.dst ? (a.dst[bi] & kRefMask) : b;
+    const bool ok = live && b < a.hot_blocks && c < a.cold_blocks;
+    if (live && g == 0 && tt == 0) { // one report per block
+        if (b >= a.hot_blocks) flag_error(a.err, kErrHotRef);
+        if (c >= a.cold_blocks) flag_error(a.err, kErrColdRef);
+    }
+    const uint32_t A = a.dict_size, n_ch = A / kEncAtoms;
+    const uint4_t* D = (const uint4_t*)(a.dict + (uint64_t)(a.dict_heads == 1 ? 0u : g) * A * HD);
+    // Dictionary chunk ch: piece p of it (threads beyond NPC idle; loads clamped into the dictionary).
+    auto load_chunk = [&](uint32_t ch) -> uint4_t { return D[(uint64_t)min(ch, n_ch - 1u) * NPC + min(tid, NPC - 1)]; };
+    uint4_t pre = load_chunk(0);
+    // This lane's token (a valid block when the request's is out of range: its code is not written).
+    const uint4_t* xp = (const uint4_t*)(a.hot + (((uint64_t)(b < a.hot_blocks ? b : 0u) * kBlockTokens + tt) * a.kv_heads + g) * HD);
+    half8_t x[PR];
+#pragma unroll
+    for (int j = 0; j < PR; ++j) x[j] = as_h8(xp[j]);
+    if (tid < NPC) sd[0][tid] = pre;
+    pre = load_chunk(1);
+    __syncthreads();
+
+    float v[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    uint32_t ix[4] = {0u, 0u, 0u, 0u};
+    for (uint32_t ch = 0; ch < n_ch; ++ch) {
+        const uint4_t* row = sd[ch & 1u];
+#pragma unroll 2
+        for (int at = 0; at < kEncAtoms; ++at) {
+            float s = -0.0f;
+#pragma unroll
+            for (int j = 0; j < PR; ++j) {
+                const half8_t d8 = as_h8(row[at * PR + j]); // same address in every lane: a broadcast
+#pragma unroll
+                for (int e = 0; e < 8; ++e) s = fmaf((float)x[j][e], (float)d8[e], s);
+            }
+            if (s > v[3]) { // NaN and -inf never enter
+                const uint32_t ai = ch * kEncAtoms + (uint32_t)at;
+                const bool g0 = s > v[0], g1 = s > v[1], g2 = s > v[2];
+                v[3] = g2 ? v[2] : s;
+                ix[3] = g2 ? ix[2] : ai;
+                v[2] = g1 ? v[1] : (g2 ? s : v[2]);
+                ix[2] = g1 ? ix[1] : (g2 ? ai : ix[2]);
+                v[1] = g0 ? v[0] : (g1 ? s : v[1]);
+                ix[1] = g0 ? ix[0] : (g1 ? ai : ix[1]);
+                v[0] = g0 ? s : v[0];
+                ix[0] = g0 ? ai : ix[0];
+            }
+        }
+        // The next chunk into the other buffer (its last readers passed the previous barrier).
+        if (tid < NPC) sd[(ch + 1u) & 1u][tid] = pre;
+        pre = load_chunk(ch + 2u);
+        __syncthreads();
+    }
+    if (!ok) return;
+    uint32_t cb[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const bool filled = v[k] != -INFINITY;
+        cb[k] = filled ? (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[k]) : 0u;
+        ix[k] = filled ? ix[k] : 0u;
+    }
+    const uint4_t code = {ix[0] | (ix[1] << 16), ix[2] | (ix[3] << 16), cb[0] | (cb[1] << 16), cb[2] | (cb[3] << 16)};
+    a.cold[(uint64_t)c * kBlockTokens * a.kv_heads + tt * a.s_tok + g * a.s_head] = code;
+}
+
+// Variance proxy of each encoded block (distiller.rs:126-159): one lane per
+// block runs the reference's loops in memory order, in f64, with no fused
+// multiply-add (the reference squares, then adds), and returns f32.  An
+// all-zero block gives 0.
+__global__ __launch_bounds__(64) void entropy_kernel(EncodeArgs a, uint32_t head_dim) {
+#pragma clang fp contract(off)
+    const uint32_t i = blockIdx.x * 64 + threadIdx.x;
+    if (i >= a.n_blocks) return;
+    const uint32_t b = a.src[i] & kRefMask;
+    if (b >= a.hot_blocks) { // reported by encode_kernel
+        a.entropy[i] = 0.0f;
+        return;
+    }
+    const uint64_t n = (uint64_t)kBlockTokens * a.kv_heads * head_dim;
+    const uint4_t* p = (const uint4_t*)(a.hot + (uint64_t)b * n);
+    bool all_zero = true;
+    double sum = -0.0;
+    for (uint64_t k = 0; k < n / 8; ++k) {
+        const uint4_t w = p[k];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float f = h2f_bits((w[e / 2] >> (16 * (e % 2))) & 0xFFFFu);
+            all_zero = all_zero && f == 0.0f;
+            sum = sum + (double)f;
+        }
+    }
+    if (all_zero) {
+        a.entropy[i] = 0.0f;
+        return;
+    }
+    const double mean = sum / (double)n;
+    double var = -0.0;
+    for (uint64_t k = 0; k < n / 8; ++k) {
+        const uint4_t w = p[k];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const double diff = (double)h2f_bits((w[e / 2] >> (16 * (e % 2))) & 0xFFFFu) - mean;
+            const double sq = diff * diff;
+            var = var + sq;
+        }
+    }
+    a.entropy[i] = (float)(var / (double)n);
+}
+
 } // namespace aw

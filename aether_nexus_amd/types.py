@@ -203,6 +203,20 @@ class DecodeDesc(ctypes.Structure):
     ]
 
 
+class EncodeDesc(ctypes.Structure):
+    """``aw_encode_desc`` (include/aether_weaver.h): a SparseCode encoder request."""
+
+    _fields_ = [
+        ("kv_heads", ctypes.c_uint32), ("head_dim", ctypes.c_uint32),
+        ("dict_size", ctypes.c_uint32), ("dict_heads", ctypes.c_uint32),
+        ("n_blocks", ctypes.c_uint32), ("flags", ctypes.c_uint32),
+        ("hot_blocks", ctypes.c_uint64), ("cold_blocks", ctypes.c_uint64),
+        ("hot", ctypes.c_void_p), ("dict", ctypes.c_void_p),
+        ("src_blocks", ctypes.c_void_p), ("dst_blocks", ctypes.c_void_p),
+        ("cold", ctypes.c_void_p), ("entropy", ctypes.c_void_p),
+    ]
+
+
 class PlanInfo(ctypes.Structure):
     """``aw_decode_plan_info``."""
 

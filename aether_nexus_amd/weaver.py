@@ -20,7 +20,7 @@ import numpy as np
 
 from . import _lib
 from .types import (AW_F_CAUSAL, AW_F_COLD_HEAD_BLOCKED, SPARSE_CODE_DTYPE, STAGES, STRUCT_SIZES, DecodeDesc,
-                    PlanInfo, WeaverParams)
+                    EncodeDesc, PlanInfo, WeaverParams)
 
 
 class WeaverError(RuntimeError):
@@ -202,6 +202,38 @@ class WeaverEngine:
         rc = self._lib.aw_decode_device(self._h, ctypes.byref(desc), _stream(stream))
         self._check(rc, "decode_device")
 
+    def encode_device(self, desc: EncodeDesc, stream: Optional[int] = None) -> None:
+        """Enqueue one SparseCode encoder request (``Distiller::distill_block``,
+        distiller.rs:171-246, over a batch of blocks; device pointers)."""
+        rc = self._lib.aw_encode_device(self._h, ctypes.byref(desc), _stream(stream))
+        self._check(rc, "encode_device")
+
+    def encode(self, hot_pool, dictionary, blocks, cold_pool, kv_heads: int, head_dim: int, dict_size: int,
+               dict_heads: int, entropy: bool = False):
+        """Host-slice encoder (copy in, encode, copy out, wait): hot block b of
+        ``blocks`` -> cold block b (distiller.rs:177).  ``cold_pool`` (uint16
+        words or SparseCode records) is updated in place; returns the blocks'
+        entropy proxies (distiller.rs:126-159) when asked."""
+        hot = _f16_bits(hot_pool)
+        dic = _f16_bits(dictionary)
+        blk = np.ascontiguousarray(blocks, dtype=np.uint32).reshape(-1)
+        if not isinstance(cold_pool, np.ndarray) or not cold_pool.flags.c_contiguous:
+            raise TypeError("cold_pool must be a C-contiguous numpy array (updated in place)")
+        if cold_pool.dtype == SPARSE_CODE_DTYPE:
+            target = cold_pool.view(np.uint16).reshape(-1, 8)
+        elif cold_pool.dtype == np.uint16 and cold_pool.shape[-1] == 8:
+            target = cold_pool.reshape(-1, 8)
+        else:
+            raise TypeError("cold pool must be SPARSE_CODE_DTYPE or uint16 words [..., 8]")
+        words = _aligned16(np.array(target, dtype=np.uint16, order="C"))
+        ent = np.zeros(blk.size, dtype=np.float32) if entropy else None
+        rc = self._lib.aw_encode(self._h, hot.ctypes.data, hot.size, dic.ctypes.data, dic.size, kv_heads, head_dim,
+                                 dict_size, dict_heads, blk.ctypes.data, blk.size, words.ctypes.data, words.shape[0],
+                                 None if ent is None else ent.ctypes.data)
+        self._check(rc, "encode")
+        np.copyto(target, words)
+        return ent
+
     def check_device_errors(self, stream: Optional[int] = None) -> None:
         self._check(self._lib.aw_engine_check_device_errors(self._h, _stream(stream)), "device check")
 
@@ -251,4 +283,19 @@ def make_desc(*, layers: int, batch: int, queries: int, q_heads: int, kv_heads: 
     d.q, d.q_latent, d.hot_k, d.hot_v = _ptr(q), _ptr(q_latent), _ptr(hot_k), _ptr(hot_v)
     d.cold, d.refs, d.seq_hot, d.seq_cold = _ptr(cold), _ptr(refs), _ptr(seq_hot), _ptr(seq_cold)
     d.dict, d.out = _ptr(dictionary), _ptr(out)
+    return d
+
+
+def make_encode_desc(*, kv_heads: int, head_dim: int, dict_size: int, dict_heads: int, hot_blocks: int,
+                     cold_blocks: int, hot, dictionary, src_blocks, cold, dst_blocks=None, entropy=None,
+                     cold_head_blocked: bool = False) -> EncodeDesc:
+    """Build an ``aw_encode_desc`` from device tensors (or raw device pointers)."""
+    d = EncodeDesc()
+    d.kv_heads, d.head_dim, d.dict_size, d.dict_heads = kv_heads, head_dim, dict_size, dict_heads
+    n = src_blocks.numel() if hasattr(src_blocks, "numel") else int(np.asarray(src_blocks).size)
+    d.n_blocks = n
+    d.flags = AW_F_COLD_HEAD_BLOCKED if cold_head_blocked else 0
+    d.hot_blocks, d.cold_blocks = hot_blocks, cold_blocks
+    d.hot, d.dict, d.src_blocks = _ptr(hot), _ptr(dictionary), _ptr(src_blocks)
+    d.dst_blocks, d.cold, d.entropy = _ptr(dst_blocks), _ptr(cold), _ptr(entropy)
     return d

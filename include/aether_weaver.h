@@ -240,6 +240,68 @@ int aw_debug_gather_codes(aw_engine* engine, const aw_sparse_code* codes, size_t
                           const uint16_t* dict, uint32_t dict_size, uint32_t head_dim,
                           uint32_t* idx, float* coef, uint16_t* atoms, void* hip_stream);
 
+/* ---- SparseCode encoder (distillation of hot blocks) ------------------------ */
+
+/* One encoder request over n_blocks hot blocks.  All pointers are DEVICE
+ * pointers.  Element layouts (f16 = raw binary16 bits):
+ *   hot        [hot_blocks][16][kv_heads][head_dim] f16 (the hot pool, fabric.rs:131-134)
+ *   dict       [dict_heads][dict_size][head_dim] f16; dict_heads is kv_heads (the
+ *              reference's per-kv-head dictionary, distiller.rs:201-202) or 1 (shared)
+ *   src_blocks [n_blocks] hot block indices to encode (bit 31 masked, as in a ref)
+ *   dst_blocks [n_blocks] cold block indices that receive the codes, or NULL: the
+ *              source index (distiller.rs:177 writes hot block b's codes at cold block b)
+ *   cold       [cold_blocks][16][kv_heads] SparseCodes; with AW_F_COLD_HEAD_BLOCKED
+ *              [cold_blocks][kv_heads][16]
+ *   entropy    optional [n_blocks] f32: the block's variance proxy (distiller.rs:126-159)
+ * flags: 0 or AW_F_COLD_HEAD_BLOCKED. */
+typedef struct aw_encode_desc {
+    uint32_t kv_heads, head_dim, dict_size, dict_heads;
+    uint32_t n_blocks, flags;
+    uint64_t hot_blocks, cold_blocks;
+    const uint16_t*  hot;
+    const uint16_t*  dict;
+    const uint32_t*  src_blocks;
+    const uint32_t*  dst_blocks;
+    aw_sparse_code*  cold;
+    float*           entropy;
+} aw_encode_desc;
+
+/* sizeof(aw_encode_desc), for bindings to check their layout.  No reference counterpart. */
+size_t aw_abi_encode_desc_size(void);
+
+/* Replaces Distiller::distill_block (distiller.rs:171-246) for a batch of
+ * blocks, asynchronous on `hip_stream`.  For every token t and kv head g of
+ * each source block, with x = hot[b][t][g][:] and D = the dictionary of head g:
+ *   s_a = sum_j f32(x_j) * f32(D[a][j]), summed in j order from -0.0 in f32
+ *         (distiller.rs:212-216; Rust >= 1.82 folds f32 sums from -0.0,
+ *         rust-version 1.85 in Cargo.toml), exactly: each step is one FMA of an
+ *         exact f16 x f16 product;
+ *   the 4 atoms with the largest s_a, ordered by s_a descending and, among
+ *   equal scores, by atom index ascending (a stable order; the reference's
+ *   sort_unstable_by at distiller.rs:221-223 leaves ties unordered, and its
+ *   test at :299-307 expects indices [0,1,2,3] for equal scores); NaN and
+ *   -inf scores are never chosen (a slot left unfilled holds the zero code's
+ *   index 0 and coefficient 0);
+ *   code = {indices: those atoms, coeffs: f16(s_a) rounded to nearest even}
+ *   (distiller.rs:225-233), written to the destination block, token t, head g.
+ * When `entropy` is set it also writes each block's variance proxy: the mean
+ * and variance of its f16 values summed in f64 in memory order, returned as f32,
+ * 0 for an all-zero block (distiller.rs:126-159). */
+int aw_encode_device(aw_engine* engine, const aw_encode_desc* desc, void* hip_stream);
+
+/* Host-slice form of aw_encode_device with copy-in / copy-out and a blocking
+ * wait, for a host that owns the pools in memory (the mmap'd Fabric,
+ * fabric.rs:359-379).  Sizes count elements: n_hot and n_dict f16 values,
+ * n_cold SparseCodes.  `hot` holds whole blocks, `dict` dict_heads
+ * dictionaries, `cold` whole blocks (read and written back in full),
+ * `blocks` the hot block indices to encode (each written to the same cold
+ * block index, distiller.rs:177), `entropy` may be NULL. */
+int aw_encode(aw_engine* engine,
+              const uint16_t* hot, size_t n_hot, const uint16_t* dict, size_t n_dict,
+              uint32_t kv_heads, uint32_t head_dim, uint32_t dict_size, uint32_t dict_heads,
+              const uint32_t* blocks, size_t n_blocks,
+              aw_sparse_code* cold, size_t n_cold, float* entropy);
+
 /* Per-stage kernel timing with HIP events recorded on the stream each kernel
  * runs on: every launch is bracketed by a pair of events.  AW_PROFILE_ON keeps
  * the pipeline as it runs unprofiled (the hot kernel on the engine's side

@@ -46,7 +46,12 @@ def lib() -> ctypes.CDLL:
         l.or_decode_f64.argtypes = [vp, vp, u64, vp, ctypes.c_int]
         l.or_qlatent_f64.argtypes = [vp, vp]
         l.or_gather_codes.argtypes = [vp, u64, vp, ctypes.c_uint32, ctypes.c_uint32, vp, vp, vp]
-        for f in ("or_decode_ref32", "or_decode_ref32_rows", "or_decode_f64", "or_qlatent_f64", "or_gather_codes"):
+        l.or_encode_blocks.argtypes = [vp, u64, ctypes.c_uint32, ctypes.c_uint32, vp, ctypes.c_uint32, ctypes.c_uint32,
+                                       vp, vp, ctypes.c_uint32, vp, u64, ctypes.c_int, vp]
+        l.or_block_entropy.argtypes = [vp, u64]
+        l.or_block_entropy.restype = ctypes.c_float
+        for f in ("or_decode_ref32", "or_decode_ref32_rows", "or_decode_f64", "or_qlatent_f64", "or_gather_codes",
+                  "or_encode_blocks"):
             getattr(l, f).restype = ctypes.c_int
         _lib = l
     return _lib
@@ -173,3 +178,38 @@ def f2h(vals: np.ndarray) -> np.ndarray:
     out = np.zeros(v.shape, dtype=np.uint16)
     lib().or_f2h_array(v.ctypes.data, out.ctypes.data, v.size)
     return out
+
+
+def encode_blocks(hot: np.ndarray, dictionary: np.ndarray, src, dst=None, cold: np.ndarray | None = None,
+                  head_blocked: bool = False, entropy: bool = False):
+    """SparseCode encoder (distiller.rs:171-246) over host arrays.
+
+    hot: f16 bits [hot_blocks, 16, kv_heads, head_dim] (uint16); dictionary: f16
+    bits [dict_heads, dict_size, head_dim]; src / dst: block indices.  Returns the
+    cold pool (uint16 words [cold_blocks, 16, kv_heads, 8], or [.., kv_heads, 16, 8]
+    when head_blocked) with the encoded blocks written, and the blocks' entropy
+    proxies when asked."""
+    hot = np.ascontiguousarray(hot, dtype=np.uint16)
+    dictionary = np.ascontiguousarray(dictionary, dtype=np.uint16)
+    hb, bs, hkv, hd = hot.shape
+    dh, a, hd2 = dictionary.shape
+    assert bs == 16 and hd2 == hd
+    src = np.ascontiguousarray(src, dtype=np.uint32)
+    dsta = None if dst is None else np.ascontiguousarray(dst, dtype=np.uint32)
+    if cold is None:
+        nb = int(max(src.max(initial=0), 0 if dsta is None else dsta.max(initial=0))) + 1
+        cold = np.zeros((nb, hkv, 16, 8) if head_blocked else (nb, 16, hkv, 8), dtype=np.uint16)
+    cold = np.ascontiguousarray(cold, dtype=np.uint16)
+    ent = np.zeros(src.size, dtype=np.float32) if entropy else None
+    rc = lib().or_encode_blocks(hot.ctypes.data, hb, hkv, hd, dictionary.ctypes.data, a, dh, src.ctypes.data,
+                                None if dsta is None else dsta.ctypes.data, src.size, cold.ctypes.data,
+                                cold.shape[0], int(head_blocked), None if ent is None else ent.ctypes.data)
+    if rc:
+        raise OracleError(f"or_encode_blocks failed: {rc}")
+    return (cold, ent) if entropy else cold
+
+
+def block_entropy(vals: np.ndarray) -> float:
+    """Variance proxy of one block's f16 values (distiller.rs:126-159)."""
+    v = np.ascontiguousarray(vals, dtype=np.uint16).ravel()
+    return float(lib().or_block_entropy(v.ctypes.data, v.size))

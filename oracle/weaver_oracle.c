@@ -24,13 +24,28 @@
  *   or_qlatent_f64    q . D^T in double (the identity of docs/YELLOWPAPER.md:84-92).
  *   or_gather_codes   SparseCode decode + atom gather (metal:182-216), bit-exact.
  *   or_h2f / or_f2h   IEEE-754 binary16 <-> binary32, round to nearest even.
+ *   or_encode_blocks  SparseCode encoder, distiller.rs:171-246: per token and kv
+ *                     head, f32 dot products with every atom summed in head-dim
+ *                     order from -0.0 (Rust >= 1.82 f32 sums; rust-version 1.85),
+ *                     a full sort by (score desc, atom index asc) with NaN last,
+ *                     the first 4 kept, coefficients f16(score).
+ *   or_block_entropy  variance proxy of distiller.rs:126-159: f64 mean and
+ *                     variance of a block's f16 values in memory order, as f32.
  *
  * Parity pins (all in tests/): the f16 conversions are checked against numpy
  * exhaustively; or_decode_f64 against closed forms (one token, equal scores,
  * unit codes, zero codes, empty pools) and the reference-derived known answers
  * (weaver.rs:369-396 inputs give 1.0 everywhere; bench.rs:113-120 inputs give
  * 0x201B); or_decode_ref32 against or_decode_f64; or_gather_codes against the
- * SparseCode byte known answer of types.rs:546-557.
+ * SparseCode byte known answer of types.rs:546-557; or_encode_blocks against
+ * the reference test distiller.rs:286-310 (zero dictionary -> indices 0,1,2,3),
+ * a one-hot dictionary (top-4 = the four largest components, coefficients their
+ * f16 values), a brute-force numpy restatement on small inputs and planted
+ * mistakes; or_block_entropy against distiller.rs:261-283 (zero block -> 0,
+ * uniform block -> 0) and numpy's f64 variance.  Parity unpinned: the order of
+ * NaN or -inf scores (the reference sorts them with partial_cmp -> Equal,
+ * leaving their order to sort_unstable_by; here they are never chosen and an
+ * unfilled slot is the zero code's).
  */
 #include <math.h>
 #include <pthread.h>
@@ -443,5 +458,97 @@ int or_gather_codes(const aw_sparse_code* codes, uint64_t n, const uint16_t* dic
             for (uint32_t j = 0; j < head_dim; ++j)
                 atoms[(4 * i + k) * head_dim + j] = a < dict_size ? dict[(uint64_t)a * head_dim + j] : 0xFFFFu;
         }
+    return AW_OK;
+}
+
+/* ------------------------------------------------------ SparseCode encoder */
+
+typedef struct {
+    float s;
+    uint32_t a;
+} or_scored;
+
+/* score descending, index ascending; NaN after every number */
+static int or_scored_cmp(const void* x, const void* y) {
+    const or_scored* p = (const or_scored*)x;
+    const or_scored* q = (const or_scored*)y;
+    const int pn = isnan(p->s), qn = isnan(q->s);
+    if (pn != qn) return pn - qn;
+    if (!pn && p->s != q->s) return p->s > q->s ? -1 : 1;
+    return p->a < q->a ? -1 : (p->a > q->a ? 1 : 0);
+}
+
+/* distiller.rs:126-159 */
+float or_block_entropy(const uint16_t* vals, uint64_t n) {
+    if (n == 0) return 0.0f;
+    int all_zero = 1;
+    for (uint64_t i = 0; i < n; ++i)
+        if (or_h2f(vals[i]) != 0.0f) {
+            all_zero = 0;
+            break;
+        }
+    if (all_zero) return 0.0f;
+    double sum = -0.0;
+    for (uint64_t i = 0; i < n; ++i) sum += (double)or_h2f(vals[i]);
+    const double mean = sum / (double)n;
+    double var = -0.0;
+    for (uint64_t i = 0; i < n; ++i) {
+        const double diff = (double)or_h2f(vals[i]) - mean;
+        var += diff * diff;
+    }
+    return (float)(var / (double)n);
+}
+
+/* distiller.rs:171-246 over a list of blocks: hot block src[i] -> cold block
+ * dst[i] (dst NULL: the same index).  cold is [cold_blocks][16][kv_heads], or
+ * [cold_blocks][kv_heads][16] when head_blocked. */
+int or_encode_blocks(const uint16_t* hot, uint64_t hot_blocks, uint32_t kv_heads, uint32_t head_dim,
+                     const uint16_t* dict, uint32_t dict_size, uint32_t dict_heads, const uint32_t* src,
+                     const uint32_t* dst, uint32_t n_blocks, aw_sparse_code* cold, uint64_t cold_blocks,
+                     int head_blocked, float* entropy) {
+    if (!kv_heads || !head_dim || !dict_size || (dict_heads != 1 && dict_heads != kv_heads)) return AW_E_INVALID_ARG;
+    or_scored* sc = (or_scored*)malloc(sizeof(or_scored) * dict_size);
+    float* x = (float*)malloc(sizeof(float) * head_dim);
+    if (!sc || !x) {
+        free(sc);
+        free(x);
+        return AW_E_INVALID_ARG;
+    }
+    const uint64_t per_block = (uint64_t)OR_BLOCK * kv_heads * head_dim;
+    for (uint32_t i = 0; i < n_blocks; ++i) {
+        const uint32_t b = src[i] & OR_REF_MASK, c = dst ? (dst[i] & OR_REF_MASK) : b;
+        if (b >= hot_blocks || c >= cold_blocks) {
+            free(sc);
+            free(x);
+            return AW_E_OOB;
+        }
+        const uint16_t* blk = hot + (uint64_t)b * per_block;
+        if (entropy) entropy[i] = or_block_entropy(blk, per_block);
+        for (uint32_t t = 0; t < OR_BLOCK; ++t)
+            for (uint32_t g = 0; g < kv_heads; ++g) {
+                const uint16_t* xv = blk + ((uint64_t)t * kv_heads + g) * head_dim;
+                for (uint32_t j = 0; j < head_dim; ++j) x[j] = or_h2f(xv[j]);
+                const uint16_t* D = dict + (uint64_t)(dict_heads == 1 ? 0 : g) * dict_size * head_dim;
+                for (uint32_t a = 0; a < dict_size; ++a) {
+                    float acc = -0.0f; /* compiled without FMA contraction: product, then sum */
+                    for (uint32_t j = 0; j < head_dim; ++j) acc = acc + x[j] * or_h2f(D[(uint64_t)a * head_dim + j]);
+                    sc[a].s = acc;
+                    sc[a].a = a;
+                }
+                qsort(sc, dict_size, sizeof(or_scored), or_scored_cmp);
+                aw_sparse_code code;
+                memset(&code, 0, sizeof code);
+                for (int k = 0; k < 4 && (uint32_t)k < dict_size; ++k) {
+                    if (isnan(sc[k].s) || sc[k].s == -INFINITY) break; /* never chosen: the zero code's slot */
+                    code.indices[k] = (uint16_t)sc[k].a;
+                    code.coeffs[k] = or_f2h(sc[k].s);
+                }
+                const uint64_t o = head_blocked ? ((uint64_t)c * kv_heads + g) * OR_BLOCK + t
+                                                : ((uint64_t)c * OR_BLOCK + t) * kv_heads + g;
+                cold[o] = code;
+            }
+    }
+    free(sc);
+    free(x);
     return AW_OK;
 }

@@ -1,0 +1,110 @@
+"""GPU parity of the SparseCode encoder (Distiller::distill_block,
+distiller.rs:171-246) and the block entropy proxy (distiller.rs:126-159)
+against the CPU oracle, bit for bit, through the C ABI (aw_encode_device,
+aw_encode) on cuda:0."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from aether_nexus_amd.types import AW_E_OOB, SPARSE_CODE_DTYPE
+from aether_nexus_amd.weaver import WeaverError, make_encode_desc
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def pools(seed, hot_blocks, hkv, hd, a, dh, zero_dict=False, scale=1.0):
+    rng = np.random.default_rng(seed)
+    hot = (rng.standard_normal((hot_blocks, 16, hkv, hd)) * scale).astype(np.float16).view(np.uint16)
+    if zero_dict:
+        d = np.zeros((dh, a, hd), np.uint16)
+    else:
+        dd = rng.standard_normal((dh, a, hd))
+        d = (dd / np.linalg.norm(dd, axis=-1, keepdims=True)).astype(np.float16).view(np.uint16)
+    return rng, hot, d
+
+
+def run_device(engine, stream, hot, d, src, dst, cold0, head_blocked, entropy):
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16) if a.dtype == np.uint16 else a).cuda()
+    hot_t, d_t = dev(hot), dev(d)
+    src_t = torch.from_numpy(np.asarray(src, np.uint32).view(np.int32)).cuda()
+    dst_t = None if dst is None else torch.from_numpy(np.asarray(dst, np.uint32).view(np.int32)).cuda()
+    cold_t = dev(cold0)
+    ent_t = torch.zeros(len(src), dtype=torch.float32, device="cuda:0") if entropy else None
+    hkv, hd = hot.shape[2], hot.shape[3]
+    desc = make_encode_desc(kv_heads=hkv, head_dim=hd, dict_size=d.shape[1], dict_heads=d.shape[0],
+                            hot_blocks=hot.shape[0], cold_blocks=cold0.shape[0], hot=hot_t, dictionary=d_t,
+                            src_blocks=src_t, dst_blocks=dst_t, cold=cold_t, entropy=ent_t,
+                            cold_head_blocked=head_blocked)
+    engine.encode_device(desc, stream=stream)
+    engine.check_device_errors(stream)
+    cold = cold_t.cpu().numpy().view(np.uint16)
+    return cold, (None if ent_t is None else ent_t.cpu().numpy())
+
+
+@pytest.mark.parametrize("hkv,hd,a,dh,head_blocked", [
+    (8, 128, 512, 8, False),    # the reference geometry (Llama8B, per-kv-head dictionary)
+    (8, 128, 4096, 1, False),   # the benchmark dictionary (4096 atoms, shared)
+    (2, 64, 256, 2, True),
+    (4, 64, 528, 1, True),      # dict_size not a power of two
+])
+def test_encode_device_bit_exact(engine, stream, hkv, hd, a, dh, head_blocked):
+    rng, hot, d = pools(11, 24, hkv, hd, a, dh)
+    src = rng.permutation(24)[:9]
+    dst = rng.permutation(30)[:9]
+    shape = (30, hkv, 16, 8) if head_blocked else (30, 16, hkv, 8)
+    cold0 = rng.integers(0, 65535, shape, dtype=np.uint16)
+    got, ent = run_device(engine, stream, hot, d, src, dst, cold0, head_blocked, True)
+    want, went = oracle.encode_blocks(hot, d, src, dst=dst, cold=cold0.copy(), head_blocked=head_blocked, entropy=True)
+    assert (got == want).all(), f"{int((got != want).any(axis=-1).sum())} codes differ"
+    assert (ent.view(np.uint32) == went.view(np.uint32)).all()
+
+
+def test_encode_zero_dictionary_picks_first_atoms(engine, stream):
+    """distiller.rs:286-310: equal scores keep atoms 0, 1, 2, 3."""
+    rng, hot, d = pools(12, 3, 8, 128, 512, 8, zero_dict=True)
+    cold0 = np.zeros((3, 16, 8, 8), np.uint16)
+    got, _ = run_device(engine, stream, hot, d, [0, 1, 2], None, cold0, False, False)
+    assert (got[..., :4] == np.array([0, 1, 2, 3], np.uint16)).all()
+    want = oracle.encode_blocks(hot, d, [0, 1, 2])
+    assert (got == want).all()
+
+
+def test_encode_entropy_edge_blocks(engine, stream):
+    """All-zero block -> 0 (also with -0.0), constant block -> 0, tiny and large values."""
+    rng, hot, d = pools(13, 4, 4, 64, 256, 4)
+    hot[0] = 0
+    hot[1] = 0x8000
+    hot[2] = np.float16(1.0).view(np.uint16)
+    hot[3] = (rng.standard_normal(hot[3].shape) * 1e-4).astype(np.float16).view(np.uint16)
+    cold0 = np.zeros((4, 16, 4, 8), np.uint16)
+    got, ent = run_device(engine, stream, hot, d, [0, 1, 2, 3], None, cold0, False, True)
+    _, went = oracle.encode_blocks(hot, d, [0, 1, 2, 3], entropy=True)
+    assert ent[0] == 0 and ent[1] == 0 and ent[2] == 0
+    assert (ent.view(np.uint32) == went.view(np.uint32)).all()
+
+
+def test_encode_host_slices(engine):
+    """aw_encode: copy in, encode, copy back; hot block b -> cold block b."""
+    rng, hot, d = pools(14, 6, 8, 128, 512, 8)
+    cold = np.zeros(6 * 16 * 8, dtype=SPARSE_CODE_DTYPE)
+    ent = engine.encode(hot, d, [4, 1], cold, kv_heads=8, head_dim=128, dict_size=512, dict_heads=8, entropy=True)
+    want, went = oracle.encode_blocks(hot, d, [4, 1], cold=np.zeros((6, 16, 8, 8), np.uint16), entropy=True)
+    assert (cold.view(np.uint16).reshape(6, 16, 8, 8) == want).all()
+    assert (ent.view(np.uint32) == went.view(np.uint32)).all()
+
+
+def test_encode_bad_block_reported(engine, stream):
+    """A source block past the hot pool is skipped and reported (AW_E_OOB);
+    the host form rejects it before launch."""
+    rng, hot, d = pools(15, 2, 4, 64, 256, 4)
+    cold0 = np.zeros((2, 16, 4, 8), np.uint16)
+    with pytest.raises(WeaverError) as e:
+        run_device(engine, stream, hot, d, [0, 7], None, cold0, False, False)
+    assert e.value.status == AW_E_OOB
+    cold = np.zeros((2, 16, 4, 8), np.uint16)
+    with pytest.raises(WeaverError) as e:
+        engine.encode(hot, d, [5], cold, kv_heads=4, head_dim=64, dict_size=256, dict_heads=4)
+    assert e.value.status == AW_E_OOB

@@ -344,3 +344,123 @@ def test_pack_codes_feeds_the_oracle():
     out = oracle.decode_f64(g, a)[0, 0, 0, 0]
     D = a["dictionary"].view(np.float16).astype(np.float64).reshape(g.dict_size, g.head_dim)
     np.testing.assert_allclose(out, D[3], rtol=1e-12)  # 16 identical tokens: their value
+
+
+# ---------------------------------------------------------------- encoder oracle
+# Pins of or_encode_blocks / or_block_entropy (distiller.rs:126-159, 171-246).
+
+def _rand_pool(rng, blocks, hkv, hd, scale=1.0):
+    return (rng.standard_normal((blocks, 16, hkv, hd)) * scale).astype(np.float16).view(np.uint16)
+
+
+def _unit_dict(rng, dh, a, hd):
+    d = rng.standard_normal((dh, a, hd))
+    return (d / np.linalg.norm(d, axis=-1, keepdims=True)).astype(np.float16).view(np.uint16)
+
+
+def test_encoder_zero_dictionary_reference_test():
+    """distiller.rs:286-310: with a zeroed dictionary every score is 0; the
+    stable order picks atoms 0, 1, 2, 3 (the reference test checks the first code)."""
+    rng = np.random.default_rng(3)
+    hot = _rand_pool(rng, 2, 8, 64)
+    d = np.zeros((8, 512, 64), np.uint16)
+    cold = oracle.encode_blocks(hot, d, [0, 1])
+    assert (cold[..., :4] == np.array([0, 1, 2, 3], np.uint16)).all()
+    assert ((cold[..., 4:] & 0x7FFF) == 0).all()  # coefficients are +-0
+
+
+def test_encoder_one_hot_dictionary():
+    """D[a] = e_a for a < head_dim, zero rows after: the score of atom a is the
+    token's component a, so the code holds the four largest components (their
+    f16 bits as coefficients) -- found here by a sort of the components."""
+    rng = np.random.default_rng(4)
+    hd, a = 64, 128
+    hot = _rand_pool(rng, 1, 4, hd)
+    d = np.zeros((1, a, hd), np.float16)
+    d[0, np.arange(hd), np.arange(hd)] = 1.0
+    cold = oracle.encode_blocks(hot, d.view(np.uint16), [0])
+    x = hot.view(np.float16).astype(np.float64)
+    for t in range(16):
+        for g in range(4):
+            comp = x[0, t, g]
+            scores = np.concatenate([comp, np.zeros(a - hd)])
+            order = sorted(range(a), key=lambda i: (-scores[i], i))[:4]
+            assert list(cold[0, t, g, :4]) == order
+            want = np.array([np.float16(scores[i]) for i in order]).view(np.uint16)
+            got = cold[0, t, g, 4:]
+            # exact: each score is one product x*1 plus zeros
+            assert (np.where(want == 0x8000, 0, want) == np.where(got == 0x8000, 0, got)).all()
+
+
+def test_encoder_matches_f64_projection():
+    """Independent formulation: numpy f64 dot products.  Where the 4th and 5th
+    largest scores differ by more than the f32 summation error bound the four
+    indices match, and every coefficient is within one f16 ulp of f16(f64 score)."""
+    rng = np.random.default_rng(5)
+    hkv, hd, a = 2, 64, 256
+    hot = _rand_pool(rng, 3, hkv, hd)
+    d = _unit_dict(rng, hkv, a, hd)
+    cold = oracle.encode_blocks(hot, d, [2, 0])
+    x = hot.view(np.float16).astype(np.float64)
+    D = d.view(np.float16).astype(np.float64)
+    checked = 0
+    for blk in (2, 0):
+        for t in range(16):
+            for g in range(hkv):
+                s = D[g] @ x[blk, t, g]
+                order = np.lexsort((np.arange(a), -s))
+                bound = 2 * hd * 2.0 ** -24 * (np.abs(D[g]) @ np.abs(x[blk, t, g])).max()
+                if s[order[3]] - s[order[4]] > bound:
+                    assert list(cold[blk, t, g, :4]) == list(order[:4])
+                    checked += 1
+                got = cold[blk, t, g, 4:].view(np.float16).astype(np.float64)
+                want = np.array([np.float16(s[i]) for i in cold[blk, t, g, :4]], dtype=np.float64)
+                ulp = np.spacing(np.abs(want).astype(np.float16)).astype(np.float64)
+                assert (np.abs(got - want) <= ulp).all()
+    assert checked > 60  # of 64 token-heads
+
+
+def test_encoder_planted_mistake_is_caught():
+    """The f64 check above must fail for a plausible mistake: the other kv head's
+    dictionary (a swapped head index)."""
+    rng = np.random.default_rng(6)
+    hkv, hd, a = 2, 64, 128
+    hot = _rand_pool(rng, 1, hkv, hd)
+    d = _unit_dict(rng, hkv, a, hd)
+    cold = oracle.encode_blocks(hot, d[::-1].copy(), [0])  # heads swapped
+    x = hot.view(np.float16).astype(np.float64)
+    D = d.view(np.float16).astype(np.float64)
+    mismatches = sum(list(cold[0, t, g, :4]) != list(np.lexsort((np.arange(a), -(D[g] @ x[0, t, g])))[:4])
+                     for t in range(16) for g in range(hkv))
+    assert mismatches > 16
+
+
+def test_encoder_layouts_and_destinations():
+    """Codes of hot block src[i] land in cold block dst[i] (default: the same
+    index, distiller.rs:177), head-blocked order is the same codes transposed, and
+    blocks not named are left as they were."""
+    rng = np.random.default_rng(7)
+    hot = _rand_pool(rng, 4, 4, 64)
+    d = _unit_dict(rng, 4, 128, 64)
+    base = oracle.encode_blocks(hot, d, [0, 1, 2, 3])
+    pre = rng.integers(0, 65535, (6, 16, 4, 8), dtype=np.uint16)
+    out = oracle.encode_blocks(hot, d, [3, 1], dst=[5, 0], cold=pre.copy())
+    assert (out[5] == base[3]).all() and (out[0] == base[1]).all()
+    assert (out[[1, 2, 3, 4]] == pre[[1, 2, 3, 4]]).all()
+    hb = oracle.encode_blocks(hot, d, [0, 1, 2, 3], head_blocked=True)
+    assert (hb == base.transpose(0, 2, 1, 3)).all()
+
+
+def test_entropy_reference_tests_and_numpy():
+    """distiller.rs:261-283: an all-zero block gives 0 and a block of 1.0 gives a
+    variance below 1e-3 (exactly 0).  Random blocks agree with numpy's f64
+    variance to 1e-12 relative before the final f32 rounding."""
+    assert oracle.block_entropy(np.zeros(512, np.uint16)) == 0.0
+    assert oracle.block_entropy(np.full(512, np.float16(1.0).view(np.uint16))) == 0.0
+    assert oracle.block_entropy(np.array([0x8000, 0], np.uint16)) == 0.0  # -0 counts as zero
+    rng = np.random.default_rng(8)
+    for scale in (1.0, 0.01, 100.0):
+        v = (rng.standard_normal(16 * 8 * 128) * scale).astype(np.float16)
+        got = oracle.block_entropy(v.view(np.uint16))
+        want = np.float32(np.var(v.astype(np.float64)))
+        assert abs(float(got) - float(want)) <= 2 * np.spacing(want)
