@@ -56,6 +56,7 @@ def parse():
     p.add_argument("--stage-sweep", action="store_true", help="per-kernel times at every batch size")
     p.add_argument("--cold-layout", choices=("reference", "head_blocked"), default="reference",
                    help="cold pool order of the main measurement (reference: [blocks][16][kv_heads])")
+    p.add_argument("--skip-encoder", action="store_true", help="skip the SparseCode encoder measurement")
     p.add_argument("--skip-alt-layout", action="store_true",
                    help="skip the extra B-max run with the other cold pool order (for clean profiles)")
     p.add_argument("--rocpd-summary", metavar="DB", help="print a per-kernel summary of a rocprofv3 database and exit")
@@ -179,6 +180,62 @@ def cpu_baseline(seconds: float, seed: int):
             "sample": f"{n} B=1 decode steps of hot 2048 + cold 32768 (32q/8kv d128, 4096 atoms, q_latent "
                       f"computed on the CPU) in {el:.1f} s, fp32 restatement of weaver_kernel.metal, "
                       f"{threads} threads"}
+
+
+VALU_FP32_FMA_TFLOPS = 78.6  # 256 CUs x 128 fp32 FMA lanes x 2.4 GHz x 2 (no packed fp32 here)
+
+
+def encoder_bench(engine, seed, reps, cpu_blocks):
+    """SparseCode encoder (distiller.rs:171-246) on the reference geometry
+    (Llama8B: 8 kv heads, head_dim 128, 512 atoms per kv head) over 8192 hot
+    blocks, the most one find_candidates pass hands over (distiller.rs:107), with
+    the entropy proxy; the CPU oracle is timed on `cpu_blocks` of them."""
+    import numpy as np
+    import torch
+    from aether_nexus_amd.weaver import make_encode_desc
+    hkv, hd, a, nb = 8, 128, 512, 8192
+    g = torch.Generator(device="cuda:0").manual_seed(seed)
+    hot = torch.randn((nb, 16, hkv, hd), generator=g, device="cuda:0").to(torch.float16)
+    dd = torch.randn((hkv, a, hd), generator=g, device="cuda:0", dtype=torch.float64)
+    dic = (dd / dd.norm(dim=-1, keepdim=True)).to(torch.float16)
+    src = torch.randperm(nb, generator=g, device="cuda:0").to(torch.int32)
+    cold = torch.zeros((nb, 16, hkv, 8), dtype=torch.int16, device="cuda:0")
+    ent = torch.zeros(nb, dtype=torch.float32, device="cuda:0")
+    desc = make_encode_desc(kv_heads=hkv, head_dim=hd, dict_size=a, dict_heads=hkv, hot_blocks=nb, cold_blocks=nb,
+                            hot=hot, dictionary=dic, src_blocks=src, cold=cold, entropy=ent)
+    st = torch.cuda.current_stream()
+    engine.encode_device(desc, stream=st.cuda_stream)
+    engine.check_device_errors(st.cuda_stream)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    ev[0].record(st)
+    for _ in range(reps):
+        engine.encode_device(desc, stream=st.cuda_stream)
+    ev[1].record(st)
+    torch.cuda.synchronize()
+    ms = ev[0].elapsed_time(ev[1]) / reps
+    tok_heads = nb * 16 * hkv
+    flops = 2.0 * tok_heads * a * hd
+    # CPU oracle on the first blocks of the same pools (one thread), checked against the GPU's codes.
+    from oracle import oracle
+    hot_h = hot.cpu().numpy().view(np.uint16)
+    dic_h = dic.cpu().numpy().view(np.uint16)
+    src_h = src.cpu().numpy().astype(np.uint32)[:cpu_blocks]
+    t0 = time.perf_counter()
+    want = oracle.encode_blocks(hot_h, dic_h, src_h, cold=np.zeros((nb, 16, hkv, 8), np.uint16))
+    cpu_s = time.perf_counter() - t0
+    got = cold.cpu().numpy().view(np.uint16)
+    same = bool((got[src_h] == want[src_h]).all())
+    return {"workload": f"{nb} blocks x 16 tokens x {hkv} kv heads, head_dim {hd}, {a} atoms per kv head, "
+                        "entropy proxy included",
+            "ms_per_call": round(ms, 4), "blocks_per_s": round(nb / (ms * 1e-3), 1),
+            "token_heads_per_s": round(tok_heads / (ms * 1e-3), 1),
+            "achieved_tflops": round(flops / (ms * 1e-3) / 1e12, 2),
+            "roofline": {"bound": "valu", "peak_tflops": VALU_FP32_FMA_TFLOPS,
+                         "frac": round(flops / (ms * 1e-3) / 1e12 / VALU_FP32_FMA_TFLOPS, 4),
+                         "note": "one exact fp32 FMA per (token, kv head, atom, dim): the reference's summation order"},
+            "cpu_baseline": {"value": round(cpu_blocks / cpu_s, 2), "unit": "blocks/s", "cores": 1, "kind": "port",
+                             "sample": f"{cpu_blocks} blocks through the oracle's restatement of distiller.rs:171-246"},
+            "codes_match_cpu": same}
 
 
 def reference_bench_config(engine, seed, steps):
@@ -428,6 +485,9 @@ def main():
         del rh
         torch.cuda.empty_cache()
     ref_cfg = reference_bench_config(engine, args.seed, 200)
+    enc = None if args.skip_encoder else encoder_bench(engine, args.seed, 5, 8 if args.no_cpu else 32)
+    if enc:
+        log(json.dumps({"encoder": enc}))
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds, args.seed)
 
     result = {
@@ -456,6 +516,7 @@ def main():
         "stages_serial_us": serial_us,
         "roofline": roofline,
         "other_cold_layout": alt,
+        "encoder": enc,
         "cpu_baseline": cpu,
         "reference_bench_config": ref_cfg,
     }
