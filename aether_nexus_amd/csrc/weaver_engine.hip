@@ -165,7 +165,8 @@ int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, const uint32_t 
         o.info.hot_tokens_per_split = (uint32_t)tps;
         o.info.hot_splits = cdiv(n_tok, tps);
     }
-    // Cold: one work-group per CU at a time (LDS bound); >= 1024 tokens per split.
+    // Cold: one work-group per CU at a time (LDS bound), one round of work-groups;
+    // >= 1024 tokens per split.
     if (d->cold_count > 0) {
         o.rc = pick_rc(R, A, max_lds);
         if (aw::cold_smem_bytes(A, (int)o.rc, 1024) > max_lds) {
@@ -176,11 +177,11 @@ int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, const uint32_t 
         o.n_chunks = cdiv(R, o.rc);
         const uint64_t n_tok = (uint64_t)d->cold_count * kBlock;
         const uint64_t items = n_lbg * o.n_chunks;
-        uint64_t want = cdiv((uint64_t)n_cu * 2, items);
-        // >= 1024 tokens per split, and bin partials (A*rc*4 bytes per split) at most
-        // twice the code bytes of the sequence.
+        uint64_t want = cdiv((uint64_t)n_cu, items);
+        // >= 1024 tokens per split, and bin partials (A*rc*4 bytes per split, written here
+        // and read again by the finish) at most half the code bytes of the sequence.
         uint64_t cap = std::max<uint64_t>(1, std::min<uint64_t>(cdiv(n_tok, 1024),
-                                                                (2 * n_tok * 16) / ((uint64_t)A * o.rc * 4)));
+                                                                (n_tok * 16) / ((uint64_t)A * o.rc * 4 * 2)));
         uint64_t S = std::max<uint64_t>(1, std::min<uint64_t>({want, cap, (uint64_t)aw::kMaxSplits}));
         uint64_t tps = align_up(cdiv(n_tok, S), 16);
         // The split's block refs live in LDS too: shorten splits until they fit.
