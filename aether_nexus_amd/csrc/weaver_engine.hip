@@ -174,15 +174,22 @@ int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, const uint32_t 
                     aw::cold_smem_bytes(A, (int)o.rc, 1024), max_lds);
             return AW_E_UNSUPPORTED;
         }
-        o.n_chunks = cdiv(R, o.rc);
         const uint64_t n_tok = (uint64_t)d->cold_count * kBlock;
-        const uint64_t items = n_lbg * o.n_chunks;
-        uint64_t want = cdiv((uint64_t)n_cu, items);
+        // Splits per (layer, sequence, kv head, row chunk) item for a chunk of rc rows:
         // >= 1024 tokens per split, and bin partials (A*rc*4 bytes per split, written here
         // and read again by the finish) at most half the code bytes of the sequence.
-        uint64_t cap = std::max<uint64_t>(1, std::min<uint64_t>(cdiv(n_tok, 1024),
-                                                                (n_tok * 16) / ((uint64_t)A * o.rc * 4 * 2)));
-        uint64_t S = std::max<uint64_t>(1, std::min<uint64_t>({want, cap, (uint64_t)aw::kMaxSplits}));
+        auto splits_for = [&](uint32_t rc) {
+            const uint64_t items = n_lbg * cdiv(R, rc);
+            const uint64_t want = cdiv((uint64_t)n_cu, items);
+            const uint64_t cap = std::max<uint64_t>(
+                1, std::min<uint64_t>(cdiv(n_tok, 1024), (n_tok * 16) / ((uint64_t)A * rc * 4 * 2)));
+            return std::max<uint64_t>(1, std::min<uint64_t>({want, cap, (uint64_t)aw::kMaxSplits}));
+        };
+        // Too few work-groups to fill the CUs: smaller row chunks (each item then reads
+        // the codes again, but does less work per token and allows more splits).
+        while (o.rc > 1 && n_lbg * cdiv(R, o.rc) * splits_for(o.rc) < (uint64_t)n_cu) o.rc /= 2;
+        o.n_chunks = cdiv(R, o.rc);
+        uint64_t S = splits_for(o.rc);
         uint64_t tps = align_up(cdiv(n_tok, S), 16);
         // The split's block refs live in LDS too: shorten splits until they fit.
         while (tps > 1024 && aw::cold_smem_bytes(A, (int)o.rc, (uint32_t)tps) > max_lds) {

@@ -90,6 +90,8 @@ class Runner:
         self.descs = [W.device_desc(self.wl, self.out, copy=c, cold_head_blocked=self.cold_hb)
                       for c in range(geom.copies)]
         self.stream = torch.cuda.Stream()
+        # The inputs were written on the current stream: order the side stream after them.
+        self.stream.wait_stream(torch.cuda.current_stream())
         self.graphs = None
         sh = self.stream.cuda_stream
         with torch.cuda.stream(self.stream):

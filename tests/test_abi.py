@@ -146,6 +146,23 @@ def test_plan_splits_and_workspace():
     assert e.value.status == AW_E_UNSUPPORTED
 
 
+def test_plan_small_batch_fills_cus():
+    """Few sequences: the cold plan halves the row chunk and adds splits until the
+    work-groups (items x splits) cover the 256 CUs, within the partial-bins bound
+    (A*rc*4 bytes per split <= half the sequence's code bytes)."""
+    from aether_nexus_amd.weaver import make_desc
+    for B, want_rc, want_splits in ((1, 1, 8), (4, 2, 4), (16, 4, 2), (64, 4, 1)):
+        g = W.hot_cold(batch=B)
+        info = plan(make_desc(layers=1, batch=B, queries=1, q_heads=32, kv_heads=8, head_dim=128, dict_size=4096,
+                              dict_heads=1, hot_count=g.hot_count, cold_count=g.cold_count,
+                              refs_stride=g.refs_stride, hot_blocks=g.hot_blocks, cold_blocks=g.cold_blocks,
+                              q=1, out=1))
+        assert (info.cold_row_chunk, info.cold_splits) == (want_rc, want_splits), B
+        items = B * 8 * (4 // info.cold_row_chunk)
+        assert items * info.cold_splits >= 256 or info.cold_row_chunk == 1
+        assert 4096 * info.cold_row_chunk * 4 * 2 <= info.cold_tokens_per_split * info.cold_splits * 16
+
+
 def test_plan_flags():
     """The head-blocked cold layout plans like the reference layout; unknown flag bits are rejected."""
     from aether_nexus_amd.types import AW_E_INVALID_ARG, AW_F_CAUSAL, AW_F_COLD_HEAD_BLOCKED
