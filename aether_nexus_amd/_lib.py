@@ -22,7 +22,7 @@ _sz = ctypes.c_size_t
 _u32 = ctypes.c_uint32
 _u64 = ctypes.c_uint64
 
-#: Every function declared in include/aether_weaver.h with its ctypes signature.
+#: Every function declared in include/*.h with its ctypes signature.
 SIGNATURES = {
     "aw_abi_version": (_u32, []),
     "aw_abi_struct_sizes": (None, [ctypes.POINTER(_sz)]),
@@ -44,6 +44,27 @@ SIGNATURES = {
     "aw_abi_encode_desc_size": (_sz, []),
     "aw_encode_device": (_c_int, [_vp, _vp, _vp]),
     "aw_encode": (_c_int, [_vp, _vp, _sz, _vp, _sz, _u32, _u32, _u32, _u32, _vp, _sz, _vp, _sz, _vp]),
+    "aw_block_entropy_device": (_c_int, [_vp, _vp, _u64, _u32, _u32, _vp, _u32, _vp, _vp]),
+    # include/aether_fabric.h
+    "aw_model_dims_preset": (_c_int, [ctypes.c_char_p, _vp]),
+    "aw_fabric_regions_compute": (_c_int, [_vp, _vp]),
+    "aw_weaver_params_from_loom": (_c_int, [_vp, _vp, _vp]),
+    "aw_fabric_create_genesis": (_c_int, [ctypes.c_char_p, _vp, ctypes.c_char_p, _sz]),
+    "aw_fabric_boot": (_c_int, [ctypes.c_char_p, _vp, _vp, ctypes.POINTER(_vp), ctypes.c_char_p, _sz]),
+    "aw_fabric_close": (None, [_vp]),
+    "aw_fabric_last_error": (ctypes.c_char_p, [_vp]),
+    "aw_fabric_regions_of": (_c_int, [_vp, _vp]),
+    "aw_fabric_looms": (_c_int, [_vp, _vp]),
+    "aw_fabric_region": (_c_int, [_vp, _u32, _c_int, ctypes.POINTER(_vp), ctypes.POINTER(_u64)]),
+    "aw_fabric_checkpoint": (_c_int, [_vp]),
+    "aw_fabric_force_checkpoint": (_c_int, [_vp]),
+    "aw_fabric_is_dirty": (_c_int, [_vp]),
+    "aw_fabric_attach_device": (_c_int, [_vp, _c_int, _u32]),
+    "aw_fabric_device_region": (_c_int, [_vp, _u32, ctypes.POINTER(_vp), ctypes.POINTER(_u64)]),
+    "aw_fabric_push": (_c_int, [_vp, _u32, _u64, _u64]),
+    "aw_fabric_pull": (_c_int, [_vp, _u32, _u64, _u64]),
+    "aw_fabric_detach_device": (_c_int, [_vp]),
+    "aw_fabric_distill": (_c_int, [_vp, _vp, ctypes.c_float, _vp, ctypes.POINTER(_u32)]),
 }
 
 _cache: dict[str, ctypes.CDLL] = {}

@@ -14,8 +14,8 @@ from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
-SOURCES = [PKG / "csrc" / "weaver_engine.hip"]
-DEPS = [PKG / "csrc" / "weaver_kernels.hpp", ROOT / "include" / "aether_weaver.h"]
+SOURCES = [PKG / "csrc" / "weaver_engine.hip", PKG / "csrc" / "fabric.hip"]
+DEPS = [PKG / "csrc" / "weaver_kernels.hpp", ROOT / "include" / "aether_weaver.h", ROOT / "include" / "aether_fabric.h"]
 OUT = PKG / "libaether_weaver.so"
 ARCH = "gfx950"
 

@@ -14,7 +14,7 @@
 #include <string>
 #include <vector>
 
-#include "../../include/aether_weaver.h"
+#include "../../include/aether_fabric.h"
 #include "weaver_kernels.hpp"
 
 static_assert(sizeof(aw_sparse_code) == 16, "SparseCode is 16 bytes (types.rs:227)");
@@ -684,6 +684,11 @@ const char* aw_status_string(int status) {
     case AW_E_HIP: return "HIP runtime error";
     case AW_E_LOAD: return "kernels not available for this device";
     case AW_E_UNSUPPORTED: return "unsupported request";
+    case AW_E_IO: return "file I/O failed";
+    case AW_E_BAD_MAGIC: return "invalid magic bytes";
+    case AW_E_VERSION: return "version mismatch";
+    case AW_E_TOO_SMALL: return "file too small";
+    case AW_E_SIGNATURE: return "signature verification failed";
     default: return "unknown status";
     }
 }
@@ -1059,6 +1064,30 @@ int encode_device(aw_engine* e, const aw_encode_desc* d, hipStream_t st) {
 int aw_encode_device(aw_engine* e, const aw_encode_desc* desc, void* stream) {
     if (!e || !desc) return AW_E_INVALID_ARG;
     return encode_device(e, desc, (hipStream_t)stream); // NULL is HIP's null stream
+}
+
+int aw_block_entropy_device(aw_engine* e, const uint16_t* hot, uint64_t hot_blocks, uint32_t kv_heads,
+                            uint32_t head_dim, const uint32_t* blocks, uint32_t n_blocks, float* entropy,
+                            void* stream) {
+    if (!e) return AW_E_INVALID_ARG;
+    if (!n_blocks) return AW_OK;
+    if (!hot || !entropy || !hot_blocks || !kv_heads || !head_dim)
+        return fail(e, AW_E_INVALID_ARG, "hot, entropy, hot_blocks, kv_heads and head_dim are required");
+    if ((uintptr_t)hot & 15u) return fail(e, AW_E_ALIGN, "hot pool pointer is not 16-byte aligned");
+    if (n_blocks >= (1u << 27)) return fail(e, AW_E_UNSUPPORTED, "n_blocks %u too large", n_blocks);
+    AW_HIP(e, hipSetDevice(e->device));
+    aw::EncodeArgs a{};
+    a.hot = hot;
+    a.src = blocks;
+    a.entropy = entropy;
+    a.err = e->err;
+    a.kv_heads = kv_heads;
+    a.n_blocks = n_blocks;
+    a.hot_blocks = hot_blocks;
+    hipLaunchKernelGGL(aw::entropy_kernel, dim3(cdiv(n_blocks, 64)), dim3(64), 0, (hipStream_t)stream, a,
+                       head_dim);
+    AW_HIP(e, hipGetLastError());
+    return AW_OK;
 }
 
 int aw_encode(aw_engine* e, const uint16_t* hot, size_t n_hot, const uint16_t* dict, size_t n_dict,

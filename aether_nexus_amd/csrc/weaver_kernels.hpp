@@ -1691,16 +1691,17 @@ __global__ __launch_bounds__(kEncThreads) void encode_kernel(EncodeArgs a) {
     a.cold[(uint64_t)c * kBlockTokens * a.kv_heads + tt * a.s_tok + g * a.s_head] = code;
 }
 
-// Variance proxy of each encoded block (distiller.rs:126-159): one lane per
+// Variance proxy of each listed block (distiller.rs:126-159): one lane per
 // block runs the reference's loops in memory order, in f64, with no fused
 // multiply-add (the reference squares, then adds), and returns f32.  An
-// all-zero block gives 0.
+// all-zero block gives 0.  Without a block list (src null) lane i takes block i.
 __global__ __launch_bounds__(64) void entropy_kernel(EncodeArgs a, uint32_t head_dim) {
 #pragma clang fp contract(off)
     const uint32_t i = blockIdx.x * 64 + threadIdx.x;
     if (i >= a.n_blocks) return;
-    const uint32_t b = a.src[i] & kRefMask;
-    if (b >= a.hot_blocks) { // reported by encode_kernel
+    const uint32_t b = a.src ? (a.src[i] & kRefMask) : i;
+    if (b >= a.hot_blocks) {
+        flag_error(a.err, kErrHotRef);
         a.entropy[i] = 0.0f;
         return;
     }

@@ -180,6 +180,12 @@ AW_E_OOB = -3
 AW_E_HIP = -4
 AW_E_LOAD = -5
 AW_E_UNSUPPORTED = -6
+# include/aether_fabric.h: one code per FabricError variant (nexus-core/src/types.rs:430-454)
+AW_E_IO = -7
+AW_E_BAD_MAGIC = -8
+AW_E_VERSION = -9
+AW_E_TOO_SMALL = -10
+AW_E_SIGNATURE = -11
 
 STAGES = ("project", "hot", "cold", "finish", "merge")
 
@@ -231,3 +237,47 @@ class PlanInfo(ctypes.Structure):
 
 STRUCT_SIZES = (ctypes.sizeof(CSparseCode), ctypes.sizeof(WeaverParams),
                 ctypes.sizeof(DecodeDesc), ctypes.sizeof(PlanInfo))
+
+
+# ---------------------------------------------------------------- the .aether Fabric
+
+REGION_IDS = {"weights": 0, "hot": 1, "cold": 2, "dict": 3, "looms": 4, "radix": 5, "obs": 6, "trace": 7}
+PERSONAS = ("Planner", "Coder", "Critic", "Reviewer")  # types.rs:293-300
+
+
+class ModelDims(ctypes.Structure):
+    """``aw_model_dims``: the ModelDims constants (nexus-core/src/types.rs:150-164) as fields."""
+
+    _fields_ = [(n, ctypes.c_uint32) for n in (
+        "layers", "q_heads", "kv_heads", "head_dim", "hidden_size", "intermediate_size", "vocab_size",
+        "block_size", "sparsity_k", "dict_size")]
+
+
+class FabricRegions(ctypes.Structure):
+    """``aw_fabric_regions``: FabricRegions (nexus-core/src/fabric.rs:74-117)."""
+
+    _fields_ = [(n, ctypes.c_uint64) for n in (
+        "weights_offset", "weights_size", "hot_pool_offset", "hot_pool_size", "cold_pool_offset",
+        "cold_pool_size", "dict_offset", "dict_size", "looms_offset", "looms_size", "radix_offset",
+        "radix_size", "obs_offset", "obs_size", "trace_offset", "trace_size", "total_size")]
+
+    def as_dict(self) -> dict:
+        return {n: getattr(self, n) for n, _ in self._fields_}
+
+
+class LoomDescriptor(ctypes.Structure):
+    """``aw_loom_descriptor``: LoomDescriptor (nexus-core/src/types.rs:311-328), 32 bytes."""
+
+    _fields_ = [
+        ("persona", ctypes.c_uint8), ("_pad0", ctypes.c_uint8 * 3),
+        ("hot_count", ctypes.c_uint32), ("cold_count", ctypes.c_uint32),
+        ("hot_refs_offset", ctypes.c_uint32), ("cold_refs_offset", ctypes.c_uint32),
+        ("token_pos", ctypes.c_uint32), ("_pad", ctypes.c_uint32 * 2),
+    ]
+
+    def as_tuple(self) -> tuple:
+        return (self.persona, self.hot_count, self.cold_count, self.hot_refs_offset, self.cold_refs_offset,
+                self.token_pos)
+
+
+assert ctypes.sizeof(LoomDescriptor) == 32 and ctypes.sizeof(ModelDims) == 40

@@ -208,6 +208,14 @@ class WeaverEngine:
         rc = self._lib.aw_encode_device(self._h, ctypes.byref(desc), _stream(stream))
         self._check(rc, "encode_device")
 
+    def block_entropy_device(self, hot, hot_blocks: int, kv_heads: int, head_dim: int, blocks, n_blocks: int,
+                             entropy, stream: Optional[int] = None) -> None:
+        """Variance proxy of hot blocks on the device (evaluate_entropy's loop,
+        distiller.rs:97-120); ``blocks`` None scans blocks 0 .. n_blocks-1."""
+        rc = self._lib.aw_block_entropy_device(self._h, _ptr(hot), hot_blocks, kv_heads, head_dim, _ptr(blocks),
+                                               n_blocks, _ptr(entropy), _stream(stream))
+        self._check(rc, "block_entropy_device")
+
     def encode(self, hot_pool, dictionary, blocks, cold_pool, kv_heads: int, head_dim: int, dict_size: int,
                dict_heads: int, entropy: bool = False):
         """Host-slice encoder (copy in, encode, copy out, wait): hot block b of

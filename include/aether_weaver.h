@@ -302,6 +302,17 @@ int aw_encode(aw_engine* engine,
               const uint32_t* blocks, size_t n_blocks,
               aw_sparse_code* cold, size_t n_cold, float* entropy);
 
+/* The variance proxy of hot blocks alone, asynchronous on `hip_stream`:
+ * entropy[i] = the proxy of hot block blocks[i] & 0x7FFFFFFF (blocks NULL:
+ * block i), as aw_encode_device computes it; a block index >= hot_blocks gives
+ * 0 and sets the engine's out-of-range flag (aw_engine_check_device_errors).
+ * `hot` holds [hot_blocks][16][kv_heads][head_dim] f16, 16-byte aligned.
+ * Replaces the per-block loop of Distiller::evaluate_entropy
+ * (distiller.rs:97-120). */
+int aw_block_entropy_device(aw_engine* engine, const uint16_t* hot, uint64_t hot_blocks, uint32_t kv_heads,
+                            uint32_t head_dim, const uint32_t* blocks, uint32_t n_blocks, float* entropy,
+                            void* hip_stream);
+
 /* Per-stage kernel timing with HIP events recorded on the stream each kernel
  * runs on: every launch is bracketed by a pair of events.  AW_PROFILE_ON keeps
  * the pipeline as it runs unprofiled (the hot kernel on the engine's side

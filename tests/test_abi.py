@@ -1,5 +1,5 @@
 """The C ABI without a GPU (CPU only): the library loads, exports every
-function include/aether_weaver.h declares, its structs match the ctypes
+function include/*.h declares, its structs match the ctypes
 mirrors, and the host-side validation and planning behave as documented.
 No compute entry point is called."""
 from __future__ import annotations
@@ -17,19 +17,22 @@ from aether_nexus_amd.types import (AW_E_ALIGN, AW_E_INVALID_ARG, AW_E_OOB, AW_E
                                     STRUCT_SIZES, DecodeDesc, PlanInfo, WeaverParams)
 from aether_nexus_amd.weaver import WeaverError, plan, validate_params
 
-HEADER = Path(__file__).resolve().parents[1] / "include" / "aether_weaver.h"
+HEADERS = sorted((Path(__file__).resolve().parents[1] / "include").glob("*.h"))
 
 
 def declared_functions():
-    text = HEADER.read_text()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(aw_[a-z0-9_]+)\s*\(", text)))
+    names = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        text = re.sub(r"#define[^\n]*", "", text)
+        names |= set(re.findall(r"\b(aw_[a-z0-9_]+)\s*\(", text))
+    return sorted(names)
 
 
 def test_library_exports_every_declared_function():
     lib = _lib.load()
     names = declared_functions()
-    assert len(names) >= 17
+    assert len(HEADERS) >= 2 and len(names) >= 40
     for n in names:
         assert hasattr(lib, n), f"{n} declared in the header but not exported"
     assert set(names) == set(_lib.SIGNATURES), "ctypes signatures out of sync with the header"
