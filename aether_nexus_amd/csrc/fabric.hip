@@ -39,7 +39,7 @@ constexpr uint64_t kLimit = 1ull << 62;
 static_assert(sizeof(aw_loom_descriptor) == 32, "LoomDescriptor is 32 bytes (repr(C))");
 
 // Staging for host <-> device copies: two pinned buffers, filled / drained by
-// up to kIoThreads threads with pread / pwrite on the file while the DMA engine
+// up to kIoThreads threads copying through the mapping while the DMA engine
 // moves the other buffer.
 constexpr uint64_t kStageBytes = 32ull << 20;
 constexpr unsigned kIoThreads = 8;
@@ -145,18 +145,7 @@ bool region_span(const aw_fabric_regions& r, uint32_t region, uint64_t* off, uin
     }
 }
 
-// Whole-range pread / pwrite with EINTR and short-transfer handling.
-bool pread_all(int fd, void* dst, uint64_t n, uint64_t off) {
-    uint8_t* p = (uint8_t*)dst;
-    while (n) {
-        const ssize_t k = pread(fd, p, (size_t)std::min<uint64_t>(n, 1ull << 30), (off_t)off);
-        if (k < 0 && errno == EINTR) continue;
-        if (k <= 0) return false;
-        p += k, off += (uint64_t)k, n -= (uint64_t)k;
-    }
-    return true;
-}
-
+// Whole-range pwrite with EINTR and short-transfer handling.
 bool pwrite_all(int fd, const void* src, uint64_t n, uint64_t off) {
     const uint8_t* p = (const uint8_t*)src;
     while (n) {
@@ -168,26 +157,31 @@ bool pwrite_all(int fd, const void* src, uint64_t n, uint64_t off) {
     return true;
 }
 
-// Runs pread (to_host false) or pwrite (true) of [off, off + n) of the file
-// against buf on up to kIoThreads threads.
-bool file_io(int fd, uint8_t* buf, uint64_t n, uint64_t off, bool write) {
+// Copies [off, off + n) of the shared mapping into buf (to_map false) or buf
+// into the mapping (true) on up to kIoThreads threads.  Through the mapping
+// rather than with pread / pwrite: concurrent pwrites to one file serialise on
+// its inode lock (write-back of the 64 MiB Llama8B cold pool: ~12 GB/s with
+// pwrite against ~37 GB/s with memcpy).
+void map_copy(uint8_t* map, uint8_t* buf, uint64_t n, uint64_t off, bool to_map) {
     const unsigned t = (unsigned)std::max<uint64_t>(1, std::min<uint64_t>(kIoThreads, n / kIoMinPerThread));
-    if (t == 1) return write ? pwrite_all(fd, buf, n, off) : pread_all(fd, buf, n, off);
+    if (t == 1) {
+        if (to_map) memcpy(map + off, buf, n);
+        else memcpy(buf, map + off, n);
+        return;
+    }
     const uint64_t per = align_up((n + t - 1) / t, 4096);
-    std::atomic<bool> ok{true};
     std::vector<std::thread> th;
     th.reserve(t);
     for (unsigned i = 0; i < t; ++i) {
         const uint64_t a = (uint64_t)i * per;
         if (a >= n) break;
         const uint64_t len = std::min(per, n - a);
-        th.emplace_back([=, &ok] {
-            const bool r = write ? pwrite_all(fd, buf + a, len, off + a) : pread_all(fd, buf + a, len, off + a);
-            if (!r) ok = false;
+        th.emplace_back([=] {
+            if (to_map) memcpy(map + off + a, buf + a, len);
+            else memcpy(buf + a, map + off + a, len);
         });
     }
     for (auto& x : th) x.join();
-    return ok;
 }
 
 } // namespace
@@ -260,8 +254,7 @@ int upload(aw_fabric* f, uint32_t region, uint64_t offset, uint64_t bytes) {
         const int b = (int)(c & 1);
         const uint64_t at = c * kStageBytes, len = std::min(kStageBytes, bytes - at);
         if (c >= 2) FAB_HIP(f, hipEventSynchronize(f->stage_ev[b]));
-        if (!file_io(f->fd, f->stage[b], len, file_off + at, false))
-            return ffail(f, AW_E_IO, "mmap failed: read of the fabric file: %s", os_error(errno).c_str());
+        map_copy(f->base, f->stage[b], len, file_off + at, false);
         FAB_HIP(f, hipMemcpyAsync(dst + at, f->stage[b], len, hipMemcpyHostToDevice, f->stream));
         FAB_HIP(f, hipEventRecord(f->stage_ev[b], f->stream));
     }
@@ -292,8 +285,7 @@ int download(aw_fabric* f, uint32_t region, uint64_t offset, uint64_t bytes) {
         const uint64_t at = c * kStageBytes, len = std::min(kStageBytes, bytes - at);
         if (c + 1 < nc && (rc = issue(c + 1))) return rc;
         FAB_HIP(f, hipEventSynchronize(f->stage_ev[b]));
-        if (!file_io(f->fd, f->stage[b], len, file_off + at, true))
-            return ffail(f, AW_E_IO, "mmap failed: write of the fabric file: %s", os_error(errno).c_str());
+        map_copy(f->base, f->stage[b], len, file_off + at, true);
     }
     FAB_HIP(f, hipStreamSynchronize(f->stream));
     return AW_OK;

@@ -19,7 +19,10 @@ Also measured in the same run:
     113-133: 64 hot + 16 cold blocks, 512-atom per-kv-head dictionary, B = 1),
     beside its published 389.6 tok/s on an M1 Pro;
   * the CPU baseline: the oracle's multi-threaded fp32 restatement of the
-    reference kernel on this host, on a bounded sample of B = 1 steps.
+    reference kernel on this host, on a bounded sample of B = 1 steps;
+  * the SparseCode encoder on 8192 Llama8B hot blocks, and the Llama8B
+    `.aether` fabric: upload of its pools into HBM, write-back of its cold pool,
+    and one Distiller cycle on the device (each beside the CPU oracle).
 """
 from __future__ import annotations
 
@@ -57,6 +60,7 @@ def parse():
     p.add_argument("--cold-layout", choices=("reference", "head_blocked"), default="reference",
                    help="cold pool order of the main measurement (reference: [blocks][16][kv_heads])")
     p.add_argument("--skip-encoder", action="store_true", help="skip the SparseCode encoder measurement")
+    p.add_argument("--skip-fabric", action="store_true", help="skip the .aether fabric residency measurement")
     p.add_argument("--skip-alt-layout", action="store_true",
                    help="skip the extra B-max run with the other cold pool order (for clean profiles)")
     p.add_argument("--rocpd-summary", metavar="DB", help="print a per-kernel summary of a rocprofv3 database and exit")
@@ -238,6 +242,90 @@ def encoder_bench(engine, seed, reps, cpu_blocks):
             "cpu_baseline": {"value": round(cpu_blocks / cpu_s, 2), "unit": "blocks/s", "cores": 1, "kind": "port",
                              "sample": f"{cpu_blocks} blocks through the oracle's restatement of distiller.rs:171-246"},
             "codes_match_cpu": same}
+
+
+PCIE_GEN5_X16_GBPS = 63.0  # per direction: 32 GT/s x 16 lanes x 128/130 encoding / 8 bits
+
+
+def fabric_bench(engine, seed, cpu_blocks):
+    """The Llama8B `.aether` fabric (hot pool 256 MiB, cold pool 64 MiB, dictionary
+    1 MiB; fabric.rs:124-186): upload of its three pools into HBM, write-back of the
+    cold pool into the mapping, and one Distiller REM cycle (distiller.rs:60-120)
+    over its 8192 hot blocks, all of them candidates (rows ~ N(0, 0.3): variance
+    proxy ~0.09 < 0.15).  The CPU oracle is timed on `cpu_blocks` blocks of the cycle."""
+    import tempfile
+
+    import numpy as np
+    from aether_nexus_amd import fabric as F
+    from oracle import oracle
+    dims = F.model_dims("llama8b")
+    with tempfile.TemporaryDirectory() as td:
+        path = os.path.join(td, "llama8b.aether")
+        F.create_genesis(path, dims)
+        fab = F.Fabric(path, dims)
+        try:
+            rng = np.random.default_rng(seed)
+            hot = fab.hot_pool_blocks(writable=True)
+            for b0 in range(0, hot.shape[0], 512):
+                hot[b0:b0 + 512] = (rng.standard_normal((512,) + hot.shape[1:], dtype=np.float32) * 0.3).astype(
+                    np.float16).view(np.uint16)
+            dd = rng.standard_normal(fab.dictionary_atoms().shape)
+            fab.dictionary_atoms(writable=True)[...] = (dd / np.linalg.norm(dd, axis=-1, keepdims=True)).astype(
+                np.float16).view(np.uint16)
+            # A fabric in service holds codes in its cold pool (its file blocks exist).
+            codes = fab.cold_pool_blocks(writable=True)
+            codes["indices"] = rng.integers(0, dims.dict_size, codes["indices"].shape)
+            codes["coeffs"] = (rng.standard_normal(codes["coeffs"].shape) * 0.5).astype(np.float16)
+            del codes
+            fab.force_checkpoint()
+            pools = ("hot", "cold", "dict")
+            r = fab.regions
+            nbytes = r.hot_pool_size + r.cold_pool_size + r.dict_size
+            t0 = time.perf_counter()
+            fab.attach_device(0, pools)
+            first = time.perf_counter() - t0
+            t0 = time.perf_counter()
+            for _ in range(3):
+                for name in pools:
+                    fab.push(name)
+            up = (time.perf_counter() - t0) / 3
+            t0 = time.perf_counter()
+            for _ in range(3):
+                fab.pull("cold")
+            down = (time.perf_counter() - t0) / 3
+            fab.force_checkpoint()
+            time.sleep(0.31)  # the cycle's checkpoint then flushes, as the reference's does after a REM pass
+            t0 = time.perf_counter()
+            n, ent = fab.distill(engine, F.DISTILL_ENTROPY_THRESHOLD)
+            cycle = time.perf_counter() - t0
+            hot_h = fab.hot_pool_blocks()
+            sample = np.arange(cpu_blocks, dtype=np.uint32)
+            t0 = time.perf_counter()
+            want_ent = [oracle.block_entropy(hot_h[b]) for b in sample]
+            cands = [int(b) for b, e in zip(sample, want_ent) if 0 < e < np.float32(F.DISTILL_ENTROPY_THRESHOLD)]
+            want = oracle.encode_blocks(hot_h, fab.dictionary_atoms(), cands)
+            cpu_s = time.perf_counter() - t0
+            got = fab.cold_pool().view(np.uint16).reshape(-1, 16, dims.kv_heads, 8)
+            same = bool(np.array_equal(np.float32(want_ent).view(np.uint32), ent[:cpu_blocks].view(np.uint32))
+                        and np.array_equal(got[cands], want[cands]))
+            del hot, hot_h, got
+        finally:
+            fab.close()
+    return {"workload": "Llama8B fabric: hot pool 8192 x 16 x 8 x 128 f16 (256 MiB), cold pool 32768 x 16 x 8 "
+                        "SparseCodes (64 MiB), dictionary 8 x 512 x 128 f16 (1 MiB); every pool written, file in the page cache",
+            "pool_bytes": int(nbytes),
+            "first_attach_ms": round(first * 1e3, 2),
+            "upload_ms": round(up * 1e3, 2), "upload_gbps": round(nbytes / up / 1e9, 2),
+            "writeback_cold_ms": round(down * 1e3, 2), "writeback_cold_gbps": round(r.cold_pool_size / down / 1e9, 2),
+            "roofline": {"bound": "pcie", "peak_gbps": PCIE_GEN5_X16_GBPS,
+                         "upload_frac": round(nbytes / up / 1e9 / PCIE_GEN5_X16_GBPS, 4),
+                         "writeback_frac": round(r.cold_pool_size / down / 1e9 / PCIE_GEN5_X16_GBPS, 4)},
+            "distill_cycle_ms": round(cycle * 1e3, 2), "distilled_blocks": int(n),
+            "distill_blocks_per_s": round(n / cycle, 1),
+            "cpu_baseline": {"value": round(cpu_blocks / cpu_s, 2), "unit": "blocks/s", "cores": 1, "kind": "port",
+                             "sample": f"entropy proxy and encoding of hot blocks 0..{cpu_blocks - 1} "
+                                       "through the oracle (distiller.rs:97-246)"},
+            "cycle_matches_cpu": same}
 
 
 def reference_bench_config(engine, seed, steps):
@@ -490,6 +578,9 @@ def main():
     enc = None if args.skip_encoder else encoder_bench(engine, args.seed, 5, 8 if args.no_cpu else 32)
     if enc:
         log(json.dumps({"encoder": enc}))
+    fab = None if args.skip_fabric else fabric_bench(engine, args.seed, 8 if args.no_cpu else 24)
+    if fab:
+        log(json.dumps({"fabric": fab}))
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds, args.seed)
 
     result = {
@@ -519,6 +610,7 @@ def main():
         "roofline": roofline,
         "other_cold_layout": alt,
         "encoder": enc,
+        "fabric": fab,
         "cpu_baseline": cpu,
         "reference_bench_config": ref_cfg,
     }

@@ -173,7 +173,7 @@ int aw_fabric_is_dirty(const aw_fabric* fabric);
 
 /* Allocates device copies of the regions in region_mask (AW_REGION_BIT of
  * HOT, COLD, DICT, ...) on HIP device `device` and uploads them.  Uploads go
- * through two pinned staging buffers: host threads read the file into one
+ * through two pinned staging buffers: host threads copy the mapping into one
  * while the DMA engine copies the other.  A region already attached is
  * uploaded again.  All regions of one fabric live on one device. */
 int aw_fabric_attach_device(aw_fabric* fabric, int device, uint32_t region_mask);
