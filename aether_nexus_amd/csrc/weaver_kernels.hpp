@@ -1691,49 +1691,109 @@ __global__ __launch_bounds__(kEncThreads) void encode_kernel(EncodeArgs a) {
     a.cold[(uint64_t)c * kBlockTokens * a.kv_heads + tt * a.s_tok + g * a.s_head] = code;
 }
 
-// Variance proxy of each listed block (distiller.rs:126-159): one lane per
-// block runs the reference's loops in memory order, in f64, with no fused
-// multiply-add (the reference squares, then adds), and returns f32.  An
+// Variance proxy of each listed block (distiller.rs:126-159), bit-exact: one
+// lane per block runs the reference's loops in memory order, in f64, with no
+// fused multiply-add (the reference squares, then adds), and returns f32; an
 // all-zero block gives 0.  Without a block list (src null) lane i takes block i.
-__global__ __launch_bounds__(64) void entropy_kernel(EncodeArgs a, uint32_t head_dim) {
+//
+// The f64 sums are sequential chains, so a block cannot be split across lanes;
+// what is parallel is the data supply.  One wave owns 64 blocks and streams
+// them in chunks of kEntChunk values: the wave loads a chunk of all 64 blocks
+// with coalesced 16-byte loads (16 lanes per 256-byte block chunk) into one of
+// two LDS tiles while every lane runs its own chain over the other tile.  Rows
+// are padded by 16 bytes so the 64 lanes' row reads spread over the banks.
+constexpr int kEntChunk = 128;                   // f16 values per block and chunk (256 bytes)
+constexpr int kEntCols = kEntChunk / 8;          // 16-byte words per row
+constexpr int kEntPitch = kEntCols + 1;          // padded row, in 16-byte words
+
+// One 16-byte word (8 values) of a block, in memory order: pass 0 adds the
+// values (and tracks whether all are zero), pass 1 adds the squared deviations.
+template <int PASS>
+__device__ inline void entropy_word(const uint4_t w, bool& all_zero, double& acc, double mean) {
 #pragma clang fp contract(off)
-    const uint32_t i = blockIdx.x * 64 + threadIdx.x;
-    if (i >= a.n_blocks) return;
-    const uint32_t b = a.src ? (a.src[i] & kRefMask) : i;
-    if (b >= a.hot_blocks) {
-        flag_error(a.err, kErrHotRef);
-        a.entropy[i] = 0.0f;
-        return;
-    }
-    const uint64_t n = (uint64_t)kBlockTokens * a.kv_heads * head_dim;
-    const uint4_t* p = (const uint4_t*)(a.hot + (uint64_t)b * n);
-    bool all_zero = true;
-    double sum = -0.0;
-    for (uint64_t k = 0; k < n / 8; ++k) {
-        const uint4_t w = p[k];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const float f = h2f_bits((w[e / 2] >> (16 * (e % 2))) & 0xFFFFu);
+    for (int e = 0; e < 8; ++e) {
+        const float f = h2f_bits((w[e / 2] >> (16 * (e % 2))) & 0xFFFFu);
+        if constexpr (PASS == 0) {
             all_zero = all_zero && f == 0.0f;
-            sum = sum + (double)f;
-        }
-    }
-    if (all_zero) {
-        a.entropy[i] = 0.0f;
-        return;
-    }
-    const double mean = sum / (double)n;
-    double var = -0.0;
-    for (uint64_t k = 0; k < n / 8; ++k) {
-        const uint4_t w = p[k];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const double diff = (double)h2f_bits((w[e / 2] >> (16 * (e % 2))) & 0xFFFFu) - mean;
+            acc = acc + (double)f;
+        } else {
+            const double diff = (double)f - mean;
             const double sq = diff * diff;
-            var = var + sq;
+            acc = acc + sq;
         }
     }
-    a.entropy[i] = (float)(var / (double)n);
+}
+
+__global__ __launch_bounds__(64) void entropy_kernel(EncodeArgs a, uint32_t head_dim) {
+    __shared__ uint4_t tile[2][64][kEntPitch];
+    __shared__ uint32_t s_blk[64];
+    const uint32_t lane = threadIdx.x;
+    const uint32_t i = blockIdx.x * 64 + lane;
+    uint32_t b = 0;
+    bool ok = false;
+    if (i < a.n_blocks) {
+        b = a.src ? (a.src[i] & kRefMask) : i;
+        ok = b < a.hot_blocks;
+        if (!ok) flag_error(a.err, kErrHotRef);
+    }
+    s_blk[lane] = ok ? b : 0xFFFFFFFFu;
+    __syncthreads();
+    const uint64_t n = (uint64_t)kBlockTokens * a.kv_heads * head_dim; // values per block
+    const uint64_t words = n / 8;                                        // 16-byte words per block
+    const uint64_t n_chunks = (words + kEntCols - 1) / kEntCols;
+    const uint4_t* hot = (const uint4_t*)a.hot;
+    // Lane l loads words (k * 64 + l) of the chunk: row r = that / kEntCols, column c.
+    uint4_t reg[kEntCols];
+    auto load = [&](uint64_t ch) {
+#pragma unroll
+        for (int k = 0; k < kEntCols; ++k) {
+            const uint32_t idx = k * 64 + lane, r = idx / kEntCols, c = idx % kEntCols;
+            const uint32_t rb = s_blk[r];
+            const uint64_t w = ch * kEntCols + c;
+            reg[k] = (rb != 0xFFFFFFFFu && w < words) ? hot[(uint64_t)rb * words + w] : uint4_t{0, 0, 0, 0};
+        }
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int k = 0; k < kEntCols; ++k) {
+            const uint32_t idx = k * 64 + lane;
+            tile[buf][idx / kEntCols][idx % kEntCols] = reg[k];
+        }
+    };
+    bool all_zero = true;
+    double mean = 0.0;
+    // Streams the whole block once per pass; the pass is a compile-time constant
+    // so the inner loops carry no branch.
+    auto stream = [&](auto pass, double acc) {
+        constexpr int P = decltype(pass)::value;
+        load(0);
+        store(0);
+        __syncthreads();
+        for (uint64_t ch = 0; ch < n_chunks; ++ch) {
+            const int cur = (int)(ch & 1);
+            const bool more = ch + 1 < n_chunks;
+            if (more) load(ch + 1);
+            const uint4_t* row = tile[cur][lane];
+            if ((ch + 1) * kEntCols <= words) {
+                uint4_t w[kEntCols];
+#pragma unroll
+                for (int c = 0; c < kEntCols; ++c) w[c] = row[c];
+#pragma unroll
+                for (int c = 0; c < kEntCols; ++c) entropy_word<P>(w[c], all_zero, acc, mean);
+            } else {
+                const uint32_t cols = (uint32_t)(words - ch * kEntCols);
+                for (uint32_t c = 0; c < cols; ++c) entropy_word<P>(row[c], all_zero, acc, mean);
+            }
+            if (more) store(cur ^ 1);
+            __syncthreads();
+        }
+        return acc;
+    };
+    const double sum = stream(std::integral_constant<int, 0>{}, -0.0);
+    mean = sum / (double)n;
+    const double var = stream(std::integral_constant<int, 1>{}, -0.0);
+    if (i < a.n_blocks) a.entropy[i] = (!ok || all_zero) ? 0.0f : (float)(var / (double)n);
 }
 
 } // namespace aw
