@@ -1483,8 +1483,11 @@ __global__ __launch_bounds__(kFinishWaves * 64) void finish_kernel(FinishArgs a)
 // One wave per row (row id lbg*R + r), four rows per work-group: lanes first
 // combine the row's splits (lane = split), then each lane merges HD/64 dims.
 // Used when there is no cold pool or when the cold output was split over
-// several atom ranges.
-template <int HD>
+// several atom ranges.  UC atom-range partials and UH hot-split partials are
+// loaded per batch: a row's partials are summed in a chain of batches, so few
+// rows with many partials (small batches) want deep batches, many rows with
+// few partials shallow ones (no clamped duplicate loads).
+template <int HD, int UC, int UH>
 __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
     constexpr int DPT = HD / 64;
     __shared__ float s_hfac[4][kMaxSplits];
@@ -1516,7 +1519,7 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
         oh[e] = 0.0f;
     }
     {
-        constexpr int U = 8; // atom ranges summed per batch of loads
+        constexpr int U = UC; // atom ranges summed per batch of loads
         for (uint32_t ar = 0; ar < n_ar; ar += U) {
             float v[U][DPT];
 #pragma unroll
@@ -1545,18 +1548,18 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
     }
     __builtin_amdgcn_wave_barrier();
     const float* hsrc = has_h ? a.hot_o + (lbg * a.hot_splits * R + r) * HD + d0 : zero;
-    for (uint32_t s0 = 0; s0 < a.hot_splits; s0 += 4) {
-        float v[4][DPT], fs[4];
+    for (uint32_t s0 = 0; s0 < a.hot_splits; s0 += UH) {
+        float v[UH][DPT], fs[UH];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < UH; ++j) {
             const uint32_t sp = min(s0 + j, a.hot_splits - 1u);
 #pragma unroll
             for (int e = 0; e < DPT; ++e) v[j][e] = hsrc[(uint64_t)sp * R * HD + e];
         }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) fs[j] = s0 + j < a.hot_splits ? s_hfac[row][s0 + j] : 0.0f;
+        for (int j = 0; j < UH; ++j) fs[j] = s0 + j < a.hot_splits ? s_hfac[row][s0 + j] : 0.0f;
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < UH; ++j)
 #pragma unroll
             for (int e = 0; e < DPT; ++e) oh[e] += fs[j] != 0.0f ? fs[j] * v[j][e] : 0.0f;
     }
