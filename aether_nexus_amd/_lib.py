@@ -60,6 +60,7 @@ SIGNATURES = {
     "aw_fabric_force_checkpoint": (_c_int, [_vp]),
     "aw_fabric_is_dirty": (_c_int, [_vp]),
     "aw_fabric_attach_device": (_c_int, [_vp, _c_int, _u32]),
+    "aw_fabric_device_flags": (_u32, [_vp]),
     "aw_fabric_device_region": (_c_int, [_vp, _u32, ctypes.POINTER(_vp), ctypes.POINTER(_u64)]),
     "aw_fabric_push": (_c_int, [_vp, _u32, _u64, _u64]),
     "aw_fabric_pull": (_c_int, [_vp, _u32, _u64, _u64]),

@@ -184,6 +184,29 @@ void map_copy(uint8_t* map, uint8_t* buf, uint64_t n, uint64_t off, bool to_map)
     for (auto& x : th) x.join();
 }
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Reorders whole cold-pool blocks of 16-byte codes between the file's order
+// [block][token][kv_head] and the head-blocked order [block][kv_head][token]
+// (to_head_blocked 1) or back (0).  One thread per code; reads are coalesced.
+__global__ __launch_bounds__(256) void cold_reorder_kernel(const u32x4* src, u32x4* dst, uint64_t n_codes,
+                                                           uint32_t block_size, uint32_t kv_heads,
+                                                           int to_head_blocked) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n_codes) return;
+    const uint64_t per = (uint64_t)block_size * kv_heads;
+    const uint64_t blk = i / per, r = i % per;
+    uint64_t j;
+    if (to_head_blocked) {
+        const uint64_t t = r / kv_heads, g = r % kv_heads;
+        j = g * block_size + t;
+    } else {
+        const uint64_t g = r / block_size, t = r % block_size;
+        j = t * kv_heads + g;
+    }
+    dst[blk * per + j] = src[i];
+}
+
 } // namespace
 
 struct aw_fabric {
@@ -203,6 +226,8 @@ struct aw_fabric {
     void* dev[AW_REGION_COUNT] = {};
     uint8_t* stage[2] = {nullptr, nullptr};
     hipEvent_t stage_ev[2] = {nullptr, nullptr};
+    bool cold_hb = false;       // device cold pool in the head-blocked order
+    uint8_t* dstage = nullptr;  // device staging for reordered cold-pool chunks
 };
 
 namespace {
@@ -291,6 +316,92 @@ int download(aw_fabric* f, uint32_t region, uint64_t offset, uint64_t bytes) {
     return AW_OK;
 }
 
+uint64_t cold_block_bytes(const aw_fabric* f) { return (uint64_t)f->dims.block_size * f->dims.kv_heads * kCodeBytes; }
+
+int launch_reorder(aw_fabric* f, const void* src, void* dst, uint64_t n_blocks, int to_hb) {
+    const uint64_t n = n_blocks * f->dims.block_size * f->dims.kv_heads;
+    if (!n) return AW_OK;
+    hipLaunchKernelGGL(cold_reorder_kernel, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, f->stream,
+                       (const u32x4*)src, (u32x4*)dst, n, f->dims.block_size, f->dims.kv_heads, to_hb);
+    FAB_HIP(f, hipGetLastError());
+    return AW_OK;
+}
+
+// The head-blocked device cold pool moves in whole blocks: bytes
+// [offset, offset + bytes) of the file's cold region are widened to the blocks
+// that hold them.  Upload: the file's blocks go through pinned and device
+// staging and are reordered into place.
+int upload_cold_hb(aw_fabric* f, uint64_t offset, uint64_t bytes) {
+    const uint64_t bb = cold_block_bytes(f), per_chunk = std::max<uint64_t>(1, kStageBytes / bb);
+    const uint64_t b0 = offset / bb, b1 = (offset + bytes + bb - 1) / bb;
+    uint8_t* pool = (uint8_t*)f->dev[AW_REGION_COLD];
+    uint64_t c = 0;
+    for (uint64_t blk = b0; blk < b1; blk += per_chunk, ++c) {
+        const int b = (int)(c & 1);
+        const uint64_t nb = std::min(per_chunk, b1 - blk), len = nb * bb;
+        if (c >= 2) FAB_HIP(f, hipEventSynchronize(f->stage_ev[b]));
+        map_copy(f->base, f->stage[b], len, f->regions.cold_pool_offset + blk * bb, false);
+        FAB_HIP(f, hipMemcpyAsync(f->dstage, f->stage[b], len, hipMemcpyHostToDevice, f->stream));
+        FAB_HIP(f, hipEventRecord(f->stage_ev[b], f->stream));
+        const int rc = launch_reorder(f, f->dstage, pool + blk * bb, nb, 1);
+        if (rc) return rc;
+    }
+    FAB_HIP(f, hipStreamSynchronize(f->stream));
+    return AW_OK;
+}
+
+// Download: whole blocks are reordered back into device staging and copied
+// out; only the requested bytes are written into the mapping.
+int download_cold_hb(aw_fabric* f, uint64_t offset, uint64_t bytes) {
+    const uint64_t bb = cold_block_bytes(f), per_chunk = std::max<uint64_t>(1, kStageBytes / bb);
+    const uint64_t b0 = offset / bb, b1 = (offset + bytes + bb - 1) / bb;
+    const uint8_t* pool = (const uint8_t*)f->dev[AW_REGION_COLD];
+    const uint64_t nc = (b1 - b0 + per_chunk - 1) / per_chunk;
+    auto issue = [&](uint64_t c) -> int {
+        const int b = (int)(c & 1);
+        const uint64_t blk = b0 + c * per_chunk, nb = std::min(per_chunk, b1 - blk);
+        int rc = launch_reorder(f, pool + blk * bb, f->dstage, nb, 0);
+        if (rc) return rc;
+        FAB_HIP(f, hipMemcpyAsync(f->stage[b], f->dstage, nb * bb, hipMemcpyDeviceToHost, f->stream));
+        FAB_HIP(f, hipEventRecord(f->stage_ev[b], f->stream));
+        return AW_OK;
+    };
+    int rc = AW_OK;
+    if (nc && (rc = issue(0))) return rc;
+    for (uint64_t c = 0; c < nc; ++c) {
+        const int b = (int)(c & 1);
+        const uint64_t blk = b0 + c * per_chunk, nb = std::min(per_chunk, b1 - blk);
+        if (c + 1 < nc && (rc = issue(c + 1))) return rc;
+        FAB_HIP(f, hipEventSynchronize(f->stage_ev[b]));
+        // This chunk holds cold-region bytes [blk * bb, (blk + nb) * bb); keep the requested part.
+        const uint64_t lo = std::max(offset, blk * bb), hi = std::min(offset + bytes, (blk + nb) * bb);
+        map_copy(f->base, f->stage[b] + (lo - blk * bb), hi - lo, f->regions.cold_pool_offset + lo, true);
+    }
+    FAB_HIP(f, hipStreamSynchronize(f->stream));
+    return AW_OK;
+}
+
+int ensure_dstage(aw_fabric* f) {
+    if (!f->dstage) FAB_HIP(f, hipMalloc((void**)&f->dstage, kStageBytes));
+    return AW_OK;
+}
+
+// Host -> device / device -> host of a byte range, in the device layout of the region.
+int move(aw_fabric* f, uint32_t region, uint64_t offset, uint64_t bytes, bool to_device) {
+    if (region == AW_REGION_COLD && f->cold_hb) {
+        uint64_t file_off = 0;
+        if (!check_range(f, region, offset, bytes, &file_off))
+            return ffail(f, AW_E_INVALID_ARG, "region %u range [%llu, +%llu) is not attached or out of bounds",
+                         region, (unsigned long long)offset, (unsigned long long)bytes);
+        int rc = ensure_staging(f);
+        if (!rc) rc = ensure_dstage(f);
+        if (rc) return rc;
+        if (!bytes) return AW_OK;
+        return to_device ? upload_cold_hb(f, offset, bytes) : download_cold_hb(f, offset, bytes);
+    }
+    return to_device ? upload(f, region, offset, bytes) : download(f, region, offset, bytes);
+}
+
 void free_device(aw_fabric* f) {
     if (f->device < 0) return;
     (void)hipSetDevice(f->device);
@@ -305,6 +416,8 @@ void free_device(aw_fabric* f) {
         f->stage_ev[i] = nullptr;
         f->stage[i] = nullptr;
     }
+    if (f->dstage) (void)hipFree(f->dstage);
+    f->dstage = nullptr;
     if (f->stream) (void)hipStreamDestroy(f->stream);
     f->stream = nullptr;
     f->device = -1;
@@ -509,7 +622,11 @@ int aw_fabric_is_dirty(const aw_fabric* f) { return f && f->dirty.load(std::memo
 
 int aw_fabric_attach_device(aw_fabric* f, int device, uint32_t mask) {
     if (!f) return AW_E_INVALID_ARG;
+    const bool hb = (mask & AW_FABRIC_COLD_HEAD_BLOCKED) != 0;
+    mask &= ~AW_FABRIC_COLD_HEAD_BLOCKED;
     if (mask & ~((1u << AW_REGION_COUNT) - 1u)) return ffail(f, AW_E_INVALID_ARG, "unknown region bits 0x%x", mask);
+    if (hb && !(mask & AW_REGION_BIT(AW_REGION_COLD)))
+        return ffail(f, AW_E_INVALID_ARG, "AW_FABRIC_COLD_HEAD_BLOCKED needs the cold region in the mask");
     if (f->device >= 0 && f->device != device)
         return ffail(f, AW_E_INVALID_ARG, "fabric is attached to device %d", f->device);
     int count = 0;
@@ -523,7 +640,8 @@ int aw_fabric_attach_device(aw_fabric* f, int device, uint32_t mask) {
         uint64_t off = 0, size = 0;
         region_span(f->regions, r, &off, &size);
         if (!f->dev[r]) FAB_HIP(f, hipMalloc(&f->dev[r], (size_t)size));
-        const int rc = upload(f, r, 0, size);
+        if (r == AW_REGION_COLD) f->cold_hb = hb;
+        const int rc = move(f, r, 0, size, true);
         if (rc) return rc;
     }
     return AW_OK;
@@ -538,18 +656,22 @@ int aw_fabric_device_region(const aw_fabric* f, uint32_t region, void** dptr, ui
     return AW_OK;
 }
 
+uint32_t aw_fabric_device_flags(const aw_fabric* f) {
+    return (f && f->dev[AW_REGION_COLD] && f->cold_hb) ? AW_F_COLD_HEAD_BLOCKED : 0u;
+}
+
 int aw_fabric_push(aw_fabric* f, uint32_t region, uint64_t offset, uint64_t bytes) {
     if (!f) return AW_E_INVALID_ARG;
     if (f->device < 0) return ffail(f, AW_E_INVALID_ARG, "fabric is not attached to a device");
     FAB_HIP(f, hipSetDevice(f->device));
-    return upload(f, region, offset, bytes);
+    return move(f, region, offset, bytes, true);
 }
 
 int aw_fabric_pull(aw_fabric* f, uint32_t region, uint64_t offset, uint64_t bytes) {
     if (!f) return AW_E_INVALID_ARG;
     if (f->device < 0) return ffail(f, AW_E_INVALID_ARG, "fabric is not attached to a device");
     FAB_HIP(f, hipSetDevice(f->device));
-    const int rc = download(f, region, offset, bytes);
+    const int rc = move(f, region, offset, bytes, false);
     if (rc == AW_OK && bytes && region != AW_REGION_TRACE) f->dirty.store(true, std::memory_order_release);
     return rc;
 }
@@ -628,6 +750,7 @@ int aw_fabric_distill(aw_fabric* f, aw_engine* e, float threshold, float* entrop
         ed.src_blocks = d_list;
         ed.dst_blocks = nullptr;
         ed.cold = (aw_sparse_code*)f->dev[AW_REGION_COLD];
+        ed.flags = f->cold_hb ? AW_F_COLD_HEAD_BLOCKED : 0u;
         rc = aw_encode_device(e, &ed, f->stream);
         if (rc) {
             release();
@@ -641,7 +764,8 @@ int aw_fabric_distill(aw_fabric* f, aw_engine* e, float threshold, float* entrop
         for (size_t i = 0; i < cand.size();) {
             size_t j = i + 1;
             while (j < cand.size() && cand[j] == cand[j - 1] + 1) ++j;
-            rc = download(f, AW_REGION_COLD, (uint64_t)cand[i] * code_block_bytes, (uint64_t)(j - i) * code_block_bytes);
+            rc = move(f, AW_REGION_COLD, (uint64_t)cand[i] * code_block_bytes, (uint64_t)(j - i) * code_block_bytes,
+                      false);
             if (rc) {
                 release();
                 return rc;

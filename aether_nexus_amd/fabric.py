@@ -18,7 +18,8 @@ from typing import Iterable, Optional
 import numpy as np
 
 from . import _lib
-from .types import (REGION_IDS, SPARSE_CODE_DTYPE, FabricRegions, LoomDescriptor, ModelDims, WeaverParams)
+from .types import (AW_F_COLD_HEAD_BLOCKED, REGION_IDS, SPARSE_CODE_DTYPE, FabricRegions, LoomDescriptor, ModelDims,
+                    WeaverParams)
 from .weaver import WeaverError, _status_text
 
 #: ModelDims presets (nexus-core/src/types.rs:166-202).
@@ -27,6 +28,8 @@ PRESETS = ("llama8b", "granite2b", "qwen05b", "deepseek_r1_1_5b")
 DISTILL_ENTROPY_THRESHOLD = 0.15
 MAX_HOT_BLOCKS = 8192
 MAX_COLD_BLOCKS = 32768
+#: aw_fabric_attach_device mask flag (include/aether_fabric.h).
+AW_FABRIC_COLD_HEAD_BLOCKED = 1 << 31
 
 
 class FabricError(WeaverError):
@@ -221,11 +224,23 @@ class Fabric:
         return bool(self._lib.aw_fabric_is_dirty(self._h))
 
     # -- residency in HBM
-    def attach_device(self, device: int = 0, regions: Iterable[str] = ("hot", "cold", "dict")) -> None:
-        mask = 0
+    def attach_device(self, device: int = 0, regions: Iterable[str] = ("hot", "cold", "dict"),
+                      cold_head_blocked: bool = False) -> None:
+        """Device copies of `regions`; ``cold_head_blocked`` keeps the device cold
+        pool in the [blocks][kv_heads][16] order (AW_FABRIC_COLD_HEAD_BLOCKED)."""
+        mask = AW_FABRIC_COLD_HEAD_BLOCKED if cold_head_blocked else 0
         for r in regions:
             mask |= 1 << REGION_IDS[r]
         self._check(self._lib.aw_fabric_attach_device(self._h, device, mask), "attach_device")
+
+    @property
+    def device_flags(self) -> int:
+        """aw_decode_desc / aw_encode_desc flags of the attached pools (AW_F_COLD_HEAD_BLOCKED or 0)."""
+        return int(self._lib.aw_fabric_device_flags(self._h))
+
+    @property
+    def cold_head_blocked(self) -> bool:
+        return bool(self.device_flags & AW_F_COLD_HEAD_BLOCKED)
 
     def device_region(self, region: str) -> tuple[int, int]:
         """(device address, bytes) of an attached region."""

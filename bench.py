@@ -293,6 +293,16 @@ def fabric_bench(engine, seed, cpu_blocks):
             for _ in range(3):
                 fab.pull("cold")
             down = (time.perf_counter() - t0) / 3
+            # The device cold pool kept head-blocked: copies reorder whole blocks on the device.
+            fab.attach_device(0, ("cold",), cold_head_blocked=True)
+            t0 = time.perf_counter()
+            for _ in range(3):
+                fab.push("cold")
+            up_hb = (time.perf_counter() - t0) / 3
+            t0 = time.perf_counter()
+            for _ in range(3):
+                fab.pull("cold")
+            down_hb = (time.perf_counter() - t0) / 3
             fab.force_checkpoint()
             time.sleep(0.31)  # the cycle's checkpoint then flushes, as the reference's does after a REM pass
             t0 = time.perf_counter()
@@ -317,6 +327,9 @@ def fabric_bench(engine, seed, cpu_blocks):
             "first_attach_ms": round(first * 1e3, 2),
             "upload_ms": round(up * 1e3, 2), "upload_gbps": round(nbytes / up / 1e9, 2),
             "writeback_cold_ms": round(down * 1e3, 2), "writeback_cold_gbps": round(r.cold_pool_size / down / 1e9, 2),
+            "cold_head_blocked": {"upload_gbps": round(r.cold_pool_size / up_hb / 1e9, 2),
+                                  "writeback_gbps": round(r.cold_pool_size / down_hb / 1e9, 2),
+                                  "note": "device cold pool in [blocks][kv_heads][16]; the REM cycle below runs on it"},
             "roofline": {"bound": "pcie", "peak_gbps": PCIE_GEN5_X16_GBPS,
                          "upload_frac": round(nbytes / up / 1e9 / PCIE_GEN5_X16_GBPS, 4),
                          "writeback_frac": round(r.cold_pool_size / down / 1e9 / PCIE_GEN5_X16_GBPS, 4)},

@@ -171,12 +171,30 @@ int aw_fabric_is_dirty(const aw_fabric* fabric);
 /* ---- residency in GPU memory (no reference counterpart: the reference runs on
  * unified memory and reads the mapping in place) ---------------------------- */
 
+/* Flag in aw_fabric_attach_device's region_mask: keep the device copy of the
+ * cold pool in the head-blocked order [blocks][kv_heads][block_size] instead of
+ * the file's [blocks][block_size][kv_heads].  The decode and the encoder read
+ * and write that order with AW_F_COLD_HEAD_BLOCKED (aw_fabric_device_flags);
+ * it gives the same output bits and shorter decode steps (one kv head's codes
+ * of a block fill whole 64-byte L2 sectors).  The file keeps its format: copies
+ * reorder whole blocks on the device, and push / pull still take byte ranges of
+ * the file's cold region.  A cold-pool push then writes whole blocks: the bytes
+ * of its first and last block outside the range come from the mapping too; a
+ * pull writes only the requested bytes into the mapping. */
+#define AW_FABRIC_COLD_HEAD_BLOCKED (1u << 31)
+
 /* Allocates device copies of the regions in region_mask (AW_REGION_BIT of
- * HOT, COLD, DICT, ...) on HIP device `device` and uploads them.  Uploads go
- * through two pinned staging buffers: host threads copy the mapping into one
- * while the DMA engine copies the other.  A region already attached is
- * uploaded again.  All regions of one fabric live on one device. */
+ * HOT, COLD, DICT, ..., optionally | AW_FABRIC_COLD_HEAD_BLOCKED) on HIP device
+ * `device` and uploads them.  Uploads go through two pinned staging buffers:
+ * host threads copy the mapping into one while the DMA engine copies the
+ * other.  A region already attached is uploaded again (in the order the flag
+ * now names).  All regions of one fabric live on one device. */
 int aw_fabric_attach_device(aw_fabric* fabric, int device, uint32_t region_mask);
+
+/* The aw_decode_desc / aw_encode_desc flags that describe the attached device
+ * pools: AW_F_COLD_HEAD_BLOCKED when the cold pool is attached head-blocked,
+ * else 0. */
+uint32_t aw_fabric_device_flags(const aw_fabric* fabric);
 
 /* Device address and size of an attached region (AW_E_INVALID_ARG if it is
  * not attached).  The device copies are ordinary device memory, 256-byte

@@ -47,9 +47,11 @@ def fill_pools(fab, rng, low=(), zero=(), const=()):
     codes["coeffs"] = (rng.standard_normal(codes["coeffs"].shape) * 0.5).astype(np.float16)
 
 
-def test_attach_pull_push_roundtrip(tmp_path):
+@pytest.mark.parametrize("hb", [False, True], ids=["file_order", "cold_head_blocked"])
+def test_attach_pull_push_roundtrip(tmp_path, hb):
     """Upload, then write-back into a zeroed mapping, gives the original bytes; a
-    partial push / pull at odd offsets across two staging chunks too."""
+    partial push / pull at odd offsets across two staging chunks too (also with
+    the device cold pool kept head-blocked, where copies move whole blocks)."""
     _, fab = booted(tmp_path)
     rng = np.random.default_rng(11)
     orig = {}
@@ -58,8 +60,9 @@ def test_attach_pull_push_roundtrip(tmp_path):
         v[...] = rng.integers(0, 256, v.size, dtype=np.uint8)
         orig[r] = v.copy()
     fab.force_checkpoint()
-    print("fabric: attach hot/cold/dict", flush=True)
-    fab.attach_device(0)
+    print(f"fabric: attach hot/cold/dict (cold head-blocked {hb})", flush=True)
+    fab.attach_device(0, cold_head_blocked=hb)
+    assert fab.cold_head_blocked == hb
     for r in orig:
         ptr, n = fab.device_region(r)
         assert ptr % 256 == 0 and n == orig[r].size
@@ -75,6 +78,20 @@ def test_attach_pull_push_roundtrip(tmp_path):
     fab.pull("hot", a, n)
     assert np.array_equal(hot[a:a + n], new)
     assert not hot[:a].any() and not hot[a + n:].any()
+    # The same on the cold pool: ranges that start and end inside a block.
+    cold = fab.region_mut("cold")
+    a, n = 2048 * 3 + 40, cold.size - 2048 * 7 - 1000
+    new = rng.integers(0, 256, n, dtype=np.uint8)
+    cold[a:a + n] = new
+    fab.push("cold", a, n)
+    cold[...] = 0
+    fab.pull("cold", a, n)
+    assert np.array_equal(cold[a:a + n], new)
+    assert not cold[:a].any() and not cold[a + n:].any()
+    cold[...] = 0
+    fab.pull("cold", 17, 3)  # three bytes of block 0
+    assert np.array_equal(cold[17:20], orig["cold"][17:20]) and not cold[:17].any() and not cold[20:].any()
+    del cold
     fab.detach_device()
     with pytest.raises(F.FabricError):
         fab.device_region("hot")
@@ -85,7 +102,8 @@ def test_attach_pull_push_roundtrip(tmp_path):
 def test_decode_from_fabric_pools(tmp_path, engine, stream):
     """aw_decode_desc pointing at the fabric's device pools (hot [8192][16][2][64],
     codes [32768][16][2], one dictionary per kv head) against the f64 oracle on the
-    mapped host pools; refs pick scattered blocks, bit 31 set on some."""
+    mapped host pools; refs pick scattered blocks, bit 31 set on some.  Then the
+    cold pool attached head-blocked: the same output bits."""
     _, fab = booted(tmp_path)
     rng = np.random.default_rng(12)
     fill_pools(fab, rng)
@@ -115,22 +133,35 @@ def test_decode_from_fabric_pools(tmp_path, engine, stream):
     err = np.abs(got - ref).max()
     rel = np.linalg.norm(got - ref) / np.linalg.norm(ref)
     assert err <= 2e-3 and rel <= 1e-3, (err, rel)
+    first = out_t.clone()
+    fab.attach_device(0, regions=("cold",), cold_head_blocked=True)
+    desc = make_desc(layers=1, batch=1, queries=1, q_heads=4, kv_heads=2, head_dim=64, dict_size=64, dict_heads=2,
+                     hot_count=H, cold_count=C, refs_stride=H + C, hot_blocks=8192, cold_blocks=32768, q=q_t,
+                     out=out_t, hot_k=fab.device_region("hot")[0], cold=fab.device_region("cold")[0], refs=refs_t,
+                     dictionary=fab.device_region("dict")[0], scale=0.125, cold_head_blocked=fab.cold_head_blocked)
+    out_t.zero_()
+    print("fabric: decode from the head-blocked device cold pool", flush=True)
+    engine.decode_device(desc, stream=stream)
+    engine.check_device_errors(stream)
+    assert torch.equal(out_t.view(torch.int16), first.view(torch.int16))
     fab.close()
 
 
-def test_distill_cycle_matches_oracle(tmp_path, engine):
+@pytest.mark.parametrize("hb", [False, True], ids=["file_order", "cold_head_blocked"])
+def test_distill_cycle_matches_oracle(tmp_path, engine, hb):
     """One REM cycle on the device copies: every proxy bit-exact, the candidates
     (0 < proxy < 0.15) exactly the low-variance blocks, their codes bit-exact at
     the same cold block index, every other cold block untouched, and the codes
-    persisted through a checkpoint and a fresh boot."""
+    persisted through a checkpoint and a fresh boot; the file's bytes are the
+    same when the device cold pool is kept head-blocked."""
     path, fab = booted(tmp_path)
     rng = np.random.default_rng(13)
     low = sorted(rng.choice(np.arange(8, 8192), 60, replace=False).tolist())
     fill_pools(fab, rng, low=low, zero=(0, 5), const=(7,))
     fab.region_mut("cold")[...] = 0xAB  # untouched blocks keep this pattern
     fab.force_checkpoint()
-    fab.attach_device(0)
-    print("fabric: distill cycle", flush=True)
+    fab.attach_device(0, cold_head_blocked=hb)
+    print(f"fabric: distill cycle (cold head-blocked {hb})", flush=True)
     n, ent = fab.distill(engine, F.DISTILL_ENTROPY_THRESHOLD)
     hot = fab.hot_pool_blocks()
     want = np.array([oracle.block_entropy(hot[b]) for b in range(8192)], np.float32)
