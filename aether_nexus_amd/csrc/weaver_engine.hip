@@ -60,6 +60,26 @@ int ensure(DevBuf& b, size_t bytes, std::string& err) {
     return AW_OK;
 }
 
+// The decode workspace grows like ensure(), but an outgrown buffer is kept
+// until the engine is destroyed instead of freed: a decode captured into a HIP
+// graph holds the address it was captured with, and a later, larger request
+// must not free it under the graph.  Growth is geometric (1.5x), so the kept
+// buffers add up to at most twice the largest one.
+int ensure_keep(DevBuf& b, size_t bytes, std::vector<void*>& retired, std::string& err) {
+    if (bytes <= b.cap && b.ptr) return AW_OK;
+    const size_t want = std::max({align_up(bytes, kAlign), kAlign, align_up(b.cap + b.cap / 2, kAlign)});
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, want);
+    if (e != hipSuccess) {
+        err = std::string("hipMalloc(") + std::to_string(want) + ") failed: " + hipGetErrorString(e);
+        return AW_E_HIP;
+    }
+    if (b.ptr) retired.push_back(b.ptr);
+    b.ptr = p;
+    b.cap = want;
+    return AW_OK;
+}
+
 // Workspace sub-allocation offsets for one request.
 struct Layout {
     aw_decode_plan_info info{};
@@ -263,6 +283,7 @@ struct aw_engine {
     uint32_t hot_wpc[3] = {12, 4, 4}; // resident hot waves per CU (RT = 1, 2, 4)
     DevBuf q, ql, hot, cold, refs, dict, out; // aw_decode copies (weaver.rs:40-46)
     DevBuf ws;                                // per-request scratch
+    std::vector<void*> retired_ws;            // outgrown scratch, kept for captured graphs
     uint32_t* err = nullptr;                  // device error word
     int profiling = 0; // AW_PROFILE_*
     struct Pending {
@@ -651,7 +672,7 @@ int decode_device(aw_engine* e, const aw_decode_desc* d, hipStream_t st) {
         return fail(e, AW_E_INVALID_ARG, "hot_count > 0 needs hot_blocks > 0");
     if (d->cold_count && ((uintptr_t)d->cold & 15u))
         return fail(e, AW_E_ALIGN, "cold pool pointer is not 16-byte aligned");
-    if ((rc = ensure(e->ws, o.info.workspace_bytes, e->last_error))) return rc;
+    if ((rc = ensure_keep(e->ws, o.info.workspace_bytes, e->retired_ws, e->last_error))) return rc;
     char* ws = (char*)e->ws.ptr;
     return d->head_dim == 64 ? run_pipeline<64>(e, d, o, ws, st) : run_pipeline<128>(e, d, o, ws, st);
 }
@@ -887,6 +908,7 @@ void aw_engine_destroy(aw_engine* e) {
     for (hipEvent_t ev : e->free_events) (void)hipEventDestroy(ev);
     for (DevBuf* b : {&e->q, &e->ql, &e->hot, &e->cold, &e->refs, &e->dict, &e->out, &e->ws})
         if (b->ptr) (void)hipFree(b->ptr);
+    for (void* p : e->retired_ws) (void)hipFree(p);
     if (e->err) (void)hipFree(e->err);
     if (e->side) (void)hipStreamSynchronize(e->side);
     if (e->ev_fork) (void)hipEventDestroy(e->ev_fork);

@@ -223,7 +223,12 @@ int aw_decode(aw_engine* engine,
  * causal drafts, score scale, shared dictionary and separate V.  Scratch comes
  * from an engine-owned workspace that grows on demand (the growth allocates).
  * Block refs and atom indices are checked on the device: a bad one is skipped
- * and recorded; aw_engine_check_device_errors reports it. */
+ * and recorded; aw_engine_check_device_errors reports it.
+ * The call may be captured into a HIP graph (stream capture): the graph keeps
+ * the workspace that call used, and the engine frees no workspace before
+ * aw_engine_destroy, so later, larger calls leave captured graphs valid.
+ * Replays and other calls on one engine share that workspace: run them one at
+ * a time (stream-ordered, or synchronised between). */
 int aw_decode_device(aw_engine* engine, const aw_decode_desc* desc, void* hip_stream);
 
 /* Wait for `hip_stream` and report AW_E_OOB if any kernel since the last check
