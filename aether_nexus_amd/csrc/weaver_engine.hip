@@ -284,6 +284,7 @@ struct aw_engine {
     DevBuf q, ql, hot, cold, refs, dict, out; // aw_decode copies (weaver.rs:40-46)
     DevBuf ws;                                // per-request scratch
     std::vector<void*> retired_ws;            // outgrown scratch, kept for captured graphs
+    DevBuf enc_ws;                            // encoder scratch: per-atom norms and flags
     uint32_t* err = nullptr;                  // device error word
     int profiling = 0; // AW_PROFILE_*
     struct Pending {
@@ -906,7 +907,7 @@ void aw_engine_destroy(aw_engine* e) {
     if (e->stream) (void)hipStreamSynchronize(e->stream);
     drain_events(e);
     for (hipEvent_t ev : e->free_events) (void)hipEventDestroy(ev);
-    for (DevBuf* b : {&e->q, &e->ql, &e->hot, &e->cold, &e->refs, &e->dict, &e->out, &e->ws})
+    for (DevBuf* b : {&e->q, &e->ql, &e->hot, &e->cold, &e->refs, &e->dict, &e->out, &e->ws, &e->enc_ws})
         if (b->ptr) (void)hipFree(b->ptr);
     for (void* p : e->retired_ws) (void)hipFree(p);
     if (e->err) (void)hipFree(e->err);
@@ -1036,8 +1037,8 @@ int encode_check(const aw_encode_desc* d, char* msg, size_t mlen) {
         put_msg(msg, mlen, "dict_heads must be 1 (shared) or kv_heads");
         return AW_E_INVALID_ARG;
     }
-    if (d->flags & ~AW_F_COLD_HEAD_BLOCKED) {
-        put_msg(msg, mlen, "unknown encoder flags 0x%x", d->flags & ~AW_F_COLD_HEAD_BLOCKED);
+    if (d->flags & ~(AW_F_COLD_HEAD_BLOCKED | AW_F_ENCODE_FULL_SCAN)) {
+        put_msg(msg, mlen, "unknown encoder flags 0x%x", d->flags & ~(AW_F_COLD_HEAD_BLOCKED | AW_F_ENCODE_FULL_SCAN));
         return AW_E_INVALID_ARG;
     }
     if (d->n_blocks >= (1u << 27)) {
@@ -1075,16 +1076,40 @@ int encode_device(aw_engine* e, const aw_encode_desc* d, hipStream_t st) {
     a.s_head = head_blocked ? kBlock : 1u;
     a.hot_blocks = d->hot_blocks;
     a.cold_blocks = d->cold_blocks;
-    const dim3 grid(cdiv((uint64_t)d->n_blocks * kBlock, aw::kEncThreads), d->kv_heads);
-    if (d->head_dim == 64)
-        hipLaunchKernelGGL(aw::encode_kernel<64>, grid, dim3(aw::kEncThreads), 0, st, a);
-    else
-        hipLaunchKernelGGL(aw::encode_kernel<128>, grid, dim3(aw::kEncThreads), 0, st, a);
-    AW_HIP(e, hipGetLastError());
+    // Scratch of the MFMA path (the atoms' norms), allocated before any work is queued.
+    const bool full_scan = (d->flags & AW_F_ENCODE_FULL_SCAN) != 0;
+    const uint64_t n_atoms = (uint64_t)d->dict_heads * d->dict_size;
+    if (!full_scan && (rc = ensure_keep(e->enc_ws, n_atoms * sizeof(aw::AtomNorm), e->retired_ws, e->last_error)))
+        return rc;
+    // The entropy proxy (few long lanes) runs on the side stream beside the encoder.
     if (d->entropy) {
-        hipLaunchKernelGGL(aw::entropy_kernel, dim3(cdiv(d->n_blocks, 64)), dim3(64), 0, st, a, d->head_dim);
+        AW_HIP(e, hipEventRecord(e->ev_fork, st));
+        AW_HIP(e, hipStreamWaitEvent(e->side, e->ev_fork, 0));
+        hipLaunchKernelGGL(aw::entropy_kernel, dim3(cdiv(d->n_blocks, aw::kEntBlocks)), dim3(64), 0, e->side, a, d->head_dim);
         AW_HIP(e, hipGetLastError());
+        AW_HIP(e, hipEventRecord(e->ev_join, e->side));
     }
+    if (full_scan) {
+        const dim3 grid(cdiv((uint64_t)d->n_blocks * kBlock, aw::kEncThreads), d->kv_heads);
+        if (d->head_dim == 64)
+            hipLaunchKernelGGL(aw::encode_kernel<64>, grid, dim3(aw::kEncThreads), 0, st, a);
+        else
+            hipLaunchKernelGGL(aw::encode_kernel<128>, grid, dim3(aw::kEncThreads), 0, st, a);
+    } else {
+        // MFMA prefilter + exact rescoring: the atoms' norms first.
+        aw::AtomNorm* dn = (aw::AtomNorm*)e->enc_ws.ptr;
+        const dim3 ngrid((uint32_t)cdiv(n_atoms, 256));
+        const dim3 grid(cdiv((uint64_t)d->n_blocks * kBlock, aw::kEncMTokens), d->kv_heads);
+        if (d->head_dim == 64) {
+            hipLaunchKernelGGL(aw::dict_norm_kernel<64>, ngrid, dim3(256), 0, st, d->dict, n_atoms, dn);
+            hipLaunchKernelGGL(aw::encode_mfma_kernel<64>, grid, dim3(aw::kEncMThreads), 0, st, a, dn);
+        } else {
+            hipLaunchKernelGGL(aw::dict_norm_kernel<128>, ngrid, dim3(256), 0, st, d->dict, n_atoms, dn);
+            hipLaunchKernelGGL(aw::encode_mfma_kernel<128>, grid, dim3(aw::kEncMThreads), 0, st, a, dn);
+        }
+    }
+    AW_HIP(e, hipGetLastError());
+    if (d->entropy) AW_HIP(e, hipStreamWaitEvent(st, e->ev_join, 0));
     return AW_OK;
 }
 
@@ -1113,7 +1138,7 @@ int aw_block_entropy_device(aw_engine* e, const uint16_t* hot, uint64_t hot_bloc
     a.kv_heads = kv_heads;
     a.n_blocks = n_blocks;
     a.hot_blocks = hot_blocks;
-    hipLaunchKernelGGL(aw::entropy_kernel, dim3(cdiv(n_blocks, 64)), dim3(64), 0, (hipStream_t)stream, a,
+    hipLaunchKernelGGL(aw::entropy_kernel, dim3(cdiv(n_blocks, aw::kEntBlocks)), dim3(64), 0, (hipStream_t)stream, a,
                        head_dim);
     AW_HIP(e, hipGetLastError());
     return AW_OK;

@@ -1694,63 +1694,442 @@ __global__ __launch_bounds__(kEncThreads) void encode_kernel(EncodeArgs a) {
     a.cold[(uint64_t)c * kBlockTokens * a.kv_heads + tt * a.s_tok + g * a.s_head] = code;
 }
 
+// ------------------------------------- encoder: MFMA prefilter, exact rescoring
+//
+// The same codes as encode_kernel (bit for bit) at a fraction of the exact FMAs.
+// For token x and atom d_a let S_a be the reference's score (f32, sequential in
+// head-dim order) and M_a the MFMA score of the same exact f16 x f16 products
+// summed in another order.  Both are sums of the HD products p_k with one
+// rounding per addition, so |M_a - S_a| <= 2*HD*u*sum|p_k| <= 2*HD*u*|x|*|d_a|
+// (u = 2^-24; Cauchy-Schwarz); the kernel uses E_a = 8*HD*u*|x|*|d_a|, four
+// times that, with the norms rounded up.  Subnormal components may be flushed by
+// the matrix unit: an atom with some gets E_a += |x|_1 * 2^-14, a token with some
+// E_a += |d_a|_1 * 2^-14 (a flushed term is below 2^-14 times its partner).  Then:
+//   T   = the 4th largest of M_a - E_a          (four atoms have S >= T, so
+//                                                 the exact 4th score is >= T);
+//   C   = { a : M_a + E_a >= T }                (holds every atom whose exact
+//                                                 score can reach the top 4);
+//   the exact S_a of the atoms of C, in ascending atom order, through the
+//   same strict-greater insertion as the full scan: the same four atoms in the
+//   same order, hence the same code.
+// Tokens with an inf or NaN component, and tokens whose candidate list
+// overflows, take the full exact scan; atoms with an inf or NaN component are
+// always candidates.
+//
+// Work-group = 4 waves x 64 tokens of one kv head (4 tiles of 16 tokens per
+// wave).  The dictionary streams through LDS in chunks of 64 atoms, twice:
+// pass 1 finds T, pass 2 collects C.  MFMA orientation M^T = D X^T with
+// v_mfma_f32_16x16x32_f16 (lane l, li = l%16, lg = l/16): A = atoms (row li of
+// the atom tile, dims 32*ks + 8*lg ..), B = the token tile (token li, the same
+// dims, held in registers), C: lane l holds token li and atoms 4*lg .. 4*lg+3.
+// Pass 2 keeps each lane's candidates of a token in its own sub-list (no
+// atomics; ascending, as the lane meets its atoms in order); pass 3: one thread
+// per token merges its 4 sub-lists and rescores the candidates exactly.
+constexpr int kEncMThreads = 256;
+constexpr int kEncMTokens = 256;  // tokens per work-group
+constexpr int kEncMChunk = 64;    // atoms per staged dictionary chunk
+constexpr int kEncMCap = 32;      // candidates kept per token
+constexpr int kEncMSub = kEncMCap / 4; // per token and lane: each of 4 lanes sees a quarter of the atoms
+constexpr uint32_t kDictBad = 1u, kDictSubnormal = 2u;
+
+typedef float float2_t __attribute__((ext_vector_type(2)));
+
+// |d_a|_2 and |d_a|_1 (rounded up) and flags (kDictBad: inf or NaN component;
+// kDictSubnormal) for every atom of every dictionary head, as {l2, l1, flags}.
+struct __attribute__((aligned(16))) AtomNorm {
+    float l2, l1;
+    uint32_t flags, pad;
+};
+template <int HD>
+__global__ __launch_bounds__(256) void dict_norm_kernel(const uint16_t* dict, uint64_t n_atoms, AtomNorm* out) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n_atoms) return;
+    const uint4_t* row = (const uint4_t*)(dict + i * HD);
+    float ss = 0.0f, s1 = 0.0f;
+    uint32_t fl = 0;
+#pragma unroll 4
+    for (int j = 0; j < HD / 8; ++j) {
+        const uint4_t w = row[j];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t bits = (w[e / 2] >> (16 * (e % 2))) & 0xFFFFu;
+            const uint32_t ex = (bits >> 10) & 31u, man = bits & 1023u;
+            fl |= ex == 31u ? kDictBad : 0u;
+            fl |= (ex == 0u && man != 0u) ? kDictSubnormal : 0u;
+            const float f = h2f_bits(bits);
+            ss = fmaf(f, f, ss);
+            s1 += fabsf(f);
+        }
+    }
+    out[i] = AtomNorm{sqrtf(ss) * 1.001f, s1 * 1.001f, fl, 0u};
+}
+
+template <int HD>
+__global__ __launch_bounds__(kEncMThreads) void encode_mfma_kernel(EncodeArgs a, const AtomNorm* dnorm) {
+    constexpr int KS = HD / 32, P = HD + 8, PR = HD / 8, NTT = 4, CH = kEncMChunk, CAP = kEncMCap;
+    constexpr int CPIECES = CH * PR, CPT = CPIECES / kEncMThreads; // 16-byte pieces per chunk / thread
+    static_assert(CPT * kEncMThreads == CPIECES, "chunk staging");
+    __shared__ __attribute__((aligned(16))) _Float16 sd[2][CH * P];
+    __shared__ AtomNorm s_dn[2][CH];
+    __shared__ __attribute__((aligned(16))) unsigned char s_lists[kEncMTokens * CAP * 2]; // pass-1 tops, then candidates
+    __shared__ float s_T[kEncMTokens];
+    __shared__ uint32_t s_cnt[kEncMTokens * 4];
+    __shared__ uint32_t s_xfl[kEncMTokens];
+    static_assert(kEncMTokens * 16 * 4 <= (int)sizeof(s_lists), "pass-1 tops fit the candidate lists");
+    float* s_top = (float*)s_lists;
+    uint16_t* s_cand = (uint16_t*)s_lists;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, li = lane & 15, lg = lane >> 4;
+    const uint32_t g = blockIdx.y;
+    const uint32_t n_tok = a.n_blocks * kBlockTokens;
+    const uint32_t tok0 = blockIdx.x * kEncMTokens;
+    const uint32_t A = a.dict_size, n_ch = (A + CH - 1) / CH;
+    const uint32_t dh = a.dict_heads == 1 ? 0u : g;
+    const uint16_t* Dg = a.dict + (uint64_t)dh * A * HD;
+    const AtomNorm* dn = dnorm + (uint64_t)dh * A;
+    constexpr float kBound = 8.0f * HD * 5.9604645e-8f; // 8 * HD * 2^-24
+    constexpr float kSub = 6.1035156e-5f;               // 2^-14: bound of a subnormal f16
+
+    // The lane's tokens (B operands) and their norms; xsub: the token has a
+    // subnormal component (its bound then takes |d_a|_1 * 2^-14 more).
+    half8_t xb[NTT][KS];
+    float kx[NTT], sx[NTT], xsub[NTT];
+    {
+        float ss[NTT], s1[NTT];
+        uint32_t fl[NTT];
+#pragma unroll
+        for (int tt = 0; tt < NTT; ++tt) {
+            const uint32_t T = min(tok0 + (uint32_t)(wave * 64 + tt * 16 + li), n_tok - 1u);
+            const uint32_t bi = T / kBlockTokens, ti = T % kBlockTokens;
+            uint32_t b = a.src[bi] & kRefMask;
+            b = b < a.hot_blocks ? b : 0u; // such a token is not written
+            const uint16_t* xp = a.hot + (((uint64_t)b * kBlockTokens + ti) * a.kv_heads + g) * HD;
+            ss[tt] = 0.0f;
+            s1[tt] = 0.0f;
+            fl[tt] = 0u;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                const uint4_t w = *(const uint4_t*)(xp + 32 * ks + 8 * lg);
+                xb[tt][ks] = as_h8(w);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const uint32_t bits = (w[e / 2] >> (16 * (e % 2))) & 0xFFFFu;
+                    const uint32_t ex = (bits >> 10) & 31u, man = bits & 1023u;
+                    fl[tt] |= ex == 31u ? 1u : 0u;                      // inf or NaN: full scan
+                    fl[tt] |= (ex == 0u && man != 0u) ? 2u : 0u;         // subnormal: wider bound
+                    const float f = h2f_bits(bits);
+                    ss[tt] = fmaf(f, f, ss[tt]);
+                    s1[tt] += fabsf(f);
+                }
+            }
+        }
+#pragma unroll
+        for (int tt = 0; tt < NTT; ++tt) {
+            ss[tt] += __shfl_xor(ss[tt], 16);
+            ss[tt] += __shfl_xor(ss[tt], 32);
+            s1[tt] += __shfl_xor(s1[tt], 16);
+            s1[tt] += __shfl_xor(s1[tt], 32);
+            fl[tt] |= __shfl_xor(fl[tt], 16);
+            fl[tt] |= __shfl_xor(fl[tt], 32);
+            kx[tt] = kBound * (sqrtf(ss[tt]) * 1.001f);
+            sx[tt] = kSub * (s1[tt] * 1.001f);
+            xsub[tt] = (fl[tt] & 2u) ? kSub : 0.0f;
+            if (lg == 0) s_xfl[wave * 64 + tt * 16 + li] = fl[tt] & 1u;
+        }
+    }
+
+    // Dictionary chunk staging: every thread loads CPT pieces (clamped into the
+    // dictionary), threads < CH also the atoms' norms.
+    uint4_t creg[CPT];
+    AtomNorm nreg{};
+    auto load_chunk = [&](uint32_t ch) {
+#pragma unroll
+        for (int k = 0; k < CPT; ++k) {
+            const int p = tid + k * kEncMThreads;
+            const uint32_t at = min(ch * CH + (uint32_t)(p / PR), A - 1u);
+            creg[k] = *(const uint4_t*)(Dg + (uint64_t)at * HD + 8 * (p % PR));
+        }
+        if (tid < CH) nreg = dn[min(ch * CH + (uint32_t)tid, A - 1u)];
+    };
+    auto store_chunk = [&](int buf) {
+#pragma unroll
+        for (int k = 0; k < CPT; ++k) {
+            const int p = tid + k * kEncMThreads;
+            *(uint4_t*)(&sd[buf][(p / PR) * P + 8 * (p % PR)]) = creg[k];
+        }
+        if (tid < CH) s_dn[buf][tid] = nreg;
+    };
+    // One pass over the dictionary.  Per atom tile, fn(acc, E, badm, atom0) gets the
+    // MFMA scores acc[tt][e] of the lane's tokens (tt) and atoms atom0 + e, one bound
+    // E[tt] for the lane's 4 atoms (from their largest norms, so >= each atom's own
+    // bound), and the mask of those atoms with an inf or NaN component.
+    auto stream = [&](auto fn) {
+        load_chunk(0);
+        store_chunk(0);
+        __syncthreads();
+        for (uint32_t ch = 0; ch < n_ch; ++ch) {
+            const int cur = (int)(ch & 1u);
+            const bool more = ch + 1 < n_ch;
+            if (more) load_chunk(ch + 1);
+            const uint32_t tiles = min((uint32_t)(CH / 16), (A - ch * CH) / 16u);
+            for (uint32_t at = 0; at < tiles; ++at) {
+                half8_t ad[KS];
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) ad[ks] = *(const half8_t*)(&sd[cur][(at * 16 + li) * P + 32 * ks + 8 * lg]);
+                float l2m = 0.0f, l1m = 0.0f;
+                uint32_t sub = 0u, badm = 0u;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) { // bad atoms (always candidates) stay out of the bound
+                    const AtomNorm nd = s_dn[cur][at * 16 + 4 * lg + e];
+                    const bool bad = (nd.flags & kDictBad) != 0u;
+                    l2m = bad ? l2m : fmaxf(l2m, nd.l2);
+                    l1m = bad ? l1m : fmaxf(l1m, nd.l1);
+                    sub |= bad ? 0u : (nd.flags & kDictSubnormal);
+                    badm |= bad ? (1u << e) : 0u;
+                }
+                float4_t acc[NTT];
+                float E[NTT];
+#pragma unroll
+                for (int tt = 0; tt < NTT; ++tt) {
+                    acc[tt] = (float4_t)0.0f;
+#pragma unroll
+                    for (int ks = 0; ks < KS; ++ks) acc[tt] = mfma16x16x32(ad[ks], xb[tt][ks], acc[tt]);
+                    E[tt] = fmaf(kx[tt], l2m, fmaf(xsub[tt], l1m, sub ? sx[tt] : 0.0f));
+                }
+                fn(acc, E, badm, ch * CH + at * 16 + 4 * lg);
+            }
+            if (more) store_chunk(cur ^ 1);
+            __syncthreads();
+        }
+    };
+
+    // Inserting y into the descending top[0..3]: max, then three medians of three.
+    auto insert4 = [](float (&t)[4], float y) {
+        const float t0 = fmaxf(t[0], y);
+        const float t1 = __builtin_amdgcn_fmed3f(t[0], t[1], y);
+        const float t2 = __builtin_amdgcn_fmed3f(t[1], t[2], y);
+        const float t3 = __builtin_amdgcn_fmed3f(t[2], t[3], y);
+        t[0] = t0;
+        t[1] = t1;
+        t[2] = t2;
+        t[3] = t3;
+    };
+    // Pass 1: per lane and token, the 4 largest of max_e(M) - E over its atom
+    // tiles: each is a lower bound of the exact score of a distinct atom, so the
+    // 4th largest over all lanes is <= the exact 4th score.
+    float top[NTT][4];
+#pragma unroll
+    for (int tt = 0; tt < NTT; ++tt)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) top[tt][k] = -INFINITY;
+    stream([&](const float4_t (&acc)[NTT], const float (&E)[NTT], uint32_t badm, uint32_t) {
+#pragma unroll
+        for (int tt = 0; tt < NTT; ++tt) {
+            float m = -INFINITY;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) m = fmaxf(m, (badm >> e) & 1u ? -INFINITY : acc[tt][e]);
+            insert4(top[tt], m - E[tt]);
+        }
+    });
+#pragma unroll
+    for (int tt = 0; tt < NTT; ++tt)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) s_top[(wave * 64 + tt * 16 + li) * 16 + lg * 4 + k] = top[tt][k];
+    if (tid < kEncMTokens) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) s_cnt[tid * 4 + q] = 0u;
+    }
+    __syncthreads();
+    {
+        // Thread tid = token tid: T = the 4th largest of its 16 values (the 4 lanes' top 4s).
+        float t4[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+        for (int k = 0; k < 16; ++k) insert4(t4, s_top[tid * 16 + k]);
+        s_T[tid] = t4[3];
+    }
+    __syncthreads();
+    float T[NTT];
+#pragma unroll
+    for (int tt = 0; tt < NTT; ++tt) T[tt] = s_T[wave * 64 + tt * 16 + li];
+    // Pass 2: the candidates, M >= T - E (M + E >= T up to a rounding the bound's
+    // slack covers) and every atom with an inf or NaN component, into sub-list
+    // (token, lg) of kEncMSub entries; counts in s_cnt (each owned by one lane).
+    stream([&](const float4_t (&acc)[NTT], const float (&E)[NTT], uint32_t badm, uint32_t atom0) {
+        uint32_t mask = 0u;
+#pragma unroll
+        for (int tt = 0; tt < NTT; ++tt) {
+            const float thr = T[tt] - E[tt];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) mask |= (acc[tt][e] >= thr || ((badm >> e) & 1u)) ? (1u << (tt * 4 + e)) : 0u;
+        }
+        while (mask) {
+            const uint32_t bit = __builtin_ctz(mask);
+            mask &= mask - 1u;
+            const uint32_t ci = (wave * 64 + (bit >> 2) * 16 + li) * 4 + lg;
+            const uint32_t k = s_cnt[ci];
+            if (k < (uint32_t)kEncMSub) s_cand[ci * kEncMSub + k] = (uint16_t)(atom0 + (bit & 3u));
+            s_cnt[ci] = k + 1u;
+        }
+    });
+
+    // Pass 3: thread = token; exact scores of the candidates in ascending atom order.
+    const uint32_t T3 = tok0 + tid;
+    const bool live = T3 < n_tok;
+    const uint32_t Tc = live ? T3 : n_tok - 1u;
+    const uint32_t bi = Tc / kBlockTokens, tt3 = Tc % kBlockTokens;
+    const uint32_t b = a.src[bi] & kRefMask;
+    const uint32_t c = a.dst ? (a.dst[bi] & kRefMask) : b;
+    const bool ok = live && b < a.hot_blocks && c < a.cold_blocks;
+    if (live && g == 0 && tt3 == 0) { // one report per block
+        if (b >= a.hot_blocks) flag_error(a.err, kErrHotRef);
+        if (c >= a.cold_blocks) flag_error(a.err, kErrColdRef);
+    }
+    if (!ok) return; // no barrier follows
+    const uint4_t* xp = (const uint4_t*)(a.hot + (((uint64_t)b * kBlockTokens + tt3) * a.kv_heads + g) * HD);
+    half8_t x[PR];
+#pragma unroll
+    for (int j = 0; j < PR; ++j) x[j] = as_h8(xp[j]);
+    float v[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    uint32_t ix[4] = {0u, 0u, 0u, 0u};
+    auto score = [&](uint32_t ai) {
+        const uint4_t* dr = (const uint4_t*)(Dg + (uint64_t)ai * HD);
+        float s = -0.0f;
+#pragma unroll
+        for (int j = 0; j < PR; ++j) {
+            const half8_t d8 = as_h8(dr[j]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) s = fmaf((float)x[j][e], (float)d8[e], s);
+        }
+        if (s > v[3]) { // NaN and -inf never enter
+            const bool g0 = s > v[0], g1 = s > v[1], g2 = s > v[2];
+            v[3] = g2 ? v[2] : s;
+            ix[3] = g2 ? ix[2] : ai;
+            v[2] = g1 ? v[1] : (g2 ? s : v[2]);
+            ix[2] = g1 ? ix[1] : (g2 ? ai : ix[2]);
+            v[1] = g0 ? v[0] : (g1 ? s : v[1]);
+            ix[1] = g0 ? ix[0] : (g1 ? ai : ix[1]);
+            v[0] = g0 ? s : v[0];
+            ix[0] = g0 ? ai : ix[0];
+        }
+    };
+    uint32_t n = 0;
+    bool full = s_xfl[tid] != 0u;
+    uint16_t* lst = s_cand + tid * CAP; // the token's 4 sub-lists, compacted in place
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t m = s_cnt[tid * 4 + q];
+        full = full || m > (uint32_t)kEncMSub;
+        for (uint32_t k = 0; !full && k < m; ++k) lst[n++] = lst[q * kEncMSub + k];
+    }
+    if (full) {
+        for (uint32_t ai = 0; ai < A; ++ai) score(ai);
+    } else {
+        for (uint32_t i = 1; i < n; ++i) { // ascending atom order (the list is the thread's own)
+            const uint16_t key = lst[i];
+            uint32_t j = i;
+            while (j > 0 && lst[j - 1] > key) {
+                lst[j] = lst[j - 1];
+                --j;
+            }
+            lst[j] = key;
+        }
+        for (uint32_t i = 0; i < n; ++i) score(lst[i]);
+    }
+    uint32_t cb[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const bool filled = v[k] != -INFINITY;
+        cb[k] = filled ? (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[k]) : 0u;
+        ix[k] = filled ? ix[k] : 0u;
+    }
+    const uint4_t code = {ix[0] | (ix[1] << 16), ix[2] | (ix[3] << 16), cb[0] | (cb[1] << 16), cb[2] | (cb[3] << 16)};
+    a.cold[(uint64_t)c * kBlockTokens * a.kv_heads + tt3 * a.s_tok + g * a.s_head] = code;
+}
+
 // Variance proxy of each listed block (distiller.rs:126-159), bit-exact: one
 // lane per block runs the reference's loops in memory order, in f64, with no
 // fused multiply-add (the reference squares, then adds), and returns f32; an
 // all-zero block gives 0.  Without a block list (src null) lane i takes block i.
 //
 // The f64 sums are sequential chains, so a block cannot be split across lanes;
-// what is parallel is the data supply.  One wave owns 64 blocks and streams
-// them in chunks of kEntChunk values: the wave loads a chunk of all 64 blocks
-// with coalesced 16-byte loads (16 lanes per 256-byte block chunk) into one of
-// two LDS tiles while every lane runs its own chain over the other tile.  Rows
-// are padded by 16 bytes so the 64 lanes' row reads spread over the banks.
+// what is parallel is the data supply.  One wave owns kEntBlocks blocks and
+// streams them in chunks of kEntChunk values: the wave loads a chunk of all its
+// blocks with coalesced 16-byte loads (16 lanes per 256-byte block chunk) into
+// one of two LDS tiles while each block's lane runs its chain over the other
+// tile.  Rows are padded by 16 bytes so the lanes' row reads spread over the
+// banks.
 constexpr int kEntChunk = 128;                   // f16 values per block and chunk (256 bytes)
 constexpr int kEntCols = kEntChunk / 8;          // 16-byte words per row
 constexpr int kEntPitch = kEntCols + 1;          // padded row, in 16-byte words
 
+// The sum of a block's values needs no particular order when it is exact:
+// f16 values are multiples of 2^-24, so when sum|v| < 2^29 every partial sum of
+// any subset is a multiple of 2^-24 below 2^53 of them, exactly representable
+// in f64, and the reference's sequential sum from -0.0 equals any other order
+// (a zero total is +0.0 both ways unless every value is a zero, and then the
+// proxy is 0 anyway).  Pass 0 sums in four independent chains and records
+// sum|v| and whether an inf or NaN occurred; a wave with a block outside the
+// exact case repeats the sum sequentially (pass 2).
+constexpr int kEntChains = 4;
+struct EntSum {
+    double s[kEntChains], m[kEntChains];
+    bool all_zero, nonfinite;
+};
+
 // One 16-byte word (8 values) of a block, in memory order: pass 0 adds the
-// values (and tracks whether all are zero), pass 1 adds the squared deviations.
+// values in kEntChains chains (and their magnitudes), pass 1 adds the squared
+// deviations, pass 2 adds the values sequentially.
 template <int PASS>
-__device__ inline void entropy_word(const uint4_t w, bool& all_zero, double& acc, double mean) {
+__device__ inline void entropy_word(const uint4_t w, EntSum& st, double& acc, double mean) {
 #pragma clang fp contract(off)
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-        const float f = h2f_bits((w[e / 2] >> (16 * (e % 2))) & 0xFFFFu);
+        const uint32_t bits = (w[e / 2] >> (16 * (e % 2))) & 0xFFFFu;
+        const float f = h2f_bits(bits);
         if constexpr (PASS == 0) {
-            all_zero = all_zero && f == 0.0f;
-            acc = acc + (double)f;
-        } else {
+            st.all_zero = st.all_zero && f == 0.0f;
+            st.nonfinite = st.nonfinite || ((bits >> 10) & 31u) == 31u;
+            st.s[e % kEntChains] = st.s[e % kEntChains] + (double)f;
+            st.m[e % kEntChains] = st.m[e % kEntChains] + (double)fabsf(f);
+        } else if constexpr (PASS == 1) {
             const double diff = (double)f - mean;
             const double sq = diff * diff;
             acc = acc + sq;
+        } else {
+            acc = acc + (double)f;
         }
     }
 }
 
+// Blocks per wave.  A wave's 64 lanes all load (the stream is latency-bound:
+// more waves keep more chunks in flight); the first kEntBlocks lanes run the
+// chains.  At 16 blocks a wave, 8192 blocks make 512 waves.
+constexpr int kEntBlocks = 16;
+
 __global__ __launch_bounds__(64) void entropy_kernel(EncodeArgs a, uint32_t head_dim) {
-    __shared__ uint4_t tile[2][64][kEntPitch];
-    __shared__ uint32_t s_blk[64];
+    constexpr int NB = kEntBlocks, PL = NB * kEntCols / 64; // 16-byte loads per lane and chunk
+    static_assert(PL * 64 == NB * kEntCols, "chunk loads");
+    __shared__ uint4_t tile[2][NB][kEntPitch];
+    __shared__ uint32_t s_blk[NB];
     const uint32_t lane = threadIdx.x;
-    const uint32_t i = blockIdx.x * 64 + lane;
+    const bool chain = lane < (uint32_t)NB; // this lane owns a block
+    const uint32_t i = blockIdx.x * NB + lane;
     uint32_t b = 0;
     bool ok = false;
-    if (i < a.n_blocks) {
+    if (chain && i < a.n_blocks) {
         b = a.src ? (a.src[i] & kRefMask) : i;
         ok = b < a.hot_blocks;
         if (!ok) flag_error(a.err, kErrHotRef);
     }
-    s_blk[lane] = ok ? b : 0xFFFFFFFFu;
+    if (chain) s_blk[lane] = ok ? b : 0xFFFFFFFFu;
     __syncthreads();
     const uint64_t n = (uint64_t)kBlockTokens * a.kv_heads * head_dim; // values per block
     const uint64_t words = n / 8;                                        // 16-byte words per block
     const uint64_t n_chunks = (words + kEntCols - 1) / kEntCols;
     const uint4_t* hot = (const uint4_t*)a.hot;
     // Lane l loads words (k * 64 + l) of the chunk: row r = that / kEntCols, column c.
-    uint4_t reg[kEntCols];
+    uint4_t reg[PL];
     auto load = [&](uint64_t ch) {
 #pragma unroll
-        for (int k = 0; k < kEntCols; ++k) {
+        for (int k = 0; k < PL; ++k) {
             const uint32_t idx = k * 64 + lane, r = idx / kEntCols, c = idx % kEntCols;
             const uint32_t rb = s_blk[r];
             const uint64_t w = ch * kEntCols + c;
@@ -1759,12 +2138,16 @@ __global__ __launch_bounds__(64) void entropy_kernel(EncodeArgs a, uint32_t head
     };
     auto store = [&](int buf) {
 #pragma unroll
-        for (int k = 0; k < kEntCols; ++k) {
+        for (int k = 0; k < PL; ++k) {
             const uint32_t idx = k * 64 + lane;
             tile[buf][idx / kEntCols][idx % kEntCols] = reg[k];
         }
     };
-    bool all_zero = true;
+    EntSum st;
+#pragma unroll
+    for (int k = 0; k < kEntChains; ++k) st.s[k] = st.m[k] = -0.0;
+    st.all_zero = true;
+    st.nonfinite = false;
     double mean = 0.0;
     // Streams the whole block once per pass; the pass is a compile-time constant
     // so the inner loops carry no branch.
@@ -1777,26 +2160,35 @@ __global__ __launch_bounds__(64) void entropy_kernel(EncodeArgs a, uint32_t head
             const int cur = (int)(ch & 1);
             const bool more = ch + 1 < n_chunks;
             if (more) load(ch + 1);
-            const uint4_t* row = tile[cur][lane];
-            if ((ch + 1) * kEntCols <= words) {
-                uint4_t w[kEntCols];
+            if (chain) {
+                const uint4_t* row = tile[cur][lane];
+                if ((ch + 1) * kEntCols <= words) {
+                    uint4_t w[kEntCols];
 #pragma unroll
-                for (int c = 0; c < kEntCols; ++c) w[c] = row[c];
+                    for (int c = 0; c < kEntCols; ++c) w[c] = row[c];
 #pragma unroll
-                for (int c = 0; c < kEntCols; ++c) entropy_word<P>(w[c], all_zero, acc, mean);
-            } else {
-                const uint32_t cols = (uint32_t)(words - ch * kEntCols);
-                for (uint32_t c = 0; c < cols; ++c) entropy_word<P>(row[c], all_zero, acc, mean);
+                    for (int c = 0; c < kEntCols; ++c) entropy_word<P>(w[c], st, acc, mean);
+                } else {
+                    const uint32_t cols = (uint32_t)(words - ch * kEntCols);
+                    for (uint32_t c = 0; c < cols; ++c) entropy_word<P>(row[c], st, acc, mean);
+                }
             }
             if (more) store(cur ^ 1);
             __syncthreads();
         }
         return acc;
     };
-    const double sum = stream(std::integral_constant<int, 0>{}, -0.0);
+    (void)stream(std::integral_constant<int, 0>{}, -0.0);
+    double sum = (st.s[0] + st.s[1]) + (st.s[2] + st.s[3]);
+    const double mag = (st.m[0] + st.m[1]) + (st.m[2] + st.m[3]);
+    const bool exact = !chain || (!st.nonfinite && mag < 536870912.0); // 2^29
+    if (__any(!exact)) { // wave-uniform: the sequential sum for the blocks that need it
+        const double seq = stream(std::integral_constant<int, 2>{}, -0.0);
+        sum = exact ? sum : seq;
+    }
     mean = sum / (double)n;
     const double var = stream(std::integral_constant<int, 1>{}, -0.0);
-    if (i < a.n_blocks) a.entropy[i] = (!ok || all_zero) ? 0.0f : (float)(var / (double)n);
+    if (chain && i < a.n_blocks) a.entropy[i] = (!ok || st.all_zero) ? 0.0f : (float)(var / (double)n);
 }
 
 } // namespace aw

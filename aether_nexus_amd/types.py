@@ -172,6 +172,7 @@ class LoomDescriptor:
 
 AW_F_CAUSAL = 1
 AW_F_COLD_HEAD_BLOCKED = 2
+AW_F_ENCODE_FULL_SCAN = 4
 
 AW_OK = 0
 AW_E_INVALID_ARG = -1

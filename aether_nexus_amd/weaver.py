@@ -19,8 +19,8 @@ from typing import Any, Optional
 import numpy as np
 
 from . import _lib
-from .types import (AW_F_CAUSAL, AW_F_COLD_HEAD_BLOCKED, SPARSE_CODE_DTYPE, STAGES, STRUCT_SIZES, DecodeDesc,
-                    EncodeDesc, PlanInfo, WeaverParams)
+from .types import (AW_F_CAUSAL, AW_F_COLD_HEAD_BLOCKED, AW_F_ENCODE_FULL_SCAN, SPARSE_CODE_DTYPE, STAGES,
+                    STRUCT_SIZES, DecodeDesc, EncodeDesc, PlanInfo, WeaverParams)
 
 
 class WeaverError(RuntimeError):
@@ -296,13 +296,14 @@ def make_desc(*, layers: int, batch: int, queries: int, q_heads: int, kv_heads: 
 
 def make_encode_desc(*, kv_heads: int, head_dim: int, dict_size: int, dict_heads: int, hot_blocks: int,
                      cold_blocks: int, hot, dictionary, src_blocks, cold, dst_blocks=None, entropy=None,
-                     cold_head_blocked: bool = False) -> EncodeDesc:
-    """Build an ``aw_encode_desc`` from device tensors (or raw device pointers)."""
+                     cold_head_blocked: bool = False, full_scan: bool = False) -> EncodeDesc:
+    """Build an ``aw_encode_desc`` from device tensors (or raw device pointers).
+    ``full_scan`` scores every atom exactly instead of prefiltering on MFMA (same codes)."""
     d = EncodeDesc()
     d.kv_heads, d.head_dim, d.dict_size, d.dict_heads = kv_heads, head_dim, dict_size, dict_heads
     n = src_blocks.numel() if hasattr(src_blocks, "numel") else int(np.asarray(src_blocks).size)
     d.n_blocks = n
-    d.flags = AW_F_COLD_HEAD_BLOCKED if cold_head_blocked else 0
+    d.flags = (AW_F_COLD_HEAD_BLOCKED if cold_head_blocked else 0) | (AW_F_ENCODE_FULL_SCAN if full_scan else 0)
     d.hot_blocks, d.cold_blocks = hot_blocks, cold_blocks
     d.hot, d.dict, d.src_blocks = _ptr(hot), _ptr(dictionary), _ptr(src_blocks)
     d.dst_blocks, d.cold, d.entropy = _ptr(dst_blocks), _ptr(cold), _ptr(entropy)

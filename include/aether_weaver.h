@@ -87,6 +87,10 @@ typedef struct aw_weaver_params {
                           producers that can write it (an encoder on the device),
                           the head-blocked order reads whole sectors; the results
                           are identical bit for bit. */
+/* aw_encode_desc only: score every atom exactly (the plain sequential scan)
+ * instead of an MFMA prefilter with exact rescoring of the atoms that can reach
+ * the top 4.  Both give the same codes; the scan is the slower reference form. */
+#define AW_F_ENCODE_FULL_SCAN 4u
 
 /* One decode call over L layers x B sequences x Q query tokens.  All pointers
  * are DEVICE pointers.  Element layouts (f16 = raw binary16 bits):
@@ -258,7 +262,7 @@ int aw_debug_gather_codes(aw_engine* engine, const aw_sparse_code* codes, size_t
  *   cold       [cold_blocks][16][kv_heads] SparseCodes; with AW_F_COLD_HEAD_BLOCKED
  *              [cold_blocks][kv_heads][16]
  *   entropy    optional [n_blocks] f32: the block's variance proxy (distiller.rs:126-159)
- * flags: 0 or AW_F_COLD_HEAD_BLOCKED. */
+ * flags: 0, AW_F_COLD_HEAD_BLOCKED, AW_F_ENCODE_FULL_SCAN (either or both). */
 typedef struct aw_encode_desc {
     uint32_t kv_heads, head_dim, dict_size, dict_heads;
     uint32_t n_blocks, flags;

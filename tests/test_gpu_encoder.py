@@ -4,6 +4,8 @@ against the CPU oracle, bit for bit, through the C ABI (aw_encode_device,
 aw_encode) on cuda:0."""
 from __future__ import annotations
 
+import zlib
+
 import numpy as np
 import pytest
 import torch
@@ -26,7 +28,7 @@ def pools(seed, hot_blocks, hkv, hd, a, dh, zero_dict=False, scale=1.0):
     return rng, hot, d
 
 
-def run_device(engine, stream, hot, d, src, dst, cold0, head_blocked, entropy):
+def run_device(engine, stream, hot, d, src, dst, cold0, head_blocked, entropy, full_scan=False):
     dev = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16) if a.dtype == np.uint16 else a).cuda()
     hot_t, d_t = dev(hot), dev(d)
     src_t = torch.from_numpy(np.asarray(src, np.uint32).view(np.int32)).cuda()
@@ -37,7 +39,7 @@ def run_device(engine, stream, hot, d, src, dst, cold0, head_blocked, entropy):
     desc = make_encode_desc(kv_heads=hkv, head_dim=hd, dict_size=d.shape[1], dict_heads=d.shape[0],
                             hot_blocks=hot.shape[0], cold_blocks=cold0.shape[0], hot=hot_t, dictionary=d_t,
                             src_blocks=src_t, dst_blocks=dst_t, cold=cold_t, entropy=ent_t,
-                            cold_head_blocked=head_blocked)
+                            cold_head_blocked=head_blocked, full_scan=full_scan)
     engine.encode_device(desc, stream=stream)
     engine.check_device_errors(stream)
     cold = cold_t.cpu().numpy().view(np.uint16)
@@ -108,3 +110,64 @@ def test_encode_bad_block_reported(engine, stream):
     with pytest.raises(WeaverError) as e:
         engine.encode(hot, d, [5], cold, kv_heads=4, head_dim=64, dict_size=256, dict_heads=4)
     assert e.value.status == AW_E_OOB
+
+
+def _unit(rng, shape):
+    dd = rng.standard_normal(shape)
+    return (dd / np.linalg.norm(dd, axis=-1, keepdims=True)).astype(np.float16)
+
+
+@pytest.mark.parametrize("case", ["subnormal_atoms", "subnormal_tokens", "inf_nan", "near_ties", "overflow_ties",
+                                  "dict_80", "dict_16"])
+def test_encode_prefilter_matches_full_scan(engine, stream, case):
+    """The MFMA prefilter with exact rescoring against the plain exact scan
+    (AW_F_ENCODE_FULL_SCAN) and the oracle, bit for bit, on inputs built to
+    stress it: subnormal components (the bound's flush slack, the token
+    fallback), inf / NaN components (always-candidate atoms, fallback tokens),
+    atoms one f16 ulp apart (MFMA and exact orders disagree), more tied atoms
+    than the candidate list holds (overflow fallback), and dictionary sizes
+    that leave a partial 64-atom chunk."""
+    rng = np.random.default_rng(zlib.crc32(case.encode()))
+    hkv, hd, a, nb = 4, 128, 256, 6
+    if case == "dict_80":
+        hd, a = 64, 80
+    if case == "dict_16":
+        a = 16
+    hot = rng.standard_normal((nb, 16, hkv, hd)).astype(np.float16)
+    d = _unit(rng, (hkv, a, hd))
+    if case == "subnormal_atoms":
+        mask = rng.random(d.shape) < 0.05
+        d[mask] = (rng.choice([-1, 1], mask.sum()) * rng.integers(1, 1024, mask.sum()) * 2.0 ** -24).astype(np.float16)
+    elif case == "subnormal_tokens":
+        mask = rng.random(hot.shape) < 0.01
+        hot[mask] = np.float16(2.0 ** -20)
+    elif case == "inf_nan":
+        d[0, 7, 3] = np.inf
+        d[1, 9, 0] = np.nan
+        d[2, 11, 5] = -np.inf
+        hot[1, 3, 0, 10] = np.nan
+        hot[2, 5, 1, 20] = np.inf
+        hot[3, 0, 3, :] = np.float16(-np.inf)
+    elif case == "near_ties":
+        # Atoms close to the tokens' best directions, and copies of them one ulp apart.
+        x = hot[:, :, 0, :].reshape(-1, hd).astype(np.float32)
+        best = x[rng.choice(x.shape[0], 8, replace=False)]
+        base = (best / np.linalg.norm(best, axis=-1, keepdims=True)).astype(np.float16)
+        for h in range(hkv):
+            for k in range(8):
+                d[h, 8 * k] = base[k]
+                for j in range(1, 8):
+                    v = base[k].view(np.uint16).copy()
+                    v[rng.integers(0, hd)] += np.uint16(1)
+                    d[h, 8 * k + j] = v.view(np.float16)
+    elif case == "overflow_ties":
+        d[:, 40:80] = d[:, 3:4]  # 41 identical atoms
+    hb = hot.view(np.uint16)
+    db = d.view(np.uint16)
+    src = rng.permutation(nb)
+    cold0 = np.zeros((nb, 16, hkv, 8), np.uint16)
+    got, _ = run_device(engine, stream, hb, db, src, None, cold0.copy(), False, False)
+    scan, _ = run_device(engine, stream, hb, db, src, None, cold0.copy(), False, False, full_scan=True)
+    want = oracle.encode_blocks(hb, db, src, cold=cold0.copy())
+    assert (scan == want).all()
+    assert (got == want).all(), f"{int((got != want).any(axis=-1).sum())} codes differ"
