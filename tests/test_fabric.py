@@ -133,6 +133,31 @@ def test_genesis_bytes_and_boot(genesis):
         assert not fab.dirty
 
 
+def test_llama8b_genesis_roundtrip(tmp_path):
+    """The reference's genesis -> boot round trip on its own geometry (fabric.rs:812-841,
+    Llama8B: an 18.6 GB file, almost all holes): personas in order, zero codes at both
+    ends of the cold pool, the header bytes, and the regions of the layout."""
+    d = F.model_dims("llama8b")
+    path = tmp_path / "llama8b.aether"
+    F.create_genesis(path, d)
+    r = FO.compute_regions(FO.PRESETS["llama8b"])
+    assert path.stat().st_size == r["total_size"]
+    with open(path, "rb") as fh:
+        assert fh.read(13) == FO.MAGIC + struct.pack("<I", FO.FORMAT_VERSION)
+        for i in range(4):
+            fh.seek(r["looms_offset"] + 32 * i)
+            assert fh.read(32) == bytes([i]) + bytes(31)
+    with F.Fabric(path, d) as fab:
+        assert fab.regions.as_dict() == r
+        assert [lm.persona for lm in fab.looms] == [0, 1, 2, 3]
+        codes = fab.cold_pool_codes()
+        assert codes.size == 32768 * 16 * 8
+        assert not codes[:64].view(np.uint16).any() and not codes[-64:].view(np.uint16).any()
+        assert fab.hot_pool_blocks().shape == (8192, 16, 8, 128)
+        assert fab.dictionary_atoms().shape == (8, 512, 128)
+    path.unlink()
+
+
 def test_boot_errors(genesis, tmp_path):
     """FabricError cases of boot_with_mode (fabric.rs:273-344), with the reference's messages."""
     d = dims(SMALL)
