@@ -1,6 +1,6 @@
 """CPU restatement of the reference's `.aether` Fabric layout and loom parsing.
 
-TEST INFRASTRUCTURE ONLY: imported by tests/ as the checker of the product's
+TEST INFRASTRUCTURE ONLY: imported by tests/ to check the product's
 fabric code (aether_nexus_amd/csrc/fabric.hip through include/aether_fabric.h),
 never by the product package.  Plain integer arithmetic on Python ints.
 

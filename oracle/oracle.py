@@ -1,7 +1,7 @@
 """ctypes binding of the CPU oracle (oracle/weaver_oracle.c).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
-cpu_baseline leg of bench.py, as the checker (or the timed CPU port), never by
+cpu_baseline leg of bench.py, to check results (or as the timed CPU port), never by
 the product package.  Functions take the host arrays produced by
 ``aether_nexus_amd.workloads.host_arrays`` plus the workload geometry.
 """

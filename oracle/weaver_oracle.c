@@ -2,8 +2,8 @@
  * weaver_oracle.c — CPU oracle for the Weaver decode path.
  *
  * TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and the
- * cpu_baseline leg of bench.py may load this library, and only as the checker
- * (or, for the baseline, as the CPU port being timed).  The product library
+ * cpu_baseline leg of bench.py may load this library, and only to check the
+ * product's results (or, for the baseline, as the CPU port being timed).  The product library
  * (aether_nexus_amd/libaether_weaver.so) never calls it and has no CPU fallback.
  *
  * The reference has no CPU Weaver implementation (WeaverEngine::decode only

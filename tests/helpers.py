@@ -1,5 +1,5 @@
 """Shared helpers of the parity tests: run a workload on the GPU through the C
-ABI and compare with the CPU oracle at the north-star tolerance
+ABI and compare with the CPU oracle at the attention tolerance
 (max-abs 2e-3, rel-L2 1e-3 against the fp64 brute force)."""
 from __future__ import annotations
 
