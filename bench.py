@@ -523,8 +523,8 @@ def main():
                               args.traffic_command))
         return 0
     if args.gpus != 1:
-        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(the Weaver path shards by sequence / kv head with no exchange; see the design notes)",
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
+              "(the Weaver path shards by sequence / kv head with no exchange)",
               file=sys.stderr)
         return 2
     import torch
