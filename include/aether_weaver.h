@@ -43,7 +43,7 @@ extern "C" {
 #define AW_E_OOB         (-3) /* block ref or atom index beyond its buffer         */
 #define AW_E_HIP         (-4) /* HIP runtime failure (no device, launch, copy ...) */
 #define AW_E_LOAD        (-5) /* kernels for this device are not in the library    */
-#define AW_E_UNSUPPORTED (-6) /* valid request this build does not implement       */
+#define AW_E_UNSUPPORTED (-6) /* valid request the library does not implement      */
 
 /* ---- reference layouts ---------------------------------------------------- */
 
