@@ -181,11 +181,52 @@ def cpu_baseline(seconds: float, seed: int):
         el = time.perf_counter() - t0
         if el >= seconds or n >= 1000:
             break
+    # One thread, briefly, beside the multi-threaded figure.
+    n1, t1 = 0, time.perf_counter()
+    while True:
+        oracle.decode_ref32(geom, arrs, 1)
+        n1 += 1
+        el1 = time.perf_counter() - t1
+        if el1 >= min(4.0, seconds / 3) or n1 >= 100:
+            break
     del np
     return {"value": n / el, "unit": "tokens/s", "cores": threads, "kind": "port",
             "sample": f"{n} B=1 decode steps of hot 2048 + cold 32768 (32q/8kv d128, 4096 atoms, q_latent "
                       f"computed on the CPU) in {el:.1f} s, fp32 restatement of weaver_kernel.metal, "
-                      f"{threads} threads"}
+                      f"{threads} threads",
+            "single_thread_value": round(n1 / el1, 3), "cpu_model": cpu_model(),
+            "host_cpus": os.cpu_count()}
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def hbm_copy_peak(mib: int = 1024, reps: int = 10) -> dict:
+    """A device-to-device copy of `mib` MiB: bytes read + written per second, the
+    attainable HBM rate beside the 8 TB/s nominal peak."""
+    import torch
+    src = torch.empty((mib << 20) // 4, dtype=torch.int32, device="cuda:0").fill_(1)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    b.record()
+    torch.cuda.synchronize()
+    gbps = 2 * src.numel() * 4 * reps / (a.elapsed_time(b) * 1e-3) / 1e9
+    del src, dst
+    torch.cuda.empty_cache()
+    return {"gbps": round(gbps, 1), "frac_of_nominal": round(gbps / PEAK_HBM_GBPS, 4),
+            "copy": f"torch copy_ of {mib} MiB int32 on one device, read + write counted"}
 
 
 VALU_FP32_FMA_TFLOPS = 78.6  # 256 CUs x 128 fp32 FMA lanes x 2.4 GHz x 2 (no packed fp32 here)
@@ -582,6 +623,15 @@ def main():
         roofline["traffic_note"] = why
     stages_us = {k: (round(v * 1e3, 2) if v else None) for k, (v, n) in stages.items()}
     serial_us = {k: (round(v * 1e3, 2) if v else None) for k, (v, n) in serial.items()}
+    # MFMA utilisation of the two dense contractions (serialized durations): the
+    # projection q . D^T and the finish bins . D (two f16 products per term: hi + lo).
+    proj_flops = 2.0 * geom.layers * geom.batch * geom.queries * geom.q_heads * geom.dict_size * geom.head_dim
+    mfma = {}
+    for k, fl in (("project", proj_flops), ("finish", 2 * proj_flops)):
+        if serial[k][0]:
+            tf = fl / (serial[k][0] * 1e-3) / 1e12
+            mfma[k] = {"gflop": round(fl / 1e9, 3), "tflops": round(tf, 1), "frac": round(tf / MFMA_F16_TFLOPS, 4)}
+    copy_peak = hbm_copy_peak()
     # The same workload with the cold pool in the head-blocked layout: a pool
     # order a device-side producer can write, whose codes of one kv head fill
     # whole 64-byte sectors (not the drop-in layout; reported beside it).
@@ -630,10 +680,13 @@ def main():
                    "dict_atoms": geom.dict_size, "cold_layout": args.cold_layout, "hip_graph": not args.no_graph},
         "achieved_gbps": row["achieved_gbps"],
         "frac_of_peak": row["frac_of_peak"],
+        "frac_of_copy_peak": round(row["achieved_gbps"] / copy_peak["gbps"], 4),
         "sweep": sweep,
         "stages_us": stages_us,
         "stages_serial_us": serial_us,
         "roofline": roofline,
+        "hbm_copy_peak": copy_peak,
+        "mfma_kernels": mfma,
         "other_cold_layout": alt,
         "encoder": enc,
         "fabric": fab,
