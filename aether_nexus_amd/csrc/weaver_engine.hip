@@ -139,8 +139,14 @@ int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, const uint32_t 
         put_msg(msg, mlen, "refs_stride %u < hot_count + cold_count", d->refs_stride);
         return AW_E_INVALID_ARG;
     }
-    if (d->flags & ~(AW_F_CAUSAL | AW_F_COLD_HEAD_BLOCKED)) {
-        put_msg(msg, mlen, "unknown flags 0x%x", d->flags & ~(AW_F_CAUSAL | AW_F_COLD_HEAD_BLOCKED));
+    constexpr uint32_t kKnown = AW_F_CAUSAL | AW_F_COLD_HEAD_BLOCKED | AW_F_SEQ_HOT_TOKENS;
+    if (d->flags & ~kKnown) {
+        put_msg(msg, mlen, "unknown flags 0x%x", d->flags & ~kKnown);
+        return AW_E_INVALID_ARG;
+    }
+    if ((uint64_t)d->hot_tokens > (uint64_t)d->hot_count * kBlock) {
+        put_msg(msg, mlen, "hot_tokens %u exceeds hot_count * 16 (%llu)", d->hot_tokens,
+                (unsigned long long)d->hot_count * kBlock);
         return AW_E_INVALID_ARG;
     }
     if (!(d->scale == d->scale) || std::isinf(d->scale)) {
@@ -167,7 +173,7 @@ int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, const uint32_t 
     // Hot: one round of waves filling the resident capacity, >= 64 tokens per wave,
     // splits <= kMaxSplits.
     if (d->hot_count > 0) {
-        const uint64_t n_tok = (uint64_t)d->hot_count * kBlock;
+        const uint64_t n_tok = d->hot_tokens ? d->hot_tokens : (uint64_t)d->hot_count * kBlock;
         // Beside the cold kernel (one 8-wave work-group per CU) one hot wave per SIMD fits.
         uint32_t wpc = hot_waves_per_cu[R <= 16 ? 0 : (R <= 32 ? 1 : 2)];
         if (d->cold_count > 0) wpc = std::min(wpc, 4u);
@@ -285,6 +291,8 @@ struct aw_engine {
     DevBuf ws;                                // per-request scratch
     std::vector<void*> retired_ws;            // outgrown scratch, kept for captured graphs
     DevBuf enc_ws;                            // encoder scratch: per-atom norms and flags
+    DevBuf iota;                              // identity block table for contiguous caches
+    uint32_t iota_n = 0;                      // entries of `iota` filled
     uint32_t* err = nullptr;                  // device error word
     int profiling = 0; // AW_PROFILE_*
     struct Pending {
@@ -428,6 +436,8 @@ int launch_hot(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* ws,
     a.splits = o.info.hot_splits;
     a.tokens_per_split = o.info.hot_tokens_per_split;
     a.causal = (d->flags & AW_F_CAUSAL) ? 1u : 0u;
+    a.n_tok_max = d->hot_tokens ? d->hot_tokens : d->hot_count * kBlock;
+    a.seq_tokens = (d->flags & AW_F_SEQ_HOT_TOKENS) ? 1u : 0u;
     a.scale_log2 = d->scale * aw::kLog2e;
     a.hot_blocks = d->hot_blocks;
     a.hot_layer = d->hot_blocks * kBlock * d->kv_heads * HD;
@@ -665,6 +675,8 @@ int decode_device(aw_engine* e, const aw_decode_desc* d, hipStream_t st) {
     if (rc) return fail(e, rc, "%s", msg);
     if (!d->out || !d->q) return fail(e, AW_E_INVALID_ARG, "q and out are required");
     if (d->hot_count && (!d->hot_k || !d->refs)) return fail(e, AW_E_INVALID_ARG, "hot_k and refs are required");
+    if ((d->flags & AW_F_SEQ_HOT_TOKENS) && !d->seq_hot)
+        return fail(e, AW_E_INVALID_ARG, "AW_F_SEQ_HOT_TOKENS needs seq_hot");
     if (d->cold_count && (!d->cold || !d->refs || !d->dict))
         return fail(e, AW_E_INVALID_ARG, "cold, refs and dict are required");
     if (d->cold_count && d->cold_blocks == 0)
@@ -907,7 +919,7 @@ void aw_engine_destroy(aw_engine* e) {
     if (e->stream) (void)hipStreamSynchronize(e->stream);
     drain_events(e);
     for (hipEvent_t ev : e->free_events) (void)hipEventDestroy(ev);
-    for (DevBuf* b : {&e->q, &e->ql, &e->hot, &e->cold, &e->refs, &e->dict, &e->out, &e->ws, &e->enc_ws})
+    for (DevBuf* b : {&e->q, &e->ql, &e->hot, &e->cold, &e->refs, &e->dict, &e->out, &e->ws, &e->enc_ws, &e->iota})
         if (b->ptr) (void)hipFree(b->ptr);
     for (void* p : e->retired_ws) (void)hipFree(p);
     if (e->err) (void)hipFree(e->err);
@@ -987,6 +999,71 @@ int aw_decode_device(aw_engine* e, const aw_decode_desc* desc, void* stream) {
     AW_HIP(e, hipSetDevice(e->device));
     hipStream_t st = (hipStream_t)stream; // NULL is HIP's null stream
     return decode_device(e, desc, st);
+}
+
+// The contiguous cache [cache_tokens][kv_heads][head_dim] is the hot pool
+// [blocks][16][kv_heads][head_dim] with block b at ref b; each group of at most
+// 64 / G queries is one causal decode whose hot_tokens place its queries at the
+// cache's end (ops.metal:549).
+int aw_multihead_attention_device(aw_engine* e, const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                                  uint16_t* out, uint32_t kv_len, uint32_t head_dim, uint32_t q_heads,
+                                  uint32_t kv_heads, uint32_t num_queries, uint64_t cache_tokens, void* stream) {
+    if (!e) return AW_E_INVALID_ARG;
+    if (!q || !k_cache || !v_cache || !out) return fail(e, AW_E_INVALID_ARG, "q, k_cache, v_cache and out are required");
+    if (num_queries == 0) return fail(e, AW_E_INVALID_ARG, "num_queries must be >= 1");
+    if ((uint64_t)kv_len + 1 < num_queries)
+        return fail(e, AW_E_INVALID_ARG, "kv_len %u is shorter than num_queries - 1 (%u): the new tokens are not in the cache",
+                    kv_len, num_queries - 1);
+    if (kv_heads == 0 || q_heads == 0 || q_heads % kv_heads)
+        return fail(e, AW_E_INVALID_ARG, "q_heads (%u) must be a positive multiple of kv_heads (%u)", q_heads, kv_heads);
+    const uint32_t G = q_heads / kv_heads;
+    if (G > 64) return fail(e, AW_E_UNSUPPORTED, "gqa group %u exceeds 64 query rows per kv head", G);
+    const uint64_t blocks = cdiv((uint64_t)kv_len, kBlock);
+    if (blocks * kBlock > cache_tokens)
+        return fail(e, AW_E_INVALID_ARG, "kv_len %u reads %llu cache tokens (whole 16-token blocks); the cache holds %llu",
+                    kv_len, (unsigned long long)(blocks * kBlock), (unsigned long long)cache_tokens);
+    if (blocks > 0xFFFFFFFFull / kBlock) return fail(e, AW_E_UNSUPPORTED, "kv_len too large");
+    AW_HIP(e, hipSetDevice(e->device));
+    hipStream_t st = (hipStream_t)stream; // NULL is HIP's null stream
+    if (blocks > e->iota_n) {
+        const size_t had = e->iota.cap;
+        int rc = ensure_keep(e->iota, blocks * 4, e->retired_ws, e->last_error);
+        if (rc) return rc;
+        const uint32_t n = (uint32_t)std::min<size_t>(e->iota.cap / 4, 0xFFFFFFFFull);
+        if (e->iota.cap != had || e->iota_n == 0) {
+            hipLaunchKernelGGL(aw::iota_kernel, dim3(cdiv(n, 256u)), dim3(256), 0, st, (uint32_t*)e->iota.ptr, n);
+            AW_HIP(e, hipGetLastError());
+        }
+        e->iota_n = n;
+    }
+    const uint32_t per = 64 / G; // queries of one call: G * queries <= 64 rows per kv head
+    const size_t qrow = (size_t)q_heads * head_dim;
+    for (uint32_t j0 = 0; j0 < num_queries; j0 += per) {
+        const uint32_t c = std::min(per, num_queries - j0);
+        // The group's last query is token kv_len - num_queries + j0 + c - 1 of the cache.
+        const uint32_t n_tok = (uint32_t)((uint64_t)kv_len + j0 + c - num_queries);
+        aw_decode_desc d{};
+        d.layers = 1;
+        d.batch = 1;
+        d.queries = c;
+        d.q_heads = q_heads;
+        d.kv_heads = kv_heads;
+        d.head_dim = head_dim;
+        d.hot_count = (uint32_t)cdiv((uint64_t)n_tok, kBlock);
+        d.hot_tokens = n_tok;
+        d.refs_stride = d.hot_count;
+        d.flags = AW_F_CAUSAL;
+        d.scale = 1.0f / std::sqrt((float)head_dim);
+        d.hot_blocks = cache_tokens / kBlock;
+        d.q = q + j0 * qrow;
+        d.hot_k = k_cache;
+        d.hot_v = v_cache;
+        d.refs = (const uint32_t*)e->iota.ptr;
+        d.out = out + j0 * qrow;
+        const int rc = decode_device(e, &d, st);
+        if (rc) return rc;
+    }
+    return AW_OK;
 }
 
 int aw_engine_check_device_errors(aw_engine* e, void* stream) {

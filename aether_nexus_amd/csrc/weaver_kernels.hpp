@@ -126,6 +126,8 @@ struct HotArgs {
     uint32_t* err;
     uint32_t batch, queries, q_heads, kv_heads, gqa, rows_r;
     uint32_t hot_count, refs_stride, splits, tokens_per_split, causal;
+    uint32_t n_tok_max;  // hot tokens of a sequence (hot_count * 16 unless the request gives fewer)
+    uint32_t seq_tokens; // seq_hot counts tokens rather than blocks
     float scale_log2;
     uint64_t hot_blocks, hot_layer, refs_layer;
 };
@@ -350,9 +352,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu((RT == 1 && 
     const int lane = threadIdx.x, li = lane & 15, lg = lane >> 4;
     const uint32_t s = blockIdx.x % a.splits, lbg = blockIdx.x / a.splits;
     const uint32_t g = lbg % a.kv_heads, lb = lbg / a.kv_heads, l = lb / a.batch;
-    uint32_t nh = a.hot_count;
-    if (a.seq_hot) nh = min(nh, a.seq_hot[lb]);
-    const uint32_t n_tok = nh * kBlockTokens;
+    uint32_t n_tok = a.n_tok_max;
+    if (a.seq_hot) {
+        const uint32_t sh = a.seq_hot[lb];
+        n_tok = min(n_tok, a.seq_tokens ? sh : min(sh, a.hot_count) * kBlockTokens);
+    }
     const uint32_t t_begin = s * a.tokens_per_split;
     const uint32_t t_end = min(t_begin + a.tokens_per_split, n_tok);
     const uint32_t R = a.rows_r;
@@ -428,10 +432,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu((RT == 1 && 
             for (int j = 0; j < KS; ++j) qop[rt][j] = (half8_t)(_Float16)0;
 
     auto process = [&](uint32_t c0, uint4_t (&kcur)[2][KS], uint4_t (&vcur)[2][KS], const bool (&okcur)[2]) {
-        // Unusable blocks (past the split or a bad ref) become zeros.
+        // Unusable blocks (past the split or a bad ref) become zeros, and so do the
+        // lane's token rows past the sequence's end inside its last block: masked
+        // scores give p = 0, but 0 * (a stale NaN or inf) would not vanish.
 #pragma unroll
         for (int tb = 0; tb < 2; ++tb)
-            if (!okcur[tb]) {
+            if (!okcur[tb] || c0 + 16u * tb + (uint32_t)li >= n_tok) {
 #pragma unroll
                 for (int j = 0; j < KS; ++j) {
                     kcur[tb][j] = (uint4_t)0u;
@@ -1569,6 +1575,12 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
 #pragma unroll
     for (int e = 0; e < DPT; ++e)
         o[e] = __builtin_bit_cast(uint16_t, (_Float16)merge_value(oh[e], Mh, Lh, oc[e], Mc, Lc));
+}
+
+// Identity block table 0 .. n-1 (a contiguous cache read as the hot pool).
+__global__ void iota_kernel(uint32_t* p, uint32_t n) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = i;
 }
 
 // ------------------------------------------------ codec check (bit-exact)

@@ -173,6 +173,7 @@ class LoomDescriptor:
 AW_F_CAUSAL = 1
 AW_F_COLD_HEAD_BLOCKED = 2
 AW_F_ENCODE_FULL_SCAN = 4
+AW_F_SEQ_HOT_TOKENS = 8
 
 AW_OK = 0
 AW_E_INVALID_ARG = -1
@@ -200,7 +201,7 @@ class DecodeDesc(ctypes.Structure):
         ("dict_size", ctypes.c_uint32), ("dict_heads", ctypes.c_uint32),
         ("hot_count", ctypes.c_uint32), ("cold_count", ctypes.c_uint32),
         ("refs_stride", ctypes.c_uint32), ("flags", ctypes.c_uint32),
-        ("scale", ctypes.c_float), ("_reserved", ctypes.c_uint32),
+        ("scale", ctypes.c_float), ("hot_tokens", ctypes.c_uint32),
         ("hot_blocks", ctypes.c_uint64), ("cold_blocks", ctypes.c_uint64),
         ("q", ctypes.c_void_p), ("q_latent", ctypes.c_void_p),
         ("hot_k", ctypes.c_void_p), ("hot_v", ctypes.c_void_p),

@@ -19,8 +19,8 @@ from typing import Any, Optional
 import numpy as np
 
 from . import _lib
-from .types import (AW_F_CAUSAL, AW_F_COLD_HEAD_BLOCKED, AW_F_ENCODE_FULL_SCAN, SPARSE_CODE_DTYPE, STAGES,
-                    STRUCT_SIZES, DecodeDesc, EncodeDesc, PlanInfo, WeaverParams)
+from .types import (AW_F_CAUSAL, AW_F_COLD_HEAD_BLOCKED, AW_F_ENCODE_FULL_SCAN, AW_F_SEQ_HOT_TOKENS,
+                    SPARSE_CODE_DTYPE, STAGES, STRUCT_SIZES, DecodeDesc, EncodeDesc, PlanInfo, WeaverParams)
 
 
 class WeaverError(RuntimeError):
@@ -202,6 +202,23 @@ class WeaverEngine:
         rc = self._lib.aw_decode_device(self._h, ctypes.byref(desc), _stream(stream))
         self._check(rc, "decode_device")
 
+    def multihead_attention(self, q, k_cache, v_cache, output, kv_len: int, head_dim: int, q_heads: int,
+                            kv_heads: int, num_queries: int, cache_tokens: Optional[int] = None,
+                            stream: Optional[int] = None) -> None:
+        """``Ops::multihead_attention`` (ops.rs:433-462, ops.metal:528-616) on the
+        device: causal GQA attention of ``num_queries`` new tokens, the last of
+        the ``kv_len`` cache positions, over contiguous [tokens][kv_heads][head_dim]
+        K and V caches, scale 1/sqrt(head_dim).  ``cache_tokens`` (the caches'
+        capacity in tokens) defaults to the K cache tensor's length."""
+        if cache_tokens is None:
+            if not hasattr(k_cache, "numel"):
+                raise WeaverError("cache_tokens is required for raw pointers", -1)
+            cache_tokens = k_cache.numel() // (kv_heads * head_dim)
+        rc = self._lib.aw_multihead_attention_device(self._h, _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(output),
+                                                     kv_len, head_dim, q_heads, kv_heads, num_queries, cache_tokens,
+                                                     _stream(stream))
+        self._check(rc, "multihead_attention")
+
     def encode_device(self, desc: EncodeDesc, stream: Optional[int] = None) -> None:
         """Enqueue one SparseCode encoder request (``Distiller::distill_block``,
         distiller.rs:171-246, over a batch of blocks; device pointers)."""
@@ -276,17 +293,22 @@ def make_desc(*, layers: int, batch: int, queries: int, q_heads: int, kv_heads: 
               dict_size: int, dict_heads: int, hot_count: int, cold_count: int, refs_stride: int,
               hot_blocks: int, cold_blocks: int, q, out, hot_k=None, hot_v=None, cold=None, refs=None,
               dictionary=None, q_latent=None, seq_hot=None, seq_cold=None, scale: float = 1.0,
-              causal: bool = False, cold_head_blocked: bool = False) -> DecodeDesc:
+              causal: bool = False, cold_head_blocked: bool = False, hot_tokens: int = 0,
+              seq_hot_tokens: bool = False) -> DecodeDesc:
     """Build an ``aw_decode_desc`` from device tensors (or raw device pointers).
     ``cold_head_blocked``: the cold pool is [L][blocks][kv_heads][16] instead of
-    the reference's [L][blocks][16][kv_heads]."""
+    the reference's [L][blocks][16][kv_heads].  ``hot_tokens``: hot tokens per
+    sequence when not whole blocks (0 = hot_count * 16); ``seq_hot_tokens``:
+    ``seq_hot`` counts tokens instead of blocks."""
     d = DecodeDesc()
     d.layers, d.batch, d.queries = layers, batch, queries
     d.q_heads, d.kv_heads, d.head_dim = q_heads, kv_heads, head_dim
     d.dict_size, d.dict_heads = dict_size, dict_heads
     d.hot_count, d.cold_count, d.refs_stride = hot_count, cold_count, refs_stride
-    d.flags = (AW_F_CAUSAL if causal else 0) | (AW_F_COLD_HEAD_BLOCKED if cold_head_blocked else 0)
+    d.flags = ((AW_F_CAUSAL if causal else 0) | (AW_F_COLD_HEAD_BLOCKED if cold_head_blocked else 0) |
+               (AW_F_SEQ_HOT_TOKENS if seq_hot_tokens else 0))
     d.scale = scale
+    d.hot_tokens = hot_tokens
     d.hot_blocks, d.cold_blocks = hot_blocks, cold_blocks
     d.q, d.q_latent, d.hot_k, d.hot_v = _ptr(q), _ptr(q_latent), _ptr(hot_k), _ptr(hot_v)
     d.cold, d.refs, d.seq_hot, d.seq_cold = _ptr(cold), _ptr(refs), _ptr(seq_hot), _ptr(seq_cold)

@@ -91,6 +91,10 @@ typedef struct aw_weaver_params {
  * instead of an MFMA prefilter with exact rescoring of the atoms that can reach
  * the top 4.  Both give the same codes; the scan is the slower reference form. */
 #define AW_F_ENCODE_FULL_SCAN 4u
+/* aw_decode_desc: seq_hot entries count hot TOKENS (<= hot_count * 16) instead
+ * of blocks, so a sequence may end inside its last block (the reference's
+ * contiguous KV cache, inference.rs:470-483).  Needs seq_hot. */
+#define AW_F_SEQ_HOT_TOKENS 8u
 
 /* One decode call over L layers x B sequences x Q query tokens.  All pointers
  * are DEVICE pointers.  Element layouts (f16 = raw binary16 bits):
@@ -105,13 +109,18 @@ typedef struct aw_weaver_params {
  *   refs     [L][B][refs_stride]: hot refs [0, hot_count), cold refs
  *            [hot_count, hot_count + cold_count) of each sequence
  *   seq_hot, seq_cold  optional [L][B] per-sequence block counts
- *            (<= hot_count / cold_count); NULL = every sequence uses the maximum
+ *            (<= hot_count / cold_count); NULL = every sequence uses the maximum;
+ *            with AW_F_SEQ_HOT_TOKENS seq_hot counts tokens
  *   dict     [L][dict_heads][dict_size][head_dim]; dict_heads is 1 (one shared
  *            dictionary) or kv_heads (the reference's per-kv-head dictionary,
  *            weaver_kernel.metal:212-215)
  *   out      [L][B][Q][q_heads][head_dim]
  * scale multiplies every score; 1.0 reproduces the reference, which applies
- * none (weaver_kernel.metal:153-160,186-190). */
+ * none (weaver_kernel.metal:153-160,186-190).
+ * hot_tokens: 0, or the hot tokens of every sequence (1 .. hot_count * 16);
+ * hot tokens past it are neither scored nor read as values (nor past a
+ * seq_hot entry).  Loads still cover whole blocks, so the pool must hold every
+ * referenced block in full. */
 typedef struct aw_decode_desc {
     uint32_t layers, batch, queries;
     uint32_t q_heads, kv_heads, head_dim;
@@ -120,7 +129,7 @@ typedef struct aw_decode_desc {
     uint32_t refs_stride;             /* >= hot_count + cold_count */
     uint32_t flags;
     float    scale;
-    uint32_t _reserved;
+    uint32_t hot_tokens;              /* 0 = hot_count * 16 */
     uint64_t hot_blocks, cold_blocks; /* pool capacity per layer, in blocks */
     const uint16_t*       q;
     const uint16_t*       q_latent;
@@ -234,6 +243,27 @@ int aw_decode(aw_engine* engine,
  * Replays and other calls on one engine share that workspace: run them one at
  * a time (stream-ordered, or synchronised between). */
 int aw_decode_device(aw_engine* engine, const aw_decode_desc* desc, void* hip_stream);
+
+/* Replaces Ops::multihead_attention (nexus-core/src/ops.rs:433-462, kernel
+ * ops.metal:528-616), the attention of InferenceEngine::forward_batch
+ * (inference.rs:546-556): causal GQA attention of num_queries new tokens over
+ * a contiguous KV cache, asynchronous on `hip_stream`.  Device pointers, f16:
+ *   q                [num_queries][q_heads][head_dim]
+ *   k_cache, v_cache [cache_tokens][kv_heads][head_dim] (positions 0 .. kv_len-1 hold
+ *                    the sequence, the new tokens last, as forward_batch writes them)
+ *   out              [num_queries][q_heads][head_dim]
+ * Query i sees cache positions p < kv_len - num_queries + 1 + i (ops.metal:549),
+ * scores scaled by 1/sqrt(head_dim) (ops.metal:557).  The cache is read as the
+ * hot pool (16-token blocks, identity block table), so cache_tokens must cover
+ * kv_len rounded up to 16 (the reference allocates MAX_SEQ_LEN = 4096 tokens,
+ * inference.rs:219,256-266).  Unlike the reference (threadgroup scores[4096],
+ * ops.metal:564) kv_len is not limited to 4096, and kv_len + 1 < num_queries is
+ * rejected instead of wrapping.  Queries beyond 64 / (q_heads / kv_heads) per
+ * call are processed in consecutive groups. */
+int aw_multihead_attention_device(aw_engine* engine, const uint16_t* q, const uint16_t* k_cache,
+                                  const uint16_t* v_cache, uint16_t* out, uint32_t kv_len,
+                                  uint32_t head_dim, uint32_t q_heads, uint32_t kv_heads,
+                                  uint32_t num_queries, uint64_t cache_tokens, void* hip_stream);
 
 /* Wait for `hip_stream` and report AW_E_OOB if any kernel since the last check
  * met an out-of-range block ref or atom index (then clears the record). */

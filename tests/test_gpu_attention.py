@@ -1,0 +1,160 @@
+"""The Weaver as the inference loop's attention on cuda:0:
+aw_multihead_attention_device (Ops::multihead_attention, ops.metal:528-616)
+against the f64 oracle, token-granular hot pools in a batched decode
+(AW_F_SEQ_HOT_TOKENS), and a speculative-verify step through KvCache
+(multi-query verify equals one query at a time; rejected drafts rolled back)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from aether_nexus_amd import inference as I
+from aether_nexus_amd.types import AW_E_INVALID_ARG
+from aether_nexus_amd.weaver import WeaverError, make_desc
+from oracle import attention_oracle as AO
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS, REL_L2 = 2e-3, 1e-3
+
+
+def assert_close(got, ref, what=""):
+    got = np.asarray(got, np.float64)
+    err = np.abs(got - ref).max() if ref.size else 0.0
+    rel = np.linalg.norm(got - ref) / max(np.linalg.norm(ref), 1e-30)
+    assert err <= MAX_ABS and rel <= REL_L2, (what, err, rel)
+
+
+def cache_case(seed, nq, kv_len, hq, hkv, d, cap):
+    """Random f16 q and caches; cache rows past kv_len hold NaN (stale memory the
+    attention must neither score nor read as values)."""
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((nq, hq, d)).astype(np.float16)
+    k = rng.standard_normal((cap, hkv, d)).astype(np.float16)
+    v = rng.standard_normal((cap, hkv, d)).astype(np.float16)
+    k[kv_len:] = np.nan
+    v[kv_len:] = np.nan
+    return q, k, v
+
+
+@pytest.mark.parametrize("nq,kv_len,hq,hkv,d", [
+    (1, 1, 32, 8, 128),      # one cached token
+    (1, 17, 32, 8, 128),     # one token into the second block
+    (4, 100, 32, 8, 128),    # verify of 3 drafts, partial last block
+    (16, 4096, 32, 8, 128),  # MAX_BATCH new tokens at MAX_SEQ_LEN
+    (3, 5000, 32, 8, 128),   # past the reference's 4096-score limit
+    (16, 37, 14, 2, 64),     # G = 7: queries in two groups of <= 9
+    (16, 15, 8, 8, 64),      # query 0 sees nothing (zeros), query 1 sees position 0
+])
+def test_multihead_attention_matches_oracle(engine, stream, nq, kv_len, hq, hkv, d):
+    cap = -(-kv_len // 16) * 16 + 16
+    q, k, v = cache_case(nq * 7919 + kv_len, nq, kv_len, hq, hkv, d, cap)
+    qt, kt, vt = (torch.from_numpy(x.view(np.int16)).cuda() for x in (q, k, v))
+    out = torch.full((nq, hq, d), float("nan"), dtype=torch.float16, device="cuda:0")
+    print(f"attention: nq {nq} kv_len {kv_len} heads {hq}/{hkv} d {d}", flush=True)
+    engine.multihead_attention(qt, kt, vt, out, kv_len, d, hq, hkv, nq, cache_tokens=cap, stream=stream)
+    engine.check_device_errors(stream)
+    ref = AO.multihead_attention_f64(q, k[:kv_len], v[:kv_len], kv_len, nq)
+    assert_close(out.float().cpu().numpy(), ref, (nq, kv_len))
+
+
+def test_multihead_attention_rejects_bad_requests(engine, stream):
+    q = torch.zeros((4, 8, 64), dtype=torch.float16, device="cuda:0")
+    kc = torch.zeros((32, 2, 64), dtype=torch.float16, device="cuda:0")
+    out = torch.empty_like(q)
+    with pytest.raises(WeaverError) as e:  # the new tokens are not all in the cache
+        engine.multihead_attention(q, kc, kc, out, 2, 64, 8, 2, 4, stream=stream)
+    assert e.value.status == AW_E_INVALID_ARG
+    with pytest.raises(WeaverError) as e:  # kv_len 33 reads block 2 (tokens 32..47) of a 32-token cache
+        engine.multihead_attention(q, kc, kc, out, 33, 64, 8, 2, 4, stream=stream)
+    assert e.value.status == AW_E_INVALID_ARG and "cache" in str(e.value)
+
+
+def test_decode_seq_hot_tokens(engine, stream):
+    """Batched causal decode with per-sequence hot TOKEN counts (AW_F_SEQ_HOT_TOKENS)
+    over scattered blocks (bit 31 set on some refs), each sequence against the
+    oracle on its blocks gathered into a contiguous cache; with hot_tokens capping
+    every sequence too."""
+    rng = np.random.default_rng(31)
+    B, Q, hq, hkv, d, hc = 3, 2, 8, 2, 64, 4
+    n_tok = np.array([5, 33, 64], np.uint32)
+    pool_blocks = 16
+    k = rng.standard_normal((pool_blocks, 16, hkv, d)).astype(np.float16)
+    v = rng.standard_normal((pool_blocks, 16, hkv, d)).astype(np.float16)
+    refs = rng.permutation(pool_blocks)[:B * hc].astype(np.uint32).reshape(B, hc)
+    for b in range(B):  # stale rows past each sequence's end
+        for t in range(int(n_tok[b]), hc * 16):
+            k[refs[b, t // 16], t % 16] = np.nan
+            v[refs[b, t // 16], t % 16] = np.nan
+    tagged = refs.copy()
+    tagged[:, 1::2] |= np.uint32(1 << 31)
+    q = rng.standard_normal((B, Q, hq, d)).astype(np.float16)
+    kt, vt, qt = (torch.from_numpy(x.view(np.int16)).cuda() for x in (k, v, q))
+    rt = torch.from_numpy(tagged.view(np.int32)).cuda()
+    st = torch.from_numpy(n_tok.view(np.int32)).cuda()
+    scale = 1.0 / np.sqrt(d)
+    for cap in (0, 40):
+        out = torch.full((B, Q, hq, d), float("nan"), dtype=torch.float16, device="cuda:0")
+        desc = make_desc(layers=1, batch=B, queries=Q, q_heads=hq, kv_heads=hkv, head_dim=d, dict_size=16,
+                         dict_heads=1, hot_count=hc, cold_count=0, refs_stride=hc, hot_blocks=pool_blocks,
+                         cold_blocks=0, q=qt, out=out, hot_k=kt, hot_v=vt, refs=rt, seq_hot=st, scale=scale,
+                         causal=True, hot_tokens=cap, seq_hot_tokens=True)
+        print(f"attention: decode with seq_hot tokens {n_tok.tolist()} cap {cap}", flush=True)
+        engine.decode_device(desc, stream=stream)
+        engine.check_device_errors(stream)
+        got = out.float().cpu().numpy()
+        for b in range(B):
+            n = int(min(n_tok[b], cap or n_tok[b]))
+            kc = k[refs[b]].reshape(hc * 16, hkv, d)
+            vc = v[refs[b]].reshape(hc * 16, hkv, d)
+            ref = AO.multihead_attention_f64(q[b], kc[:n], vc[:n], n, Q)  # its scale is 1/sqrt(d) too
+            assert_close(got[b], ref, (b, n, cap))
+
+
+def test_speculative_verify_step(engine, stream):
+    """KvCache over 2 layers (Llama-3.1-8B heads): a 40-token prompt, then a verify
+    step of last_token + 3 drafts in one multi-query call.  Each of its rows
+    equals a one-query call over the cache cut at that token; the accept rule then
+    rolls the position back to the kept tokens."""
+    rng = np.random.default_rng(41)
+    hq, hkv, d, layers = 32, 8, 128, 2
+    cache = I.KvCache(layers, hkv, d, max_seq_len=256)
+    dev = "cuda:0"
+
+    def rows(n):
+        return torch.from_numpy(rng.standard_normal((n, hkv, d)).astype(np.float16)).to(dev)
+
+    for chunk in (16, 16, 8):  # prompt in forward_batch-sized pieces
+        for layer in range(layers):
+            cache.append(layer, rows(chunk), rows(chunk))
+        cache.advance(chunk)
+    p0 = cache.push_loom()
+    assert p0 == 40
+    nv = 4
+    q = torch.from_numpy(rng.standard_normal((nv, hq, d)).astype(np.float16)).to(dev)
+    for layer in range(layers):
+        cache.append(layer, rows(nv), rows(nv))
+    outs = []
+    for layer in range(layers):
+        out = torch.empty((nv, hq, d), dtype=torch.float16, device=dev)
+        cache.attend(engine, layer, q, out, stream=stream)
+        outs.append(out)
+    engine.check_device_errors(stream)
+    for layer in range(layers):
+        kc = cache.k[layer][:p0 + nv].cpu().numpy()
+        vc = cache.v[layer][:p0 + nv].cpu().numpy()
+        ref = AO.multihead_attention_f64(q.cpu().numpy(), kc, vc, p0 + nv, nv)
+        assert_close(outs[layer].float().cpu().numpy(), ref, ("verify", layer))
+        for i in range(nv):  # one query at a time: token p0 + i is the newest
+            one = torch.empty((1, hq, d), dtype=torch.float16, device=dev)
+            engine.multihead_attention(q[i:i + 1], cache.k[layer], cache.v[layer], one, p0 + i + 1, d, hq, hkv, 1,
+                                       cache_tokens=cache.capacity, stream=stream)
+            assert_close(one[0].float().cpu().numpy(), outs[layer][i].double().cpu().numpy(), ("step", i))
+    cache.advance(nv)
+    logits = np.zeros((nv, 10), np.float32)
+    logits[[0, 1, 2, 3], [6, 2, 9, 1]] = 1.0
+    new = I.accept_drafts([6, 3, 4], logits)
+    assert new == [6, 2]
+    cache.pop_loom(I.rollback_position(cache.push_loom(), 3, len(new)))
+    assert cache.position == p0 + 2
