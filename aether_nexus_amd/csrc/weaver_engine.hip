@@ -619,12 +619,13 @@ int launch_merge(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* w
     const uint64_t gx = cdiv(a.total_rows, 4);
     if (gx > 0x7FFFFFFFull) return fail(e, AW_E_UNSUPPORTED, "merge grid too large");
     StageTimer t(e, AW_STAGE_MERGE, st);
-    // Deep load batches when the rows have many partials (measured: B = 1 step
-    // 51.9 -> 47.8 us), shallow ones otherwise (B = 64: 16 ranges, 2 hot splits).
+    // Deep load batches when the rows have many partials (measured at B = 1: 45.2 us
+    // a step with 16 float4 loads per batch, 45.9 with 8), shallow ones otherwise
+    // (B = 64: 16 ranges, 2 hot splits).
     if (a.n_ar > 16 || a.hot_splits > 8)
-        hipLaunchKernelGGL((aw::merge_kernel<HD, 32, 16>), dim3((uint32_t)gx), dim3(256), 0, st, a);
+        hipLaunchKernelGGL((aw::merge_kernel<HD, 16>), dim3((uint32_t)gx), dim3(256), 0, st, a);
     else
-        hipLaunchKernelGGL((aw::merge_kernel<HD, 8, 4>), dim3((uint32_t)gx), dim3(256), 0, st, a);
+        hipLaunchKernelGGL((aw::merge_kernel<HD, 4>), dim3((uint32_t)gx), dim3(256), 0, st, a);
     AW_HIP(e, hipGetLastError());
     return AW_OK;
 }

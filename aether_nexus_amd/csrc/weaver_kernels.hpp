@@ -1487,24 +1487,25 @@ __global__ __launch_bounds__(kFinishWaves * 64) void finish_kernel(FinishArgs a)
 // --------------------------------------------------- log-sum-exp merge
 //
 // One wave per row (row id lbg*R + r), four rows per work-group: lanes first
-// combine the row's splits (lane = split), then each lane merges HD/64 dims.
+// combine the row's splits (lane = split), then the partial outputs are summed.
 // Used when there is no cold pool or when the cold output was split over
-// several atom ranges.  UC atom-range partials and UH hot-split partials are
-// loaded per batch: a row's partials are summed in a chain of batches, so few
-// rows with many partials (small batches) want deep batches, many rows with
-// few partials shallow ones (no clamped duplicate loads).
-template <int HD, int UC, int UH>
+// several atom ranges.  A partial's HD floats are read as float4 pieces by
+// LP = HD/4 lanes, so one load instruction covers PG = 64/LP partials (two at
+// HD = 128) and a batch of U instructions U*PG of them; the PG lane groups'
+// sums are added by shuffles at the end.  Rows with many partials (small
+// batches: 64 atom ranges, 64 hot splits) want deep batches, rows with few
+// shallow ones (no clamped duplicate loads).  Every load is unconditional
+// (clamped indices, masked at use), and the first batch of hot partials is
+// issued before the split factors are worked out.
+template <int HD, int U>
 __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
-    constexpr int DPT = HD / 64;
+    constexpr int LP = HD / 4, PG = 64 / LP;
     __shared__ float s_hfac[4][kMaxSplits];
     const int tid = threadIdx.x, row = tid / 64, lane = tid % 64;
     const uint64_t rowid = (uint64_t)blockIdx.x * 4 + row;
     if (rowid >= a.total_rows) return; // whole wave: no barrier follows
     const uint32_t R = a.rows_r;
     const uint64_t lbg = rowid / R, r = rowid % R;
-    float Mc = -INFINITY, Lc = 0.0f, Mh = -INFINITY, Lh = 0.0f;
-    // Every load below is unconditional (clamped indices; absent arrays read the zero
-    // code) and masked at use, so they are all in flight together.
     const bool has_c = a.ocp != nullptr, has_h = a.hot_splits > 0;
     const float* zero = (const float*)&g_zero_code;
     const uint32_t cs = has_c ? min((uint32_t)lane, a.cold_splits - 1u) : 0u;
@@ -1515,31 +1516,29 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
     float cl = (has_c ? a.cold_l : zero)[cb];
     float hm = (has_h ? a.hot_m : zero)[hb];
     float hl = (has_h ? a.hot_l : zero)[hb];
-    const int d0 = lane * DPT;
-    float oc[DPT], oh[DPT];
+    const uint32_t sub = (uint32_t)lane / LP, d0 = 4u * ((uint32_t)lane % LP);
+    // Cold atom-range partials: plain sum (every range carries the row's factors).
+    float4_t oc = (float4_t)0.0f;
+    const uint32_t n_ar = has_c ? a.n_ar : 0u;
     const float* csrc = has_c ? a.ocp + rowid * a.n_ar * HD + d0 : zero;
-    const uint32_t n_ar = has_c ? a.n_ar : 1u;
+    for (uint32_t a0 = 0; a0 < n_ar; a0 += U * PG) {
+        float4_t v[U];
 #pragma unroll
-    for (int e = 0; e < DPT; ++e) {
-        oc[e] = 0.0f;
-        oh[e] = 0.0f;
+        for (int j = 0; j < U; ++j) v[j] = *(const float4_t*)(csrc + (uint64_t)min(a0 + j * PG + sub, n_ar - 1u) * HD);
+#pragma unroll
+        for (int j = 0; j < U; ++j) oc += a0 + j * PG + sub < n_ar ? v[j] : (float4_t)0.0f;
     }
-    {
-        constexpr int U = UC; // atom ranges summed per batch of loads
-        for (uint32_t ar = 0; ar < n_ar; ar += U) {
-            float v[U][DPT];
+    // First batch of hot partials, before the factors (S = 0: the zero code, unused).
+    const uint32_t S = a.hot_splits;
+    const float* hsrc = has_h ? a.hot_o + (lbg * S * R + r) * HD + d0 : zero;
+    auto load_hot = [&](uint32_t s0, float4_t (&v)[U]) {
 #pragma unroll
-            for (int j = 0; j < U; ++j) {
-                const uint32_t aj = has_c ? min(ar + j, n_ar - 1u) : 0u;
-#pragma unroll
-                for (int e = 0; e < DPT; ++e) v[j][e] = csrc[has_c ? aj * HD + e : 0];
-            }
-#pragma unroll
-            for (int j = 0; j < U; ++j)
-#pragma unroll
-                for (int e = 0; e < DPT; ++e) oc[e] += (has_c && ar + j < n_ar) ? v[j][e] : 0.0f;
-        }
-    }
+        for (int j = 0; j < U; ++j)
+            v[j] = *(const float4_t*)(hsrc + (has_h ? (uint64_t)min(s0 + j * PG + sub, S - 1u) * R * HD : 0));
+    };
+    float4_t vh[U];
+    load_hot(0, vh);
+    float Mc = -INFINITY, Lc = 0.0f, Mh = -INFINITY, Lh = 0.0f;
     {
         const bool cv = has_c && (uint32_t)lane < a.cold_splits;
         const bool hv = has_h && (uint32_t)lane < a.hot_splits;
@@ -1553,28 +1552,32 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
         if (lane < kMaxSplits) s_hfac[row][lane] = f;
     }
     __builtin_amdgcn_wave_barrier();
-    const float* hsrc = has_h ? a.hot_o + (lbg * a.hot_splits * R + r) * HD + d0 : zero;
-    for (uint32_t s0 = 0; s0 < a.hot_splits; s0 += UH) {
-        float v[UH][DPT], fs[UH];
+    float4_t oh = (float4_t)0.0f;
+    for (uint32_t s0 = 0; s0 < S; s0 += U * PG) {
+        if (s0) load_hot(s0, vh);
+        float fs[U];
 #pragma unroll
-        for (int j = 0; j < UH; ++j) {
-            const uint32_t sp = min(s0 + j, a.hot_splits - 1u);
-#pragma unroll
-            for (int e = 0; e < DPT; ++e) v[j][e] = hsrc[(uint64_t)sp * R * HD + e];
+        for (int j = 0; j < U; ++j) {
+            const uint32_t sp = s0 + j * PG + sub;
+            fs[j] = sp < S ? s_hfac[row][min(sp, S - 1u)] : 0.0f;
         }
 #pragma unroll
-        for (int j = 0; j < UH; ++j) fs[j] = s0 + j < a.hot_splits ? s_hfac[row][s0 + j] : 0.0f;
-#pragma unroll
-        for (int j = 0; j < UH; ++j)
-#pragma unroll
-            for (int e = 0; e < DPT; ++e) oh[e] += fs[j] != 0.0f ? fs[j] * v[j][e] : 0.0f;
+        for (int j = 0; j < U; ++j) oh += fs[j] != 0.0f ? fs[j] * vh[j] : (float4_t)0.0f;
     }
+#pragma unroll
+    for (int o = LP; o < 64; o *= 2)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            oc[e] += __shfl_xor(oc[e], o);
+            oh[e] += __shfl_xor(oh[e], o);
+        }
+    if (sub != 0) return;
     const uint64_t lb = lbg / a.kv_heads, g = lbg % a.kv_heads;
     const uint64_t q = r / a.gqa, h = g * a.gqa + r % a.gqa;
-    uint16_t* o = a.out + ((lb * a.queries + q) * a.q_heads + h) * HD + d0;
+    half4_t hv;
 #pragma unroll
-    for (int e = 0; e < DPT; ++e)
-        o[e] = __builtin_bit_cast(uint16_t, (_Float16)merge_value(oh[e], Mh, Lh, oc[e], Mc, Lc));
+    for (int e = 0; e < 4; ++e) hv[e] = (_Float16)merge_value(oh[e], Mh, Lh, oc[e], Mc, Lc);
+    *(half4_t*)(a.out + ((lb * a.queries + q) * a.q_heads + h) * HD + d0) = hv;
 }
 
 // Identity block table 0 .. n-1 (a contiguous cache read as the hot pool).

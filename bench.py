@@ -61,6 +61,7 @@ def parse():
                    help="cold pool order of the main measurement (reference: [blocks][16][kv_heads])")
     p.add_argument("--skip-encoder", action="store_true", help="skip the SparseCode encoder measurement")
     p.add_argument("--skip-fabric", action="store_true", help="skip the .aether fabric residency measurement")
+    p.add_argument("--skip-attention", action="store_true", help="skip the inference-attention measurement")
     p.add_argument("--skip-alt-layout", action="store_true",
                    help="skip the extra B-max run with the other cold pool order (for clean profiles)")
     p.add_argument("--rocpd-summary", metavar="DB", help="print a per-kernel summary of a rocprofv3 database and exit")
@@ -296,6 +297,77 @@ def encoder_bench(engine, seed, reps, cpu_blocks):
             "cpu_baseline": {"value": round(cpu_blocks / cpu_s, 2), "unit": "blocks/s", "cores": 1, "kind": "port",
                              "sample": f"{cpu_blocks} blocks through the oracle's restatement of distiller.rs:171-246"},
             "codes_match_cpu": same}
+
+
+def attention_bench(engine, seed, reps, cpu_seconds):
+    """The Weaver as the inference loop's attention (Ops::multihead_attention,
+    ops.metal:528-616): one forward's attention over the 32 layers of
+    Llama-3.1-8B (32q/8kv, head_dim 128) with every layer's K and V caches at
+    MAX_SEQ_LEN = 4096 tokens (inference.rs:219), for a decode step (1 new token)
+    and a verify step (last token + 3 drafts, agent.rs:337-355), captured in a
+    HIP graph.  Algorithmic bytes per layer: the K and V rows read (4096 x 8 x 128
+    x 2 bytes each) plus q and out."""
+    import numpy as np
+    import torch
+    from types import SimpleNamespace
+    layers, hq, hkv, hd, kv_len = 32, 32, 8, 128, 4096
+    g = torch.Generator(device="cuda:0").manual_seed(seed)
+    kc = [torch.randn((kv_len, hkv, hd), generator=g, device="cuda:0").to(torch.float16) for _ in range(layers)]
+    vc = [torch.randn((kv_len, hkv, hd), generator=g, device="cuda:0").to(torch.float16) for _ in range(layers)]
+    res = {"workload": f"{layers} layers x multihead_attention over K and V caches of {kv_len} tokens, "
+                       f"{hq}q/{hkv}kv heads, head_dim {hd} (Llama-3.1-8B at MAX_SEQ_LEN)"}
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    for name, nq in (("decode", 1), ("verify_3_drafts", 4)):
+        q = torch.randn((nq, hq, hd), generator=g, device="cuda:0").to(torch.float16)
+        outs = [torch.empty((nq, hq, hd), dtype=torch.float16, device="cuda:0") for _ in range(layers)]
+        with torch.cuda.stream(st):
+            def forward(s):
+                for l in range(layers):
+                    engine.multihead_attention(q, kc[l], vc[l], outs[l], kv_len, hd, hq, hkv, nq,
+                                               cache_tokens=kv_len, stream=s)
+            forward(st.cuda_stream)  # sizes the workspace and the block table before capture
+            engine.check_device_errors(st.cuda_stream)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=st):
+                forward(torch.cuda.current_stream().cuda_stream)
+            for _ in range(3):
+                graph.replay()
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+            ev[0].record(st)
+            for _ in range(reps):
+                graph.replay()
+            ev[1].record(st)
+        torch.cuda.synchronize()
+        ms = ev[0].elapsed_time(ev[1]) / reps
+        alg = layers * (kv_len * hkv * hd * 2 * 2 + 2 * nq * hq * hd * 2)
+        gbps = alg / (ms * 1e-3) / 1e9
+        res[name] = {"new_tokens": nq, "ms_per_forward": round(ms, 4), "us_per_layer": round(ms * 1e3 / layers, 2),
+                     "alg_bytes_per_forward": alg, "achieved_gbps": round(gbps, 1),
+                     "frac_of_peak": round(gbps / PEAK_HBM_GBPS, 4)}
+        del graph
+    # CPU: the oracle's fp32 restatement of the same attention (a hot pool of
+    # 16-token blocks, identity block table, causal) on one layer of the decode step.
+    from oracle import oracle
+    threads = max(1, min(16, os.cpu_count() or 1))
+    geom = SimpleNamespace(layers=1, batch=1, queries=1, q_heads=hq, kv_heads=hkv, head_dim=hd, dict_size=16,
+                           dict_heads=1, hot_count=kv_len // 16, cold_count=0, refs_stride=kv_len // 16, causal=True,
+                           scale=1.0 / math.sqrt(hd), hot_blocks=kv_len // 16, cold_blocks=0)
+    arrs = {"q": q[:1].cpu().numpy().view(np.uint16), "hot_k": kc[0].cpu().numpy().view(np.uint16),
+            "hot_v": vc[0].cpu().numpy().view(np.uint16), "refs": np.arange(kv_len // 16, dtype=np.uint32)}
+    n, t0 = 0, time.perf_counter()
+    while True:
+        oracle.decode_ref32(geom, arrs, threads)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= cpu_seconds or n >= 2000:
+            break
+    res["cpu_baseline"] = {"value": round(n / el / layers, 3), "unit": "decode forwards/s (32 layers)",
+                           "cores": threads, "kind": "port",
+                           "sample": f"{n} single-layer decode attentions ({kv_len} cached tokens) through the "
+                                     f"oracle's fp32 restatement in {el:.1f} s, {threads} threads"}
+    res["gpu_forwards_per_s"] = round(1e3 / res["decode"]["ms_per_forward"], 1)
+    return res
 
 
 PCIE_GEN5_X16_GBPS = 63.0  # per direction: 32 GT/s x 16 lanes x 128/130 encoding / 8 bits
@@ -657,6 +729,9 @@ def main():
     fab = None if args.skip_fabric else fabric_bench(engine, args.seed, 8 if args.no_cpu else 24)
     if fab:
         log(json.dumps({"fabric": fab}))
+    att = None if args.skip_attention else attention_bench(engine, args.seed, 20, 0.5 if args.no_cpu else 3.0)
+    if att:
+        log(json.dumps({"inference_attention": att}))
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds, args.seed)
 
     result = {
@@ -690,6 +765,7 @@ def main():
         "other_cold_layout": alt,
         "encoder": enc,
         "fabric": fab,
+        "inference_attention": att,
         "cpu_baseline": cpu,
         "reference_bench_config": ref_cfg,
     }
