@@ -7,6 +7,8 @@ behind the C ABI of include/aether_weaver.h.
   types      layout contract (SparseCode, WeaverParams, ModelDims, aw_decode_desc)
   weaver     WeaverEngine: mirror of the reference engine over the C ABI
   workloads  seeded synthetic decode workloads
+  fabric     the .aether file's pools resident in HBM, and the Distiller's REM cycle
+  inference  KV cache over aw_multihead_attention_device and the speculative-verify rule
   build      hipcc build of libaether_weaver.so
 """
 from .types import (SPARSE_CODE_DTYPE, DecodeDesc, Granite2B, Llama8B, LoomDescriptor, ModelDims, PlanInfo,

@@ -79,6 +79,21 @@ def lib_path(path: str | os.PathLike | None = None) -> Path:
     return Path(env) if env else DEFAULT_LIB
 
 
+def _share_torch_runtime() -> None:
+    """Put PyTorch's HIP runtime in the process before this library is opened.
+
+    PyTorch-ROCm ships its own libamdhip64 and loads it into the global symbol
+    scope, so a library opened after ``import torch`` binds its HIP calls to that
+    runtime and both share one device context (streams and pointers pass freely
+    between them).  Opened first, this library would start the system runtime,
+    and a second runtime started later in the same process then finds no device.
+    Without PyTorch the library uses the system runtime alone."""
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+
+
 def load(path: str | os.PathLike | None = None) -> ctypes.CDLL:
     """Load the library and declare every exported signature.
 
@@ -93,6 +108,7 @@ def load(path: str | os.PathLike | None = None) -> ctypes.CDLL:
         raise FileNotFoundError(
             f"{p} not found: build it with `python -c 'import __graft_entry__ as g; g.build()'` "
             "(hipcc --offload-arch=gfx950); there is no CPU fallback")
+    _share_torch_runtime()
     lib = ctypes.CDLL(key)
     for name, (res, args) in SIGNATURES.items():
         fn = getattr(lib, name)
