@@ -10,7 +10,11 @@ bins, bins . D and merge) over the whole batch, inputs resident in HBM.
 
 Pools are replicated over several disjoint block sets ("copies") and the steps
 rotate through them, so every step reads at least ~512 MB of distinct data and
-the 256 MB Infinity Cache cannot serve repeats.
+the 256 MB Infinity Cache cannot serve repeats.  The cold pool sits in HBM in
+the head-blocked order [blocks][kv_heads][16] (how the .aether fabric keeps it
+on the device: same codes, one kv head's 16 codes of a block contiguous); the
+reference's file order [blocks][16][kv_heads] is measured beside it, with
+output bits checked identical (`--cold-layout` swaps the two).
 
 Also measured in the same run:
   * per-kernel durations with HIP events on the stream each kernel runs on
@@ -57,8 +61,9 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--stage-sweep", action="store_true", help="per-kernel times at every batch size")
-    p.add_argument("--cold-layout", choices=("reference", "head_blocked"), default="reference",
-                   help="cold pool order of the main measurement (reference: [blocks][16][kv_heads])")
+    p.add_argument("--cold-layout", choices=("reference", "head_blocked"), default="head_blocked",
+                   help="cold pool order in HBM of the main measurement: head_blocked ([blocks][kv_heads][16], "
+                        "how the fabric keeps it on the device) or reference ([blocks][16][kv_heads], the file order)")
     p.add_argument("--skip-encoder", action="store_true", help="skip the SparseCode encoder measurement")
     p.add_argument("--skip-fabric", action="store_true", help="skip the .aether fabric residency measurement")
     p.add_argument("--skip-attention", action="store_true", help="skip the inference-attention measurement")
@@ -529,7 +534,9 @@ def rocpd_summary(db: str, name_filter: str) -> str:
     return "\n".join(lines)
 
 
-TRAFFIC_FILE = ROOT / "profiles" / "traffic_b64.txt"
+def traffic_file(layout: str) -> Path:
+    """The committed FETCH/WRITE traffic profile of the B = 64 pipeline with `layout`."""
+    return ROOT / "profiles" / f"traffic_b64_{layout}.txt"
 
 
 def sources_digest() -> str:
@@ -577,7 +584,7 @@ def _counters(db: str) -> dict:
     return {k: {cn: v / len(nd[k]) for cn, v in d.items()} for k, d in per.items()}
 
 
-def traffic_summary(fetch_db: str, write_db: str, copy_mib: int, command: str) -> str:
+def traffic_summary(fetch_db: str, write_db: str, copy_mib: int, command: str, layout: str) -> str:
     """HBM bytes per launch of each aw:: kernel (largest grid = the B = 64 launch)
     from a FETCH_SIZE and a WRITE_SIZE pass, each scaled by what the counter
     reads for the calibration copy of `copy_mib` MiB in the same pass."""
@@ -593,6 +600,7 @@ def traffic_summary(fetch_db: str, write_db: str, copy_mib: int, command: str) -
     ff, fw = copy_bytes / (cf * 1024), copy_bytes / (cw * 1024)
     lines = ["# HBM traffic per launch, hot 2048 + cold 32768 per kv head, B = 64 (32q/8kv, d128, 4096 atoms)",
              f"# command: {command}",
+             f"# cold_layout: {layout}",
              f"# sources: {sources_digest()}",
              f"copy_bytes {copy_bytes} kernel {ck_f[0][:48]!r} fetch_kib {cf:.0f} write_kib {cw:.0f}",
              f"factor_fetch {ff:.4f} factor_write {fw:.4f}"]
@@ -610,13 +618,17 @@ def traffic_summary(fetch_db: str, write_db: str, copy_mib: int, command: str) -
     return "\n".join(lines)
 
 
-def read_traffic(kernel: str):
-    """Traffic bytes per launch of `kernel` from the committed profile, or
-    (None, reason) when absent or measured on other sources."""
-    if not TRAFFIC_FILE.exists():
-        return None, "no traffic profile"
-    txt = TRAFFIC_FILE.read_text().splitlines()
+def read_traffic(kernel: str, layout: str):
+    """Traffic bytes per launch of `kernel` from the committed profile of the
+    cold-pool `layout`, or (None, reason) when absent or measured on other sources."""
+    f = traffic_file(layout)
+    if not f.exists():
+        return None, f"no traffic profile for the {layout} cold layout"
+    txt = f.read_text().splitlines()
     digest = next((ln.split()[-1] for ln in txt if ln.startswith("# sources:")), None)
+    measured = next((ln.split()[-1] for ln in txt if ln.startswith("# cold_layout:")), None)
+    if measured != layout:
+        return None, f"traffic profile measured with the {measured} cold layout"
     if digest != sources_digest():
         return None, "traffic profile measured on other kernel sources"
     for ln in txt:
@@ -633,7 +645,7 @@ def main():
         return 0
     if args.traffic_summary:
         print(traffic_summary(args.traffic_summary[0], args.traffic_summary[1], args.copy_calibration or 256,
-                              args.traffic_command))
+                              args.traffic_command, args.cold_layout))
         return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
@@ -685,7 +697,7 @@ def main():
     dur_ms = stages[dom][0]
     achieved = kb_per_launch[dom] / (dur_ms * 1e-3) / 1e9
     alone = kb_per_launch[dom] / (serial[dom][0] * 1e-3) / 1e9
-    traffic, why = read_traffic(f"{dom}_kernel") if args.cold_layout == "reference" else (None, "reference layout only")
+    traffic, why = read_traffic(f"{dom}_kernel", args.cold_layout)
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                 "frac": round(achieved / PEAK_HBM_GBPS, 4), "traffic": traffic, "kernel": f"{dom}_kernel",
                 "alg_bytes_per_launch": int(kb_per_launch[dom]), "avg_launch_us": round(dur_ms * 1e3, 2),
@@ -704,9 +716,9 @@ def main():
             tf = fl / (serial[k][0] * 1e-3) / 1e12
             mfma[k] = {"gflop": round(fl / 1e9, 3), "tflops": round(tf, 1), "frac": round(tf / MFMA_F16_TFLOPS, 4)}
     copy_peak = hbm_copy_peak()
-    # The same workload with the cold pool in the head-blocked layout: a pool
-    # order a device-side producer can write, whose codes of one kv head fill
-    # whole 64-byte sectors (not the drop-in layout; reported beside it).
+    # The same workload with the cold pool in the other order (by default the
+    # reference's file order [blocks][16][kv_heads], where one kv head's code is
+    # 16 bytes of every 128-byte token line): output bits must be identical.
     alt = None
     if not args.skip_alt_layout:
         other = "head_blocked" if args.cold_layout == "reference" else "reference"
@@ -714,11 +726,18 @@ def main():
         ms_hb = rh.time_steps(args.steps, args.warmup)
         same = bool(torch.equal(rh.out.view(torch.int16), r.out.view(torch.int16)))
         gb_hb = geom.algorithmic_bytes()["total"] / (ms_hb * 1e-3) / 1e9
+        alt_st = rh.stage_times(args.steps, mode=1)
         alt = {"cold_layout": other, "ms_per_step": round(ms_hb, 5),
                "tokens_per_s": round(geom.batch / (ms_hb * 1e-3), 1), "achieved_gbps": round(gb_hb, 1),
                "frac_of_peak": round(gb_hb / PEAK_HBM_GBPS, 4), "output_bit_identical": same,
-               "stages_us": {k: (round(v * 1e3, 2) if v else None)
-                             for k, (v, n) in rh.stage_times(args.steps, mode=1).items()}}
+               "stages_us": {k: (round(v * 1e3, 2) if v else None) for k, (v, n) in alt_st.items()}}
+        if alt_st["cold"][0]:
+            ach = kb_per_launch["cold"] / (alt_st["cold"][0] * 1e-3) / 1e9
+            tr, why_alt = read_traffic("cold_kernel", other)
+            alt["cold_roofline"] = {"achieved": round(ach, 1), "frac": round(ach / PEAK_HBM_GBPS, 4),
+                                    "avg_launch_us": round(alt_st["cold"][0] * 1e3, 2), "traffic": tr}
+            if why_alt:
+                alt["cold_roofline"]["traffic_note"] = why_alt
         log(json.dumps({"other_cold_layout": alt}))
         del rh
         torch.cuda.empty_cache()
@@ -749,7 +768,7 @@ def main():
         "data": "synthetic",
         "config": {"workload": f"Weaver decode, hot 2048 f16 tokens + cold 32768 SparseCodes per kv head, "
                                f"32q/8kv heads, head_dim 128, shared 4096x128 f16 dictionary, B={geom.batch}, "
-                               f"one query token, scale 1/sqrt(128)",
+                               f"one query token, scale 1/sqrt(128), cold pool {args.cold_layout} in HBM",
                    "batch": geom.batch, "hot_tokens": geom.hot_count * 16, "cold_tokens": geom.cold_count * 16,
                    "q_heads": geom.q_heads, "kv_heads": geom.kv_heads, "head_dim": geom.head_dim,
                    "dict_atoms": geom.dict_size, "cold_layout": args.cold_layout, "hip_graph": not args.no_graph},
