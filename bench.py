@@ -705,6 +705,14 @@ def main():
                 "serialized_frac": round(alone / PEAK_HBM_GBPS, 4)}
     if why:
         roofline["traffic_note"] = why
+    # The phase the two bandwidth-bound kernels share: hot beside cold, from the
+    # cold launch to the later of the two ends (both event pairs start together).
+    phase_ms = max(stages["cold"][0] or 0.0, stages["hot"][0] or 0.0)
+    if phase_ms:
+        pb = kb_per_launch["hot"] + kb_per_launch["cold"]
+        roofline["hot_cold_phase"] = {"alg_bytes": int(pb), "us": round(phase_ms * 1e3, 2),
+                                      "achieved": round(pb / (phase_ms * 1e-3) / 1e9, 1),
+                                      "frac": round(pb / (phase_ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}
     stages_us = {k: (round(v * 1e3, 2) if v else None) for k, (v, n) in stages.items()}
     serial_us = {k: (round(v * 1e3, 2) if v else None) for k, (v, n) in serial.items()}
     # MFMA utilisation of the two dense contractions (serialized durations): the
