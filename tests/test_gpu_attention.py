@@ -39,6 +39,7 @@ def cache_case(seed, nq, kv_len, hq, hkv, d, cap):
 
 
 @pytest.mark.parametrize("nq,kv_len,hq,hkv,d", [
+    (1, 0, 8, 2, 64),        # an empty cache: zeros
     (1, 1, 32, 8, 128),      # one cached token
     (1, 17, 32, 8, 128),     # one token into the second block
     (4, 100, 32, 8, 128),    # verify of 3 drafts, partial last block
