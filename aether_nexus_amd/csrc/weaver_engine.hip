@@ -1027,14 +1027,14 @@ int aw_multihead_attention_device(aw_engine* e, const uint16_t* q, const uint16_
     AW_HIP(e, hipSetDevice(e->device));
     hipStream_t st = (hipStream_t)stream; // NULL is HIP's null stream
     if (blocks > e->iota_n) {
-        const size_t had = e->iota.cap;
+        // Grown (and kept, like the workspace) on the host's side: filled with a
+        // synchronous copy, so calls on any stream see it complete.
         int rc = ensure_keep(e->iota, blocks * 4, e->retired_ws, e->last_error);
         if (rc) return rc;
         const uint32_t n = (uint32_t)std::min<size_t>(e->iota.cap / 4, 0xFFFFFFFFull);
-        if (e->iota.cap != had || e->iota_n == 0) {
-            hipLaunchKernelGGL(aw::iota_kernel, dim3(cdiv(n, 256u)), dim3(256), 0, st, (uint32_t*)e->iota.ptr, n);
-            AW_HIP(e, hipGetLastError());
-        }
+        std::vector<uint32_t> ids(n);
+        for (uint32_t i = 0; i < n; ++i) ids[i] = i;
+        AW_HIP(e, hipMemcpy(e->iota.ptr, ids.data(), (size_t)n * 4, hipMemcpyHostToDevice));
         e->iota_n = n;
     }
     const uint32_t per = 64 / G; // queries of one call: G * queries <= 64 rows per kv head

@@ -1580,12 +1580,6 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
     *(half4_t*)(a.out + ((lb * a.queries + q) * a.q_heads + h) * HD + d0) = hv;
 }
 
-// Identity block table 0 .. n-1 (a contiguous cache read as the hot pool).
-__global__ void iota_kernel(uint32_t* p, uint32_t n) {
-    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) p[i] = i;
-}
-
 // ------------------------------------------------ codec check (bit-exact)
 __global__ void gather_codes_kernel(const uint4_t* codes, uint64_t n, const uint16_t* dict, uint32_t A,
                                     uint32_t HD, uint32_t* idx, float* coef, uint16_t* atoms, uint32_t* err) {
