@@ -1580,6 +1580,102 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
     *(half4_t*)(a.out + ((lb * a.queries + q) * a.q_heads + h) * HD + d0) = hv;
 }
 
+// Merge for few rows (fewer than CUs: small batches, one sequence's attention):
+// one 4-wave work-group per row, the row's partials dealt over the 4 waves (wave
+// w takes partial groups w, w + 4, ...), so each wave needs a quarter of the load
+// batches; the waves' sums meet in LDS and are added in wave order.  Split
+// factors: every wave combines the statistics itself (lane = split) and reads a
+// split's factor from its lane with a shuffle.
+template <int HD, int U>
+__global__ __launch_bounds__(256) void merge_row_kernel(MergeArgs a) {
+    constexpr int LP = HD / 4, PG = 64 / LP, NWV = 4;
+    __shared__ float4_t s_part[2][NWV][LP];
+    const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
+    const uint64_t rowid = blockIdx.x;
+    const uint32_t R = a.rows_r;
+    const uint64_t lbg = rowid / R, r = rowid % R;
+    const bool has_c = a.ocp != nullptr, has_h = a.hot_splits > 0;
+    const float* zero = (const float*)&g_zero_code;
+    const uint32_t cs = has_c ? min((uint32_t)lane, a.cold_splits - 1u) : 0u;
+    const uint32_t hs = has_h ? min((uint32_t)lane, a.hot_splits - 1u) : 0u;
+    const uint64_t cb = has_c ? (lbg * a.cold_splits + cs) * R + r : 0;
+    const uint64_t hb = has_h ? (lbg * a.hot_splits + hs) * R + r : 0;
+    float cm = (has_c ? a.cold_m : zero)[cb];
+    float cl = (has_c ? a.cold_l : zero)[cb];
+    float hm = (has_h ? a.hot_m : zero)[hb];
+    float hl = (has_h ? a.hot_l : zero)[hb];
+    const uint32_t sub = (uint32_t)lane / LP, d0 = 4u * ((uint32_t)lane % LP);
+    // Partial index of this lane for slot j of the batch starting at p0.
+    auto pidx = [&](uint32_t p0, int j) { return p0 + (uint32_t)(j * NWV + wave) * PG + sub; };
+    constexpr uint32_t STEP = (uint32_t)(U * NWV * PG);
+    float4_t oc = (float4_t)0.0f;
+    const uint32_t n_ar = has_c ? a.n_ar : 0u;
+    const float* csrc = has_c ? a.ocp + rowid * a.n_ar * HD + d0 : zero;
+    for (uint32_t a0 = 0; a0 < n_ar; a0 += STEP) {
+        float4_t v[U];
+#pragma unroll
+        for (int j = 0; j < U; ++j) v[j] = *(const float4_t*)(csrc + (uint64_t)min(pidx(a0, j), n_ar - 1u) * HD);
+#pragma unroll
+        for (int j = 0; j < U; ++j) oc += pidx(a0, j) < n_ar ? v[j] : (float4_t)0.0f;
+    }
+    const uint32_t S = a.hot_splits;
+    const float* hsrc = has_h ? a.hot_o + (lbg * S * R + r) * HD + d0 : zero;
+    auto load_hot = [&](uint32_t s0, float4_t (&v)[U]) {
+#pragma unroll
+        for (int j = 0; j < U; ++j)
+            v[j] = *(const float4_t*)(hsrc + (has_h ? (uint64_t)min(pidx(s0, j), S - 1u) * R * HD : 0));
+    };
+    float4_t vh[U];
+    load_hot(0, vh); // before the factors are known
+    float Mc = -INFINITY, Lc = 0.0f, Mh = -INFINITY, Lh = 0.0f, fh = 0.0f;
+    {
+        const bool cv = has_c && (uint32_t)lane < a.cold_splits;
+        const bool hv = has_h && (uint32_t)lane < a.hot_splits;
+        cm = cv ? cm : -INFINITY;
+        cl = cv ? cl : 0.0f;
+        hm = hv ? hm : -INFINITY;
+        hl = hv ? hl : 0.0f;
+        float f;
+        combine_splits(cm, cl, Mc, Lc, f);
+        combine_splits(hm, hl, Mh, Lh, fh); // fh: factor of hot split `lane`
+    }
+    float4_t oh = (float4_t)0.0f;
+    for (uint32_t s0 = 0; s0 < S; s0 += STEP) {
+        if (s0) load_hot(s0, vh);
+#pragma unroll
+        for (int j = 0; j < U; ++j) {
+            const uint32_t sp = pidx(s0, j);
+            const float fs = __shfl(fh, (int)min(sp, S - 1u)); // splits <= kMaxSplits <= 64 lanes
+            oh += (sp < S && fs != 0.0f) ? fs * vh[j] : (float4_t)0.0f;
+        }
+    }
+#pragma unroll
+    for (int o = LP; o < 64; o *= 2)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            oc[e] += __shfl_xor(oc[e], o);
+            oh[e] += __shfl_xor(oh[e], o);
+        }
+    if (sub == 0) {
+        s_part[0][wave][lane] = oc;
+        s_part[1][wave][lane] = oh;
+    }
+    __syncthreads();
+    if (wave != 0 || sub != 0) return;
+    float4_t c4 = s_part[0][0][lane], h4 = s_part[1][0][lane];
+#pragma unroll
+    for (int w = 1; w < NWV; ++w) {
+        c4 += s_part[0][w][lane];
+        h4 += s_part[1][w][lane];
+    }
+    const uint64_t lb = lbg / a.kv_heads, g = lbg % a.kv_heads;
+    const uint64_t q = r / a.gqa, h = g * a.gqa + r % a.gqa;
+    half4_t hv;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) hv[e] = (_Float16)merge_value(h4[e], Mh, Lh, c4[e], Mc, Lc);
+    *(half4_t*)(a.out + ((lb * a.queries + q) * a.q_heads + h) * HD + d0) = hv;
+}
+
 // ------------------------------------------------ codec check (bit-exact)
 __global__ void gather_codes_kernel(const uint4_t* codes, uint64_t n, const uint16_t* dict, uint32_t A,
                                     uint32_t HD, uint32_t* idx, float* coef, uint16_t* atoms, uint32_t* err) {
