@@ -622,8 +622,9 @@ int launch_merge(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* w
     // Deep load batches when the rows have many partials (measured at B = 1: 45.2 us
     // a step with 16 float4 loads per batch, 45.9 with 8), shallow ones otherwise
     // (B = 64: 16 ranges, 2 hot splits).
-    if (a.total_rows < e->n_cu && (a.n_ar > 8 || a.hot_splits > 8))
-        // Few rows with many partials: a work-group per row, its waves splitting them.
+    if (a.total_rows <= 4ull * e->n_cu && (a.n_ar > 8 || a.hot_splits > 8))
+        // Few rows with many partials: a work-group per row, its waves splitting them
+        // (measured to B = 32; B = 8 step 58.2 -> 55.8 us).
         hipLaunchKernelGGL((aw::merge_row_kernel<HD, 8>), dim3((uint32_t)a.total_rows), dim3(256), 0, st, a);
     else if (a.n_ar > 16 || a.hot_splits > 8)
         hipLaunchKernelGGL((aw::merge_kernel<HD, 16>), dim3((uint32_t)gx), dim3(256), 0, st, a);
