@@ -159,3 +159,25 @@ def test_speculative_verify_step(engine, stream):
     assert new == [6, 2]
     cache.pop_loom(I.rollback_position(cache.push_loom(), 3, len(new)))
     assert cache.position == p0 + 2
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_multihead_attention_random_shapes(engine, stream, seed):
+    """Seeded random shapes: 1-16 new tokens, 0-3000 cached positions, GQA groups
+    1-8, head_dim 64 or 128, the cache's capacity 0-40 tokens past the last
+    block read; NaN in every row past kv_len."""
+    rng = np.random.default_rng(500 + seed)
+    hkv = int(rng.choice([1, 2, 4, 8]))
+    hq = hkv * int(rng.choice([1, 2, 4, 7, 8]))
+    d = int(rng.choice([64, 128]))
+    nq = int(rng.integers(1, 17))
+    kv_len = int(rng.integers(nq - 1, 3001))
+    cap = -(-kv_len // 16) * 16 + int(rng.integers(0, 41))
+    q, k, v = cache_case(9000 + seed, nq, kv_len, hq, hkv, d, max(cap, 1))
+    qt, kt, vt = (torch.from_numpy(x.view(np.int16)).cuda() for x in (q, k, v))
+    out = torch.full((nq, hq, d), float("nan"), dtype=torch.float16, device="cuda:0")
+    print(f"attention random {seed}: nq {nq} kv_len {kv_len} cap {cap} heads {hq}/{hkv} d {d}", flush=True)
+    engine.multihead_attention(qt, kt, vt, out, kv_len, d, hq, hkv, nq, cache_tokens=cap, stream=stream)
+    engine.check_device_errors(stream)
+    ref = AO.multihead_attention_f64(q, k[:kv_len], v[:kv_len], kv_len, nq)
+    assert_close(out.float().cpu().numpy(), ref, (seed, nq, kv_len))
