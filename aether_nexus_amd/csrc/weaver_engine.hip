@@ -170,15 +170,16 @@ int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, const uint32_t 
     o.info.rows_per_kv_head = R;
     o.info.computes_q_latent = (d->cold_count > 0 && d->q_latent == nullptr) ? 1u : 0u;
 
-    // Hot: one round of waves filling the resident capacity, >= 128 tokens per wave,
-    // splits <= kMaxSplits.
+    // Hot: one round of waves filling the resident capacity, splits <= kMaxSplits.
     if (d->hot_count > 0) {
         const uint64_t n_tok = d->hot_tokens ? d->hot_tokens : (uint64_t)d->hot_count * kBlock;
         // Beside the cold kernel (one 8-wave work-group per CU) one hot wave per SIMD fits.
         uint32_t wpc = hot_waves_per_cu[R <= 16 ? 0 : (R <= 32 ? 1 : 2)];
         if (d->cold_count > 0) wpc = std::min(wpc, 4u);
         uint64_t want = cdiv((uint64_t)n_cu * std::max(1u, wpc), n_lbg);
-        uint64_t cap = std::max<uint64_t>(1, cdiv(n_tok, 128)); // 64: B <= 4 steps 1-2% slower
+        // >= 128 tokens per wave beside the cold kernel (64: B <= 4 steps 1-3% slower);
+        // >= 64 alone (one-sequence attention 11.9 -> 11.1 us per layer against 128).
+        uint64_t cap = std::max<uint64_t>(1, cdiv(n_tok, d->cold_count > 0 ? 128 : 64));
         uint64_t S = std::max<uint64_t>(1, std::min<uint64_t>({want, cap, (uint64_t)aw::kMaxSplits}));
         // A split holds at most 64 blocks (its refs live in one register of the wave).
         S = std::max<uint64_t>(S, cdiv(n_tok, 64 * kBlock));
