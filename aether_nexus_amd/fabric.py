@@ -20,7 +20,7 @@ import numpy as np
 from . import _lib
 from .types import (AW_F_COLD_HEAD_BLOCKED, REGION_IDS, SPARSE_CODE_DTYPE, FabricRegions, LoomDescriptor, ModelDims,
                     WeaverParams)
-from .weaver import WeaverError, _status_text
+from .weaver import WeaverError, _status_text, make_desc
 
 #: ModelDims presets (nexus-core/src/types.rs:166-202).
 PRESETS = ("llama8b", "granite2b", "qwen05b", "deepseek_r1_1_5b")
@@ -241,6 +241,29 @@ class Fabric:
     @property
     def cold_head_blocked(self) -> bool:
         return bool(self.device_flags & AW_F_COLD_HEAD_BLOCKED)
+
+    def decode_desc(self, q, out, refs, *, hot_count: int, cold_count: int, batch: int = 1, queries: int = 1,
+                    refs_stride: Optional[int] = None, scale: float = 1.0, causal: bool = False, q_latent=None,
+                    seq_hot=None, seq_cold=None, hot_tokens: int = 0, seq_hot_tokens: bool = False):
+        """An ``aw_decode_desc`` over this fabric's device pools, the way the
+        reference's kernel reads the mapped pools (one layer; per-kv-head
+        dictionary; score scale 1.0 unless given): pool addresses, capacities
+        (MAX_HOT_BLOCKS, MAX_COLD_BLOCKS) and the cold order flag come from the
+        attachment, so a head-blocked device cold pool is always read as such.
+        ``q``, ``out``, ``refs`` and the optional arrays are the caller's device
+        tensors or pointers, as for ``make_desc``."""
+        dm = self.dims
+        return make_desc(layers=1, batch=batch, queries=queries, q_heads=dm.q_heads, kv_heads=dm.kv_heads,
+                         head_dim=dm.head_dim, dict_size=dm.dict_size, dict_heads=dm.kv_heads, hot_count=hot_count,
+                         cold_count=cold_count,
+                         refs_stride=hot_count + cold_count if refs_stride is None else refs_stride,
+                         hot_blocks=MAX_HOT_BLOCKS, cold_blocks=MAX_COLD_BLOCKS, q=q, out=out,
+                         hot_k=self.device_region("hot")[0] if hot_count else None,
+                         cold=self.device_region("cold")[0] if cold_count else None, refs=refs,
+                         dictionary=self.device_region("dict")[0] if cold_count else None, q_latent=q_latent,
+                         seq_hot=seq_hot, seq_cold=seq_cold, scale=scale, causal=causal,
+                         cold_head_blocked=self.cold_head_blocked, hot_tokens=hot_tokens,
+                         seq_hot_tokens=seq_hot_tokens)
 
     def device_region(self, region: str) -> tuple[int, int]:
         """(device address, bytes) of an attached region."""

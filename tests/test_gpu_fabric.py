@@ -134,6 +134,11 @@ def test_decode_from_fabric_pools(tmp_path, engine, stream):
     rel = np.linalg.norm(got - ref) / np.linalg.norm(ref)
     assert err <= 2e-3 and rel <= 1e-3, (err, rel)
     first = out_t.clone()
+    # The fabric's own descriptor: the same bits.
+    out_t.zero_()
+    engine.decode_device(fab.decode_desc(q_t, out_t, refs_t, hot_count=H, cold_count=C, scale=0.125), stream=stream)
+    engine.check_device_errors(stream)
+    assert torch.equal(out_t.view(torch.int16), first.view(torch.int16))
     fab.attach_device(0, regions=("cold",), cold_head_blocked=True)
     desc = make_desc(layers=1, batch=1, queries=1, q_heads=4, kv_heads=2, head_dim=64, dict_size=64, dict_heads=2,
                      hot_count=H, cold_count=C, refs_stride=H + C, hot_blocks=8192, cold_blocks=32768, q=q_t,
@@ -142,6 +147,10 @@ def test_decode_from_fabric_pools(tmp_path, engine, stream):
     out_t.zero_()
     print("fabric: decode from the head-blocked device cold pool", flush=True)
     engine.decode_device(desc, stream=stream)
+    engine.check_device_errors(stream)
+    assert torch.equal(out_t.view(torch.int16), first.view(torch.int16))
+    out_t.zero_()  # the fabric's descriptor carries the head-blocked flag by itself
+    engine.decode_device(fab.decode_desc(q_t, out_t, refs_t, hot_count=H, cold_count=C, scale=0.125), stream=stream)
     engine.check_device_errors(stream)
     assert torch.equal(out_t.view(torch.int16), first.view(torch.int16))
     fab.close()
