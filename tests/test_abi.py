@@ -17,7 +17,8 @@ from aether_nexus_amd.types import (AW_E_ALIGN, AW_E_INVALID_ARG, AW_E_OOB, AW_E
                                     STRUCT_SIZES, DecodeDesc, PlanInfo, WeaverParams)
 from aether_nexus_amd.weaver import WeaverError, plan, validate_params
 
-HEADERS = sorted((Path(__file__).resolve().parents[1] / "include").glob("*.h"))
+ROOT = Path(__file__).resolve().parents[1]
+HEADERS = sorted((ROOT / "include").glob("*.h"))
 
 
 def declared_functions():
@@ -195,3 +196,46 @@ def test_engine_create_without_gpu_fails_cleanly():
     h = ctypes.c_void_p()
     rc = lib.aw_engine_create(0, ctypes.byref(h))
     assert rc != 0 and not h.value
+
+
+def test_headers_compile_as_c_and_match_the_library(tmp_path):
+    """A C99 host (the way a Rust or C binding sees the ABI): both headers
+    compile with -pedantic -Werror, and a program linked against the library
+    finds the struct sizes it reports and the field offsets the Python
+    bindings use."""
+    import shutil
+    import subprocess
+    if shutil.which("gcc") is None:
+        pytest.skip("no gcc")
+    src = tmp_path / "abi.c"
+    src.write_text("""
+#include <stddef.h>
+#include <stdio.h>
+#include "aether_weaver.h"
+#include "aether_fabric.h"
+int main(void) {
+    size_t s[4];
+    aw_abi_struct_sizes(s);
+    printf("%zu %zu %zu %zu %zu %zu %zu %u\\n", sizeof(aw_sparse_code), sizeof(aw_weaver_params),
+           sizeof(aw_decode_desc), sizeof(aw_decode_plan_info), offsetof(aw_decode_desc, hot_tokens),
+           offsetof(aw_decode_desc, q), offsetof(aw_decode_desc, out), aw_abi_version());
+    return !(s[0] == sizeof(aw_sparse_code) && s[1] == sizeof(aw_weaver_params) && s[2] == sizeof(aw_decode_desc) &&
+             s[3] == sizeof(aw_decode_plan_info));
+}
+""")
+    lib = Path(_lib.lib_path()).resolve()
+    exe = tmp_path / "abi"
+    r = subprocess.run(["gcc", "-std=c99", "-Wall", "-Wextra", "-pedantic", "-Werror", f"-I{ROOT / 'include'}", str(src),
+                        "-o", str(exe), f"-L{lib.parent}", "-laether_weaver", f"-Wl,-rpath,{lib.parent}"],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, (r.stdout, r.stderr)
+    vals = [int(x) for x in r.stdout.split()]
+    assert vals[:4] == list(STRUCT_SIZES)
+    assert vals[4:7] == [DecodeDesc.hot_tokens.offset, DecodeDesc.q.offset, DecodeDesc.out.offset]
+    assert vals[7] == lib_abi_version()
+
+
+def lib_abi_version() -> int:
+    return _lib.load().aw_abi_version()
