@@ -1875,7 +1875,7 @@ __global__ __launch_bounds__(kEncMThreads) void encode_mfma_kernel(EncodeArgs a,
     constexpr int CPIECES = CH * PR, CPT = CPIECES / kEncMThreads; // 16-byte pieces per chunk / thread
     static_assert(CPT * kEncMThreads == CPIECES, "chunk staging");
     __shared__ __attribute__((aligned(16))) _Float16 sd[2][CH * P];
-    __shared__ AtomNorm s_dn[2][CH];
+    __shared__ uint4_t s_gs[2][CH / 4]; // per group of 4 atoms: max l2, max l1 (good atoms; float bits), sub flag, bad mask
     __shared__ __attribute__((aligned(16))) unsigned char s_lists[kEncMTokens * CAP * 2]; // pass-1 tops, then candidates
     __shared__ float s_T[kEncMTokens];
     __shared__ uint32_t s_cnt[kEncMTokens * 4];
@@ -1962,7 +1962,20 @@ __global__ __launch_bounds__(kEncMThreads) void encode_mfma_kernel(EncodeArgs a,
             const int p = tid + k * kEncMThreads;
             *(uint4_t*)(&sd[buf][(p / PR) * P + 8 * (p % PR)]) = creg[k];
         }
-        if (tid < CH) s_dn[buf][tid] = nreg;
+        if (tid < CH) { // wave 0: lane = atom; quads of lanes = the groups of 4 atoms of a tile row
+            const bool bad = (nreg.flags & kDictBad) != 0u;
+            float l2 = bad ? 0.0f : nreg.l2, l1 = bad ? 0.0f : nreg.l1;
+            uint32_t sub = bad ? 0u : (nreg.flags & kDictSubnormal), badm = bad ? (1u << (tid & 3)) : 0u;
+#pragma unroll
+            for (int o = 1; o < 4; o *= 2) {
+                l2 = fmaxf(l2, __shfl_xor(l2, o));
+                l1 = fmaxf(l1, __shfl_xor(l1, o));
+                sub |= (uint32_t)__shfl_xor((int)sub, o);
+                badm |= (uint32_t)__shfl_xor((int)badm, o);
+            }
+            if ((tid & 3) == 0)
+                s_gs[buf][tid / 4] = (uint4_t){__builtin_bit_cast(uint32_t, l2), __builtin_bit_cast(uint32_t, l1), sub, badm};
+        }
     };
     // One pass over the dictionary.  Per atom tile, fn(acc, E, badm, atom0) gets the
     // MFMA scores acc[tt][e] of the lane's tokens (tt) and atoms atom0 + e, one bound
@@ -1981,17 +1994,10 @@ __global__ __launch_bounds__(kEncMThreads) void encode_mfma_kernel(EncodeArgs a,
                 half8_t ad[KS];
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks) ad[ks] = *(const half8_t*)(&sd[cur][(at * 16 + li) * P + 32 * ks + 8 * lg]);
-                float l2m = 0.0f, l1m = 0.0f;
-                uint32_t sub = 0u, badm = 0u;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) { // bad atoms (always candidates) stay out of the bound
-                    const AtomNorm nd = s_dn[cur][at * 16 + 4 * lg + e];
-                    const bool bad = (nd.flags & kDictBad) != 0u;
-                    l2m = bad ? l2m : fmaxf(l2m, nd.l2);
-                    l1m = bad ? l1m : fmaxf(l1m, nd.l1);
-                    sub |= bad ? 0u : (nd.flags & kDictSubnormal);
-                    badm |= bad ? (1u << e) : 0u;
-                }
+                // The lane's 4 atoms: bad atoms (always candidates) stay out of the bound.
+                const uint4_t gs = s_gs[cur][at * 4 + lg];
+                const float l2m = __builtin_bit_cast(float, gs[0]), l1m = __builtin_bit_cast(float, gs[1]);
+                const uint32_t sub = gs[2], badm = gs[3];
                 float4_t acc[NTT];
                 float E[NTT];
 #pragma unroll
