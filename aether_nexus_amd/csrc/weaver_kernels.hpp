@@ -2211,13 +2211,16 @@ __device__ inline void entropy_word(const uint4_t w, EntSum& st, double& acc, do
 }
 
 // Blocks per wave.  A wave's 64 lanes all load (the stream is latency-bound:
-// more waves keep more chunks in flight); the first kEntBlocks lanes run the
-// chains.  At 16 blocks a wave, 8192 blocks make 512 waves.
+// more waves keep more chunks in flight) and all sum the values for the mean,
+// four lanes per block; the first kEntBlocks lanes run the sequential chains
+// (the variance, and the mean when its sums are not exact).  At 16 blocks a
+// wave, 8192 blocks make 512 waves.
 constexpr int kEntBlocks = 16;
 
 __global__ __launch_bounds__(64) void entropy_kernel(EncodeArgs a, uint32_t head_dim) {
     constexpr int NB = kEntBlocks, PL = NB * kEntCols / 64; // 16-byte loads per lane and chunk
     static_assert(PL * 64 == NB * kEntCols, "chunk loads");
+    static_assert(NB * 4 == 64 && kEntCols % 4 == 0, "four lanes per block in the mean pass");
     __shared__ uint4_t tile[2][NB][kEntPitch];
     __shared__ uint32_t s_blk[NB];
     const uint32_t lane = threadIdx.x;
@@ -2271,7 +2274,17 @@ __global__ __launch_bounds__(64) void entropy_kernel(EncodeArgs a, uint32_t head
             const int cur = (int)(ch & 1);
             const bool more = ch + 1 < n_chunks;
             if (more) load(ch + 1);
-            if (chain) {
+            if constexpr (P == 0) {
+                // Every lane: a quarter of the words of block lane / 4 (exact sums
+                // are the same in any order; the quarters are added after the pass).
+                constexpr uint32_t QW = kEntCols / 4;
+                const uint4_t* row = tile[cur][lane / 4];
+                const uint32_t cols = (ch + 1) * kEntCols <= words ? (uint32_t)kEntCols : (uint32_t)(words - ch * kEntCols);
+                const uint32_t c0 = (lane % 4) * QW;
+#pragma unroll
+                for (uint32_t c = 0; c < QW; ++c)
+                    if (c0 + c < cols) entropy_word<0>(row[c0 + c], st, acc, mean);
+            } else if (chain) {
                 const uint4_t* row = tile[cur][lane];
                 if ((ch + 1) * kEntCols <= words) {
                     uint4_t w[kEntCols];
@@ -2290,8 +2303,23 @@ __global__ __launch_bounds__(64) void entropy_kernel(EncodeArgs a, uint32_t head
         return acc;
     };
     (void)stream(std::integral_constant<int, 0>{}, -0.0);
-    double sum = (st.s[0] + st.s[1]) + (st.s[2] + st.s[3]);
-    const double mag = (st.m[0] + st.m[1]) + (st.m[2] + st.m[3]);
+    // Lanes 4r .. 4r+3 hold block r's quarter sums: added (exact whenever the
+    // test below passes) and handed to lane r, the block's owner.
+    double s4 = (st.s[0] + st.s[1]) + (st.s[2] + st.s[3]);
+    double m4 = (st.m[0] + st.m[1]) + (st.m[2] + st.m[3]);
+    uint32_t az = st.all_zero ? 1u : 0u, nf = st.nonfinite ? 1u : 0u;
+#pragma unroll
+    for (int o = 1; o < 4; o *= 2) {
+        s4 += __shfl_xor(s4, o);
+        m4 += __shfl_xor(m4, o);
+        az &= (uint32_t)__shfl_xor((int)az, o);
+        nf |= (uint32_t)__shfl_xor((int)nf, o);
+    }
+    const int src = (int)(chain ? lane * 4u : 0u);
+    double sum = __shfl(s4, src);
+    const double mag = __shfl(m4, src);
+    st.all_zero = __shfl((int)az, src) != 0;
+    st.nonfinite = __shfl((int)nf, src) != 0;
     const bool exact = !chain || (!st.nonfinite && mag < 536870912.0); // 2^29
     if (__any(!exact)) { // wave-uniform: the sequential sum for the blocks that need it
         const double seq = stream(std::integral_constant<int, 2>{}, -0.0);

@@ -88,6 +88,36 @@ def test_encode_entropy_edge_blocks(engine, stream):
     assert (ent.view(np.uint32) == went.view(np.uint32)).all()
 
 
+def test_entropy_sequential_fallback_blocks(engine, stream):
+    """Blocks outside the exact-sum case (sum of magnitudes >= 2^29, inf, NaN, -inf)
+    in the same waves as ordinary blocks: every proxy bit-exact against the
+    oracle's sequential f64 sums, except that a NaN proxy only has to be NaN (the
+    sign of a NaN that inf - inf creates is the platform's: negative on the
+    oracle's x86, positive on ARM, where the reference runs, and on this GPU; the
+    candidate rule 0 < e < 0.15 rejects either)."""
+    rng = np.random.default_rng(15)
+    nb = 40
+    hot = (rng.standard_normal((nb, 16, 8, 128)) * 3).astype(np.float16)
+    hot[3] = (np.sign(rng.standard_normal(hot[3].shape)) * 60000).astype(np.float16)  # |sum| >= 2^29
+    hot[7, 5, 2, 9] = np.inf
+    hot[20, 0, 0, 0] = np.nan
+    hot[21, 15, 7, 127] = -np.inf
+    big = rng.standard_normal(hot[33].shape) * 30000  # past 65504: infinities of both signs
+    hot[33] = np.where(np.abs(big) > 65504, np.copysign(np.inf, big), big).astype(np.float16)
+    bits = hot.view(np.uint16)
+    want = np.array([oracle.block_entropy(bits[b]) for b in range(nb)], np.float32)
+    hot_t = torch.from_numpy(bits.view(np.int16)).cuda()
+    ent = torch.zeros(nb, dtype=torch.float32, device="cuda:0")
+    print("encoder: entropy fallback blocks", flush=True)
+    engine.block_entropy_device(hot_t, nb, 8, 128, None, nb, ent, stream=stream)
+    engine.check_device_errors(stream)
+    got = ent.cpu().numpy()
+    nan = np.isnan(want)
+    assert nan[[7, 20, 21, 33]].all() and np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32)), np.nonzero(got != want)
+    assert want[3] > 1e9  # the 2^29 case took the sequential sums
+
+
 def test_encode_host_slices(engine):
     """aw_encode: copy in, encode, copy back; hot block b -> cold block b."""
     rng, hot, d = pools(14, 6, 8, 128, 512, 8)
