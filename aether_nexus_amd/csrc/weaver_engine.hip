@@ -180,15 +180,17 @@ int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, const uint32_t 
         // >= 128 tokens per wave beside the cold kernel (64: B <= 4 steps 1-3% slower);
         // >= 64 alone (one-sequence attention 11.9 -> 11.1 us per layer against 128).
         uint64_t cap = std::max<uint64_t>(1, cdiv(n_tok, d->cold_count > 0 ? 128 : 64));
-        uint64_t S = std::max<uint64_t>(1, std::min<uint64_t>({want, cap, (uint64_t)aw::kMaxSplits}));
-        // A split holds at most 64 blocks (its refs live in one register of the wave).
-        S = std::max<uint64_t>(S, cdiv(n_tok, 64 * kBlock));
-        if (S > (uint64_t)aw::kMaxSplits) {
-            put_msg(msg, mlen, "hot pool of %llu tokens needs more than %d splits of 1024 tokens",
-                    (unsigned long long)n_tok, aw::kMaxSplits);
+        const uint64_t S = std::max<uint64_t>(1, std::min<uint64_t>({want, cap, (uint64_t)aw::kMaxSplits}));
+        // A split's block refs are staged in the hot kernel's LDS (4 bytes each,
+        // sized per launch): at most kMaxHotSplitBlocks, so 64 splits cover
+        // 64 * 4096 blocks = 4 Mi tokens per sequence.
+        const uint64_t tps = align_up(cdiv(n_tok, S), 32);
+        if (tps > (uint64_t)aw::kMaxHotSplitBlocks * kBlock) {
+            put_msg(msg, mlen, "hot pool of %llu tokens exceeds %d splits of %u blocks (%llu tokens per sequence)",
+                    (unsigned long long)n_tok, aw::kMaxSplits, aw::kMaxHotSplitBlocks,
+                    (unsigned long long)aw::kMaxSplits * aw::kMaxHotSplitBlocks * kBlock);
             return AW_E_UNSUPPORTED;
         }
-        uint64_t tps = align_up(cdiv(n_tok, S), 32);
         o.info.hot_tokens_per_split = (uint32_t)tps;
         o.info.hot_splits = cdiv(n_tok, tps);
     }
@@ -436,6 +438,7 @@ int launch_hot(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* ws,
     a.refs_stride = d->refs_stride;
     a.splits = o.info.hot_splits;
     a.tokens_per_split = o.info.hot_tokens_per_split;
+    a.refs_cap = (uint32_t)align_up(cdiv(a.tokens_per_split, kBlock), 4);
     a.causal = (d->flags & AW_F_CAUSAL) ? 1u : 0u;
     a.n_tok_max = d->hot_tokens ? d->hot_tokens : d->hot_count * kBlock;
     a.seq_tokens = (d->flags & AW_F_SEQ_HOT_TOKENS) ? 1u : 0u;
@@ -447,7 +450,8 @@ int launch_hot(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* ws,
     if (grid > 0x7FFFFFFFull) return fail(e, AW_E_UNSUPPORTED, "hot grid too large");
     StageTimer t(e, AW_STAGE_HOT, st);
     const uint32_t R = a.rows_r;
-#define AW_LAUNCH_HOT(RTV, SV) hipLaunchKernelGGL((aw::hot_kernel<HD, RTV, SV>), dim3((uint32_t)grid), dim3(64), 0, st, a)
+    const size_t smem = (size_t)a.refs_cap * 4; // the split's block refs
+#define AW_LAUNCH_HOT(RTV, SV) hipLaunchKernelGGL((aw::hot_kernel<HD, RTV, SV>), dim3((uint32_t)grid), dim3(64), smem, st, a)
     const bool sepv = a.hot_v != nullptr;
     if (R <= 16) {
         if (sepv) AW_LAUNCH_HOT(1, true); else AW_LAUNCH_HOT(1, false);

@@ -46,7 +46,8 @@ constexpr uint32_t kBlockTokens = 16;      // tokens per block (ModelDims::BLOCK
 constexpr uint32_t kRefMask = 0x7FFFFFFFu; // weaver_kernel.metal:145,174
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kColdThreads = 512;
-constexpr int kMaxSplits = 64;
+constexpr int kMaxSplits = 64;              // splits per row: the merges combine them lane = split
+constexpr uint32_t kMaxHotSplitBlocks = 4096; // hot blocks per split (16 KiB of LDS refs): 4 Mi tokens per sequence
 
 // Error bits written to the engine's device error word.
 constexpr uint32_t kErrHotRef = 1u, kErrColdRef = 2u, kErrAtom = 4u;
@@ -126,6 +127,7 @@ struct HotArgs {
     uint32_t* err;
     uint32_t batch, queries, q_heads, kv_heads, gqa, rows_r;
     uint32_t hot_count, refs_stride, splits, tokens_per_split, causal;
+    uint32_t refs_cap;   // block refs the launch's LDS holds per split (>= tokens_per_split / 16)
     uint32_t n_tok_max;  // hot tokens of a sequence (hot_count * 16 unless the request gives fewer)
     uint32_t seq_tokens; // seq_hot counts tokens rather than blocks
     float scale_log2;
@@ -340,11 +342,10 @@ __global__ __launch_bounds__(kProjThreads) void project_kernel(ProjArgs a) {
 // LDS pitch HD+4 halves (66 words at HD=128) puts the four token rows 4*lg+e'
 // of one read on disjoint 8-bank groups.
 //
-// A split holds at most 64 blocks; their refs are staged in LDS once.  Every
-// global load of the loop is
-// unconditional (a bad ref reads block 0 and the chunk's registers are zeroed
-// before use), so the next chunk's loads really stay in flight while the
-// current chunk is computed.
+// A split holds at most kMaxHotSplitBlocks blocks; their refs are staged in
+// (dynamic) LDS once.  Every global load of the loop is unconditional (a bad
+// ref reads block 0 and the chunk's registers are zeroed before use), so the
+// next chunk's loads really stay in flight while the current chunk is computed.
 template <int HD, int RT, bool SEPV>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu((RT == 1 && !SEPV) ? 3 : 1))) void hot_kernel(HotArgs a) {
     constexpr int KS = HD / 32, NB = HD / 16, P = HD + 4;
@@ -361,14 +362,15 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu((RT == 1 && 
     const uint32_t t_end = min(t_begin + a.tokens_per_split, n_tok);
     const uint32_t R = a.rows_r;
 
-    // Block refs of this split (tokens_per_split <= 64 blocks), staged in LDS:
-    // the loop reads them with LDS loads, which never wait behind the K loads.
-    __shared__ uint32_t s_refs[64];
+    // Block refs of this split (at most refs_cap = tokens_per_split / 16 blocks,
+    // dynamic LDS sized by the launch), staged once: the loop reads them with LDS
+    // loads, which never wait behind the K loads.
+    extern __shared__ uint32_t s_refs[];
     const uint32_t blk0 = t_begin / kBlockTokens;
     const uint32_t n_blk = t_end > t_begin ? (t_end - t_begin + kBlockTokens - 1) / kBlockTokens : 0u;
     {
         const uint32_t* refs = a.refs + (uint64_t)l * a.refs_layer + (uint64_t)(lb % a.batch) * a.refs_stride;
-        s_refs[lane] = refs[blk0 + min((uint32_t)lane, n_blk ? n_blk - 1u : 0u)] & kRefMask;
+        for (uint32_t i = (uint32_t)lane; i < n_blk; i += 64u) s_refs[i] = refs[blk0 + i] & kRefMask;
         __syncthreads();
     }
 
@@ -404,7 +406,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu((RT == 1 && 
         for (int tb = 0; tb < 2; ++tb) {
             const uint32_t bi = (c0 - t_begin) / kBlockTokens + tb;
             const bool in = c0 + 16 * tb < t_end;
-            const uint32_t ref = s_refs[min(bi, 63u)];
+            const uint32_t ref = s_refs[min(bi, a.refs_cap - 1u)]; // entries past n_blk: `in` is false
             ok[tb] = in && ref < a.hot_blocks;
             bad |= in && !ok[tb];
             const uint32_t pr = ok[tb] ? ref : 0u;

@@ -117,6 +117,10 @@ typedef struct aw_weaver_params {
  *   out      [L][B][Q][q_heads][head_dim]
  * scale multiplies every score; 1.0 reproduces the reference, which applies
  * none (weaver_kernel.metal:153-160,186-190).
+ * Hot pools: a sequence's hot tokens run in at most 64 splits of at most 4096
+ * blocks, so hot_count (or hot_tokens / 16) may reach 262144 blocks = 4 Mi
+ * tokens per sequence; the reference Fabric holds MAX_HOT_BLOCKS = 8192
+ * (types.rs:500).  Larger requests return AW_E_UNSUPPORTED.
  * hot_tokens: 0, or the hot tokens of every sequence (1 .. hot_count * 16);
  * hot tokens past it are neither scored nor read as values (nor past a
  * seq_hot entry).  Loads still cover whole blocks, so the pool must hold every
@@ -257,7 +261,8 @@ int aw_decode_device(aw_engine* engine, const aw_decode_desc* desc, void* hip_st
  * hot pool (16-token blocks, identity block table), so cache_tokens must cover
  * kv_len rounded up to 16 (the reference allocates MAX_SEQ_LEN = 4096 tokens,
  * inference.rs:219,256-266).  Unlike the reference (threadgroup scores[4096],
- * ops.metal:564) kv_len is not limited to 4096, and kv_len + 1 < num_queries is
+ * ops.metal:564) kv_len is not limited to 4096: it may reach 4 Mi positions
+ * (the hot-pool limit of aw_decode_device), and kv_len + 1 < num_queries is
  * rejected instead of wrapping.  Queries beyond 64 / (q_heads / kv_heads) per
  * call are processed in consecutive groups. */
 int aw_multihead_attention_device(aw_engine* engine, const uint16_t* q, const uint16_t* k_cache,

@@ -167,6 +167,36 @@ def test_plan_small_batch_fills_cus():
         assert 4096 * info.cold_row_chunk * 4 * 2 <= info.cold_tokens_per_split * info.cold_splits * 16
 
 
+def test_plan_full_hot_region():
+    """The reference's whole hot region, MAX_HOT_BLOCKS = 8192 blocks (types.rs:500),
+    plans at Llama-8B geometry with and without a cold pool, and so does a
+    131072-token contiguous cache; the limit is 64 splits of 4096 blocks."""
+    from aether_nexus_amd.weaver import make_desc
+    for hot, cold, B in ((4097, 0, 1), (8192, 0, 1), (8192, 2048, 1), (8192, 2048, 4), (8192, 0, 64)):
+        info = plan(make_desc(layers=1, batch=B, queries=1, q_heads=32, kv_heads=8, head_dim=128,
+                              dict_size=4096 if cold else 0, dict_heads=1, hot_count=hot, cold_count=cold,
+                              refs_stride=hot + cold, hot_blocks=hot, cold_blocks=max(cold, 1), q=1, out=1))
+        assert 1 <= info.hot_splits <= 64, (hot, cold, B)
+        assert info.hot_tokens_per_split % 32 == 0 and info.hot_tokens_per_split <= 4096 * 16
+        assert info.hot_splits * info.hot_tokens_per_split >= hot * 16
+        assert (info.hot_splits - 1) * info.hot_tokens_per_split < hot * 16  # no empty split
+    # Causal verify step over a 131072-token cache (aw_multihead_attention_device's decode).
+    info = plan(make_desc(layers=1, batch=1, queries=4, q_heads=32, kv_heads=8, head_dim=128, dict_size=0,
+                          dict_heads=1, hot_count=8192, cold_count=0, refs_stride=8192, hot_blocks=8192,
+                          cold_blocks=0, q=1, out=1, causal=True, hot_tokens=131072))
+    assert info.hot_splits == 64 and info.hot_tokens_per_split == 2048
+    top = 64 * 4096
+    info = plan(make_desc(layers=1, batch=1, queries=1, q_heads=32, kv_heads=8, head_dim=128, dict_size=0,
+                          dict_heads=1, hot_count=top, cold_count=0, refs_stride=top, hot_blocks=top,
+                          cold_blocks=0, q=1, out=1))
+    assert info.hot_splits == 64 and info.hot_tokens_per_split == 4096 * 16
+    with pytest.raises(WeaverError) as e:
+        plan(make_desc(layers=1, batch=1, queries=1, q_heads=32, kv_heads=8, head_dim=128, dict_size=0,
+                       dict_heads=1, hot_count=top + 1, cold_count=0, refs_stride=top + 1, hot_blocks=top + 1,
+                       cold_blocks=0, q=1, out=1))
+    assert e.value.status == AW_E_UNSUPPORTED and "4096 blocks" in str(e.value)
+
+
 def test_plan_flags():
     """The head-blocked cold layout plans like the reference layout; unknown flag bits are rejected."""
     from aether_nexus_amd.types import AW_E_INVALID_ARG, AW_F_CAUSAL, AW_F_COLD_HEAD_BLOCKED

@@ -45,6 +45,7 @@ def cache_case(seed, nq, kv_len, hq, hkv, d, cap):
     (4, 100, 32, 8, 128),    # verify of 3 drafts, partial last block
     (16, 4096, 32, 8, 128),  # MAX_BATCH new tokens at MAX_SEQ_LEN
     (3, 5000, 32, 8, 128),   # past the reference's 4096-score limit
+    (4, 131072, 32, 8, 128), # 8192 blocks: the reference Fabric's whole hot region (types.rs:500)
     (16, 37, 14, 2, 64),     # G = 7: queries in two groups of <= 9
     (16, 15, 8, 8, 64),      # query 0 sees nothing (zeros), query 1 sees position 0
 ])

@@ -138,9 +138,16 @@ def test_out_of_range_refs_are_reported(engine, stream):
 
 
 def sampled_rows(geom, n, seed):
-    total = geom.layers * geom.batch * geom.queries * geom.q_heads
+    """n random output rows, plus one q head of every kv head (a different member
+    of each GQA group) in the first and last query of the first and last
+    sequence of the first and last layer.  Row id = ((l*B + b)*Q + q)*Hq + h."""
+    L, B, Q, Hq, Hkv = geom.layers, geom.batch, geom.queries, geom.q_heads, geom.kv_heads
+    G = Hq // Hkv
+    total = L * B * Q * Hq
+    fixed = [((l * B + b) * Q + q) * Hq + g * G + (g + l + b + q) % G
+             for l in {0, L - 1} for b in {0, B - 1} for q in {0, Q - 1} for g in range(Hkv)]
     rng = np.random.default_rng(seed)
-    return np.unique(np.concatenate([[0, total - 1], rng.integers(0, total, n)])).astype(np.uint64)
+    return np.unique(np.concatenate([fixed, rng.integers(0, total, n)])).astype(np.uint64)
 
 
 def full_size(engine, stream, geom, seed, n_rows, what):
@@ -193,18 +200,29 @@ def test_repeat_calls_bit_identical(engine, stream):
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
 
 
+@pytest.mark.parametrize("cold_count", [0, 2048], ids=["hot_only", "hot_cold"])
+def test_full_hot_region_8192_blocks(engine, stream, cold_count):
+    """The reference Fabric's whole hot region, MAX_HOT_BLOCKS = 8192 blocks of 16
+    tokens (types.rs:500), which its kernel walks for any hot_count
+    (weaver_kernel.metal:143-168): B = 1, 32 q / 8 kv heads, d 128, 131072 hot
+    tokens, alone and with 2048 cold blocks; every row against the fp64 oracle."""
+    geom = W.hot_cold(hot_count=8192, cold_count=cold_count)
+    full_size(engine, stream, geom, 56 + cold_count, 64, f"hot 8192 blocks + cold {cold_count} blocks")
+    torch.cuda.empty_cache()
+
+
 def test_full_size_sweep_b64(engine, stream):
     """hot 2048 + cold 32768 per kv head, B = 64: the benchmark shape."""
-    full_size(engine, stream, W.sweep(64), 50, 12, "sweep B64 (sampled rows)")
+    full_size(engine, stream, W.sweep(64), 50, 64, "sweep B64 (sampled rows)")
 
 
 def test_full_size_batched_zipf(engine, stream):
     """B = 64, hot 1024 + cold 131072 SparseCodes per kv head, Zipf(1.1) atoms."""
-    full_size(engine, stream, W.batched(), 51, 8, "batched B64 Zipf (sampled rows)")
+    full_size(engine, stream, W.batched(), 51, 64, "batched B64 Zipf (sampled rows)")
 
 
 def test_full_size_spec_verify(engine, stream):
     """32 layers, B = 8, 8 causal drafts, hot 2048 + cold 65536 per kv head,
     per-layer 4096 x 128 dictionary."""
-    full_size(engine, stream, W.spec_verify(), 52, 10, "spec-verify L32 (sampled rows)")
+    full_size(engine, stream, W.spec_verify(), 52, 64, "spec-verify L32 (sampled rows)")
     torch.cuda.empty_cache()
