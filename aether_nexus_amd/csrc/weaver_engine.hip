@@ -11,6 +11,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -278,6 +279,41 @@ int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, const uint32_t 
 
 } // namespace
 
+// ------------------------------------------------- fixed scratch (no allocation)
+//
+// Scratch of aw_decode_device_noalloc: one file-scope device array, which every
+// GPU the library runs on holds (its own copy, at its own address) until the
+// process ends.  Host code never uses the array's name as an address: the name
+// is a host-side stand-in.  The device address comes from hipGetSymbolAddress,
+// once per device with that device current (at engine creation), and is kept
+// per device in g_scratch_ptr.
+static_assert(AW_NOALLOC_SCRATCH_BYTES % 256 == 0, "scratch size");
+static __device__ __align__(256) unsigned char scratch[AW_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on `device`, which must be current.
+hipError_t scratch_address(int device, void** out) {
+    *out = nullptr;
+    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[device]) {
+        void* p = nullptr;
+        const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (err != hipSuccess) return err;
+        if (!p) return hipErrorInvalidSymbol;
+        g_scratch_ptr[device] = p;
+    }
+    *out = g_scratch_ptr[device];
+    return hipSuccess;
+}
+
+} // namespace
+
 // ------------------------------------------------------------------ engine
 
 struct aw_engine {
@@ -293,6 +329,7 @@ struct aw_engine {
     DevBuf q, ql, hot, cold, refs, dict, out; // aw_decode copies (weaver.rs:40-46)
     DevBuf ws;                                // per-request scratch
     std::vector<void*> retired_ws;            // outgrown scratch, kept for captured graphs
+    void* scratch = nullptr;                  // this device's `scratch` array (aw_decode_device_noalloc)
     DevBuf enc_ws;                            // encoder scratch: per-atom norms and flags
     DevBuf iota;                              // identity block table for contiguous caches
     uint32_t iota_n = 0;                      // entries of `iota` filled
@@ -678,7 +715,9 @@ int run_pipeline(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* w
     return AW_OK;
 }
 
-int decode_device(aw_engine* e, const aw_decode_desc* d, hipStream_t st) {
+// no_alloc: scratch from the device's fixed `scratch` array instead of the
+// engine workspace; nothing is allocated (no workspace growth, no timing events).
+int decode_device(aw_engine* e, const aw_decode_desc* d, hipStream_t st, bool no_alloc = false) {
     Layout o;
     char msg[256] = {0};
     int rc = plan(d, e->max_lds, e->n_cu, e->hot_wpc, &o, msg, sizeof msg);
@@ -695,6 +734,21 @@ int decode_device(aw_engine* e, const aw_decode_desc* d, hipStream_t st) {
         return fail(e, AW_E_INVALID_ARG, "hot_count > 0 needs hot_blocks > 0");
     if (d->cold_count && ((uintptr_t)d->cold & 15u))
         return fail(e, AW_E_ALIGN, "cold pool pointer is not 16-byte aligned");
+    if (no_alloc) {
+        if (o.info.workspace_bytes > (uint64_t)AW_NOALLOC_SCRATCH_BYTES)
+            return fail(e, AW_E_UNSUPPORTED,
+                        "request needs %llu bytes of scratch; the no-allocation entry point has %llu "
+                        "(use aw_decode_device, or split the request over layers or sequences)",
+                        (unsigned long long)o.info.workspace_bytes, (unsigned long long)AW_NOALLOC_SCRATCH_BYTES);
+        if (!e->scratch) return fail(e, AW_E_HIP, "the device's scratch array has no address");
+        // Stage timers create events: keep them off for this call.
+        const int prof = e->profiling;
+        e->profiling = AW_PROFILE_OFF;
+        char* ws = (char*)e->scratch;
+        rc = d->head_dim == 64 ? run_pipeline<64>(e, d, o, ws, st) : run_pipeline<128>(e, d, o, ws, st);
+        e->profiling = prof;
+        return rc;
+    }
     if ((rc = ensure_keep(e->ws, o.info.workspace_bytes, e->retired_ws, e->last_error))) return rc;
     char* ws = (char*)e->ws.ptr;
     return d->head_dim == 64 ? run_pipeline<64>(e, d, o, ws, st) : run_pipeline<128>(e, d, o, ws, st);
@@ -915,7 +969,9 @@ int aw_engine_create(int device, aw_engine** out) {
         // no system-scope cache writeback.
         hipEventCreateWithFlags(&e->ev_fork, hipEventDisableTiming | hipEventDisableSystemFence) != hipSuccess ||
         hipEventCreateWithFlags(&e->ev_join, hipEventDisableTiming | hipEventDisableSystemFence) != hipSuccess ||
-        hipMalloc((void**)&e->err, 256) != hipSuccess || hipMemset(e->err, 0, 256) != hipSuccess) {
+        hipMalloc((void**)&e->err, 256) != hipSuccess || hipMemset(e->err, 0, 256) != hipSuccess ||
+        // The fixed scratch array's address on this device (current since hipSetDevice above).
+        scratch_address(device, &e->scratch) != hipSuccess) {
         aw_engine_destroy(e);
         return AW_E_HIP;
     }
@@ -1009,6 +1065,13 @@ int aw_decode_device(aw_engine* e, const aw_decode_desc* desc, void* stream) {
     AW_HIP(e, hipSetDevice(e->device));
     hipStream_t st = (hipStream_t)stream; // NULL is HIP's null stream
     return decode_device(e, desc, st);
+}
+
+int aw_decode_device_noalloc(aw_engine* e, const aw_decode_desc* desc, void* stream) {
+    if (!e) return AW_E_INVALID_ARG;
+    AW_HIP(e, hipSetDevice(e->device));
+    hipStream_t st = (hipStream_t)stream; // NULL is HIP's null stream
+    return decode_device(e, desc, st, /*no_alloc=*/true);
 }
 
 // The contiguous cache [cache_tokens][kv_heads][head_dim] is the hot pool

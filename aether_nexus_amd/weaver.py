@@ -202,6 +202,12 @@ class WeaverEngine:
         rc = self._lib.aw_decode_device(self._h, ctypes.byref(desc), _stream(stream))
         self._check(rc, "decode_device")
 
+    def decode_device_noalloc(self, desc: DecodeDesc, stream: Optional[int] = None) -> None:
+        """``decode_device`` with its scratch in the library's fixed per-GPU array
+        (AW_NOALLOC_SCRATCH_BYTES): allocates nothing; larger requests raise."""
+        rc = self._lib.aw_decode_device_noalloc(self._h, ctypes.byref(desc), _stream(stream))
+        self._check(rc, "decode_device_noalloc")
+
     def multihead_attention(self, q, k_cache, v_cache, output, kv_len: int, head_dim: int, q_heads: int,
                             kv_heads: int, num_queries: int, cache_tokens: Optional[int] = None,
                             stream: Optional[int] = None) -> None:

@@ -248,6 +248,23 @@ int aw_decode(aw_engine* engine,
  * a time (stream-ordered, or synchronised between). */
 int aw_decode_device(aw_engine* engine, const aw_decode_desc* desc, void* hip_stream);
 
+/* No reference counterpart.  For callers that cannot allocate device memory:
+ * code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc.  The same decode as aw_decode_device (same kernels, same output
+ * bits), but it allocates nothing: its scratch is a fixed device array of
+ * AW_NOALLOC_SCRATCH_BYTES that every GPU the library runs on holds until the
+ * process ends (its address is looked up once per device, at
+ * aw_engine_create).  A request whose scratch (aw_decode_plan_info.
+ * workspace_bytes) exceeds it returns AW_E_UNSUPPORTED: 96 MiB covers a
+ * one-layer decode of 64 sequences at hot 2048 + cold 32768 tokens (67 MiB),
+ * not a 32-layer call in one piece.  Stage timing (aw_engine_set_profiling) is
+ * not recorded for these calls.  Every call on one GPU, from any engine,
+ * shares that GPU's array and leaves its contents behind: calls (and graph
+ * replays) that overlap on one GPU race; order them on one stream or
+ * synchronise between them. */
+#define AW_NOALLOC_SCRATCH_BYTES ((uint64_t)96 << 20)
+int aw_decode_device_noalloc(aw_engine* engine, const aw_decode_desc* desc, void* hip_stream);
+
 /* Replaces Ops::multihead_attention (nexus-core/src/ops.rs:433-462, kernel
  * ops.metal:528-616), the attention of InferenceEngine::forward_batch
  * (inference.rs:546-556): causal GQA attention of num_queries new tokens over

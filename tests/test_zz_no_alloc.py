@@ -1,0 +1,51 @@
+"""aw_decode_device_noalloc on cuda:0 through the C ABI: the decode with its
+scratch in the library's fixed per-GPU array gives the same output bits as
+aw_decode_device (which takes its scratch from the engine workspace), on two
+calls in a row, the second smaller; a request whose scratch exceeds the array
+is rejected before anything runs."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from aether_nexus_amd import workloads as W
+from aether_nexus_amd.types import AW_E_UNSUPPORTED, AW_NOALLOC_SCRATCH_BYTES
+from aether_nexus_amd.weaver import WeaverError, plan
+
+pytestmark = pytest.mark.gpu
+
+
+def decode_both(engine, stream, geom, seed):
+    wl = W.generate(geom, seed=seed, device="cuda:0")
+    ref = torch.full(wl.out_shape(), float("nan"), dtype=torch.float16, device="cuda:0")
+    out = torch.full(wl.out_shape(), float("nan"), dtype=torch.float16, device="cuda:0")
+    print(f"no-alloc: {geom.batch} seq, hot {geom.hot_count} + cold {geom.cold_count} blocks, "
+          f"scratch {plan(W.device_desc(wl, out)).workspace_bytes} bytes", flush=True)
+    engine.decode_device_noalloc(W.device_desc(wl, out), stream=stream)
+    engine.check_device_errors(stream)
+    engine.decode_device(W.device_desc(wl, ref), stream=stream)
+    engine.check_device_errors(stream)
+    assert torch.isfinite(out.float()).all()
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+
+
+def test_noalloc_matches_decode_device(engine, stream):
+    # 64 sequences at hot 2048 + cold 32768 tokens (67 MiB of scratch), then a
+    # smaller ragged request: the second call reuses the array the first left behind.
+    big = W.sweep(64)
+    small = W.hot_cold(batch=3, hot_count=5, cold_count=40, dict_size=256, queries=2, causal=True)
+    decode_both(engine, stream, big, seed=71)
+    decode_both(engine, stream, small, seed=72)
+
+
+def test_noalloc_rejects_requests_beyond_its_scratch(engine, stream):
+    geom = W.sweep(64, layers=2)  # 135 MiB of scratch
+    wl = W.generate(geom, seed=73, device="cuda:0")
+    out = torch.full(wl.out_shape(), float("nan"), dtype=torch.float16, device="cuda:0")
+    desc = W.device_desc(wl, out)
+    assert plan(desc).workspace_bytes > AW_NOALLOC_SCRATCH_BYTES
+    with pytest.raises(WeaverError) as e:
+        engine.decode_device_noalloc(desc, stream=stream)
+    assert e.value.status == AW_E_UNSUPPORTED and "scratch" in str(e.value)
+    torch.cuda.synchronize()
+    assert torch.isnan(out.float()).all()  # nothing ran
