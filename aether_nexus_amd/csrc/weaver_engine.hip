@@ -1352,6 +1352,21 @@ int aw_encode(aw_engine* e, const uint16_t* hot, size_t n_hot, const uint16_t* d
     return aw_engine_check_device_errors(e, e->stream);
 }
 
+int aw_debug_read_stream(aw_engine* e, const void* buf, uint64_t bytes, uint32_t waves_per_cu, uint32_t* sink,
+                         void* stream) {
+    if (!e) return AW_E_INVALID_ARG;
+    if (!buf || !sink || !bytes || (bytes & 15u) || ((uintptr_t)buf & 15u))
+        return fail(e, AW_E_INVALID_ARG, "buf (16-byte aligned), sink and bytes (a multiple of 16) are required");
+    if (waves_per_cu < 4 || waves_per_cu > 64 || (waves_per_cu & 3u))
+        return fail(e, AW_E_INVALID_ARG, "waves_per_cu %u must be a multiple of 4 in [4, 64]", waves_per_cu);
+    AW_HIP(e, hipSetDevice(e->device));
+    const uint32_t grid = e->n_cu * (waves_per_cu / 4); // 4 waves per 256-thread work-group
+    hipLaunchKernelGGL(aw::read_stream_kernel<8>, dim3(grid), dim3(256), 0, (hipStream_t)stream,
+                       (const aw::uint4_t*)buf, bytes / 16, sink);
+    AW_HIP(e, hipGetLastError());
+    return AW_OK;
+}
+
 int aw_engine_set_profiling(aw_engine* e, int enable) {
     if (!e) return AW_E_INVALID_ARG;
     if (enable < AW_PROFILE_OFF || enable > AW_PROFILE_SERIAL) return fail(e, AW_E_INVALID_ARG, "profiling mode %d", enable);

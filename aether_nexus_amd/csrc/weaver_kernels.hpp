@@ -553,8 +553,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu((RT == 1 && 
 // ----------------------------------------------- cold pool, scores + bins
 //
 // Work item = (layer*batch+seq, chunk of RC query rows, split) x kv head g.
-// LDS: q_latent table [A][RC] f16; per atom NP = ceil(RC/2) 64-bit bins,
-// each holding two rows' sums as 32-bit fixed point; the split's block refs.
+// LDS: q_latent table [A][RC] f16; NP = ceil(RC/2) planes of A 64-bit bins,
+// each bin holding two rows' sums as 32-bit fixed point; the split's block refs.
+// Planes [NP][A] rather than [A][NP]: a wave's 64 random atoms then spread
+// over every bank pair of the LDS (measured on gfx950: ds_add_u64 at random
+// atoms 0.21 cycles per lane and CU in planes, 0.28 with the 16-byte atom
+// stride of [A][2], 0.11 with no bank conflicts).
 //
 // Integer bins: on gfx950 an LDS ds_add_f32 retires about one lane per 3
 // cycles per CU whatever the addresses, ds_add_u64 about one lane per 0.3
@@ -639,7 +643,7 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
     const uint32_t n_blk = (t_end - t_begin + 15) / 16; // t_begin is a multiple of 16
     const uint32_t n_wt = (t_end - t_begin + WT - 1) / WT;
     _Float16* qtab = (_Float16*)smem;
-    uint64_t* bins = (uint64_t*)(smem + qtab_bytes);       // [A][NP]
+    uint64_t* bins = (uint64_t*)(smem + qtab_bytes);       // [NP][A]: one plane per row pair
     uint32_t* sref = (uint32_t*)(bins + (uint64_t)A * NP); // [n_blk] physical blocks, ~0 = invalid
     float* red = (float*)(sref + ((n_blk + 3) & ~3u));    // [NW][NR]
 
@@ -956,7 +960,7 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
                         else pmx = fmaxf(pmx, ps[0]);
 #pragma unroll
                         for (int j = 0; j < 4; ++j) {
-                            uint64_t* bp = bins + ia[j] * NP;
+                            uint64_t* bp = bins + ia[j]; // plane pp at bp + pp * A
                             const float cj = (float)coef(cw, j);
 #pragma unroll
                             for (int pp = 0; pp < NP; ++pp) {
@@ -965,7 +969,7 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
                                     (2 * pp + 1 < RC) ? __builtin_bit_cast(uint32_t, fmaf(ps[min(2 * pp + 1, RC - 1)], cj, kMagic))
                                                       : 0x4B400000u;
                                 const uint64_t wv = (((uint64_t)b1 << 32) | b0) - kMagic2;
-                                __hip_atomic_fetch_add(bp + pp, wv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                                __hip_atomic_fetch_add(bp + pp * A, wv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
                             }
                         }
                     }
@@ -1088,7 +1092,7 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
     for (uint32_t at = tid; at < A; at += NT) {
 #pragma unroll
         for (int pp = 0; pp < NP; ++pp) {
-            const uint64_t wv = bins[at * NP + pp];
+            const uint64_t wv = bins[pp * A + at];
             const int32_t v0 = (int32_t)(uint32_t)wv;
             const int32_t v1 = (int32_t)((uint32_t)(wv >> 32) + (v0 < 0 ? 1u : 0u));
 #pragma unroll
@@ -1676,6 +1680,34 @@ __global__ __launch_bounds__(256) void merge_row_kernel(MergeArgs a) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) hv[e] = (_Float16)merge_value(h4[e], Mh, Lh, c4[e], Mc, Lc);
     *(half4_t*)(a.out + ((lb * a.queries + q) * a.q_heads + h) * HD + d0) = hv;
+}
+
+// ------------------------------------------------ read-only HBM stream
+//
+// Attainable read bandwidth: every lane issues U 16-byte loads (grid-strided,
+// so a wave's load covers 1 KiB of consecutive bytes) before folding them.  A
+// wave writes its XOR fold (64 words, one per lane) only when it equals
+// kReadSinkMagic, so nothing is written in practice but the loads cannot be
+// elided.
+constexpr uint32_t kReadSinkMagic = 0xA5A5A5A5u;
+
+template <int U>
+__global__ __launch_bounds__(256) void read_stream_kernel(const uint4_t* p, uint64_t n16, uint32_t* sink) {
+    const uint64_t nth = (uint64_t)gridDim.x * 256u;
+    uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+    uint4_t acc = (uint4_t)0u;
+    for (; i + (uint64_t)(U - 1) * nth < n16; i += (uint64_t)U * nth) {
+        uint4_t v[U];
+#pragma unroll
+        for (int j = 0; j < U; ++j) v[j] = p[i + (uint64_t)j * nth];
+#pragma unroll
+        for (int j = 0; j < U; ++j) acc ^= v[j];
+    }
+    for (; i < n16; i += nth) acc ^= p[i];
+    uint32_t x = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x ^= (uint32_t)__shfl_xor((int)x, o);
+    if (x == kReadSinkMagic) sink[threadIdx.x & 63u] = x; // lane-indexed: a vector store
 }
 
 // ------------------------------------------------ codec check (bit-exact)

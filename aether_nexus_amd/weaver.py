@@ -202,6 +202,11 @@ class WeaverEngine:
         rc = self._lib.aw_decode_device(self._h, ctypes.byref(desc), _stream(stream))
         self._check(rc, "decode_device")
 
+    def read_stream(self, buf, nbytes: int, waves_per_cu: int, sink, stream: Optional[int] = None) -> None:
+        """Enqueue a read-only stream over ``nbytes`` of ``buf`` (attainable HBM read rate)."""
+        rc = self._lib.aw_debug_read_stream(self._h, _ptr(buf), nbytes, waves_per_cu, _ptr(sink), _stream(stream))
+        self._check(rc, "read_stream")
+
     def decode_device_noalloc(self, desc: DecodeDesc, stream: Optional[int] = None) -> None:
         """``decode_device`` with its scratch in the library's fixed per-GPU array
         (AW_NOALLOC_SCRATCH_BYTES): allocates nothing; larger requests raise."""

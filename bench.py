@@ -67,6 +67,10 @@ def parse():
     p.add_argument("--skip-encoder", action="store_true", help="skip the SparseCode encoder measurement")
     p.add_argument("--skip-fabric", action="store_true", help="skip the .aether fabric residency measurement")
     p.add_argument("--skip-attention", action="store_true", help="skip the inference-attention measurement")
+    p.add_argument("--configs", default="2,4,5",
+                   help="BASELINE configurations timed beside the sweep (comma list of 2, 4, 5; empty for none)")
+    p.add_argument("--only-configs", action="store_true",
+                   help="time only the --configs lines (no sweep, no other measurement) and print them")
     p.add_argument("--skip-alt-layout", action="store_true",
                    help="skip the extra B-max run with the other cold pool order (for clean profiles)")
     p.add_argument("--rocpd-summary", metavar="DB", help="print a per-kernel summary of a rocprofv3 database and exit")
@@ -233,6 +237,87 @@ def hbm_copy_peak(mib: int = 1024, reps: int = 10) -> dict:
     torch.cuda.empty_cache()
     return {"gbps": round(gbps, 1), "frac_of_nominal": round(gbps / PEAK_HBM_GBPS, 4),
             "copy": f"torch copy_ of {mib} MiB int32 on one device, read + write counted"}
+
+
+def hbm_read_peak(engine, mib: int = 2048, reps: int = 10) -> dict:
+    """The library's read-only stream kernel (aw_debug_read_stream: 16-byte loads,
+    8 in flight per lane, nothing written) over `mib` MiB, eight times the
+    Infinity Cache: bytes read per second at 8, 16 and 32 waves per CU, the best
+    beside the 8 TB/s nominal peak."""
+    import torch
+    nbytes = mib << 20
+    buf = torch.zeros(nbytes // 4, dtype=torch.int32, device="cuda:0")
+    sink = torch.zeros(64, dtype=torch.int32, device="cuda:0")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    rates = {}
+    for wpc in (8, 16, 32):
+        with torch.cuda.stream(s):
+            engine.read_stream(buf, nbytes, wpc, sink, stream=s.cuda_stream)
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(s)
+            for _ in range(reps):
+                engine.read_stream(buf, nbytes, wpc, sink, stream=s.cuda_stream)
+            b.record(s)
+        torch.cuda.synchronize()
+        rates[wpc] = nbytes * reps / (a.elapsed_time(b) * 1e-3) / 1e9
+    best = max(rates, key=rates.get)
+    del buf, sink
+    torch.cuda.empty_cache()
+    return {"gbps": round(rates[best], 1), "frac_of_nominal": round(rates[best] / PEAK_HBM_GBPS, 4),
+            "waves_per_cu": best, "by_waves_per_cu": {str(k): round(v, 1) for k, v in rates.items()},
+            "read": f"aw_debug_read_stream over {mib} MiB, {reps} passes, bytes read counted"}
+
+
+# BASELINE configurations timed beside the sweep (config 3 is the sweep at B = 1).
+CONFIGS = {
+    "2": "hot-only exact f16 decode, 32q/8kv heads, head_dim 128, hot 4096 tokens, no cold pool, B=1, "
+         "one query, scale 1/sqrt(128)",
+    "4": "batched hot+cold decode, B=64, hot 1024 f16 tokens + cold 131072 SparseCodes per kv head "
+         "(Zipf(1.1) atom indices), shared 4096x128 dictionary, 32q/8kv, head_dim 128",
+    "5": "speculative-verify decode over 32 layers, B=8 x 8 causal draft queries, hot 2048 + cold 65536 "
+         "per kv head, per-layer 4096x128 dictionary, 32q/8kv, head_dim 128",
+}
+
+
+def config_geom(key: str):
+    from aether_nexus_amd import workloads as W
+    return {"2": W.hot_only, "4": W.batched, "5": W.spec_verify}[key]()
+
+
+def config_line(engine, key: str, args) -> dict:
+    """One BASELINE configuration, timed like the sweep (HIP graph replay, pools
+    rotated past the Infinity Cache), with its dominant bandwidth-bound kernel."""
+    import torch
+    from dataclasses import replace
+    g0 = config_geom(key)
+    geom = replace(g0, copies=copies_for(g0))
+    hb = args.cold_layout == "head_blocked" and g0.cold_count > 0
+    r = Runner(engine, geom, args.seed, not args.no_graph, cold_head_blocked=hb)
+    ms = r.time_steps(args.steps, args.warmup)
+    ab = geom.algorithmic_bytes()["total"]
+    gbps = ab / (ms * 1e-3) / 1e9
+    stages = r.stage_times(args.steps, mode=1)
+    serial = r.stage_times(args.steps, mode=2)
+    kb = kernel_bytes(geom)
+    dom = max((k for k in ("hot", "cold") if serial[k][0]), key=lambda k: serial[k][0])
+    pipe, alone = stages[dom][0], serial[dom][0]
+    row = {"config": key, "workload": CONFIGS[key], "layers": geom.layers, "batch": geom.batch,
+           "queries": geom.queries, "tokens_per_step": geom.tokens, "ms_per_step": round(ms, 5),
+           "tokens_per_s": round(geom.tokens / (ms * 1e-3), 1), "alg_bytes_per_step": int(ab),
+           "achieved_gbps": round(gbps, 1), "frac_of_peak": round(gbps / PEAK_HBM_GBPS, 4),
+           "cold_layout": ("head_blocked" if hb else "reference") if g0.cold_count else None,
+           "copies": geom.copies,
+           "dominant_kernel": {"kernel": f"{dom}_kernel", "alg_bytes_per_launch": int(kb[dom]),
+                               "avg_launch_us": round(pipe * 1e3, 2),
+                               "frac": round(kb[dom] / (pipe * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
+                               "serialized_launch_us": round(alone * 1e3, 2),
+                               "serialized_frac": round(kb[dom] / (alone * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)},
+           "stages_us": {k: (round(v * 1e3, 2) if v else None) for k, (v, n) in stages.items()},
+           "stages_serial_us": {k: (round(v * 1e3, 2) if v else None) for k, (v, n) in serial.items()}}
+    del r
+    torch.cuda.empty_cache()
+    return row
 
 
 VALU_FP32_FMA_TFLOPS = 78.6  # 256 CUs x 128 fp32 FMA lanes x 2.4 GHz x 2 (no packed fp32 here)
@@ -659,6 +744,19 @@ def main():
     batches = [int(x) for x in args.batches.split(",") if x]
     engine = WeaverEngine()
     log(f"device: {engine.device_name()}")
+    config_keys = [k for k in args.configs.split(",") if k]
+    for k in config_keys:
+        if k not in CONFIGS:
+            print(f"unknown config {k} (choose from {', '.join(CONFIGS)})", file=sys.stderr)
+            return 2
+    if args.only_configs:
+        rows = []
+        for k in config_keys:
+            rows.append(config_line(engine, k, args))
+            log(json.dumps(rows[-1]))
+        engine.close()
+        print(json.dumps({"configs": rows}), flush=True)
+        return 0
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
     sweep = []
@@ -724,6 +822,8 @@ def main():
             tf = fl / (serial[k][0] * 1e-3) / 1e12
             mfma[k] = {"gflop": round(fl / 1e9, 3), "tflops": round(tf, 1), "frac": round(tf / MFMA_F16_TFLOPS, 4)}
     copy_peak = hbm_copy_peak()
+    read_peak = hbm_read_peak(engine)
+    log(json.dumps({"hbm_read_peak": read_peak}))
     # The same workload with the cold pool in the other order (by default the
     # reference's file order [blocks][16][kv_heads], where one kv head's code is
     # 16 bytes of every 128-byte token line): output bits must be identical.
@@ -749,6 +849,10 @@ def main():
         log(json.dumps({"other_cold_layout": alt}))
         del rh
         torch.cuda.empty_cache()
+    configs = []
+    for k in config_keys:
+        configs.append(config_line(engine, k, args))
+        log(json.dumps(configs[-1]))
     ref_cfg = reference_bench_config(engine, args.seed, 200)
     enc = None if args.skip_encoder else encoder_bench(engine, args.seed, 5, 8 if args.no_cpu else 32)
     if enc:
@@ -783,11 +887,14 @@ def main():
         "achieved_gbps": row["achieved_gbps"],
         "frac_of_peak": row["frac_of_peak"],
         "frac_of_copy_peak": round(row["achieved_gbps"] / copy_peak["gbps"], 4),
+        "frac_of_read_peak": round(row["achieved_gbps"] / read_peak["gbps"], 4),
         "sweep": sweep,
         "stages_us": stages_us,
         "stages_serial_us": serial_us,
         "roofline": roofline,
         "hbm_copy_peak": copy_peak,
+        "hbm_read_peak": read_peak,
+        "configs": configs,
         "mfma_kernels": mfma,
         "other_cold_layout": alt,
         "encoder": enc,

@@ -374,6 +374,17 @@ int aw_block_entropy_device(aw_engine* engine, const uint16_t* hot, uint64_t hot
                             uint32_t head_dim, const uint32_t* blocks, uint32_t n_blocks, float* entropy,
                             void* hip_stream);
 
+/* No reference counterpart: a read-only HBM stream, for measuring the
+ * attainable read bandwidth beside the 8 TB/s nominal peak (the decode's
+ * pools are only read).  Reads `bytes` (a multiple of 16) from the 16-byte
+ * aligned device buffer `buf` with 16-byte loads, 8 in flight per lane,
+ * `waves_per_cu` waves per CU (a multiple of 4, 4 .. 64), XOR-folding each
+ * wave's data into one word; a wave writes its word into `sink` (64 u32,
+ * device) only when it equals 0xA5A5A5A5, so the loads cannot be elided and
+ * the stream writes (almost) nothing.  Asynchronous on `hip_stream`. */
+int aw_debug_read_stream(aw_engine* engine, const void* buf, uint64_t bytes, uint32_t waves_per_cu,
+                         uint32_t* sink, void* hip_stream);
+
 /* Per-stage kernel timing with HIP events recorded on the stream each kernel
  * runs on: every launch is bracketed by a pair of events.  AW_PROFILE_ON keeps
  * the pipeline as it runs unprofiled (the hot kernel on the engine's side

@@ -226,3 +226,22 @@ def test_full_size_spec_verify(engine, stream):
     per-layer 4096 x 128 dictionary."""
     full_size(engine, stream, W.spec_verify(), 52, 64, "spec-verify L32 (sampled rows)")
     torch.cuda.empty_cache()
+
+
+def test_read_stream_reads_the_buffer(engine, stream):
+    """aw_debug_read_stream (the attainable-read-rate probe): a zero buffer leaves
+    the sink untouched; one word set to the sink value makes the wave that reads
+    it (lane 0 of wave 0: the first 16 bytes) write it to every sink word."""
+    nbytes = 64 << 20
+    buf = torch.zeros(nbytes // 4, dtype=torch.int32, device="cuda:0")
+    sink = torch.zeros(64, dtype=torch.int32, device="cuda:0")
+    engine.read_stream(buf, nbytes, 16, sink, stream=stream)
+    torch.cuda.synchronize()
+    assert int(sink.abs().sum()) == 0
+    magic = np.array([0xA5A5A5A5], dtype=np.uint32).view(np.int32)[0]
+    buf[0] = int(magic)
+    engine.read_stream(buf, nbytes, 16, sink, stream=stream)
+    torch.cuda.synchronize()
+    assert bool((sink == int(magic)).all())
+    with pytest.raises(WeaverError):
+        engine.read_stream(buf, nbytes - 8, 16, sink, stream=stream)  # not a multiple of 16 bytes
