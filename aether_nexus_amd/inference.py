@@ -19,13 +19,27 @@ and ``push_loom`` / ``pop_loom`` (:437-446):
 the agent loop (agent.rs:337-399): the target model runs [last_token] + drafts
 as one multi-query step (``attend`` with num_tokens = drafts + 1), and the
 drafts are kept while they match the target's samples.
+
+``WeaverKvCache`` is the same cache with the Weaver's two tiers
+(weaver_kernel.metal:118-240): the newest ``hot_window`` tokens stay exact f16 K
+and V rows in 16-token blocks, and whole blocks older than that are distilled
+into SparseCodes of a per-layer dictionary (``Distiller::distill_block``,
+distiller.rs:171-246, run by ``aw_encode_device``), so that ``attend`` is one
+hot+cold ``aw_decode_device`` per layer with q_latent = q . D^T computed on the
+device.  A SparseCode is the Weaver's one row per token and kv head, used as
+both key and value (the reference's pools hold one KV tensor,
+weaver_kernel.metal:162-166,206-219): the cold tier encodes the K rows, and a
+cold token's value is that same reconstruction.
 """
 from __future__ import annotations
 
+import math
 from typing import Callable, Optional, Sequence
 
 import numpy as np
 import torch
+
+from .weaver import make_desc, make_encode_desc
 
 MAX_SEQ_LEN = 4096  # InferenceEngine::MAX_SEQ_LEN (inference.rs:219)
 MAX_BATCH = 16  # InferenceEngine::MAX_BATCH (inference.rs:221): tokens per forward_batch
@@ -100,6 +114,212 @@ class KvCache:
         """inference.rs:443-446: tokens after saved_position are overwritten later."""
         if not 0 <= saved_position <= self.max_seq_len:
             raise KvCacheError(f"position {saved_position} outside the cache")
+        self.position = saved_position
+
+
+class WeaverKvCache:
+    """One sequence's per-layer KV cache in the Weaver's two tiers, on one device.
+
+    Tokens [0, cold_tokens) are cold: whole 16-token blocks of SparseCodes
+    ``[cold_capacity][kv_heads][16]`` (head-blocked device order) per layer.
+    Tokens [cold_tokens, position) are hot: exact f16 K and V rows in a ring of
+    16-token blocks ``[hot_capacity][16][kv_heads][head_dim]`` per layer.  One
+    block table serves every layer: hot refs (oldest block first) then cold refs.
+
+    ``distill(engine)`` moves the oldest whole hot blocks beyond ``hot_window``
+    tokens into the cold tier (the Distiller pass, distiller.rs:60-120, with the
+    blocks chosen by age instead of the entropy proxy).  ``pop_loom`` may roll
+    back into the hot tier only: distilled tokens are final.
+
+    ``dictionaries``: f16 ``[layers][dict_heads][dict_size][head_dim]`` on the
+    device, dict_heads 1 (shared) or kv_heads (the reference's per-kv-head
+    dictionary, fabric.rs:159-166)."""
+
+    def __init__(self, layers: int, kv_heads: int, head_dim: int, dictionaries: torch.Tensor,
+                 hot_window: int = 2048, max_seq_len: int = 65536, max_batch: int = MAX_BATCH, device="cuda:0"):
+        if layers < 1 or kv_heads < 1 or head_dim < 1 or max_batch < 1 or hot_window < BLOCK_TOKENS:
+            raise KvCacheError("layers, kv_heads, head_dim, max_batch >= 1 and hot_window >= 16 required")
+        if dictionaries.dim() != 4 or dictionaries.shape[0] != layers or dictionaries.shape[3] != head_dim or \
+                dictionaries.shape[1] not in (1, kv_heads) or dictionaries.dtype != torch.float16:
+            raise KvCacheError("dictionaries must be f16 [layers][1 or kv_heads][dict_size][head_dim]")
+        self.layers, self.kv_heads, self.head_dim = layers, kv_heads, head_dim
+        self.dict_heads, self.dict_size = int(dictionaries.shape[1]), int(dictionaries.shape[2])
+        self.dictionaries = dictionaries.contiguous()
+        self.hot_window, self.max_seq_len, self.max_batch = hot_window, max_seq_len, max_batch
+        self.device = device
+        # After distill the hot tier holds at most hot_window + 15 tokens (whole
+        # blocks leave); a forward batch comes on top.
+        self.hot_capacity = -(-(hot_window + BLOCK_TOKENS - 1 + max_batch) // BLOCK_TOKENS)
+        self.cold_capacity = max(1, -(-max_seq_len // BLOCK_TOKENS))
+        hshape = (self.hot_capacity, BLOCK_TOKENS, kv_heads, head_dim)
+        self.k = [torch.zeros(hshape, dtype=torch.float16, device=device) for _ in range(layers)]
+        self.v = [torch.zeros(hshape, dtype=torch.float16, device=device) for _ in range(layers)]
+        cshape = (self.cold_capacity, kv_heads, BLOCK_TOKENS, 8)  # 8 int16 words = one 16-byte code
+        self.cold = [torch.zeros(cshape, dtype=torch.int16, device=device) for _ in range(layers)]
+        self.position = 0
+        self.cold_blocks = 0   # cold tokens = 16 * cold_blocks
+        self.hot_first = 0     # ring slot of the oldest hot block
+        self._refs = torch.zeros(self.hot_capacity + self.cold_capacity, dtype=torch.int32, device=device)
+        self._refs_key = None
+
+    # -- bookkeeping
+    @property
+    def cold_tokens(self) -> int:
+        return self.cold_blocks * BLOCK_TOKENS
+
+    def hot_tokens(self, end: Optional[int] = None) -> int:
+        return (self.position if end is None else end) - self.cold_tokens
+
+    def check_batch(self, num_tokens: int) -> None:
+        """forward_batch's guards (inference.rs:462-475)."""
+        if num_tokens == 0 or num_tokens > self.max_batch:
+            raise KvCacheError(f"Batch size {num_tokens} unsupported (max {self.max_batch})")
+        if self.position + num_tokens > self.max_seq_len:
+            raise KvCacheError(f"KV cache exhausted: position {self.position} + {num_tokens} >= MAX_SEQ_LEN "
+                               f"{self.max_seq_len}.")
+        if self.hot_tokens() + num_tokens > self.hot_capacity * BLOCK_TOKENS:
+            raise KvCacheError("hot tier full: distill before appending more tokens")
+
+    def _slot(self, hot_token: int) -> tuple[int, int]:
+        return (self.hot_first + hot_token // BLOCK_TOKENS) % self.hot_capacity, hot_token % BLOCK_TOKENS
+
+    def _write(self, layer: int, k: torch.Tensor, v: torch.Tensor) -> None:
+        t, n = self.hot_tokens(), k.shape[0]
+        i = 0
+        while i < n:  # block by block (the ring may wrap)
+            slot, off = self._slot(t + i)
+            m = min(BLOCK_TOKENS - off, n - i)
+            self.k[layer][slot, off:off + m].copy_(k[i:i + m])
+            self.v[layer][slot, off:off + m].copy_(v[i:i + m])
+            i += m
+
+    def refs(self, hot_blocks: int) -> torch.Tensor:
+        """The block table: hot ring slots oldest first, then cold blocks 0 ..
+        (rebuilt only when the tiers change)."""
+        key = (self.hot_first, hot_blocks, self.cold_blocks)
+        if key != self._refs_key:
+            hot = (self.hot_first + np.arange(hot_blocks)) % self.hot_capacity
+            table = np.concatenate([hot, np.arange(self.cold_blocks)]).astype(np.int32)
+            self._refs[:table.size].copy_(torch.from_numpy(table))
+            self._refs_key = key
+        return self._refs
+
+    # -- the decode loop's calls
+    def append(self, layer: int, k: torch.Tensor, v: torch.Tensor) -> None:
+        """Write the new tokens' K and V rows [num_tokens][kv_heads][head_dim] at the
+        current position of `layer` (inference.rs:547-550), into the hot tier."""
+        n = k.shape[0]
+        self.check_batch(n)
+        if tuple(k.shape) != (n, self.kv_heads, self.head_dim) or tuple(v.shape) != tuple(k.shape):
+            raise KvCacheError(f"k and v must be [{n}][{self.kv_heads}][{self.head_dim}]")
+        self._write(layer, k, v)
+
+    def attend(self, engine, layer: int, q: torch.Tensor, out: torch.Tensor, stream: Optional[int] = None) -> None:
+        """Causal GQA attention of the new tokens (cache positions position ..
+        position + num_tokens - 1, appended first) over both tiers of `layer`:
+        one aw_decode_device with scale 1/sqrt(head_dim) (ops.metal:557) and
+        q_latent computed on the device; query i sees every cold token and hot
+        tokens up to its own position (ops.metal:549)."""
+        n, q_heads, head_dim = q.shape
+        self.check_batch(n)
+        if head_dim != self.head_dim or q_heads % self.kv_heads or tuple(out.shape) != tuple(q.shape):
+            raise KvCacheError("q and out must be [num_tokens][q_heads][head_dim], q_heads a multiple of kv_heads")
+        hot_tok = self.hot_tokens(self.position + n)
+        hot_blocks = -(-hot_tok // BLOCK_TOKENS)
+        refs = self.refs(hot_blocks)
+        desc = make_desc(layers=1, batch=1, queries=n, q_heads=q_heads, kv_heads=self.kv_heads, head_dim=head_dim,
+                         dict_size=self.dict_size, dict_heads=self.dict_heads, hot_count=hot_blocks,
+                         cold_count=self.cold_blocks, refs_stride=max(hot_blocks + self.cold_blocks, 1),
+                         hot_blocks=self.hot_capacity, cold_blocks=self.cold_capacity, q=q, out=out,
+                         hot_k=self.k[layer], hot_v=self.v[layer], cold=self.cold[layer] if self.cold_blocks else None,
+                         refs=refs, dictionary=self.dictionaries[layer] if self.cold_blocks else None,
+                         scale=1.0 / math.sqrt(head_dim), causal=True, cold_head_blocked=True,
+                         hot_tokens=hot_tok)
+        engine.decode_device(desc, stream=stream)
+
+    def advance(self, num_tokens: int) -> None:
+        """The position after a forward pass of num_tokens tokens (inference.rs:631)."""
+        self.check_batch(num_tokens)
+        self.position += num_tokens
+
+    def distill(self, engine, stream: Optional[int] = None) -> int:
+        """Encode the oldest whole hot blocks beyond the hot window into the cold
+        tier of every layer (aw_encode_device: top-4 atoms of the layer's
+        dictionary by dot product, coefficient f16(dot), distiller.rs:171-246),
+        and drop them from the hot ring.  Returns the number of blocks moved."""
+        over = self.hot_tokens() - self.hot_window
+        n = over // BLOCK_TOKENS if over > 0 else 0
+        if n == 0:
+            return 0
+        if self.cold_blocks + n > self.cold_capacity:
+            raise KvCacheError("cold tier full")
+        src = torch.tensor([(self.hot_first + i) % self.hot_capacity for i in range(n)], dtype=torch.int32,
+                           device=self.device)
+        dst = torch.arange(self.cold_blocks, self.cold_blocks + n, dtype=torch.int32, device=self.device)
+        for layer in range(self.layers):
+            desc = make_encode_desc(kv_heads=self.kv_heads, head_dim=self.head_dim, dict_size=self.dict_size,
+                                    dict_heads=self.dict_heads, hot_blocks=self.hot_capacity,
+                                    cold_blocks=self.cold_capacity, hot=self.k[layer],
+                                    dictionary=self.dictionaries[layer], src_blocks=src, dst_blocks=dst,
+                                    cold=self.cold[layer], cold_head_blocked=True)
+            engine.encode_device(desc, stream=stream)
+        self.cold_blocks += n
+        self.hot_first = (self.hot_first + n) % self.hot_capacity
+        return n
+
+    def extend(self, engine, ks, vs, stream: Optional[int] = None) -> None:
+        """Load a prompt of many tokens (per-layer [n][kv_heads][head_dim] rows) at
+        the current position, distilling as the hot tier fills.  Into an empty hot
+        tier, the whole blocks that would leave the window at once are encoded
+        straight from the prompt rows (read as a [n/16][16][kv_heads][head_dim]
+        pool), without passing through the hot ring."""
+        n = ks[0].shape[0]
+        i = 0
+        if self.hot_tokens() == 0 and n > self.hot_window:
+            nb = (n - self.hot_window) // BLOCK_TOKENS
+            if self.cold_blocks + nb > self.cold_capacity or self.position + n > self.max_seq_len:
+                raise KvCacheError("prompt longer than the cache")
+            src = torch.arange(nb, dtype=torch.int32, device=self.device)
+            dst = torch.arange(self.cold_blocks, self.cold_blocks + nb, dtype=torch.int32, device=self.device)
+            for layer in range(self.layers):
+                rows = ks[layer][:nb * BLOCK_TOKENS]
+                if not rows.is_contiguous():  # read in place by the asynchronous encoder
+                    raise KvCacheError("prompt rows must be contiguous [n][kv_heads][head_dim]")
+                desc = make_encode_desc(kv_heads=self.kv_heads, head_dim=self.head_dim, dict_size=self.dict_size,
+                                        dict_heads=self.dict_heads, hot_blocks=nb, cold_blocks=self.cold_capacity,
+                                        hot=rows, dictionary=self.dictionaries[layer], src_blocks=src,
+                                        dst_blocks=dst, cold=self.cold[layer], cold_head_blocked=True)
+                engine.encode_device(desc, stream=stream)
+            self.cold_blocks += nb
+            self.position += nb * BLOCK_TOKENS
+            i = nb * BLOCK_TOKENS
+        while i < n:
+            if self.position + 1 > self.max_seq_len:
+                raise KvCacheError("prompt longer than the cache")
+            room = self.hot_capacity * BLOCK_TOKENS - self.hot_tokens()
+            m = min(room, n - i)
+            if m <= 0:
+                raise KvCacheError("hot window too small to make room")
+            for layer in range(self.layers):
+                self._write(layer, ks[layer][i:i + m], vs[layer][i:i + m])
+            self.position += m
+            i += m
+            self.distill(engine, stream)
+
+    def reset(self) -> None:
+        """inference.rs:637-639: the next token starts a new sequence."""
+        self.position = self.cold_blocks = self.hot_first = 0
+        self._refs_key = None
+
+    def push_loom(self) -> int:
+        """inference.rs:437-439."""
+        return self.position
+
+    def pop_loom(self, saved_position: int) -> None:
+        """inference.rs:443-446, within the hot tier (distilled tokens are final)."""
+        if not self.cold_tokens <= saved_position <= self.position:
+            raise KvCacheError(f"position {saved_position} outside the hot tier "
+                               f"[{self.cold_tokens}, {self.position}]")
         self.position = saved_position
 
 

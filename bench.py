@@ -436,6 +436,7 @@ def attention_bench(engine, seed, reps, cpu_seconds):
                      "alg_bytes_per_forward": alg, "achieved_gbps": round(gbps, 1),
                      "frac_of_peak": round(gbps / PEAK_HBM_GBPS, 4)}
         del graph
+    res["tiered"] = tiered_attention_bench(engine, seed, reps)
     # CPU: the oracle's fp32 restatement of the same attention (a hot pool of
     # 16-token blocks, identity block table, causal) on one layer of the decode step.
     from oracle import oracle
@@ -457,6 +458,72 @@ def attention_bench(engine, seed, reps, cpu_seconds):
                            "sample": f"{n} single-layer decode attentions ({kv_len} cached tokens) through the "
                                      f"oracle's fp32 restatement in {el:.1f} s, {threads} threads"}
     res["gpu_forwards_per_s"] = round(1e3 / res["decode"]["ms_per_forward"], 1)
+    return res
+
+
+def tiered_attention_bench(engine, seed, reps, layers=32, hot=2048, cold=32768):
+    """The same forward's attention over WeaverKvCache: per layer a hot window of
+    2048 exact K and V tokens plus 32768 cold tokens distilled into SparseCodes of
+    the layer's 512-atom per-kv-head dictionaries (the reference's Llama8B
+    geometry), one hot+cold aw_decode_device per layer with q_latent computed on
+    the device, the 32 layers captured in a HIP graph.  Algorithmic bytes per
+    layer: hot K and V rows, cold codes, the dictionary, block refs, q and out."""
+    import torch
+    from aether_nexus_amd.inference import WeaverKvCache
+    hq, hkv, hd, atoms = 32, 8, 128, 512
+    g = torch.Generator(device="cuda:0").manual_seed(seed + 1)
+    dd = torch.randn((layers, hkv, atoms, hd), generator=g, device="cuda:0", dtype=torch.float32)
+    dicts = (dd / dd.norm(dim=-1, keepdim=True)).to(torch.float16)
+    n = hot + cold
+    cache = WeaverKvCache(layers, hkv, hd, dicts, hot_window=hot, max_seq_len=n + 64)
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):  # a prompt of n tokens per layer (K rows reused as V rows)
+        ks = [torch.randn((n, hkv, hd), generator=g, device="cuda:0").to(torch.float16) for _ in range(layers)]
+        cache.extend(engine, ks, ks, stream=st.cuda_stream)
+    torch.cuda.synchronize()
+    del ks
+    res = {"workload": f"{layers} layers x Weaver attention over a hot window of {hot} f16 K/V tokens + {cold} "
+                       f"cold SparseCodes per kv head ({atoms}-atom per-kv-head dictionaries), {hq}q/{hkv}kv "
+                       f"heads, head_dim {hd}",
+           "cold_tokens": cache.cold_tokens, "hot_tokens": cache.hot_tokens()}
+    p0 = cache.position
+    for name, nq in (("decode", 1), ("verify_3_drafts", 4)):
+        q = torch.randn((nq, hq, hd), generator=g, device="cuda:0").to(torch.float16)
+        rows = torch.randn((nq, hkv, hd), generator=g, device="cuda:0").to(torch.float16)
+        outs = [torch.empty((nq, hq, hd), dtype=torch.float16, device="cuda:0") for _ in range(layers)]
+        with torch.cuda.stream(st):
+            for l in range(layers):
+                cache.append(l, rows, rows)
+
+            def forward(s):
+                for l in range(layers):
+                    cache.attend(engine, l, q, outs[l], stream=s)
+            forward(st.cuda_stream)  # sizes the workspace and the block table before capture
+            engine.check_device_errors(st.cuda_stream)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=st):
+                forward(torch.cuda.current_stream().cuda_stream)
+            for _ in range(3):
+                graph.replay()
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+            ev[0].record(st)
+            for _ in range(reps):
+                graph.replay()
+            ev[1].record(st)
+        torch.cuda.synchronize()
+        ms = ev[0].elapsed_time(ev[1]) / reps
+        n_hot = hot + nq
+        alg = layers * (n_hot * hkv * hd * 2 * 2 + cold * hkv * 16 + hkv * atoms * hd * 2
+                        + (-(-n_hot // 16) + cold // 16) * 4 + 2 * nq * hq * hd * 2)
+        gbps = alg / (ms * 1e-3) / 1e9
+        res[name] = {"new_tokens": nq, "ms_per_forward": round(ms, 4), "us_per_layer": round(ms * 1e3 / layers, 2),
+                     "alg_bytes_per_forward": alg, "achieved_gbps": round(gbps, 1),
+                     "frac_of_peak": round(gbps / PEAK_HBM_GBPS, 4)}
+        cache.pop_loom(p0)
+        del graph
+    del cache
+    torch.cuda.empty_cache()
     return res
 
 

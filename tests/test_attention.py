@@ -150,3 +150,70 @@ def test_kv_cache_bookkeeping():
         c.pop_loom(41)
     c.reset()
     assert c.position == 0
+
+
+class _RecordingEngine:
+    """Stands in for WeaverEngine on the CPU: records the requests it is handed."""
+
+    def __init__(self):
+        self.encodes, self.decodes = [], []
+
+    def encode_device(self, desc, stream=None):
+        self.encodes.append((desc.n_blocks, desc.hot_blocks, desc.flags))
+
+    def decode_device(self, desc, stream=None):
+        self.decodes.append({f: getattr(desc, f) for f in ("queries", "hot_count", "cold_count", "refs_stride",
+                                                            "hot_tokens", "flags", "hot_blocks", "cold_blocks")})
+
+
+def test_weaver_kv_cache_tiers():
+    """WeaverKvCache's host logic: the prompt's old blocks go straight to the
+    cold tier, the hot ring keeps the window, distill moves whole blocks by age,
+    the block table lists hot ring slots oldest first then cold blocks, and
+    rollback stays inside the hot tier."""
+    from aether_nexus_amd.types import AW_F_CAUSAL, AW_F_COLD_HEAD_BLOCKED
+    layers, hkv, d, win = 2, 2, 8, 32
+    dicts = torch.zeros((layers, 1, 64, d), dtype=torch.float16)
+    c = I.WeaverKvCache(layers, hkv, d, dicts, hot_window=win, max_seq_len=400, max_batch=4, device="cpu")
+    assert c.hot_capacity == -(-(win + 15 + 4) // 16) and c.cold_capacity == 25
+    eng = _RecordingEngine()
+    n = 100
+    ks = [torch.arange(n * hkv * d, dtype=torch.float32).reshape(n, hkv, d).to(torch.float16) + l for l in range(2)]
+    vs = [-x for x in ks]
+    c.extend(eng, ks, vs)
+    # (100 - 32) // 16 = 4 blocks encoded from the prompt rows; 36 tokens stay hot.
+    assert (c.position, c.cold_blocks, c.hot_tokens()) == (100, 4, 36)
+    assert eng.encodes == [(4, 4, AW_F_COLD_HEAD_BLOCKED)] * layers
+    assert torch.equal(c.k[1][0], ks[1][64:80]) and torch.equal(c.v[0][2, :4], vs[0][96:100])
+    # A verify step of 4 tokens: queries see both tiers, the new tokens last in the hot tier.
+    q = torch.zeros((4, 4, d), dtype=torch.float16)
+    for layer in range(layers):
+        c.append(layer, ks[layer][:4], vs[layer][:4])
+        c.attend(eng, layer, q, torch.empty_like(q))
+    got = eng.decodes[-1]
+    assert got == {"queries": 4, "hot_count": 3, "cold_count": 4, "refs_stride": 7, "hot_tokens": 40,
+                   "flags": AW_F_CAUSAL | AW_F_COLD_HEAD_BLOCKED, "hot_blocks": c.hot_capacity,
+                   "cold_blocks": c.cold_capacity}
+    assert c.refs(3)[:7].tolist() == [0, 1, 2, 0, 1, 2, 3]
+    saved = c.push_loom()
+    c.advance(4)
+    c.pop_loom(saved + 1)  # one draft kept
+    assert c.position == 101
+    # Distill by age: 101 - 64 = 37 hot tokens, nothing leaves (a block leaves at 48);
+    # 12 more make 49 -> the oldest hot block leaves.
+    assert c.distill(eng) == 0
+    for _ in range(3):
+        for layer in range(layers):
+            c.append(layer, ks[layer][:4], vs[layer][:4])
+        c.advance(4)
+    assert c.distill(eng) == 1 and (c.cold_blocks, c.hot_first, c.hot_tokens()) == (5, 1, 33)
+    assert eng.encodes[-1] == (1, c.hot_capacity, AW_F_COLD_HEAD_BLOCKED)
+    assert c.refs(2)[:7].tolist() == [1, 2, 0, 1, 2, 3, 4]
+    with pytest.raises(I.KvCacheError, match="hot tier"):
+        c.pop_loom(79)  # inside the cold tier now
+    with pytest.raises(I.KvCacheError, match="Batch size 5"):
+        c.check_batch(5)
+    with pytest.raises(I.KvCacheError):
+        I.WeaverKvCache(layers, hkv, d, dicts[:1], hot_window=win, device="cpu")
+    c.reset()
+    assert (c.position, c.cold_blocks, c.hot_first) == (0, 0, 0)

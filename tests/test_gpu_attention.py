@@ -182,3 +182,88 @@ def test_multihead_attention_random_shapes(engine, stream, seed):
     engine.check_device_errors(stream)
     ref = AO.multihead_attention_f64(q, k[:kv_len], v[:kv_len], kv_len, nq)
     assert_close(out.float().cpu().numpy(), ref, (seed, nq, kv_len))
+
+
+def decompress_cold(cold_hb, dictionary):
+    """Cold rows in f64 from the head-blocked pool [blocks][kv_heads][16][8 words]
+    and dictionaries [dict_heads][A][d]: row (block*16 + t, g) = sum_k c_k D_g[idx_k]."""
+    w = cold_hb.cpu().numpy().view(np.uint16)
+    nb, hkv = w.shape[0], w.shape[1]
+    idx = w[..., :4].astype(np.int64)                                  # [nb][hkv][16][4]
+    coef = w[..., 4:].copy().view(np.float16).astype(np.float64)       # [nb][hkv][16][4]
+    dic = dictionary.cpu().numpy().astype(np.float64)                   # [dh][A][d]
+    rows = np.zeros((nb, 16, hkv, dic.shape[-1]))
+    for g in range(hkv):
+        dg = dic[g if dic.shape[0] > 1 else 0]
+        rows[:, :, g, :] = np.einsum("btk,btkd->btd", coef[:, g], dg[idx[:, g]])
+    return rows.reshape(nb * 16, hkv, -1)
+
+
+def hot_rows(cache, layer, n_hot):
+    """The hot tier's K and V rows in token order, from the block ring."""
+    ks, vs = [], []
+    for i in range(-(-n_hot // 16)):
+        slot = (cache.hot_first + i) % cache.hot_capacity
+        ks.append(cache.k[layer][slot])
+        vs.append(cache.v[layer][slot])
+    k = torch.cat(ks)[:n_hot].float().cpu().numpy()
+    v = torch.cat(vs)[:n_hot].float().cpu().numpy()
+    return k, v
+
+
+def test_weaver_kv_cache_verify_step(engine, stream):
+    """WeaverKvCache at Llama-3.1-8B heads over 2 layers with the reference's
+    512-atom per-kv-head dictionaries: a 34816-token prompt leaves 2048 hot and
+    32768 cold tokens (distilled by aw_encode_device); a verify step of
+    last_token + 3 drafts then runs one hot+cold aw_decode_device per layer.  Each
+    layer's rows match the fp64 brute force over [decompressed cold rows; hot K/V
+    rows] (decode_f64's math on the same pools: a cold token is sum_k c_k D[idx_k]
+    as key and value), every row equals a one-query step, and a kept draft rolls
+    the position back."""
+    hq, hkv, d, layers, A, n = 32, 8, 128, 2, 512, 34816
+    gen = torch.Generator(device="cuda:0")
+    gen.manual_seed(44)
+    dd = torch.randn((layers, hkv, A, d), generator=gen, device="cuda:0", dtype=torch.float64)
+    dicts = (dd / dd.norm(dim=-1, keepdim=True)).to(torch.float16)
+    cache = I.WeaverKvCache(layers, hkv, d, dicts, hot_window=2048, max_seq_len=40000)
+    ks = [torch.randn((n, hkv, d), generator=gen, device="cuda:0").to(torch.float16) for _ in range(layers)]
+    vs = [torch.randn((n, hkv, d), generator=gen, device="cuda:0").to(torch.float16) for _ in range(layers)]
+    print("weaver cache: prompt of 34816 tokens", flush=True)
+    cache.extend(engine, ks, vs, stream=stream)
+    engine.check_device_errors(stream)
+    assert (cache.cold_tokens, cache.hot_tokens()) == (32768, 2048)
+    p0, nv = cache.position, 4
+    q = torch.randn((nv, hq, d), generator=gen, device="cuda:0").to(torch.float16)
+    new_k = [torch.randn((nv, hkv, d), generator=gen, device="cuda:0").to(torch.float16) for _ in range(layers)]
+    new_v = [torch.randn((nv, hkv, d), generator=gen, device="cuda:0").to(torch.float16) for _ in range(layers)]
+    outs = []
+    for layer in range(layers):
+        cache.append(layer, new_k[layer], new_v[layer])
+        out = torch.full((nv, hq, d), float("nan"), dtype=torch.float16, device="cuda:0")
+        cache.attend(engine, layer, q, out, stream=stream)
+        outs.append(out)
+    engine.check_device_errors(stream)
+    qn = q.float().cpu().numpy()
+    for layer in range(layers):
+        cold = decompress_cold(cache.cold[layer][:cache.cold_blocks], dicts[layer])
+        hk, hv = hot_rows(cache, layer, 2048 + nv)
+        ref = AO.multihead_attention_f64(qn, np.concatenate([cold, hk]), np.concatenate([cold, hv]), p0 + nv, nv)
+        assert_close(outs[layer].float().cpu().numpy(), ref, ("tiered verify", layer))
+    cache.advance(nv)
+    for i in range(nv):  # one query at a time: token p0 + i is the newest
+        cache.pop_loom(p0)
+        if i:
+            cache.advance(i)
+        for layer in range(layers):
+            one = torch.empty((1, hq, d), dtype=torch.float16, device="cuda:0")
+            cache.attend(engine, layer, q[i:i + 1], one, stream=stream)
+            assert_close(one[0].float().cpu().numpy(), outs[layer][i].double().cpu().numpy(), ("tiered step", i))
+    cache.pop_loom(p0)
+    cache.advance(nv)
+    logits = np.zeros((nv, 10), np.float32)
+    logits[[0, 1, 2, 3], [6, 2, 9, 1]] = 1.0
+    new = I.accept_drafts([6, 3, 4], logits)
+    cache.pop_loom(I.rollback_position(cache.push_loom(), 3, len(new)))
+    assert cache.position == p0 + 2 and cache.cold_tokens == 32768
+    del ks, vs
+    torch.cuda.empty_cache()
