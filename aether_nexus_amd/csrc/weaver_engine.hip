@@ -89,6 +89,7 @@ struct Layout {
     uint32_t n_ar = 1;     // atom ranges of the finish
     uint32_t atoms_per_range = 0;
     uint32_t tiles_per_group = 0, rows_per_group = 0, n_groups = 0;
+    bool qf32 = false;     // q_latent computed on the device, kept in fp32
     size_t off_ql = 0, off_dt = 0, off_hm = 0, off_hl = 0, off_ho = 0;
     size_t off_cm = 0, off_cl = 0, off_ca = 0, off_cw = 0, off_ocp = 0;
 };
@@ -102,10 +103,10 @@ uint32_t dt_pitch(uint32_t A) { return A + 64; }
 uint32_t w_pitch(uint32_t A) { return A + 32; }
 
 // Largest cold row chunk (1, 2 or 4) whose LDS tables fit (with at least one
-// 1024-token split's block refs).
-uint32_t pick_rc(uint32_t R, uint32_t A, size_t max_lds) {
+// 1024-token split's block refs), for a q_latent table of qbytes per entry.
+uint32_t pick_rc(uint32_t R, uint32_t A, size_t max_lds, uint32_t qbytes) {
     uint32_t rc = R >= 4 ? 4 : (R >= 2 ? 2 : 1);
-    while (rc > 1 && aw::cold_smem_bytes(A, (int)rc, 1024) > max_lds) rc /= 2;
+    while (rc > 1 && aw::cold_smem_bytes(A, (int)rc, 1024, qbytes) > max_lds) rc /= 2;
     return rc;
 }
 
@@ -140,7 +141,7 @@ int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, const uint32_t 
         put_msg(msg, mlen, "refs_stride %u < hot_count + cold_count", d->refs_stride);
         return AW_E_INVALID_ARG;
     }
-    constexpr uint32_t kKnown = AW_F_CAUSAL | AW_F_COLD_HEAD_BLOCKED | AW_F_SEQ_HOT_TOKENS;
+    constexpr uint32_t kKnown = AW_F_CAUSAL | AW_F_COLD_HEAD_BLOCKED | AW_F_SEQ_HOT_TOKENS | AW_F_QLATENT_F32;
     if (d->flags & ~kKnown) {
         put_msg(msg, mlen, "unknown flags 0x%x", d->flags & ~kKnown);
         return AW_E_INVALID_ARG;
@@ -170,6 +171,11 @@ int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, const uint32_t 
     o = Layout{};
     o.info.rows_per_kv_head = R;
     o.info.computes_q_latent = (d->cold_count > 0 && d->q_latent == nullptr) ? 1u : 0u;
+    // Computed on the device, q_latent is rounded to f16 like the reference's
+    // buffer, or kept in fp32 on request (workspace and the cold kernel's LDS
+    // table): f16 rounding moves a score by up to 2^-11 of sum_k |c_k q_latent[idx_k]|.
+    o.qf32 = o.info.computes_q_latent != 0 && (d->flags & AW_F_QLATENT_F32) != 0;
+    const uint32_t qbytes = o.qf32 ? 4u : 2u;
 
     // Hot: one round of waves filling the resident capacity, splits <= kMaxSplits.
     if (d->hot_count > 0) {
@@ -198,10 +204,10 @@ int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, const uint32_t 
     // Cold: one work-group per CU at a time (LDS bound), one round of work-groups;
     // >= 1024 tokens per split.
     if (d->cold_count > 0) {
-        o.rc = pick_rc(R, A, max_lds);
-        if (aw::cold_smem_bytes(A, (int)o.rc, 1024) > max_lds) {
+        o.rc = pick_rc(R, A, max_lds, qbytes);
+        if (aw::cold_smem_bytes(A, (int)o.rc, 1024, qbytes) > max_lds) {
             put_msg(msg, mlen, "dict_size %u needs %zu bytes of LDS, device allows %zu", A,
-                    aw::cold_smem_bytes(A, (int)o.rc, 1024), max_lds);
+                    aw::cold_smem_bytes(A, (int)o.rc, 1024, qbytes), max_lds);
             return AW_E_UNSUPPORTED;
         }
         const uint64_t n_tok = (uint64_t)d->cold_count * kBlock;
@@ -222,7 +228,7 @@ int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, const uint32_t 
         uint64_t S = splits_for(o.rc);
         uint64_t tps = align_up(cdiv(n_tok, S), 16);
         // The split's block refs live in LDS too: shorten splits until they fit.
-        while (tps > 1024 && aw::cold_smem_bytes(A, (int)o.rc, (uint32_t)tps) > max_lds) {
+        while (tps > 1024 && aw::cold_smem_bytes(A, (int)o.rc, (uint32_t)tps, qbytes) > max_lds) {
             ++S;
             tps = align_up(cdiv(n_tok, S), 16);
         }
@@ -257,7 +263,7 @@ int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, const uint32_t 
         off = align_up(off + bytes, kAlign);
         return at;
     };
-    if (o.info.computes_q_latent) o.off_ql = take((uint64_t)d->layers * d->batch * d->queries * d->q_heads * A * 2);
+    if (o.info.computes_q_latent) o.off_ql = take((uint64_t)d->layers * d->batch * d->queries * d->q_heads * A * qbytes);
     if (d->cold_count > 0) o.off_dt = take((uint64_t)d->layers * d->dict_heads * dt_pitch(A) * HD * 2);
     if (o.info.hot_splits) {
         const uint64_t n = n_lbg * o.info.hot_splits * R;
@@ -416,7 +422,8 @@ int launch_project(aw_engine* e, const aw_decode_desc* d, const Layout& o, char*
     aw::ProjArgs a{};
     a.q = d->q;
     a.dict = d->dict;
-    a.ql = o.info.computes_q_latent ? (uint16_t*)(ws + o.off_ql) : nullptr;
+    a.ql = o.info.computes_q_latent && !o.qf32 ? (uint16_t*)(ws + o.off_ql) : nullptr;
+    a.qlf = o.qf32 ? (float*)(ws + o.off_ql) : nullptr;
     a.dt = (uint16_t*)(ws + o.off_dt);
     a.dt_pitch = dt_pitch(d->dict_size);
     a.batch = d->batch;
@@ -430,7 +437,7 @@ int launch_project(aw_engine* e, const aw_decode_desc* d, const Layout& o, char*
     a.rows_per_group = d->batch * d->queries * (d->dict_heads == 1 ? d->q_heads : a.gqa);
     a.dict_layer = (uint64_t)d->dict_heads * d->dict_size * HD;
     // Without q_latent to compute, one row block per atom block only writes D^T.
-    const uint32_t rows = a.ql ? a.rows_per_group : 1;
+    const uint32_t rows = (a.ql || a.qlf) ? a.rows_per_group : 1;
     const uint32_t gz = d->layers * d->dict_heads;
     const uint32_t A = d->dict_size;
     StageTimer t(e, AW_STAGE_PROJECT, st);
@@ -508,6 +515,19 @@ int launch_hot(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* ws,
 constexpr int kColdCPT = 2;
 constexpr int kColdPD = 4;
 
+// cold_kernel instance for a row chunk of 1, 2 or 4, a power-of-two dictionary
+// or not, and an f16 or fp32 q_latent table.
+const void* cold_kernel_fn(uint32_t rc, bool pow2, bool qf32) {
+#define AW_COLD(RCV) \
+    { {(const void*)aw::cold_kernel<RCV, kColdCPT, kColdPD, false, false>,  \
+       (const void*)aw::cold_kernel<RCV, kColdCPT, kColdPD, false, true>},  \
+      {(const void*)aw::cold_kernel<RCV, kColdCPT, kColdPD, true, false>,   \
+       (const void*)aw::cold_kernel<RCV, kColdCPT, kColdPD, true, true>} }
+    static const void* const table[3][2][2] = {AW_COLD(1), AW_COLD(2), AW_COLD(4)};
+#undef AW_COLD
+    return table[rc == 4 ? 2 : (rc == 2 ? 1 : 0)][pow2 ? 1 : 0][qf32 ? 1 : 0];
+}
+
 int launch_cold(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* ws, hipStream_t st) {
     aw::ColdArgs a{};
     const uint32_t HD = d->head_dim, A = d->dict_size, G = d->q_heads / d->kv_heads;
@@ -541,7 +561,9 @@ int launch_cold(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* ws
     a.s_head = head_blocked ? kBlock : 1u;
     a.refs_layer = (uint64_t)d->batch * d->refs_stride;
     // q_latent [L][B][Q][Hq][A], computed on the device or the caller's.
-    a.ql = o.info.computes_q_latent ? (const uint16_t*)(ws + o.off_ql) : d->q_latent;
+    a.ql = o.info.computes_q_latent ? nullptr : d->q_latent;
+    a.qlf = o.qf32 ? (const float*)(ws + o.off_ql) : nullptr;
+    if (o.info.computes_q_latent && !o.qf32) a.ql = (const uint16_t*)(ws + o.off_ql);
     a.s_lb = (uint64_t)d->queries * d->q_heads * A;
     a.s_g = (uint64_t)G * A;
     a.s_q = (uint64_t)d->q_heads * A;
@@ -551,36 +573,18 @@ int launch_cold(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* ws
     const uint64_t n_wg = (uint64_t)cdiv(a.n_units, 8) * 8 * d->kv_heads;
     if (n_wg > 0x7FFFFFFFull) return fail(e, AW_E_UNSUPPORTED, "cold grid too large");
     a.n_wg = (uint32_t)n_wg;
-    const size_t smem = aw::cold_smem_bytes(A, (int)o.rc, a.tokens_per_split);
+    const size_t smem = aw::cold_smem_bytes(A, (int)o.rc, a.tokens_per_split, o.qf32 ? 4u : 2u);
     const bool pow2 = (A & (A - 1u)) == 0u;
+    const void* fn = cold_kernel_fn(o.rc, pow2, o.qf32);
     // One resident round of work-groups (a multiple of 8: each keeps its XCD).
-    const void* fn = o.rc == 4 ? (pow2 ? (const void*)aw::cold_kernel<4, kColdCPT, kColdPD, true>
-                                       : (const void*)aw::cold_kernel<4, kColdCPT, kColdPD, false>)
-                   : o.rc == 2 ? (pow2 ? (const void*)aw::cold_kernel<2, kColdCPT, kColdPD, true>
-                                       : (const void*)aw::cold_kernel<2, kColdCPT, kColdPD, false>)
-                               : (pow2 ? (const void*)aw::cold_kernel<1, kColdCPT, kColdPD, true>
-                                       : (const void*)aw::cold_kernel<1, kColdCPT, kColdPD, false>);
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, aw::kColdThreads, smem) != hipSuccess || per_cu < 1)
         per_cu = 1;
     const uint64_t resident = std::max<uint64_t>(8, ((uint64_t)e->n_cu * per_cu) / 8 * 8);
     const uint64_t grid = std::min<uint64_t>(n_wg, resident);
     StageTimer t(e, AW_STAGE_COLD, st);
-#define AW_LAUNCH_COLD(RCV, P2)                                                                                    \
-    hipLaunchKernelGGL((aw::cold_kernel<RCV, kColdCPT, kColdPD, P2>), dim3((uint32_t)grid), dim3(aw::kColdThreads), \
-                       smem, st, a)
-    switch (o.rc) {
-    case 4:
-        if (pow2) AW_LAUNCH_COLD(4, true); else AW_LAUNCH_COLD(4, false);
-        break;
-    case 2:
-        if (pow2) AW_LAUNCH_COLD(2, true); else AW_LAUNCH_COLD(2, false);
-        break;
-    default:
-        if (pow2) AW_LAUNCH_COLD(1, true); else AW_LAUNCH_COLD(1, false);
-        break;
-    }
-#undef AW_LAUNCH_COLD
+    void* args[] = {&a};
+    AW_HIP(e, hipLaunchKernel(fn, dim3((uint32_t)grid), dim3(aw::kColdThreads), args, smem, st));
     AW_HIP(e, hipGetLastError());
     return AW_OK;
 }
@@ -926,7 +930,7 @@ int aw_engine_create(int device, aw_engine** out) {
     e->n_cu = (uint32_t)prop.multiProcessorCount;
     int rc = AW_OK;
     if (!rc) rc = check_kernel(e, aw::hot_kernel<128, 1, false>, "hot_kernel");
-    if (!rc) rc = check_kernel(e, aw::cold_kernel<4, kColdCPT, kColdPD, true>, "cold_kernel");
+    if (!rc) rc = check_kernel(e, aw::cold_kernel<4, kColdCPT, kColdPD, true, false>, "cold_kernel");
     if (!rc) rc = check_kernel(e, aw::finish_kernel<128, true>, "finish_kernel");
     if (rc) {
         delete e;
@@ -944,14 +948,11 @@ int aw_engine_create(int device, aw_engine** out) {
     }
     // Let the cold, finish and projection kernels use the device's full LDS.
     {
-        const void* fns[] = {(const void*)aw::cold_kernel<4, kColdCPT, kColdPD, true>,
-                             (const void*)aw::cold_kernel<4, kColdCPT, kColdPD, false>,
-                             (const void*)aw::cold_kernel<2, kColdCPT, kColdPD, true>,
-                             (const void*)aw::cold_kernel<2, kColdCPT, kColdPD, false>,
-                             (const void*)aw::cold_kernel<1, kColdCPT, kColdPD, true>,
-                             (const void*)aw::cold_kernel<1, kColdCPT, kColdPD, false>};
-        for (const void* f : fns)
-            (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)e->max_lds);
+        for (uint32_t rcv : {1u, 2u, 4u})
+            for (bool p2 : {false, true})
+                for (bool qf : {false, true})
+                    (void)hipFuncSetAttribute(cold_kernel_fn(rcv, p2, qf), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                              (int)e->max_lds);
         const void* fin[] = {(const void*)aw::finish_kernel<128, true>, (const void*)aw::finish_kernel<128, false>,
                              (const void*)aw::finish_kernel<64, true>, (const void*)aw::finish_kernel<64, false>};
         for (const void* f : fin)

@@ -106,7 +106,8 @@ __device__ inline void combine_splits(float m, float l, float& M, float& L, floa
 struct ProjArgs {
     const uint16_t* q;    // [L][B][Q][Hq][HD]
     const uint16_t* dict; // [L][dict_heads][A][HD]
-    uint16_t* ql;         // [L][B][Q][Hq][A] f16, or null: transpose only
+    uint16_t* ql;         // [L][B][Q][Hq][A] f16, or null
+    float* qlf;           // [L][B][Q][Hq][A] fp32, or null (both null: transpose only)
     uint16_t* dt;         // [L][dict_heads][HD][dt_pitch] f16: D^T for the finish
     uint32_t dt_pitch;    // A + padding: rows of D^T do not alias one L2 channel
     uint32_t batch, queries, q_heads, kv_heads, gqa, rows_r;
@@ -135,7 +136,8 @@ struct HotArgs {
 };
 
 struct ColdArgs {
-    const uint16_t* ql; // q_latent, addressed through the strides below
+    const uint16_t* ql;  // q_latent (f16), addressed through the strides below
+    const float* qlf;    // or q_latent in fp32 (computed on the device), same strides
     const uint4_t* cold;
     const uint32_t* refs;
     const uint32_t* seq_cold;
@@ -265,7 +267,8 @@ __global__ __launch_bounds__(kProjThreads) void project_kernel(ProjArgs a) {
 
     const int wr = wave / WA, wa = wave % WA;
     float4_t acc[MT][NT];
-    if (a.ql != nullptr) {
+    const bool want = a.ql != nullptr || a.qlf != nullptr;
+    if (want) {
         half8_t aop[NT][KS];
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt)
@@ -304,7 +307,18 @@ __global__ __launch_bounds__(kProjThreads) void project_kernel(ProjArgs a) {
             *(uint4_t*)(dt + (uint64_t)d * a.dt_pitch + at) = (uint4_t){w[0], w[1], w[2], w[3]};
         }
     }
-    if (a.ql != nullptr) {
+    if (a.qlf != nullptr) {
+        // fp32 rows straight from the accumulators: a lane holds atoms 4*lg .. +3
+        // of row li of each tile (16 contiguous bytes; A % 16 == 0).
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const uint32_t i = row0 + wr * (TR / WR) + mt * 16 + li;
+                const uint32_t at = atom0 + wa * (TA / WA) + nt * 16 + 4 * lg;
+                if (i < a.rows_per_group && at < A) *(float4_t*)(a.qlf + qrow_of(i) * A + at) = acc[mt][nt];
+            }
+    } else if (a.ql != nullptr) {
         constexpr int OP = TA + 8; // halves per staged output row
         __syncthreads(); // every wave is done with the staged q and dictionary
         _Float16* so = sq;
@@ -602,8 +616,9 @@ constexpr uint64_t kMagic2 = 0x4B4000004B400000ull;   // two magic patterns
 // takes tiles w, w + NW, w + 2*NW, ... (so the first NW tiles, the planning
 // sample, cover the split's first NT*CPT tokens).  The assignment is static, so
 // every float sum runs in the same order on every call.
-template <int RC, int CPT, int PD, bool POW2>
+template <int RC, int CPT, int PD, bool POW2, bool QF32>
 __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
+    using QT = std::conditional_t<QF32, float, _Float16>; // q_latent table element
     constexpr int NT = kColdThreads, NW = NT / 64, NP = (RC + 1) / 2;
     constexpr int NB = RC + 2;      // values of the end-of-split reductions
     constexpr int NR = 2 * RC + 2;  // LDS slots per wave: the plan's (max, sum) pairs and max|c|
@@ -639,10 +654,10 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
         return;
     }
 
-    const uint32_t qtab_bytes = (A * RC * 2 + 15) & ~15u;
+    const uint32_t qtab_bytes = (A * RC * (uint32_t)sizeof(QT) + 15) & ~15u;
     const uint32_t n_blk = (t_end - t_begin + 15) / 16; // t_begin is a multiple of 16
     const uint32_t n_wt = (t_end - t_begin + WT - 1) / WT;
-    _Float16* qtab = (_Float16*)smem;
+    QT* qtab = (QT*)smem;
     uint64_t* bins = (uint64_t*)(smem + qtab_bytes);       // [NP][A]: one plane per row pair
     uint32_t* sref = (uint32_t*)(bins + (uint64_t)A * NP); // [n_blk] physical blocks, ~0 = invalid
     float* red = (float*)(sref + ((n_blk + 3) & ~3u));    // [NW][NR]
@@ -708,8 +723,12 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const float cj = (float)coef(cw, j);
-            const _Float16* qp = qtab + ia[j] * RC;
-            if constexpr (RC == 4) {
+            const QT* qp = qtab + ia[j] * RC;
+            if constexpr (RC == 4 && QF32) {
+                const float4_t qv = *(const float4_t*)qp;
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) sc[rr] = fmaf(cj, qv[rr], sc[rr]);
+            } else if constexpr (RC == 4) {
                 const half4_t qv = *(const half4_t*)qp;
 #pragma unroll
                 for (int rr = 0; rr < 4; ++rr) sc[rr] = fmaf(cj, (float)qv[rr], sc[rr]);
@@ -762,13 +781,33 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
                             : 0;
     }
     // Atom-contiguous rows (s_a == 1, q_latent's layout) load as 16-byte pieces of
-    // 8 atoms per row, interleaved into [A][RC] in registers.
-    const bool qvec = a.s_a == 1 && (A % 8) == 0 && ((uintptr_t)a.ql & 15u) == 0;
+    // 8 f16 (or 4 fp32) atoms per row, interleaved into [A][RC] in registers.
+    const bool qvec = QF32 || (a.s_a == 1 && (A % 8) == 0 && ((uintptr_t)a.ql & 15u) == 0);
+    constexpr uint32_t QPA = QF32 ? 4u : 8u; // atoms per 16-byte piece
     uint4_t qw[RC];
     if (qvec) {
 #pragma unroll
-        for (int rr = 0; rr < RC; ++rr) qw[rr] = *(const uint4_t*)(a.ql + rbase[rr] + (uint64_t)min((uint32_t)tid, A / 8 - 1) * 8);
+        for (int rr = 0; rr < RC; ++rr) {
+            const uint64_t at = rbase[rr] + (uint64_t)min((uint32_t)tid, A / QPA - 1) * QPA;
+            qw[rr] = QF32 ? *(const uint4_t*)(a.qlf + at) : *(const uint4_t*)(a.ql + at);
+        }
     }
+    // fp32 table: piece a4 of every row (4 atoms) into [A][RC].
+    auto put_qf = [&](uint32_t a4, uint4_t (&w)[RC]) {
+        uint4_t v[RC];
+#pragma unroll
+        for (int rr = 0; rr < RC; ++rr) v[rr] = rok[rr] ? w[rr] : (uint4_t)0u;
+        if constexpr (RC == 4) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) *(uint4_t*)(qtab + (a4 * 4 + e) * 4) = (uint4_t){v[0][e], v[1][e], v[2][e], v[3][e]};
+        } else if constexpr (RC == 2) {
+            // atoms 4*a4 .. +3 x rows 0, 1: two 16-byte stores
+            *(uint4_t*)(qtab + a4 * 8) = (uint4_t){v[0].x, v[1].x, v[0].y, v[1].y};
+            *(uint4_t*)(qtab + a4 * 8 + 4) = (uint4_t){v[0].z, v[1].z, v[0].w, v[1].w};
+        } else {
+            *(uint4_t*)(qtab + a4 * 4) = v[0]; // one row: the piece as it is
+        }
+    };
     auto put_q = [&](uint32_t a8, uint4_t (&w)[RC]) {
 #pragma unroll
         for (int rr = 0; rr < RC; ++rr)
@@ -778,7 +817,9 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
             _Float16 hv[RC];
 #pragma unroll
             for (int rr = 0; rr < RC; ++rr) hv[rr] = __builtin_bit_cast(_Float16, (uint16_t)(w[rr][e / 2] >> (16 * (e % 2))));
-            if constexpr (RC == 4) {
+            if constexpr (QF32) {
+                (void)hv; // the f16 table only
+            } else if constexpr (RC == 4) {
                 half4_t v4 = {hv[0], hv[1], hv[2], hv[3]};
                 *(half4_t*)(qtab + (a8 * 8 + e) * 4) = v4;
             } else {
@@ -813,7 +854,15 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
     }
     // Tables into LDS: q_latent rows of this chunk (rows past R are zero) and the
     // split's block refs, resolved once so code addresses come from LDS.
-    if (qvec) {
+    if constexpr (QF32) {
+        if ((uint32_t)tid < A / 4) put_qf(tid, qw);
+        for (uint32_t a4 = tid + NT; a4 < A / 4; a4 += NT) {
+            uint4_t w[RC];
+#pragma unroll
+            for (int rr = 0; rr < RC; ++rr) w[rr] = *(const uint4_t*)(a.qlf + rbase[rr] + (uint64_t)a4 * 4);
+            put_qf(a4, w);
+        }
+    } else if (qvec) {
         if ((uint32_t)tid < A / 8) put_q(tid, qw);
         for (uint32_t a8 = tid + NT; a8 < A / 8; a8 += NT) {
             uint4_t w[RC];
@@ -1127,18 +1176,18 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
 // Persistent: work-group i takes work items i, i + gridDim.x, ... (gridDim.x a
 // multiple of 8, so each keeps its XCD), so the grid is one resident round and
 // the hot kernel can run beside it in the resources it leaves free.
-template <int RC, int CPT, int PD, bool POW2>
+template <int RC, int CPT, int PD, bool POW2, bool QF32>
 __global__ __launch_bounds__(kColdThreads) void cold_kernel(ColdArgs a) {
     for (uint32_t wg = blockIdx.x; wg < a.n_wg; wg += gridDim.x) {
-        cold_unit<RC, CPT, PD, POW2>(a, wg);
+        cold_unit<RC, CPT, PD, POW2, QF32>(a, wg);
         __syncthreads(); // the next item rewrites the LDS tables
     }
 }
 
-// Shared-memory bytes of cold_kernel<RC> for a dictionary of A atoms and
-// splits of `tokens_per_split` tokens.
-inline size_t cold_smem_bytes(uint32_t A, int RC, uint32_t tokens_per_split) {
-    const size_t qtab = ((size_t)A * RC * 2 + 15) & ~(size_t)15;
+// Shared-memory bytes of cold_kernel<RC> for a dictionary of A atoms, splits of
+// `tokens_per_split` tokens and a q_latent table of `qbytes` (2 or 4) per entry.
+inline size_t cold_smem_bytes(uint32_t A, int RC, uint32_t tokens_per_split, uint32_t qbytes) {
+    const size_t qtab = ((size_t)A * RC * qbytes + 15) & ~(size_t)15;
     const int NW = kColdThreads / 64, NP = (RC + 1) / 2;
     const size_t n_blk = ((size_t)(tokens_per_split + 15) / 16 + 3) & ~(size_t)3;
     return qtab + (size_t)A * NP * 8 + n_blk * 4 + (size_t)NW * (2 * RC + 2) * 4;

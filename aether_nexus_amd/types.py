@@ -174,6 +174,7 @@ AW_F_CAUSAL = 1
 AW_F_COLD_HEAD_BLOCKED = 2
 AW_F_ENCODE_FULL_SCAN = 4
 AW_F_SEQ_HOT_TOKENS = 8
+AW_F_QLATENT_F32 = 16
 AW_NOALLOC_SCRATCH_BYTES = 96 << 20  # scratch of aw_decode_device_noalloc
 
 AW_OK = 0

@@ -19,7 +19,7 @@ from typing import Any, Optional
 import numpy as np
 
 from . import _lib
-from .types import (AW_F_CAUSAL, AW_F_COLD_HEAD_BLOCKED, AW_F_ENCODE_FULL_SCAN, AW_F_SEQ_HOT_TOKENS,
+from .types import (AW_F_CAUSAL, AW_F_COLD_HEAD_BLOCKED, AW_F_ENCODE_FULL_SCAN, AW_F_SEQ_HOT_TOKENS, AW_F_QLATENT_F32,
                     SPARSE_CODE_DTYPE, STAGES, STRUCT_SIZES, DecodeDesc, EncodeDesc, PlanInfo, WeaverParams)
 
 
@@ -305,19 +305,20 @@ def make_desc(*, layers: int, batch: int, queries: int, q_heads: int, kv_heads: 
               hot_blocks: int, cold_blocks: int, q, out, hot_k=None, hot_v=None, cold=None, refs=None,
               dictionary=None, q_latent=None, seq_hot=None, seq_cold=None, scale: float = 1.0,
               causal: bool = False, cold_head_blocked: bool = False, hot_tokens: int = 0,
-              seq_hot_tokens: bool = False) -> DecodeDesc:
+              seq_hot_tokens: bool = False, q_latent_f32: bool = False) -> DecodeDesc:
     """Build an ``aw_decode_desc`` from device tensors (or raw device pointers).
     ``cold_head_blocked``: the cold pool is [L][blocks][kv_heads][16] instead of
     the reference's [L][blocks][16][kv_heads].  ``hot_tokens``: hot tokens per
     sequence when not whole blocks (0 = hot_count * 16); ``seq_hot_tokens``:
-    ``seq_hot`` counts tokens instead of blocks."""
+    ``seq_hot`` counts tokens instead of blocks; ``q_latent_f32``: a q_latent
+    computed on the device stays fp32 (AW_F_QLATENT_F32)."""
     d = DecodeDesc()
     d.layers, d.batch, d.queries = layers, batch, queries
     d.q_heads, d.kv_heads, d.head_dim = q_heads, kv_heads, head_dim
     d.dict_size, d.dict_heads = dict_size, dict_heads
     d.hot_count, d.cold_count, d.refs_stride = hot_count, cold_count, refs_stride
     d.flags = ((AW_F_CAUSAL if causal else 0) | (AW_F_COLD_HEAD_BLOCKED if cold_head_blocked else 0) |
-               (AW_F_SEQ_HOT_TOKENS if seq_hot_tokens else 0))
+               (AW_F_SEQ_HOT_TOKENS if seq_hot_tokens else 0) | (AW_F_QLATENT_F32 if q_latent_f32 else 0))
     d.scale = scale
     d.hot_tokens = hot_tokens
     d.hot_blocks, d.cold_blocks = hot_blocks, cold_blocks

@@ -251,10 +251,12 @@ def head_blocked(cold: torch.Tensor) -> torch.Tensor:
     return cold.permute(0, 1, 3, 2, 4).contiguous()
 
 
-def device_desc(wl: Workload, out: torch.Tensor, copy: int = 0, cold_head_blocked: Optional[torch.Tensor] = None):
+def device_desc(wl: Workload, out: torch.Tensor, copy: int = 0, cold_head_blocked: Optional[torch.Tensor] = None,
+                q_latent_f32: bool = False):
     """``aw_decode_desc`` for a workload whose tensors live on the GPU.
     ``cold_head_blocked``: the workload's cold pool reordered by head_blocked();
-    the descriptor then points at it and sets AW_F_COLD_HEAD_BLOCKED."""
+    the descriptor then points at it and sets AW_F_COLD_HEAD_BLOCKED.
+    ``q_latent_f32``: a q_latent computed on the device stays fp32."""
     from .weaver import make_desc
     g = wl.geom
     return make_desc(layers=g.layers, batch=g.batch, queries=g.queries, q_heads=g.q_heads, kv_heads=g.kv_heads,
@@ -264,4 +266,4 @@ def device_desc(wl: Workload, out: torch.Tensor, copy: int = 0, cold_head_blocke
                      cold=wl.cold if cold_head_blocked is None else cold_head_blocked,
                      refs=wl.refs[copy], dictionary=wl.dictionary, q_latent=wl.q_latent, seq_hot=wl.seq_hot,
                      seq_cold=wl.seq_cold, scale=g.scale, causal=g.causal,
-                     cold_head_blocked=cold_head_blocked is not None)
+                     cold_head_blocked=cold_head_blocked is not None, q_latent_f32=q_latent_f32)

@@ -95,13 +95,22 @@ typedef struct aw_weaver_params {
  * of blocks, so a sequence may end inside its last block (the reference's
  * contiguous KV cache, inference.rs:470-483).  Needs seq_hot. */
 #define AW_F_SEQ_HOT_TOKENS 8u
+/* aw_decode_desc: when q_latent is NULL (computed on the device), keep it in
+ * fp32 (workspace and the cold kernel's LDS table) instead of rounding it to
+ * f16 like the reference's q_latent buffer (weaver_kernel.metal:111).  A
+ * score moves by up to 2^-11 of sum_k |c_k q_latent[idx_k]| under f16
+ * rounding; peaked softmaxes (large coefficients, large q) amplify that past
+ * the 2e-3 tolerance.  Costs about a tenth of the cold kernel's time (16-byte
+ * table reads per term instead of 8).  Ignored when q_latent is given. */
+#define AW_F_QLATENT_F32 16u
 
 /* One decode call over L layers x B sequences x Q query tokens.  All pointers
  * are DEVICE pointers.  Element layouts (f16 = raw binary16 bits):
  *   q        [L][B][Q][q_heads][head_dim]
  *   q_latent [L][B][Q][q_heads][dict_size] or NULL (then q . D^T is computed
  *            on the device, fp32 accumulation, stored as f16 like the
- *            reference's q_latent buffer, weaver_kernel.metal:111)
+ *            reference's q_latent buffer, weaver_kernel.metal:111, or kept in
+ *            fp32 with AW_F_QLATENT_F32)
  *   hot_k    [L][hot_blocks][16][kv_heads][head_dim]
  *   hot_v    same as hot_k, or NULL: V is the K row (reference, metal:162-166)
  *   cold     [L][cold_blocks][16][kv_heads]   (16-byte aligned; with

@@ -9,12 +9,12 @@ MAX_ABS = 2e-3
 REL_L2 = 1e-3
 
 
-def run_gpu(engine, wl, stream, copy: int = 0):
+def run_gpu(engine, wl, stream, copy: int = 0, q_latent_f32: bool = False):
     import torch
     from aether_nexus_amd import workloads as W
     dev = wl.to("cuda:0")
     out = torch.full(dev.out_shape(), float("nan"), dtype=torch.float16, device="cuda:0")
-    engine.decode_device(W.device_desc(dev, out, copy=copy), stream=stream)
+    engine.decode_device(W.device_desc(dev, out, copy=copy, q_latent_f32=q_latent_f32), stream=stream)
     engine.check_device_errors(stream)
     return out.cpu().numpy()
 

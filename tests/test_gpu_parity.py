@@ -144,6 +144,42 @@ def test_cold_only_large_coefficients(engine, stream):
     assert_close(got, oracle.decode_f64(geom, a), "cold-only, coef std 6, f16 q_latent given")
 
 
+@pytest.mark.parametrize("hot_count,batch", [(0, 1), (8, 2)], ids=["cold_only", "hot_cold_b2"])
+def test_peaked_softmax_device_q_latent(engine, stream, hot_count, batch):
+    """The same peaked softmax (coefficient std 6, q std 2) with q_latent left
+    NULL, against the fp64 brute force, which never forms q_latent: computed on
+    the device and kept in fp32 (AW_F_QLATENT_F32), q_latent leaves every output within 2e-3 of the
+    exact value beyond the f16 output's own rounding, where an f16 q_latent
+    (the reference's buffer) moves the fp64 decode itself by more than 2e-3."""
+    geom = W.hot_cold(batch=batch, hot_count=hot_count, cold_count=256, coef_std=6.0, q_std=2.0)
+    wl = W.generate(geom, seed=13)
+    got = run_gpu(engine, wl, stream, q_latent_f32=True)
+    ref = oracle.decode_f64(geom, W.host_arrays(wl))
+    got64 = got.astype(np.float64)
+    # Outputs here reach [4, 8), where the f16 output's own half-ulp is 1.95e-3,
+    # about the whole 2e-3 bar: the bar applies to each element's error beyond
+    # that rounding.  Scores reach |s| ~ 25 (log2 units), so even fp32 rounding
+    # of q_latent moves them by ~1e-4; an f16 q_latent moves them 2^13 times more.
+    assert np.abs(ref).max() >= 4.0
+    half_ulp = np.spacing(np.abs(got).astype(np.float16)).astype(np.float64) / 2
+    excess = np.abs(got64 - ref) - half_ulp
+    rel = np.linalg.norm(got64 - ref) / np.linalg.norm(ref)
+    print(f"peaked, device q_latent, hot {hot_count}: max-abs {np.abs(got64 - ref).max():.2e}, beyond f16 "
+          f"rounding {excess.max():.2e}, rel-L2 {rel:.2e}", flush=True)
+    assert excess.max() <= 2e-3 and rel <= 1e-3
+    if hot_count:
+        return
+    # The f16 q_latent the reference would be handed misses by far more (CPU oracle, same inputs).
+    a = W.host_arrays(wl)
+    a["q_latent"] = oracle.qlatent_f64(geom, a).astype(np.float16).view(np.uint16)
+    err16 = np.abs(oracle.decode_f64(geom, a) - ref).max()
+    print(f"peaked: the same with an f16 q_latent (fp64 decode): max-abs {err16:.2e}", flush=True)
+    assert err16 > 2e-3 and excess.max() < err16
+    # The default (f16 q_latent, the reference's buffer) on the device: that same envelope.
+    dflt = run_gpu(engine, wl, stream).astype(np.float64)
+    assert np.abs(dflt - ref).max() > 2e-3 and np.abs(dflt - ref).max() < 2 * err16 + 2e-3
+
+
 def test_cold_many_tiles_small_coefficients(engine, stream):
     check(engine, stream, W.hot_cold(batch=2, hot_count=8, cold_count=2048, coef_std=0.05), seed=12,
           what="hot+cold, coef std 0.05")

@@ -294,6 +294,26 @@ def test_q_latent_identity():
     np.testing.assert_allclose(ql, np.einsum("hd,had->ha", q, D[np.arange(g.q_heads) // g.gqa]), rtol=1e-12)
 
 
+def test_f16_q_latent_envelope_on_a_peaked_softmax():
+    """Why device-computed q_latent stays fp32: with coefficient std 6 and q std
+    2 the reference's f16 q_latent buffer alone moves the fp64 decode past the
+    2e-3 tolerance (f16 rounding shifts each score by up to 2^-11 of
+    sum_k |c_k q_latent[idx_k]|, and a peaked softmax amplifies it), while an fp32
+    q_latent stays well inside it."""
+    geom = W.hot_cold(hot_count=0, cold_count=256, coef_std=6.0, q_std=2.0)
+    a = base_arrays(geom, seed=11)
+    exact = oracle.decode_f64(geom, a)
+    ql = oracle.qlatent_f64(geom, a)
+    b = dict(a)
+    b["q_latent"] = f16(ql).reshape(-1)
+    err16 = np.abs(oracle.decode_f64(geom, b) - exact).max()
+    assert err16 > 2e-3, err16
+    # fp32 rounding of q_latent: scores move by 2^-24 relative, 2^13 times less.
+    q32 = ql.astype(np.float32).astype(np.float64)
+    scale = geom.scale * (np.abs(q32).max() * 4 * 6.0 * 4)  # generous bound on |score| (coefficients within 4 std)
+    assert scale * 2.0 ** -24 < 1e-5
+
+
 def test_ref32_restatement_matches_f64():
     """The fp32 kernel-order restatement and the fp64 brute force agree to the
     accuracy of fp32 accumulation and f16 rounding of q_latent and outputs."""
