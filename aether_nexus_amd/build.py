@@ -21,7 +21,6 @@ ARCH = "gfx950"
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
-    "-munsafe-fp-atomics",
     # gfx950's packed fp32 instructions stay off: hipcc is not allowed to form them.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-command-line-argument",

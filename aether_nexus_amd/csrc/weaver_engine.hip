@@ -61,13 +61,27 @@ int ensure(DevBuf& b, size_t bytes, std::string& err) {
     return AW_OK;
 }
 
+// True when `st` is being captured into a HIP graph (then nothing may be
+// allocated or copied synchronously on its behalf).
+bool capturing(hipStream_t st) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+}
+
 // The decode workspace grows like ensure(), but an outgrown buffer is kept
 // until the engine is destroyed instead of freed: a decode captured into a HIP
 // graph holds the address it was captured with, and a later, larger request
 // must not free it under the graph.  Growth is geometric (1.5x), so the kept
-// buffers add up to at most twice the largest one.
-int ensure_keep(DevBuf& b, size_t bytes, std::vector<void*>& retired, std::string& err) {
+// buffers add up to at most twice the largest one.  A call being captured
+// cannot grow it: it returns AW_E_UNSUPPORTED, asking for an eager call of
+// that size first.
+int ensure_keep(DevBuf& b, size_t bytes, std::vector<void*>& retired, std::string& err, hipStream_t st) {
     if (bytes <= b.cap && b.ptr) return AW_OK;
+    if (capturing(st)) {
+        err = "the workspace must grow to " + std::to_string(bytes) +
+              " bytes during stream capture: make one eager call of this size (or larger) before capturing";
+        return AW_E_UNSUPPORTED;
+    }
     const size_t want = std::max({align_up(bytes, kAlign), kAlign, align_up(b.cap + b.cap / 2, kAlign)});
     void* p = nullptr;
     hipError_t e = hipMalloc(&p, want);
@@ -753,7 +767,7 @@ int decode_device(aw_engine* e, const aw_decode_desc* d, hipStream_t st, bool no
         e->profiling = prof;
         return rc;
     }
-    if ((rc = ensure_keep(e->ws, o.info.workspace_bytes, e->retired_ws, e->last_error))) return rc;
+    if ((rc = ensure_keep(e->ws, o.info.workspace_bytes, e->retired_ws, e->last_error, st))) return rc;
     char* ws = (char*)e->ws.ptr;
     return d->head_dim == 64 ? run_pipeline<64>(e, d, o, ws, st) : run_pipeline<128>(e, d, o, ws, st);
 }
@@ -1102,7 +1116,7 @@ int aw_multihead_attention_device(aw_engine* e, const uint16_t* q, const uint16_
     if (blocks > e->iota_n) {
         // Grown (and kept, like the workspace) on the host's side: filled with a
         // synchronous copy, so calls on any stream see it complete.
-        int rc = ensure_keep(e->iota, blocks * 4, e->retired_ws, e->last_error);
+        int rc = ensure_keep(e->iota, blocks * 4, e->retired_ws, e->last_error, st);
         if (rc) return rc;
         const uint32_t n = (uint32_t)std::min<size_t>(e->iota.cap / 4, 0xFFFFFFFFull);
         std::vector<uint32_t> ids(n);
@@ -1230,7 +1244,7 @@ int encode_device(aw_engine* e, const aw_encode_desc* d, hipStream_t st) {
     // Scratch of the MFMA path (the atoms' norms), allocated before any work is queued.
     const bool full_scan = (d->flags & AW_F_ENCODE_FULL_SCAN) != 0;
     const uint64_t n_atoms = (uint64_t)d->dict_heads * d->dict_size;
-    if (!full_scan && (rc = ensure_keep(e->enc_ws, n_atoms * sizeof(aw::AtomNorm), e->retired_ws, e->last_error)))
+    if (!full_scan && (rc = ensure_keep(e->enc_ws, n_atoms * sizeof(aw::AtomNorm), e->retired_ws, e->last_error, st)))
         return rc;
     // The entropy proxy (few long lanes) runs on the side stream beside the encoder.
     if (d->entropy) {

@@ -252,7 +252,10 @@ int aw_decode(aw_engine* engine,
  * and recorded; aw_engine_check_device_errors reports it.
  * The call may be captured into a HIP graph (stream capture): the graph keeps
  * the workspace that call used, and the engine frees no workspace before
- * aw_engine_destroy, so later, larger calls leave captured graphs valid.
+ * aw_engine_destroy, so later, larger calls leave captured graphs valid.  A
+ * call being captured cannot grow the workspace (that allocates): it returns
+ * AW_E_UNSUPPORTED, enqueueing nothing; make one eager call of the same (or a
+ * larger) request first.
  * Replays and other calls on one engine share that workspace: run them one at
  * a time (stream-ordered, or synchronised between). */
 int aw_decode_device(aw_engine* engine, const aw_decode_desc* desc, void* hip_stream);
@@ -290,7 +293,9 @@ int aw_decode_device_noalloc(aw_engine* engine, const aw_decode_desc* desc, void
  * ops.metal:564) kv_len is not limited to 4096: it may reach 4 Mi positions
  * (the hot-pool limit of aw_decode_device), and kv_len + 1 < num_queries is
  * rejected instead of wrapping.  Queries beyond 64 / (q_heads / kv_heads) per
- * call are processed in consecutive groups. */
+ * call are processed in consecutive groups.  Like aw_decode_device, a call
+ * being captured into a HIP graph cannot grow the engine's workspace or its
+ * block table: make one eager call with that kv_len (or longer) first. */
 int aw_multihead_attention_device(aw_engine* engine, const uint16_t* q, const uint16_t* k_cache,
                                   const uint16_t* v_cache, uint16_t* out, uint32_t kv_len,
                                   uint32_t head_dim, uint32_t q_heads, uint32_t kv_heads,

@@ -8,6 +8,7 @@ the product package.  Functions take the host arrays produced by
 from __future__ import annotations
 
 import ctypes
+import os
 import subprocess
 from pathlib import Path
 
@@ -16,7 +17,8 @@ import numpy as np
 from aether_nexus_amd.types import AW_F_CAUSAL, DecodeDesc
 
 HERE = Path(__file__).resolve().parent
-LIB = HERE / "libweaver_oracle.so"
+# WEAVER_ORACLE_LIB: another build of the same source (the sanitizer run's).
+LIB = Path(os.environ.get("WEAVER_ORACLE_LIB") or HERE / "libweaver_oracle.so")
 SRC = HERE / "weaver_oracle.c"
 
 _lib = None

@@ -166,10 +166,11 @@ static int ref32_row(const geom_t* g, uint64_t row, uint16_t* out_row, float* ql
     const uint32_t kvh = h / g->G;
     const uint16_t* qrow = d->q + row * D;
     const uint32_t* refs = d->refs + l * g->refs_layer + (uint64_t)b * d->refs_stride;
-    const uint16_t* hot_k = d->hot_k + l * g->hot_layer;
+    const uint16_t* hot_k = d->hot_k ? d->hot_k + l * g->hot_layer : NULL; /* no offset on an absent pool */
     const uint16_t* hot_v = d->hot_v ? d->hot_v + l * g->hot_layer : hot_k;
-    const aw_sparse_code* cold = d->cold + l * g->cold_layer;
-    const uint16_t* dict = d->dict + l * g->dict_layer + (d->dict_heads == 1 ? 0 : (uint64_t)kvh * A * D);
+    const aw_sparse_code* cold = d->cold ? d->cold + l * g->cold_layer : NULL;
+    const uint16_t* dict =
+        d->dict ? d->dict + l * g->dict_layer + (d->dict_heads == 1 ? 0 : (uint64_t)kvh * A * D) : NULL;
     const uint32_t nh = seq_count(d->seq_hot, d->hot_count, l, b, d->batch);
     const uint32_t nc = seq_count(d->seq_cold, d->cold_count, l, b, d->batch);
     const uint64_t limit = hot_limit(d, nh, q);
@@ -262,10 +263,11 @@ static int f64_row(const geom_t* g, uint64_t row, double* out_row, double* score
     const uint32_t kvh = h / g->G;
     const uint16_t* qrow = d->q + row * D;
     const uint32_t* refs = d->refs + l * g->refs_layer + (uint64_t)b * d->refs_stride;
-    const uint16_t* hot_k = d->hot_k + l * g->hot_layer;
+    const uint16_t* hot_k = d->hot_k ? d->hot_k + l * g->hot_layer : NULL; /* no offset on an absent pool */
     const uint16_t* hot_v = d->hot_v ? d->hot_v + l * g->hot_layer : hot_k;
-    const aw_sparse_code* cold = d->cold + l * g->cold_layer;
-    const uint16_t* dict = d->dict + l * g->dict_layer + (d->dict_heads == 1 ? 0 : (uint64_t)kvh * A * D);
+    const aw_sparse_code* cold = d->cold ? d->cold + l * g->cold_layer : NULL;
+    const uint16_t* dict =
+        d->dict ? d->dict + l * g->dict_layer + (d->dict_heads == 1 ? 0 : (uint64_t)kvh * A * D) : NULL;
     const uint32_t nh = seq_count(d->seq_hot, d->hot_count, l, b, d->batch);
     const uint32_t nc = seq_count(d->seq_cold, d->cold_count, l, b, d->batch);
     const uint64_t limit = hot_limit(d, nh, q);
@@ -436,7 +438,8 @@ int or_qlatent_f64(const aw_decode_desc* d, double* out) {
         uint32_t l, b, q, h;
         row_split(&g, row, &l, &b, &q, &h);
         uint32_t kvh = h / g.G;
-        const uint16_t* dict = d->dict + l * g.dict_layer + (d->dict_heads == 1 ? 0 : (uint64_t)kvh * A * D);
+        const uint16_t* dict =
+            d->dict ? d->dict + l * g.dict_layer + (d->dict_heads == 1 ? 0 : (uint64_t)kvh * A * D) : NULL;
         for (uint32_t a = 0; a < A; ++a) {
             double s = 0.0;
             for (uint32_t i = 0; i < D; ++i)

@@ -46,3 +46,44 @@ def test_graph_replays_match_eager(engine, geom, hb):
             _ = (out2.float() * 2).sum()
             torch.cuda.synchronize()
     engine.check_device_errors(s.cuda_stream)
+
+
+def test_capture_refuses_workspace_growth():
+    """A call being captured cannot grow the engine's workspace (hipMalloc is not
+    capturable): it returns AW_E_UNSUPPORTED before enqueueing anything; after
+    one eager call of that size the same capture works and replays the eager
+    output bits."""
+    from aether_nexus_amd.types import AW_E_UNSUPPORTED
+    from aether_nexus_amd.weaver import WeaverEngine, WeaverError
+    eng = WeaverEngine()  # a fresh engine: no workspace yet
+    try:
+        wl = W.generate(W.hot_cold(batch=2), seed=23, device="cuda:0")
+        out = torch.full(wl.out_shape(), float("nan"), dtype=torch.float16, device="cuda:0")
+        desc = W.device_desc(wl, out)
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        print("graph: capture before any eager call", flush=True)
+        with torch.cuda.stream(s):
+            g0 = torch.cuda.CUDAGraph()
+            with pytest.raises(WeaverError) as e:
+                with torch.cuda.graph(g0, stream=s):
+                    eng.decode_device(desc, stream=torch.cuda.current_stream().cuda_stream)
+            assert e.value.status == AW_E_UNSUPPORTED and "eager" in str(e.value)
+            del g0
+            torch.cuda.synchronize()
+            assert torch.isnan(out.float()).all()  # nothing ran
+            eng.decode_device(desc, stream=s.cuda_stream)
+            eng.check_device_errors(s.cuda_stream)
+            eager = out.clone()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=s):
+                eng.decode_device(desc, stream=torch.cuda.current_stream().cuda_stream)
+            for _ in range(2):
+                out.fill_(float("nan"))
+                g.replay()
+                torch.cuda.synchronize()
+                assert torch.equal(out.view(torch.int16), eager.view(torch.int16))
+        del g
+    finally:
+        torch.cuda.synchronize()
+        eng.close()
