@@ -325,6 +325,10 @@ def make_desc(*, layers: int, batch: int, queries: int, q_heads: int, kv_heads: 
     d.q, d.q_latent, d.hot_k, d.hot_v = _ptr(q), _ptr(q_latent), _ptr(hot_k), _ptr(hot_v)
     d.cold, d.refs, d.seq_hot, d.seq_cold = _ptr(cold), _ptr(refs), _ptr(seq_hot), _ptr(seq_cold)
     d.dict, d.out = _ptr(dictionary), _ptr(out)
+    # The descriptor holds raw addresses: keep the tensors behind them alive as
+    # long as it is (a temporary such as a reordered pool would otherwise go back
+    # to torch's cache, and torch.cuda.graph's empty_cache would unmap it).
+    d._keep = (q, out, hot_k, hot_v, cold, refs, dictionary, q_latent, seq_hot, seq_cold)
     return d
 
 
@@ -341,4 +345,5 @@ def make_encode_desc(*, kv_heads: int, head_dim: int, dict_size: int, dict_heads
     d.hot_blocks, d.cold_blocks = hot_blocks, cold_blocks
     d.hot, d.dict, d.src_blocks = _ptr(hot), _ptr(dictionary), _ptr(src_blocks)
     d.dst_blocks, d.cold, d.entropy = _ptr(dst_blocks), _ptr(cold), _ptr(entropy)
+    d._keep = (hot, dictionary, src_blocks, dst_blocks, cold, entropy)  # as in make_desc
     return d

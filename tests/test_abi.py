@@ -217,6 +217,35 @@ def test_plan_flags():
     assert e.value.status == AW_E_INVALID_ARG
 
 
+def test_descriptors_keep_their_tensors_alive():
+    """A descriptor holds raw addresses, so it keeps the tensors behind them
+    alive: a temporary (a pool reordered for the call) is not returned to
+    torch's cache while the descriptor, or a graph captured from it, may still
+    read it."""
+    import gc
+    import weakref
+    import torch
+    from aether_nexus_amd.weaver import make_desc, make_encode_desc
+    reordered = torch.zeros(64, 16, 8, 8, dtype=torch.int16).permute(0, 2, 1, 3).contiguous()
+    ref = weakref.ref(reordered)
+    d = make_desc(layers=1, batch=1, queries=1, q_heads=32, kv_heads=8, head_dim=128, dict_size=4096, dict_heads=1,
+                  hot_count=0, cold_count=64, refs_stride=64, hot_blocks=0, cold_blocks=64, q=1, out=1,
+                  cold=reordered)
+    del reordered
+    gc.collect()
+    assert ref() is not None and d.cold == d._keep[4].data_ptr()
+    src = torch.arange(4, dtype=torch.int32)
+    sref = weakref.ref(src)
+    e = make_encode_desc(kv_heads=8, head_dim=128, dict_size=512, dict_heads=8, hot_blocks=4, cold_blocks=4,
+                         hot=1, dictionary=1, src_blocks=src, cold=1)
+    del src
+    gc.collect()
+    assert sref() is not None and e.src_blocks == e._keep[2].data_ptr()
+    del d, e
+    gc.collect()
+    assert sref() is None
+
+
 def test_engine_create_without_gpu_fails_cleanly():
     """No GPU in this container: creation reports an error instead of crashing."""
     import torch
