@@ -69,6 +69,18 @@ SIGNATURES = {
     "aw_fabric_pull": (_c_int, [_vp, _u32, _u64, _u64]),
     "aw_fabric_detach_device": (_c_int, [_vp]),
     "aw_fabric_distill": (_c_int, [_vp, _vp, ctypes.c_float, _vp, ctypes.POINTER(_u32)]),
+    # include/aether_ops.h
+    "aw_ops_copy_buffer": (_c_int, [_vp, _vp, _vp, _u32, _u32, _u32, _vp]),
+    "aw_ops_embed_lookup": (_c_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _vp]),
+    "aw_ops_rms_norm": (_c_int, [_vp, _vp, _vp, _vp, _u32, _u32, ctypes.c_float, _vp]),
+    "aw_ops_rope": (_c_int, [_vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, ctypes.c_float, _vp]),
+    "aw_ops_matmul": (_c_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _vp]),
+    "aw_ops_matmul_scaled": (_c_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, ctypes.c_float, _vp]),
+    "aw_ops_silu_gate": (_c_int, [_vp, _vp, _vp, _vp, _u32, _vp]),
+    "aw_ops_add_residual": (_c_int, [_vp, _vp, _vp, _u32, _vp]),
+    "aw_ops_add_bias": (_c_int, [_vp, _vp, _vp, _u32, _u32, _vp]),
+    "aw_ops_scale_f16": (_c_int, [_vp, _vp, _u32, ctypes.c_float, _vp]),
+    "aw_ops_causal_attention": (_c_int, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u64, _vp]),
 }
 
 _cache: dict[str, ctypes.CDLL] = {}

@@ -14,8 +14,9 @@ from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
-SOURCES = [PKG / "csrc" / "weaver_engine.hip", PKG / "csrc" / "fabric.hip"]
-DEPS = [PKG / "csrc" / "weaver_kernels.hpp", ROOT / "include" / "aether_weaver.h", ROOT / "include" / "aether_fabric.h"]
+SOURCES = [PKG / "csrc" / "weaver_engine.hip", PKG / "csrc" / "fabric.hip", PKG / "csrc" / "ops.hip"]
+DEPS = [PKG / "csrc" / "weaver_kernels.hpp", PKG / "csrc" / "ops_kernels.hpp", PKG / "csrc" / "engine_internal.hpp",
+        ROOT / "include" / "aether_weaver.h", ROOT / "include" / "aether_fabric.h", ROOT / "include" / "aether_ops.h"]
 OUT = PKG / "libaether_weaver.so"
 ARCH = "gfx950"
 

@@ -16,6 +16,7 @@
 #include <vector>
 
 #include "../../include/aether_fabric.h"
+#include "engine_internal.hpp"
 #include "weaver_kernels.hpp"
 
 static_assert(sizeof(aw_sparse_code) == 16, "SparseCode is 16 bytes (types.rs:227)");
@@ -1164,10 +1165,12 @@ int aw_engine_check_device_errors(aw_engine* e, void* stream) {
     if (!word) return AW_OK;
     AW_HIP(e, hipMemsetAsync(e->err, 0, 4, st));
     AW_HIP(e, hipStreamSynchronize(st));
-    return fail(e, AW_E_OOB, "device saw out-of-range input:%s%s%s (the affected tokens or terms were skipped)",
+    return fail(e, AW_E_OOB, "device saw out-of-range input:%s%s%s%s (the affected tokens or terms were skipped)",
                 (word & aw::kErrHotRef) ? " hot block ref" : "", (word & aw::kErrColdRef) ? " cold block ref" : "",
-                (word & aw::kErrAtom) ? " atom index" : "");
+                (word & aw::kErrAtom) ? " atom index" : "",
+                (word & aw_engine_internal::kErrTokenBit) ? " token id" : "");
 }
+
 
 int aw_debug_gather_codes(aw_engine* e, const aw_sparse_code* codes, size_t n, const uint16_t* dict,
                           uint32_t dict_size, uint32_t head_dim, uint32_t* idx, float* coef, uint16_t* atoms,
@@ -1408,3 +1411,22 @@ int aw_engine_reset_stage_stats(aw_engine* e) {
 }
 
 } // extern "C"
+
+// ------------------------------------------------- for the library's other sources
+
+namespace aw_engine_internal {
+
+int device(const aw_engine* e) { return e->device; }
+uint32_t compute_units(const aw_engine* e) { return e->n_cu; }
+uint32_t* error_word(const aw_engine* e) { return e->err; }
+int fail(aw_engine* e, int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    if (e) e->last_error = buf;
+    return code;
+}
+
+} // namespace aw_engine_internal

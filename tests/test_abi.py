@@ -258,7 +258,7 @@ def test_engine_create_without_gpu_fails_cleanly():
 
 
 def test_headers_compile_as_c_and_match_the_library(tmp_path):
-    """A C99 host (the way a Rust or C binding sees the ABI): both headers
+    """A C99 host (the way a Rust or C binding sees the ABI): the headers
     compile with -pedantic -Werror, and a program linked against the library
     finds the struct sizes it reports and the field offsets the Python
     bindings use."""
@@ -272,6 +272,7 @@ def test_headers_compile_as_c_and_match_the_library(tmp_path):
 #include <stdio.h>
 #include "aether_weaver.h"
 #include "aether_fabric.h"
+#include "aether_ops.h"
 int main(void) {
     size_t s[4];
     aw_abi_struct_sizes(s);
