@@ -67,19 +67,28 @@ int launch_gemm(aw_engine* e, const uint16_t* a, const uint16_t* b, void* c, uin
     g.vec_out = n % 4 == 0 && aligned(c, F32 ? 16 : 8);
     const bool vec = k % 8 == 0 && aligned(a, 16) && aligned(b, 16);
     const dim3 skinny_grid((uint32_t)cdiv64(n, 16));
-#define AW_SKINNY(MT)                                                                                        \
-    do {                                                                                                     \
-        if (vec)                                                                                             \
-            hipLaunchKernelGGL((awo::gemm_skinny_kernel<MT, 8, true, F32>), skinny_grid, dim3(512), 0, st, g);  \
-        else                                                                                                 \
-            hipLaunchKernelGGL((awo::gemm_skinny_kernel<MT, 8, false, F32>), skinny_grid, dim3(512), 0, st, g); \
+    // Few weight tiles (up to 4 work-groups per CU): 16 waves per tile, so a K of
+    // 4096 is in flight at once; many tiles: 8 waves, more work-groups resident
+    // (measured at M = 1: 4096 x 4096 10.8 -> 9.6 us, 14336 x 4096 33.1 -> 28.6 us
+    // with 16 waves; 128256 x 4096 183 us with 8 waves, 214 with 16).
+    const bool wide = cdiv64(n, 16) <= 4ull * ei::compute_units(e);
+#define AW_SKINNY(MT, NW)                                                                                         \
+    do {                                                                                                          \
+        if (vec)                                                                                                  \
+            hipLaunchKernelGGL((awo::gemm_skinny_kernel<MT, NW, true, F32>), skinny_grid, dim3(NW * 64), 0, st, g);  \
+        else                                                                                                      \
+            hipLaunchKernelGGL((awo::gemm_skinny_kernel<MT, NW, false, F32>), skinny_grid, dim3(NW * 64), 0, st, g); \
     } while (0)
-    if (m <= 16)
-        AW_SKINNY(1);
+    if (m <= 16 && wide)
+        AW_SKINNY(1, 16);
+    else if (m <= 16)
+        AW_SKINNY(1, 8);
+    else if (m <= 32 && wide)
+        AW_SKINNY(2, 16);
     else if (m <= 32)
-        AW_SKINNY(2);
+        AW_SKINNY(2, 8);
     else if (m <= 64)
-        AW_SKINNY(4);
+        AW_SKINNY(4, 8);
     else {
         const dim3 grid((uint32_t)cdiv64(n, awo::kTileN), (uint32_t)cdiv64(m, awo::kTileM));
         if (grid.y > 65535u) return ei::fail(e, AW_E_UNSUPPORTED, "matmul: m = %u rows exceed the grid", m);

@@ -67,6 +67,8 @@ def parse():
     p.add_argument("--skip-encoder", action="store_true", help="skip the SparseCode encoder measurement")
     p.add_argument("--skip-fabric", action="store_true", help="skip the .aether fabric residency measurement")
     p.add_argument("--skip-attention", action="store_true", help="skip the inference-attention measurement")
+    p.add_argument("--skip-ops", action="store_true", help="skip the dense-ops measurement (products, decode forward)")
+    p.add_argument("--only-ops", action="store_true", help="time only the dense ops and print them")
     p.add_argument("--configs", default="2,4,5",
                    help="BASELINE configurations timed beside the sweep (comma list of 2, 4, 5; empty for none)")
     p.add_argument("--only-configs", action="store_true",
@@ -527,6 +529,160 @@ def tiered_attention_bench(engine, seed, reps, layers=32, hot=2048, cold=32768):
     return res
 
 
+# Llama-3.1-8B, the dense shapes of the inference loop (inference.rs:13-159 presets).
+LLAMA8B = dict(hidden=4096, q_heads=32, kv_heads=8, head_dim=128, inter=14336, vocab=128256, layers=32, eps=1e-5,
+               theta=500000.0, max_seq=4096)
+PEAK_F16_TFLOPS = 2500.0
+
+
+def _graph_time(fn, st, reps):
+    """ms per replay of `fn(stream)` captured in a HIP graph (one eager call first),
+    after the work already queued on torch's current stream (the inputs)."""
+    import torch
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        fn(st.cuda_stream)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=st):
+            fn(torch.cuda.current_stream().cuda_stream)
+        for _ in range(2):
+            graph.replay()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        ev[0].record(st)
+        for _ in range(reps):
+            graph.replay()
+        ev[1].record(st)
+    torch.cuda.synchronize()
+    ms = ev[0].elapsed_time(ev[1]) / reps
+    del graph
+    return ms
+
+
+def ops_bench(engine, seed, read_peak_gbps, reps=10):
+    """The dense ops (ops.metal:16-635) on MI355X at Llama-3.1-8B shapes.
+
+    * Each product of a layer, one launch at a time: decode (M = 1) and verify
+      (M = 16, forward_batch's MAX_BATCH) are bound by the weight bytes (N*K*2,
+      plus activations and output), measured against 8 TB/s and the read-only
+      stream peak; prefill-sized M = 2048 by the matrix cores (2*M*N*K flops
+      against 2.5 PFLOP/s f16).  The weights are rotated over copies that
+      together exceed the 256 MiB Infinity Cache, so the bytes come from HBM.
+    * One whole decode forward (InferenceEngine::forward_batch,
+      inference.rs:456-634): embedding, 32 layers of RMSNorm, q/k/v products,
+      RoPE, the cache append, multihead attention over 4096 cached tokens, the
+      output product, residual, RMSNorm, gated MLP and residual, then the final
+      norm and the f32 lm_head, captured in one HIP graph, random weights.
+      Bytes per forward: every weight once plus the K and V caches read."""
+    import torch
+    from aether_nexus_amd.ops import OpsEngine
+    c = LLAMA8B
+    ops = OpsEngine(engine)
+    g = torch.Generator(device="cuda:0").manual_seed(seed)
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+
+    def randn(*shape, std=1.0):
+        return (torch.randn(shape, generator=g, device="cuda:0") * std).to(torch.float16)
+
+    H, I, V = c["hidden"], c["inter"], c["vocab"]
+    kvd = c["kv_heads"] * c["head_dim"]
+    shapes = [("q_proj, o_proj", H, H), ("k_proj, v_proj", kvd, H), ("gate_proj, up_proj", I, H),
+              ("down_proj", H, I), ("lm_head (f32, scaled)", V, H)]
+    products = []
+    for name, n, k in shapes:
+        copies = max(1, min(16, math.ceil(2 * MALL_BYTES / (n * k * 2))))
+        ws = [randn(n, k, std=k ** -0.5) for _ in range(copies)]
+        scaled = name.startswith("lm_head")
+        for m in (1, 16, 2048):
+            if m == 2048 and scaled:
+                continue
+            a = randn(m, k)
+            outs = [torch.empty((m, n), dtype=torch.float32 if scaled else torch.float16, device="cuda:0")
+                    for _ in range(copies)]
+            launches = copies * max(1, 64 // copies) if m < 2048 else copies * 2
+
+            def fn(s, ws=ws, a=a, outs=outs, m=m, n=n, k=k, scaled=scaled, launches=launches):
+                for i in range(launches):
+                    j = i % len(ws)
+                    if scaled:
+                        ops.matmul_scaled(a, ws[j], outs[j], m, n, k, 1.0 / 8.0, stream=s)
+                    else:
+                        ops.matmul(a, ws[j], outs[j], m, n, k, stream=s)
+            us = _graph_time(fn, st, 3) * 1e3 / launches
+            row = {"product": name, "m": m, "n": n, "k": k, "us": round(us, 2)}
+            if m < 2048:
+                nbytes = n * k * 2 + m * k * 2 + m * n * (4 if scaled else 2)
+                gbps = nbytes / (us * 1e-6) / 1e9
+                row.update(bound="hbm", bytes=nbytes, achieved_gbps=round(gbps, 1),
+                           frac_of_peak=round(gbps / PEAK_HBM_GBPS, 4), frac_of_read_peak=round(gbps / read_peak_gbps, 4))
+            else:
+                tf = 2.0 * m * n * k / (us * 1e-6) / 1e12
+                row.update(bound="mfma", flops=2 * m * n * k, achieved_tflops=round(tf, 1),
+                           frac_of_peak=round(tf / PEAK_F16_TFLOPS, 4))
+            products.append(row)
+            log(json.dumps(row))
+            del outs, a
+        del ws
+        torch.cuda.empty_cache()
+    res = {"workload": "Llama-3.1-8B shapes: hidden 4096, 32q/8kv heads x 128, MLP 14336, vocab 128256",
+           "products": products}
+
+    # One decode forward of 32 layers.
+    L, hq, hkv, hd, S = c["layers"], c["q_heads"], c["kv_heads"], c["head_dim"], c["max_seq"]
+    lw = [{"ln1": randn(H, std=0.1) + 1, "ln2": randn(H, std=0.1) + 1, "wq": randn(H, H, std=H ** -0.5),
+           "wk": randn(kvd, H, std=H ** -0.5), "wv": randn(kvd, H, std=H ** -0.5), "wo": randn(H, H, std=H ** -0.5),
+           "wg": randn(I, H, std=H ** -0.5), "wu": randn(I, H, std=H ** -0.5), "wd": randn(H, I, std=I ** -0.5),
+           "kc": randn(S, hkv, hd), "vc": randn(S, hkv, hd)} for _ in range(L)]
+    embed, lm_head, final_ln = randn(V, H), randn(V, H, std=H ** -0.5), randn(H, std=0.1) + 1
+    res["forward"] = {}
+    for name, t in (("decode", 1), ("verify_3_drafts", 4)):
+        pos = S - t  # the new tokens fill the cache's last positions: attention over all 4096
+        ids = torch.randint(0, V, (t,), generator=g, device="cuda:0", dtype=torch.int32)
+        hid, norm = (torch.empty((t, H), dtype=torch.float16, device="cuda:0") for _ in range(2))
+        q, k, v = (torch.empty((t, n), dtype=torch.float16, device="cuda:0") for n in (H, kvd, kvd))
+        att, proj, down = (torch.empty((t, H), dtype=torch.float16, device="cuda:0") for _ in range(3))
+        gate, up, ffn = (torch.empty((t, I), dtype=torch.float16, device="cuda:0") for _ in range(3))
+        logits = torch.empty((t, V), dtype=torch.float32, device="cuda:0")
+
+        def forward(s, t=t, pos=pos, ids=ids, hid=hid, norm=norm, q=q, k=k, v=v, att=att, proj=proj, down=down,
+                    gate=gate, up=up, ffn=ffn, logits=logits):
+            ops.embed_lookup(ids, embed, hid, H, t, V, stream=s)
+            for w in lw:
+                ops.rms_norm(hid, w["ln1"], norm, H, t, c["eps"], stream=s)
+                ops.matmul(norm, w["wq"], q, t, H, H, stream=s)
+                ops.matmul(norm, w["wk"], k, t, kvd, H, stream=s)
+                ops.matmul(norm, w["wv"], v, t, kvd, H, stream=s)
+                ops.rope(q, k, t, hq, hkv, hd, pos, c["theta"], stream=s)
+                ops.copy_buffer(k, w["kc"], kvd * t, 0, pos * kvd, stream=s)
+                ops.copy_buffer(v, w["vc"], kvd * t, 0, pos * kvd, stream=s)
+                ops.multihead_attention(q, w["kc"], w["vc"], att, pos + t, hd, hq, hkv, t, cache_tokens=S, stream=s)
+                ops.matmul(att, w["wo"], proj, t, H, H, stream=s)
+                ops.add_residual(hid, proj, H * t, stream=s)
+                ops.rms_norm(hid, w["ln2"], norm, H, t, c["eps"], stream=s)
+                ops.matmul(norm, w["wg"], gate, t, I, H, stream=s)
+                ops.matmul(norm, w["wu"], up, t, I, H, stream=s)
+                ops.silu_gate(gate, up, ffn, I * t, stream=s)
+                ops.matmul(ffn, w["wd"], down, t, H, I, stream=s)
+                ops.add_residual(hid, down, H * t, stream=s)
+            ops.rms_norm(hid, final_ln, norm, H, t, c["eps"], stream=s)
+            ops.matmul_scaled(norm, lm_head, logits, t, V, H, 1.0, stream=s)
+        ms = _graph_time(forward, st, reps)
+        ops.check_device_errors(st.cuda_stream)
+        assert torch.isfinite(logits).all(), "non-finite logits"
+        nbytes = L * (2 * H * H + 2 * kvd * H + 3 * I * H + 2 * H) * 2 + V * H * 2 + L * 2 * S * kvd * 2
+        gbps = nbytes / (ms * 1e-3) / 1e9
+        res["forward"][name] = {"new_tokens": t, "ms_per_forward": round(ms, 4), "tokens_per_s": round(t / (ms * 1e-3), 1),
+                                "bytes_per_forward": nbytes, "achieved_gbps": round(gbps, 1),
+                                "frac_of_peak": round(gbps / PEAK_HBM_GBPS, 4),
+                                "frac_of_read_peak": round(gbps / read_peak_gbps, 4)}
+        log(json.dumps({name: res["forward"][name]}))
+    res["forward"]["workload"] = (f"InferenceEngine::forward_batch at Llama-3.1-8B: {L} layers, random f16 weights, "
+                                  f"K/V caches of {S} tokens per layer, f32 lm_head over {V} tokens, one HIP graph")
+    del lw, embed, lm_head
+    torch.cuda.empty_cache()
+    return res
+
+
 PCIE_GEN5_X16_GBPS = 63.0  # per direction: 32 GT/s x 16 lanes x 128/130 encoding / 8 bits
 
 
@@ -824,6 +980,12 @@ def main():
         engine.close()
         print(json.dumps({"configs": rows}), flush=True)
         return 0
+    if args.only_ops:
+        rp = hbm_read_peak(engine)
+        out = ops_bench(engine, args.seed, rp["gbps"])
+        engine.close()
+        print(json.dumps({"hbm_read_peak": rp, "dense_ops": out}), flush=True)
+        return 0
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
     sweep = []
@@ -925,6 +1087,7 @@ def main():
     if enc:
         log(json.dumps({"encoder": enc}))
     fab = None if args.skip_fabric else fabric_bench(engine, args.seed, 8 if args.no_cpu else 24)
+    dense = None if args.skip_ops else ops_bench(engine, args.seed, read_peak["gbps"])
     if fab:
         log(json.dumps({"fabric": fab}))
     att = None if args.skip_attention else attention_bench(engine, args.seed, 20, 0.5 if args.no_cpu else 3.0)
@@ -966,6 +1129,7 @@ def main():
         "other_cold_layout": alt,
         "encoder": enc,
         "fabric": fab,
+        "dense_ops": dense,
         "inference_attention": att,
         "cpu_baseline": cpu,
         "reference_bench_config": ref_cfg,

@@ -161,8 +161,10 @@ def test_rope(ops, tokens, hq, hkv, hd, start):
         assert np.array_equal(bits(host(tk)), bits(k))  # no k heads: untouched
 
 
-SHAPES = [(1, 1, 1), (1, 5, 7), (1, 1000, 4096), (3, 33, 64), (16, 1024, 4096), (17, 100, 200), (64, 256, 520),
-          (65, 130, 96), (200, 300, 520), (256, 1024, 4096), (130, 77, 13)]
+# M <= 16, 32, 64 take the skinny kernel with 1, 2, 4 row tiles (16 waves up to 4 weight tiles per CU, 8
+# beyond: N = 20000 and 49155), larger M the tiled one; K % 8 != 0 the element-wise loads.
+SHAPES = [(1, 1, 1), (1, 5, 7), (1, 1000, 4096), (3, 33, 64), (16, 1024, 4096), (17, 100, 200), (20, 20000, 64),
+          (64, 256, 520), (65, 130, 96), (200, 300, 520), (256, 1024, 4096), (130, 77, 13)]
 
 
 def check_product(got, a, b, k, what, scale=1.0, f16_out=True):
