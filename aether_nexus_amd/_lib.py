@@ -81,6 +81,9 @@ SIGNATURES = {
     "aw_ops_add_bias": (_c_int, [_vp, _vp, _vp, _u32, _u32, _vp]),
     "aw_ops_scale_f16": (_c_int, [_vp, _vp, _u32, ctypes.c_float, _vp]),
     "aw_ops_causal_attention": (_c_int, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u64, _vp]),
+    "aw_ops_matmul_add_residual": (_c_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, ctypes.c_float, _vp]),
+    "aw_ops_matmul_silu_gate": (_c_int, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _vp]),
+    "aw_ops_matmul_qkv": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _vp]),
 }
 
 _cache: dict[str, ctypes.CDLL] = {}

@@ -51,33 +51,79 @@ int launch_ew(aw_engine* e, const awo::EwArgs& p, bool vec, hipStream_t st) {
     return AW_OK;
 }
 
-template <bool F32>
-int launch_gemm(aw_engine* e, const uint16_t* a, const uint16_t* b, void* c, uint32_t m, uint32_t n, uint32_t k,
-                float scale, hipStream_t st) {
-    if (m == 0 || n == 0) return AW_OK;
-    if (!a || !b || !c) return ei::fail(e, AW_E_INVALID_ARG, "matmul: null pointer");
+// One weight matrix of a product: B [n][k] (and B2, the up weights of a fused
+// SiLU gate), output C [m][n].
+struct Product {
+    const uint16_t* b;
+    const uint16_t* b2;
+    void* c;
+    uint32_t n;
+};
+
+// The products `p[0 .. np)` over the same activations a [m][k], one launch when
+// m <= 64 (skinny), one launch each otherwise (tiled).  EPI picks the store;
+// F32 the scaled fp32 output of matmul_scaled.
+template <awo::Epi EPI, bool F32>
+int launch_products(aw_engine* e, const char* what, const uint16_t* a, const Product* p, int np, uint32_t m,
+                    uint32_t k, float scale, hipStream_t st) {
+    if (m == 0) return AW_OK;
+    if (!a) return ei::fail(e, AW_E_INVALID_ARG, "%s: null pointer", what);
     awo::GemmArgs g{};
     g.A = a;
-    g.B = b;
-    g.C = c;
     g.M = m;
-    g.N = n;
     g.K = k;
     g.scale = scale;
-    g.vec_out = n % 4 == 0 && aligned(c, F32 ? 16 : 8);
-    const bool vec = k % 8 == 0 && aligned(a, 16) && aligned(b, 16);
-    const dim3 skinny_grid((uint32_t)cdiv64(n, 16));
+    bool vec = k % 8 == 0 && aligned(a, 16);
+    uint64_t tiles = 0;
+    for (int i = 0; i < np; ++i) {
+        if (!p[i].b || !p[i].c || (EPI == awo::Epi::SiluGate && !p[i].b2))
+            return ei::fail(e, AW_E_INVALID_ARG, "%s: null pointer", what);
+        vec = vec && aligned(p[i].b, 16) && (EPI != awo::Epi::SiluGate || aligned(p[i].b2, 16));
+        g.g[g.groups].B = p[i].b;
+        g.g[g.groups].B2 = p[i].b2;
+        g.g[g.groups].C = p[i].c;
+        g.g[g.groups].N = p[i].n;
+        g.g[g.groups].tiles = (uint32_t)cdiv64(p[i].n, 16);
+        g.g[g.groups].vec_out = p[i].n % 4 == 0 && aligned(p[i].c, F32 ? 16 : 8);
+        tiles += cdiv64(p[i].n, 16);
+        if (p[i].n) ++g.groups; // empty products drop out
+    }
+    if (!g.groups) return AW_OK;
+    if (m > 64) {
+        if (EPI == awo::Epi::SiluGate)
+            return ei::fail(e, AW_E_UNSUPPORTED, "%s: m = %u rows (the fused gate takes m <= 64; use matmul and "
+                                                 "silu_gate)", what, m);
+        // One tiled launch per product, group 0 of its own arguments.
+        for (uint32_t i = 0; i < g.groups; ++i) {
+            awo::GemmArgs t = g;
+            t.g[0] = g.g[i];
+            t.groups = 1;
+            const dim3 grid((uint32_t)cdiv64(t.g[0].N, awo::kTileN), (uint32_t)cdiv64(m, awo::kTileM));
+            if (grid.y > 65535u) return ei::fail(e, AW_E_UNSUPPORTED, "%s: m = %u rows exceed the grid", what, m);
+            if constexpr (EPI != awo::Epi::SiluGate) {
+                if (vec)
+                    hipLaunchKernelGGL((awo::gemm_tiled_kernel<true, F32, EPI>), grid, dim3(256), 0, st, t);
+                else
+                    hipLaunchKernelGGL((awo::gemm_tiled_kernel<false, F32, EPI>), grid, dim3(256), 0, st, t);
+            }
+        }
+        OPS_HIP(e, hipGetLastError());
+        return AW_OK;
+    }
+    if (tiles > 0x7FFFFFFFull) return ei::fail(e, AW_E_UNSUPPORTED, "%s: grid too large", what);
+    const dim3 grid((uint32_t)tiles);
     // Few weight tiles (up to 4 work-groups per CU): 16 waves per tile, so a K of
     // 4096 is in flight at once; many tiles: 8 waves, more work-groups resident
     // (measured at M = 1: 4096 x 4096 10.8 -> 9.6 us, 14336 x 4096 33.1 -> 28.6 us
-    // with 16 waves; 128256 x 4096 183 us with 8 waves, 214 with 16).
-    const bool wide = cdiv64(n, 16) <= 4ull * ei::compute_units(e);
-#define AW_SKINNY(MT, NW)                                                                                         \
-    do {                                                                                                          \
-        if (vec)                                                                                                  \
-            hipLaunchKernelGGL((awo::gemm_skinny_kernel<MT, NW, true, F32>), skinny_grid, dim3(NW * 64), 0, st, g);  \
-        else                                                                                                      \
-            hipLaunchKernelGGL((awo::gemm_skinny_kernel<MT, NW, false, F32>), skinny_grid, dim3(NW * 64), 0, st, g); \
+    // with 16 waves; 128256 x 4096 183 us with 8 waves, 214 with 16).  The wave
+    // count does not change the sums.
+    const bool wide = tiles <= 4ull * ei::compute_units(e);
+#define AW_SKINNY(MT, NW)                                                                                        \
+    do {                                                                                                         \
+        if (vec)                                                                                                 \
+            hipLaunchKernelGGL((awo::gemm_skinny_kernel<MT, NW, true, F32, EPI>), grid, dim3(NW * 64), 0, st, g);  \
+        else                                                                                                     \
+            hipLaunchKernelGGL((awo::gemm_skinny_kernel<MT, NW, false, F32, EPI>), grid, dim3(NW * 64), 0, st, g); \
     } while (0)
     if (m <= 16 && wide)
         AW_SKINNY(1, 16);
@@ -87,16 +133,8 @@ int launch_gemm(aw_engine* e, const uint16_t* a, const uint16_t* b, void* c, uin
         AW_SKINNY(2, 16);
     else if (m <= 32)
         AW_SKINNY(2, 8);
-    else if (m <= 64)
+    else
         AW_SKINNY(4, 8);
-    else {
-        const dim3 grid((uint32_t)cdiv64(n, awo::kTileN), (uint32_t)cdiv64(m, awo::kTileM));
-        if (grid.y > 65535u) return ei::fail(e, AW_E_UNSUPPORTED, "matmul: m = %u rows exceed the grid", m);
-        if (vec)
-            hipLaunchKernelGGL((awo::gemm_tiled_kernel<true, F32>), grid, dim3(256), 0, st, g);
-        else
-            hipLaunchKernelGGL((awo::gemm_tiled_kernel<false, F32>), grid, dim3(256), 0, st, g);
-    }
 #undef AW_SKINNY
     OPS_HIP(e, hipGetLastError());
     return AW_OK;
@@ -176,14 +214,43 @@ int aw_ops_matmul(aw_engine* e, const uint16_t* a, const uint16_t* b, uint16_t* 
                   uint32_t k, void* stream) {
     int rc = enter(e);
     if (rc) return rc;
-    return launch_gemm<false>(e, a, b, output, m, n, k, 1.0f, (hipStream_t)stream);
+    const Product p{b, nullptr, output, n};
+    return launch_products<awo::Epi::Store, false>(e, "matmul", a, &p, 1, m, k, 1.0f, (hipStream_t)stream);
 }
 
 int aw_ops_matmul_scaled(aw_engine* e, const uint16_t* a, const uint16_t* b, float* output, uint32_t m, uint32_t n,
                          uint32_t k, float scale, void* stream) {
     int rc = enter(e);
     if (rc) return rc;
-    return launch_gemm<true>(e, a, b, output, m, n, k, scale, (hipStream_t)stream);
+    const Product p{b, nullptr, output, n};
+    return launch_products<awo::Epi::Store, true>(e, "matmul_scaled", a, &p, 1, m, k, scale, (hipStream_t)stream);
+}
+
+int aw_ops_matmul_add_residual(aw_engine* e, const uint16_t* a, const uint16_t* b, uint16_t* x, uint32_t m,
+                               uint32_t n, uint32_t k, float residual_multiplier, void* stream) {
+    int rc = enter(e);
+    if (rc) return rc;
+    const Product p{b, nullptr, x, n};
+    return launch_products<awo::Epi::Residual, false>(e, "matmul_add_residual", a, &p, 1, m, k, residual_multiplier,
+                                                      (hipStream_t)stream);
+}
+
+int aw_ops_matmul_silu_gate(aw_engine* e, const uint16_t* a, const uint16_t* b_gate, const uint16_t* b_up,
+                            uint16_t* output, uint32_t m, uint32_t n, uint32_t k, void* stream) {
+    int rc = enter(e);
+    if (rc) return rc;
+    const Product p{b_gate, b_up, output, n};
+    return launch_products<awo::Epi::SiluGate, false>(e, "matmul_silu_gate", a, &p, 1, m, k, 1.0f,
+                                                      (hipStream_t)stream);
+}
+
+int aw_ops_matmul_qkv(aw_engine* e, const uint16_t* a, const uint16_t* b_q, const uint16_t* b_k, const uint16_t* b_v,
+                      uint16_t* q, uint16_t* k_out, uint16_t* v_out, uint32_t m, uint32_t n_q, uint32_t n_kv,
+                      uint32_t k, void* stream) {
+    int rc = enter(e);
+    if (rc) return rc;
+    const Product p[3] = {{b_q, nullptr, q, n_q}, {b_k, nullptr, k_out, n_kv}, {b_v, nullptr, v_out, n_kv}};
+    return launch_products<awo::Epi::Store, false>(e, "matmul_qkv", a, p, 3, m, k, 1.0f, (hipStream_t)stream);
 }
 
 int aw_ops_silu_gate(aw_engine* e, const uint16_t* gate, const uint16_t* up, uint16_t* output, uint32_t size,

@@ -27,7 +27,16 @@ typedef uint32_t uint2_t __attribute__((ext_vector_type(2)));
 constexpr uint32_t kErrToken = aw_engine_internal::kErrTokenBit;
 
 __device__ inline float h2f(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
-__device__ inline uint16_t f2h(float x) { return __builtin_bit_cast(uint16_t, (_Float16)x); }
+// f16 of an fp32 value, rounded twice as the reference's half(float expression)
+// is: the expression to fp32, then to f16.  The empty asm makes x an fp32 value
+// in a register, so the compiler cannot fuse the multiply or add that produced
+// it into a mixed-precision instruction (v_fma_mixlo_f16) that rounds the exact
+// result once, straight to f16 (measured: 1-ulp differences in ~1 of 20000
+// SiLU outputs, between kernels that fused and kernels that did not).
+__device__ inline uint16_t f2h(float x) {
+    __asm__ volatile("" : "+v"(x));
+    return __builtin_bit_cast(uint16_t, (_Float16)x);
+}
 __device__ inline void flag(uint32_t* err, uint32_t bit) {
     __hip_atomic_fetch_or(err, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -229,72 +238,128 @@ __device__ inline half8_t piece(const uint16_t* base, uint64_t row, uint32_t K, 
     }
 }
 
-// Four results C[m][n .. n+3] of one lane, masked to M x N.
-template <bool F32>
-__device__ inline void store4(void* C, uint32_t M, uint32_t N, uint32_t m, uint32_t n, float4_t v, float scale,
-                              bool vec_out) {
-    if (m >= M || n >= N) return;
-    if constexpr (F32) {
-        float* c = (float*)C + (uint64_t)m * N + n;
-        const float4_t r = v * scale;
-        if (vec_out && n + 4 <= N) {
-            *(float4_t*)c = r;
-        } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-                if (n + e < N) c[e] = r[e];
-        }
+// What a product does with its fp32 result at the store:
+//   Store     C = f16(acc), or acc * scale in fp32 (F32);
+//   Residual  C (the residual stream x) = f16(x + f16(f16(acc) * scale)): matmul,
+//             scale_f16 by the residual multiplier, add_residual (ops.rs:266-296,
+//             :350-363, :315-327), the same bits in one pass;
+//   SiluGate  C = f16(silu(f16(acc)) * f16(acc2)) with acc2 the product with a second
+//             weight matrix: the gate and up matmuls then silu_gate (ops.rs:266-312).
+enum class Epi : int { Store = 0, Residual = 1, SiluGate = 2 };
+
+template <Epi EPI, bool F32>
+__device__ inline void epi_store(void* C, uint64_t at, float v, float v2, float scale) {
+    if constexpr (EPI == Epi::Store) {
+        if constexpr (F32) ((float*)C)[at] = v * scale;
+        else ((uint16_t*)C)[at] = f2h(v);
+    } else if constexpr (EPI == Epi::Residual) {
+        uint16_t* x = (uint16_t*)C;
+        x[at] = ew_one<Ew::Add>(x[at], ew_one<Ew::Scale>(f2h(v), 0, scale), 0.0f);
     } else {
-        uint16_t* c = (uint16_t*)C + (uint64_t)m * N + n;
-        if (vec_out && n + 4 <= N) {
-            const uint2_t r = {(uint32_t)f2h(v[0]) | ((uint32_t)f2h(v[1]) << 16),
-                               (uint32_t)f2h(v[2]) | ((uint32_t)f2h(v[3]) << 16)};
-            *(uint2_t*)c = r;
-        } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-                if (n + e < N) c[e] = f2h(v[e]);
-        }
+        ((uint16_t*)C)[at] = ew_one<Ew::Silu>(f2h(v), f2h(v2), 0.0f);
     }
 }
 
+// Four results C[m][n .. n+3] of one lane, masked to M x N; `vec_out` (N % 4 == 0,
+// C aligned) stores them with one 16- or 8-byte store.
+template <Epi EPI, bool F32>
+__device__ inline void store4(void* C, uint32_t M, uint32_t N, uint32_t m, uint32_t n, float4_t v, float4_t v2,
+                              float scale, bool vec_out) {
+    if (m >= M || n >= N) return;
+    const uint64_t at = (uint64_t)m * N + n;
+    if constexpr (EPI == Epi::Store && F32) {
+        if (vec_out && n + 4 <= N) {
+            *(float4_t*)((float*)C + at) = v * scale;
+            return;
+        }
+    } else if constexpr (EPI != Epi::Residual) {
+        if (vec_out && n + 4 <= N) {
+            uint16_t h[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                h[e] = EPI == Epi::Store ? f2h(v[e]) : ew_one<Ew::Silu>(f2h(v[e]), f2h(v2[e]), 0.0f);
+            *(uint2_t*)((uint16_t*)C + at) = (uint2_t){(uint32_t)h[0] | ((uint32_t)h[1] << 16),
+                                                       (uint32_t)h[2] | ((uint32_t)h[3] << 16)};
+            return;
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+        if (n + e < N) epi_store<EPI, F32>(C, at + e, v[e], v2[e], scale);
+}
+
+// One weight matrix of a product (up to three share the activations A: the q, k
+// and v projections in one launch).
+struct GemmGroup {
+    const uint16_t* B;  // [N][K]
+    const uint16_t* B2; // SiluGate: the up weights [N][K]
+    void* C;            // [M][N]
+    uint32_t N;
+    uint32_t tiles;     // skinny: 16-row weight tiles of this group
+    bool vec_out;       // N % 4 == 0 and C aligned for 4-element stores
+};
+
 struct GemmArgs {
     const uint16_t* A; // [M][K]
-    const uint16_t* B; // [N][K]
-    void* C;           // [M][N]
-    uint32_t M, N, K;
-    float scale;       // f32 output only
-    bool vec_out;      // N % 4 == 0: 8- or 16-byte output stores
+    GemmGroup g[3];
+    uint32_t groups;
+    uint32_t M, K;
+    float scale; // f32 output only
 };
 
 // Skinny products (M <= 16 * MT: decode and verify steps).  A work-group of
-// NW waves owns 16 weight rows; its waves split K in 64-wide chunks (wave w
-// takes chunks w, w + NW, ...), so each row is streamed in whole 128-byte
-// lines, U chunks in flight per wave.  The weights are read once for all MT
-// tiles of 16 activation rows.  The waves' partial sums meet in LDS and are
-// added in wave order (deterministic).  Bound: HBM, N*K*2 bytes of weights.
+// NW waves owns 16 weight rows; K is cut into 64-wide chunks (a 128-byte line
+// per weight row), chunk c summed into partial slot c % 16, and wave w owns the
+// slots w, w + NW, ...: each wave streams its rows in whole lines, U chunks in
+// flight, and the weights are read once for all MT tiles of 16 activation
+// rows.  The slots are added as sum over j < 8 of (slot j + slot j + 8), in
+// that order, whatever NW (8: a wave holds both slots of a pair; 16: the pair
+// meets in LDS), so the bits depend on neither NW nor the grouping of the
+// products.  Bound: HBM, N*K*2 bytes of weights.
 constexpr int kSkinnyU = 4;
+constexpr int kSkinnySlots = 16;
 
-template <int MT, int NW, bool VEC, bool F32>
+template <int MT, int NW, bool VEC, bool F32, Epi EPI>
 __global__ __launch_bounds__(NW * 64) void gemm_skinny_kernel(GemmArgs a) {
-    __shared__ float4_t s_part[NW][MT][64];
+    constexpr bool DUAL = EPI == Epi::SiluGate;
+    constexpr int NA = DUAL ? 2 : 1;                 // accumulated products
+    constexpr int SPW = kSkinnySlots / NW;           // slots per wave
+    static_assert(kSkinnyU % SPW == 0, "chunk u of a batch lands in slot u % SPW");
+    __shared__ float4_t s_pair[NA][kSkinnySlots / 2][MT][64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, li = lane & 15, lg = lane >> 4;
-    const uint32_t n0 = blockIdx.x * 16u;
-    const uint64_t wrow = min(n0 + (uint32_t)li, a.N - 1u); // this lane's weight row (clamped)
+    // This work-group's group and tile (uniform selects, no dynamic indexing).
+    uint32_t tile = blockIdx.x;
+    const bool in0 = tile < a.g[0].tiles;
+    if (!in0) tile -= a.g[0].tiles;
+    const bool in1 = !in0 && (a.groups < 3 || tile < a.g[1].tiles);
+    if (!in0 && !in1) tile -= a.g[1].tiles;
+    const GemmGroup& G = in0 ? a.g[0] : (in1 ? a.g[1] : a.g[2]);
+    const uint16_t* B = G.B;
+    const uint16_t* B2 = G.B2;
+    const uint32_t N = G.N;
+    const uint32_t n0 = tile * 16u;
+    const uint64_t wrow = min(n0 + (uint32_t)li, N - 1u); // this lane's weight row (clamped)
     uint64_t arow[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) arow[mt] = min((uint32_t)(mt * 16 + li), a.M - 1u);
-    float4_t acc[MT];
+    float4_t acc[NA][SPW][MT];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) acc[mt] = (float4_t)0.0f;
+    for (int x = 0; x < NA; ++x)
+#pragma unroll
+        for (int j = 0; j < SPW; ++j)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) acc[x][j][mt] = (float4_t)0.0f;
     const uint32_t n_chunks = (a.K + 63u) / 64u;
     for (uint32_t c0 = (uint32_t)wave; c0 < n_chunks; c0 += (uint32_t)(NW * kSkinnyU)) {
-        half8_t wv[kSkinnyU][2];
+        half8_t wv[NA][kSkinnyU][2];
 #pragma unroll
         for (int u = 0; u < kSkinnyU; ++u) {
             const uint32_t k = (c0 + (uint32_t)(u * NW)) * 64u + 8u * (uint32_t)lg;
 #pragma unroll
-            for (int h = 0; h < 2; ++h) wv[u][h] = piece<VEC>(a.B, wrow, a.K, k + 32u * h);
+            for (int h = 0; h < 2; ++h) {
+                wv[0][u][h] = piece<VEC>(B, wrow, a.K, k + 32u * h);
+                if constexpr (DUAL) wv[NA - 1][u][h] = piece<VEC>(B2, wrow, a.K, k + 32u * h);
+            }
         }
 #pragma unroll
         for (int u = 0; u < kSkinnyU; ++u) {
@@ -302,35 +367,64 @@ __global__ __launch_bounds__(NW * 64) void gemm_skinny_kernel(GemmArgs a) {
 #pragma unroll
             for (int h = 0; h < 2; ++h)
 #pragma unroll
-                for (int mt = 0; mt < MT; ++mt)
-                    acc[mt] = mfma(wv[u][h], piece<VEC>(a.A, arow[mt], a.K, k + 32u * h), acc[mt]);
+                for (int mt = 0; mt < MT; ++mt) {
+                    const half8_t xo = piece<VEC>(a.A, arow[mt], a.K, k + 32u * h);
+#pragma unroll
+                    for (int x = 0; x < NA; ++x) acc[x][u % SPW][mt] = mfma(wv[x][u][h], xo, acc[x][u % SPW][mt]);
+                }
         }
     }
+    // Pairs (slot j, slot j + 8) for j < 8 into LDS.
+    if constexpr (SPW == 2) {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) s_part[wave][mt][lane] = acc[mt];
+        for (int x = 0; x < NA; ++x)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) s_pair[x][wave][mt][lane] = acc[x][0][mt] + acc[x][1][mt];
+    } else {
+        if (wave >= kSkinnySlots / 2)
+#pragma unroll
+            for (int x = 0; x < NA; ++x)
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) s_pair[x][wave - kSkinnySlots / 2][mt][lane] = acc[x][0][mt];
+        __syncthreads();
+        if (wave < kSkinnySlots / 2)
+#pragma unroll
+            for (int x = 0; x < NA; ++x)
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+                    s_pair[x][wave][mt][lane] = acc[x][0][mt] + s_pair[x][wave][mt][lane];
+    }
     __syncthreads();
-    // Wave mt' < MT finishes tile mt'; the sums run over the waves in order.
+    // Wave mt' < MT finishes tile mt': the 8 pairs in order.
     if (wave < MT) {
-        float4_t s = s_part[0][wave][lane];
+        float4_t r[NA];
 #pragma unroll
-        for (int w = 1; w < NW; ++w) s += s_part[w][wave][lane];
-        store4<F32>(a.C, a.M, a.N, (uint32_t)(wave * 16 + li), n0 + 4u * (uint32_t)lg, s, a.scale, a.vec_out);
+        for (int x = 0; x < NA; ++x) {
+            r[x] = s_pair[x][0][wave][lane];
+#pragma unroll
+            for (int j = 1; j < kSkinnySlots / 2; ++j) r[x] += s_pair[x][j][wave][lane];
+        }
+        store4<EPI, F32>(G.C, a.M, N, (uint32_t)(wave * 16 + li), n0 + 4u * (uint32_t)lg, r[0], r[NA - 1], a.scale,
+                         G.vec_out);
     }
 }
 
 // General products (prefill-sized M): 128 x 128 output tiles, 4 waves of 64 x 64
 // (4 x 4 MFMA tiles each), k-steps of 32 staged in LDS with the next step's
-// loads in registers while the current step is multiplied.  Bound: the matrix
-// cores for large M, N, K.
+// loads in registers while the current step is multiplied.  One weight matrix
+// (group 0).  Bound: the matrix cores for large M, N, K.
 constexpr int kTileM = 128, kTileN = 128, kTileK = 32, kTilePitch = kTileK + 8; // halves per staged row
 
-template <bool VEC, bool F32>
+template <bool VEC, bool F32, Epi EPI>
 __global__ __launch_bounds__(256) void gemm_tiled_kernel(GemmArgs a) {
+    static_assert(EPI != Epi::SiluGate, "one weight matrix");
     __shared__ __attribute__((aligned(16))) _Float16 sB[2][kTileN * kTilePitch]; // weights
     __shared__ __attribute__((aligned(16))) _Float16 sA[2][kTileM * kTilePitch]; // activations
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, li = lane & 15, lg = lane >> 4;
     const int wn = wave & 1, wm = wave >> 1;
     const uint32_t n0 = blockIdx.x * kTileN, m0 = blockIdx.y * kTileM;
+    const uint16_t* B = a.g[0].B;
+    const uint32_t N = a.g[0].N;
     // Staging: 512 pieces of 8 halves per operand tile, two per thread: piece p =
     // (row p / 4, k 8 * (p % 4)).
     auto load = [&](uint32_t k0, half8_t (&pb)[2], half8_t (&pa)[2]) {
@@ -338,7 +432,7 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(GemmArgs a) {
         for (int j = 0; j < 2; ++j) {
             const int p = tid + 256 * j;
             const uint32_t r = (uint32_t)(p >> 2), k = k0 + 8u * (uint32_t)(p & 3);
-            pb[j] = piece<VEC>(a.B, min(n0 + r, a.N - 1u), a.K, k);
+            pb[j] = piece<VEC>(B, min(n0 + r, N - 1u), a.K, k);
             pa[j] = piece<VEC>(a.A, min(m0 + r, a.M - 1u), a.K, k);
         }
     };
@@ -380,8 +474,9 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(GemmArgs a) {
     for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            store4<F32>(a.C, a.M, a.N, m0 + (uint32_t)(wm * 64 + j * 16 + li), n0 + (uint32_t)(wn * 64 + i * 16 + 4 * lg),
-                        acc[i][j], a.scale, a.vec_out);
+            store4<EPI, F32>(a.g[0].C, a.M, N, m0 + (uint32_t)(wm * 64 + j * 16 + li),
+                             n0 + (uint32_t)(wn * 64 + i * 16 + 4 * lg), acc[i][j], acc[i][j], a.scale,
+                             a.g[0].vec_out);
 }
 
 } // namespace awo

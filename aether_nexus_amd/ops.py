@@ -182,6 +182,37 @@ class OpsEngine:
         self._call("aw_ops_causal_attention", _ptr(q), _ptr(k), _ptr(v), _ptr(output), kv_len, head_dim,
                    cache_tokens, _stream(stream))
 
+    # -- fused forms (no reference counterpart): the same output bits as the separate calls
+    def matmul_add_residual(self, a, b, x, m: int, n: int, k: int, residual_multiplier: float = 1.0,
+                            stream: Optional[int] = None) -> None:
+        """matmul, scale_f16 by ``residual_multiplier``, add_residual into x, in one launch
+        (forward_batch's o_proj and down_proj steps, inference.rs:564-572,592-600)."""
+        _f16(a, m * k, "matmul_add_residual a")
+        _f16(b, n * k, "matmul_add_residual b")
+        _f16(x, m * n, "matmul_add_residual x")
+        self._call("aw_ops_matmul_add_residual", _ptr(a), _ptr(b), _ptr(x), m, n, k, residual_multiplier,
+                   _stream(stream))
+
+    def matmul_silu_gate(self, a, b_gate, b_up, output, m: int, n: int, k: int, stream: Optional[int] = None) -> None:
+        """The gate and up matmuls and silu_gate in one launch (inference.rs:586-591); m <= 64."""
+        _f16(a, m * k, "matmul_silu_gate a")
+        _f16(b_gate, n * k, "matmul_silu_gate b_gate")
+        _f16(b_up, n * k, "matmul_silu_gate b_up")
+        _f16(output, m * n, "matmul_silu_gate output")
+        self._call("aw_ops_matmul_silu_gate", _ptr(a), _ptr(b_gate), _ptr(b_up), _ptr(output), m, n, k,
+                   _stream(stream))
+
+    def matmul_qkv(self, a, b_q, b_k, b_v, q, k_out, v_out, m: int, n_q: int, n_kv: int, k: int,
+                   stream: Optional[int] = None) -> None:
+        """The q, k and v matmuls in one launch (inference.rs:518-523)."""
+        _f16(a, m * k, "matmul_qkv a")
+        for t, n, w in ((b_q, n_q, "b_q"), (b_k, n_kv, "b_k"), (b_v, n_kv, "b_v")):
+            _f16(t, n * k, f"matmul_qkv {w}")
+        for t, n, w in ((q, n_q, "q"), (k_out, n_kv, "k_out"), (v_out, n_kv, "v_out")):
+            _f16(t, m * n, f"matmul_qkv {w}")
+        self._call("aw_ops_matmul_qkv", _ptr(a), _ptr(b_q), _ptr(b_k), _ptr(b_v), _ptr(q), _ptr(k_out), _ptr(v_out),
+                   m, n_q, n_kv, k, _stream(stream))
+
     def multihead_attention(self, q, k_cache, v_cache, output, kv_len: int, head_dim: int, q_heads: int,
                             kv_heads: int, num_queries: int, cache_tokens: Optional[int] = None,
                             stream: Optional[int] = None) -> None:

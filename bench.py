@@ -572,7 +572,10 @@ def ops_bench(engine, seed, read_peak_gbps, reps=10):
       RoPE, the cache append, multihead attention over 4096 cached tokens, the
       output product, residual, RMSNorm, gated MLP and residual, then the final
       norm and the f32 lm_head, captured in one HIP graph, random weights.
-      Bytes per forward: every weight once plus the K and V caches read."""
+      Bytes per forward: every weight once plus the K and V caches read.  The
+      "_fused" forwards make the same computation with the fused products (q/k/v
+      in one launch, the residual adds and the SiLU gate in the products'
+      stores) and must give the same logits bit for bit."""
     import torch
     from aether_nexus_amd.ops import OpsEngine
     c = LLAMA8B
@@ -635,9 +638,13 @@ def ops_bench(engine, seed, read_peak_gbps, reps=10):
            "kc": randn(S, hkv, hd), "vc": randn(S, hkv, hd)} for _ in range(L)]
     embed, lm_head, final_ln = randn(V, H), randn(V, H, std=H ** -0.5), randn(H, std=0.1) + 1
     res["forward"] = {}
-    for name, t in (("decode", 1), ("verify_3_drafts", 4)):
+    ref_logits = {}
+    # decode, then verify: each fused run directly after the separate calls it must equal (a
+    # forward rewrites the cache rows at its own positions, which the other step type reads).
+    for name, t, fused in (("decode", 1, False), ("decode_fused", 1, True), ("verify_3_drafts", 4, False),
+                           ("verify_3_drafts_fused", 4, True)):
         pos = S - t  # the new tokens fill the cache's last positions: attention over all 4096
-        ids = torch.randint(0, V, (t,), generator=g, device="cuda:0", dtype=torch.int32)
+        ids = torch.arange(t, dtype=torch.int32, device="cuda:0") * 7919 + 11
         hid, norm = (torch.empty((t, H), dtype=torch.float16, device="cuda:0") for _ in range(2))
         q, k, v = (torch.empty((t, n), dtype=torch.float16, device="cuda:0") for n in (H, kvd, kvd))
         att, proj, down = (torch.empty((t, H), dtype=torch.float16, device="cuda:0") for _ in range(3))
@@ -648,6 +655,19 @@ def ops_bench(engine, seed, read_peak_gbps, reps=10):
                     gate=gate, up=up, ffn=ffn, logits=logits):
             ops.embed_lookup(ids, embed, hid, H, t, V, stream=s)
             for w in lw:
+                if fused:  # the same bits in 10 launches per layer instead of 16
+                    ops.rms_norm(hid, w["ln1"], norm, H, t, c["eps"], stream=s)
+                    ops.matmul_qkv(norm, w["wq"], w["wk"], w["wv"], q, k, v, t, H, kvd, H, stream=s)
+                    ops.rope(q, k, t, hq, hkv, hd, pos, c["theta"], stream=s)
+                    ops.copy_buffer(k, w["kc"], kvd * t, 0, pos * kvd, stream=s)
+                    ops.copy_buffer(v, w["vc"], kvd * t, 0, pos * kvd, stream=s)
+                    ops.multihead_attention(q, w["kc"], w["vc"], att, pos + t, hd, hq, hkv, t, cache_tokens=S,
+                                            stream=s)
+                    ops.matmul_add_residual(att, w["wo"], hid, t, H, H, 1.0, stream=s)
+                    ops.rms_norm(hid, w["ln2"], norm, H, t, c["eps"], stream=s)
+                    ops.matmul_silu_gate(norm, w["wg"], w["wu"], ffn, t, I, H, stream=s)
+                    ops.matmul_add_residual(ffn, w["wd"], hid, t, H, I, 1.0, stream=s)
+                    continue
                 ops.rms_norm(hid, w["ln1"], norm, H, t, c["eps"], stream=s)
                 ops.matmul(norm, w["wq"], q, t, H, H, stream=s)
                 ops.matmul(norm, w["wk"], k, t, kvd, H, stream=s)
@@ -669,9 +689,18 @@ def ops_bench(engine, seed, read_peak_gbps, reps=10):
         ms = _graph_time(forward, st, reps)
         ops.check_device_errors(st.cuda_stream)
         assert torch.isfinite(logits).all(), "non-finite logits"
+        # Every replay starts from the same embedding rows and rewrites the same cache
+        # positions, so the fused forward must give the unfused one's logits bit for bit.
+        base = name.replace("_fused", "")
+        if fused:
+            same = bool(torch.equal(logits, ref_logits[base]))
+            assert same, f"{name}: logits differ from the separate calls"
+        else:
+            ref_logits[name] = logits.clone()
         nbytes = L * (2 * H * H + 2 * kvd * H + 3 * I * H + 2 * H) * 2 + V * H * 2 + L * 2 * S * kvd * 2
         gbps = nbytes / (ms * 1e-3) / 1e9
-        res["forward"][name] = {"new_tokens": t, "ms_per_forward": round(ms, 4), "tokens_per_s": round(t / (ms * 1e-3), 1),
+        res["forward"][name] = {"new_tokens": t, "fused": fused, "launches_per_layer": 10 if fused else 16,
+                                "ms_per_forward": round(ms, 4), "tokens_per_s": round(t / (ms * 1e-3), 1),
                                 "bytes_per_forward": nbytes, "achieved_gbps": round(gbps, 1),
                                 "frac_of_peak": round(gbps / PEAK_HBM_GBPS, 4),
                                 "frac_of_read_peak": round(gbps / read_peak_gbps, 4)}

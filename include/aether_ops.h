@@ -104,6 +104,32 @@ int aw_ops_causal_attention(aw_engine* engine, const uint16_t* q, const uint16_t
 
 /* Ops::multihead_attention is aw_multihead_attention_device (aether_weaver.h). */
 
+/* ---- fused forms (no reference counterpart) --------------------------------
+ * Pairs and triples of the calls above that forward_batch makes back to back
+ * (inference.rs:518-600), each in one launch, with the output bits of the
+ * separate calls: a product's bits do not depend on how many products share a
+ * launch (its K partial sums are added in a fixed order). */
+
+/* aw_ops_matmul, aw_ops_scale_f16 of its output by residual_multiplier, then
+ * aw_ops_add_residual of it into x (ops.rs:266-296, :350-363, :315-327; the
+ * o_proj and down_proj steps, inference.rs:564-572,592-600):
+ * p = f16(a . b^T), p = f16(p * residual_multiplier), x [m][n] = f16(x + p).
+ * A multiplier of 1 (the reference skips the scale then) gives the same bits. */
+int aw_ops_matmul_add_residual(aw_engine* engine, const uint16_t* a, const uint16_t* b, uint16_t* x, uint32_t m,
+                               uint32_t n, uint32_t k, float residual_multiplier, void* hip_stream);
+
+/* aw_ops_matmul with b_gate and with b_up, then aw_ops_silu_gate (ops.rs:266-312;
+ * inference.rs:586-591): output [m][n] = f16(silu(f16(a . b_gate^T)) * f16(a . b_up^T)).
+ * m <= 64 (decode and verify steps); larger m returns AW_E_UNSUPPORTED. */
+int aw_ops_matmul_silu_gate(aw_engine* engine, const uint16_t* a, const uint16_t* b_gate, const uint16_t* b_up,
+                            uint16_t* output, uint32_t m, uint32_t n, uint32_t k, void* hip_stream);
+
+/* The three aw_ops_matmul calls of the q, k and v projections (inference.rs:518-523):
+ * q [m][n_q] = a . b_q^T, k_out [m][n_kv] = a . b_k^T, v_out [m][n_kv] = a . b_v^T. */
+int aw_ops_matmul_qkv(aw_engine* engine, const uint16_t* a, const uint16_t* b_q, const uint16_t* b_k,
+                      const uint16_t* b_v, uint16_t* q, uint16_t* k_out, uint16_t* v_out, uint32_t m, uint32_t n_q,
+                      uint32_t n_kv, uint32_t k, void* hip_stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -200,6 +200,69 @@ def test_matmul_scaled(ops, m, n, k):
     check_product(host(out), a, b, k, f"matmul_scaled {m}x{n}x{k}", scale=1.0 / 6.0, f16_out=False)
 
 
+@pytest.mark.parametrize("m", [1, 5, 16, 17, 33, 64, 65])
+def test_fused_products_match_the_separate_calls(ops, m):
+    """matmul_add_residual, matmul_silu_gate and matmul_qkv give the bits of the
+    calls they fuse (inference.rs:518-600), at every skinny tile count and in the
+    tiled range (m = 65: the residual form; the fused gate is refused there)."""
+    import torch
+    from aether_nexus_amd.types import AW_E_UNSUPPORTED
+    from aether_nexus_amd.weaver import WeaverError
+    rng = np.random.default_rng(100 + m)
+    n, nkv, k = 96, 40, 264
+    a = dev(f16(rng, m, k))
+
+    def z(*shape):
+        return torch.zeros(shape, dtype=torch.float16, device="cuda:0")
+    for mult in (1.0, 0.5):
+        b = dev(f16(rng, n, k, scale=0.1))
+        x0 = f16(rng, m, n)
+        x1, x2, p = dev(x0), dev(x0), z(m, n)
+        ops.matmul(a, b, p, m, n, k)
+        if mult != 1.0:
+            ops.scale_f16(p, m * n, mult)
+        ops.add_residual(x1, p, m * n)
+        ops.matmul_add_residual(a, b, x2, m, n, k, mult)
+        assert torch.equal(x1.view(torch.int16), x2.view(torch.int16)), ("residual", mult)
+    bg, bu = dev(f16(rng, n, k, scale=0.1)), dev(f16(rng, n, k, scale=0.1))
+    if m <= 64:
+        g, u, f1, f2 = z(m, n), z(m, n), z(m, n), z(m, n)
+        ops.matmul(a, bg, g, m, n, k)
+        ops.matmul(a, bu, u, m, n, k)
+        ops.silu_gate(g, u, f1, m * n)
+        ops.matmul_silu_gate(a, bg, bu, f2, m, n, k)
+        assert torch.equal(f1.view(torch.int16), f2.view(torch.int16)), "silu gate"
+    else:
+        with pytest.raises(WeaverError) as e:
+            ops.matmul_silu_gate(a, bg, bu, z(m, n), m, n, k)
+        assert e.value.status == AW_E_UNSUPPORTED
+    bq, bk, bv = dev(f16(rng, n, k, scale=0.1)), dev(f16(rng, nkv, k, scale=0.1)), dev(f16(rng, nkv, k, scale=0.1))
+    sep = [z(m, n), z(m, nkv), z(m, nkv)]
+    for w, o, nn in zip((bq, bk, bv), sep, (n, nkv, nkv)):
+        ops.matmul(a, w, o, m, nn, k)
+    fused = [z(m, n), z(m, nkv), z(m, nkv)]
+    ops.matmul_qkv(a, bq, bk, bv, *fused, m, n, nkv, k)
+    for s_, f_ in zip(sep, fused):
+        assert torch.equal(s_.view(torch.int16), f_.view(torch.int16)), "qkv"
+
+
+def test_product_bits_do_not_depend_on_the_wave_count(ops):
+    """A product takes 16 waves per weight tile when the tiles are few and 8 when
+    they are many; the same rows give the same bits either way (the K partial
+    sums are added in one fixed order)."""
+    import torch
+    rng = np.random.default_rng(5)
+    k = 1000
+    for m in (1, 30):
+        a = dev(f16(rng, m, k))
+        big = f16(rng, 20000, k, scale=0.05)  # 1250 weight tiles: 8 waves
+        small_out = torch.zeros((m, 96), dtype=torch.float16, device="cuda:0")
+        big_out = torch.zeros((m, 20000), dtype=torch.float16, device="cuda:0")
+        ops.matmul(a, dev(big[:96]), small_out, m, 96, k)  # 6 tiles: 16 waves
+        ops.matmul(a, dev(big), big_out, m, 20000, k)
+        assert torch.equal(small_out.view(torch.int16), big_out[:, :96].contiguous().view(torch.int16)), m
+
+
 def test_causal_attention(ops):
     rng = np.random.default_rng(11)
     for kv_len, hd in ((100, 128), (16, 64), (1, 128)):
