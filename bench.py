@@ -877,14 +877,15 @@ def traffic_file(layout: str) -> Path:
 
 
 def sources_digest() -> str:
-    """sha256 over the HIP sources, so a traffic profile is only used for the
-    kernels it was measured on."""
+    """sha256 over the decode path's HIP sources (the kernels and their
+    launches), so a traffic profile is only used for the kernels it was
+    measured on."""
     import hashlib
     h = hashlib.sha256()
-    for f in sorted((ROOT / "aether_nexus_amd" / "csrc").glob("*")):
-        if f.suffix in (".hip", ".hpp", ".h"):
-            h.update(f.name.encode())
-            h.update(f.read_bytes())
+    for name in ("weaver_engine.hip", "weaver_kernels.hpp"):
+        f = ROOT / "aether_nexus_amd" / "csrc" / name
+        h.update(f.name.encode())
+        h.update(f.read_bytes())
     return h.hexdigest()[:16]
 
 
