@@ -531,16 +531,26 @@ constexpr int kColdCPT = 2;
 constexpr int kColdPD = 4;
 
 // cold_kernel instance for a row chunk of 1, 2 or 4, a power-of-two dictionary
-// or not, and an f16 or fp32 q_latent table.
-const void* cold_kernel_fn(uint32_t rc, bool pow2, bool qf32) {
-#define AW_COLD(RCV) \
-    { {(const void*)aw::cold_kernel<RCV, kColdCPT, kColdPD, false, false>,  \
-       (const void*)aw::cold_kernel<RCV, kColdCPT, kColdPD, false, true>},  \
-      {(const void*)aw::cold_kernel<RCV, kColdCPT, kColdPD, true, false>,   \
-       (const void*)aw::cold_kernel<RCV, kColdCPT, kColdPD, true, true>} }
-    static const void* const table[3][2][2] = {AW_COLD(1), AW_COLD(2), AW_COLD(4)};
+// or not, an f16 or fp32 q_latent table, and buffer loads (a layer's pool within
+// aw::kColdWindow bytes) or 64-bit addresses.
+const void* cold_kernel_fn(uint32_t rc, bool pow2, bool qf32, bool buf) {
+#define AW_COLD_B(RCV, P2)                                                                    \
+    { {(const void*)aw::cold_kernel<RCV, kColdCPT, kColdPD, P2, false, false>,              \
+       (const void*)aw::cold_kernel<RCV, kColdCPT, kColdPD, P2, false, true>},              \
+      {(const void*)aw::cold_kernel<RCV, kColdCPT, kColdPD, P2, true, false>,               \
+       (const void*)aw::cold_kernel<RCV, kColdCPT, kColdPD, P2, true, true>} }
+#define AW_COLD(RCV) {AW_COLD_B(RCV, false), AW_COLD_B(RCV, true)}
+    static const void* const table[3][2][2][2] = {AW_COLD(1), AW_COLD(2), AW_COLD(4)};
 #undef AW_COLD
-    return table[rc == 4 ? 2 : (rc == 2 ? 1 : 0)][pow2 ? 1 : 0][qf32 ? 1 : 0];
+#undef AW_COLD_B
+    return table[rc == 4 ? 2 : (rc == 2 ? 1 : 0)][pow2 ? 1 : 0][qf32 ? 1 : 0][buf ? 1 : 0];
+}
+
+// Buffer loads cover the codes when a layer's pool fits the resource window and
+// the largest in-block token offset added to the "no code" offset stays below 2^32.
+bool cold_uses_buffer(const aw_decode_desc* d) {
+    const uint64_t blk_bytes = (uint64_t)kBlock * d->kv_heads * 16u;
+    return d->kv_heads <= 256 && d->cold_blocks * blk_bytes <= aw::kColdWindow;
 }
 
 int launch_cold(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* ws, hipStream_t st) {
@@ -590,7 +600,7 @@ int launch_cold(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* ws
     a.n_wg = (uint32_t)n_wg;
     const size_t smem = aw::cold_smem_bytes(A, (int)o.rc, a.tokens_per_split, o.qf32 ? 4u : 2u);
     const bool pow2 = (A & (A - 1u)) == 0u;
-    const void* fn = cold_kernel_fn(o.rc, pow2, o.qf32);
+    const void* fn = cold_kernel_fn(o.rc, pow2, o.qf32, cold_uses_buffer(d));
     // One resident round of work-groups (a multiple of 8: each keeps its XCD).
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, aw::kColdThreads, smem) != hipSuccess || per_cu < 1)
@@ -945,7 +955,7 @@ int aw_engine_create(int device, aw_engine** out) {
     e->n_cu = (uint32_t)prop.multiProcessorCount;
     int rc = AW_OK;
     if (!rc) rc = check_kernel(e, aw::hot_kernel<128, 1, false>, "hot_kernel");
-    if (!rc) rc = check_kernel(e, aw::cold_kernel<4, kColdCPT, kColdPD, true, false>, "cold_kernel");
+    if (!rc) rc = check_kernel(e, aw::cold_kernel<4, kColdCPT, kColdPD, true, false, true>, "cold_kernel");
     if (!rc) rc = check_kernel(e, aw::finish_kernel<128, true>, "finish_kernel");
     if (rc) {
         delete e;
@@ -966,8 +976,9 @@ int aw_engine_create(int device, aw_engine** out) {
         for (uint32_t rcv : {1u, 2u, 4u})
             for (bool p2 : {false, true})
                 for (bool qf : {false, true})
-                    (void)hipFuncSetAttribute(cold_kernel_fn(rcv, p2, qf), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                              (int)e->max_lds);
+                    for (bool bf : {false, true})
+                        (void)hipFuncSetAttribute(cold_kernel_fn(rcv, p2, qf, bf),
+                                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)e->max_lds);
         const void* fin[] = {(const void*)aw::finish_kernel<128, true>, (const void*)aw::finish_kernel<128, false>,
                              (const void*)aw::finish_kernel<64, true>, (const void*)aw::finish_kernel<64, false>};
         for (const void* f : fin)

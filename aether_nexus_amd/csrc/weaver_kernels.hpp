@@ -567,12 +567,18 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu((RT == 1 && 
 // ----------------------------------------------- cold pool, scores + bins
 //
 // Work item = (layer*batch+seq, chunk of RC query rows, split) x kv head g.
-// LDS: q_latent table [A][RC] f16; NP = ceil(RC/2) planes of A 64-bit bins,
-// each bin holding two rows' sums as 32-bit fixed point; the split's block refs.
-// Planes [NP][A] rather than [A][NP]: a wave's 64 random atoms then spread
-// over every bank pair of the LDS (measured on gfx950: ds_add_u64 at random
-// atoms 0.21 cycles per lane and CU in planes, 0.28 with the 16-byte atom
-// stride of [A][2], 0.11 with no bank conflicts).
+// LDS: the q_latent table of the RC rows and NP = ceil(RC/2) 64-bit bins per
+// atom, each bin holding two rows' sums as 32-bit fixed point; the split's
+// block refs.
+//   RC = 4, f16 table: one 24-byte record per atom, [bin rows 0-1][bin rows
+//     2-3][q_latent rows 0-3], so one address (atom * 24) serves the table read
+//     and both bins.  6 * atom mod 64 takes every even bank, so a wave's 64
+//     random atoms spread over the bank pairs as they do in separate planes.
+//   otherwise: table [A][RC], then planes [NP][A] of bins.  Planes rather than
+//     [A][NP]: a wave's 64 random atoms then spread over every bank pair of the
+//     LDS (measured on gfx950: ds_add_u64 at random atoms 0.21 cycles per lane
+//     and CU in planes, 0.28 with the 16-byte atom stride of [A][2], 0.11 with
+//     no bank conflicts).
 //
 // Integer bins: on gfx950 an LDS ds_add_f32 retires about one lane per 3
 // cycles per CU whatever the addresses, ds_add_u64 about one lane per 0.3
@@ -595,19 +601,35 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu((RT == 1 && 
 // split is recomputed exactly: a pass for the per-row maxima, a pass for the
 // exact bound, a pass for the bins.
 //
-// Every global load of the streaming loop is unconditional (out-of-range and
-// bad-ref tokens read an all-zero code and get p = 0 by a select), so the
+// Code loads.  BUF (a layer's pool of at most kColdWindow bytes): buffer loads
+// through a resource whose base is the item's kv head in the layer's pool; the
+// staged block refs are byte offsets (ref * block bytes) and a bad ref or a
+// token past the split becomes kBadCodeOff, which lies past the resource's
+// range, so the load returns the all-zero code.  Otherwise 64-bit addresses,
+// bad refs reading g_zero_code.  Every load of the streaming loop is
+// unconditional (prefetches past the split re-read its last tile), so the
 // compiler can count loads in flight and the PD-deep ring really prefetches.
+// Tiles wholly inside the split, in a split without bad refs, are consumed
+// without per-token masks; the split's last partial tile masks p to zero for
+// tokens that read the zero code.
 //
 // The kv heads of one (sequence, chunk, split) run on one XCD (work-groups are
 // dealt round-robin over the 8 XCDs), so the 128-byte lines interleaving their
 // 16-byte codes come from HBM once per XCD L2.
-// All-zero code read by tokens outside the split or behind a bad ref; global
-// (not constant) memory, so every code load stays a global load.
+// All-zero code read by tokens behind a bad ref on the 64-bit address path;
+// global (not constant) memory, so every code load stays a global load.
 __device__ __attribute__((aligned(16))) uint4_t g_zero_code = {0u, 0u, 0u, 0u};
 
 constexpr float kMagic = 12582912.0f;                 // 1.5 * 2^23
 constexpr uint64_t kMagic2 = 0x4B4000004B400000ull;   // two magic patterns
+constexpr uint32_t kBadCodeOff = 0xFFFF0000u;         // staged offset of a token without a code
+constexpr uint64_t kColdWindow = kBadCodeOff;         // largest layer pool (bytes) the buffer loads cover
+constexpr uint32_t kColdRefPad = 16;                  // staged refs are padded to whole wave tiles
+constexpr uint32_t kBufferWord3 = 0x00020000u;        // gfx9 buffer resource word 3 (32-bit data format)
+constexpr uint32_t kColdRec = 24;                     // bytes of an RC = 4 f16 atom record
+
+typedef uint16_t ushort2_t __attribute__((ext_vector_type(2)));
+typedef int16_t short2_t __attribute__((ext_vector_type(2)));
 
 // One work item `wg` (its index in the full grid of work items; the kernel below
 // walks them persistently, one work-group per CU slot).
@@ -616,13 +638,17 @@ constexpr uint64_t kMagic2 = 0x4B4000004B400000ull;   // two magic patterns
 // takes tiles w, w + NW, w + 2*NW, ... (so the first NW tiles, the planning
 // sample, cover the split's first NT*CPT tokens).  The assignment is static, so
 // every float sum runs in the same order on every call.
-template <int RC, int CPT, int PD, bool POW2, bool QF32>
+template <int RC, int CPT, int PD, bool POW2, bool QF32, bool BUF>
 __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
     using QT = std::conditional_t<QF32, float, _Float16>; // q_latent table element
     constexpr int NT = kColdThreads, NW = NT / 64, NP = (RC + 1) / 2;
     constexpr int NB = RC + 2;      // values of the end-of-split reductions
-    constexpr int NR = 2 * RC + 2;  // LDS slots per wave: the plan's (max, sum) pairs and max|c|
+    constexpr int NR = 2 * RC + 3;  // LDS slots per wave: the plan's (max, sum) pairs, max|c|, bad refs
     constexpr uint32_t WT = 64u * CPT; // tokens of one wave tile
+    constexpr uint32_t RPT = WT / 16;  // block refs of one wave tile
+    static_assert(kColdRefPad % RPT == 0, "ref padding");
+    constexpr bool REC = RC == 4 && !QF32;
+    constexpr uint32_t kBad = BUF ? kBadCodeOff : ~0u;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6); // uniform, so tile branches stay scalar
@@ -655,54 +681,82 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
     }
 
     const uint32_t qtab_bytes = (A * RC * (uint32_t)sizeof(QT) + 15) & ~15u;
+    const uint32_t tab_bytes = REC ? A * kColdRec : qtab_bytes + A * NP * 8u;
     const uint32_t n_blk = (t_end - t_begin + 15) / 16; // t_begin is a multiple of 16
     const uint32_t n_wt = (t_end - t_begin + WT - 1) / WT;
-    QT* qtab = (QT*)smem;
-    uint64_t* bins = (uint64_t*)(smem + qtab_bytes);       // [NP][A]: one plane per row pair
-    uint32_t* sref = (uint32_t*)(bins + (uint64_t)A * NP); // [n_blk] physical blocks, ~0 = invalid
-    float* red = (float*)(sref + ((n_blk + 3) & ~3u));    // [NW][NR]
+    const uint32_t n_ref = n_wt * RPT;                   // staged refs, padded to whole wave tiles
+    QT* qtab = (QT*)smem;                                  // [A][RC] (not REC)
+    uint64_t* bins = (uint64_t*)(smem + qtab_bytes);       // [NP][A] (not REC)
+    uint32_t* sref = (uint32_t*)(smem + tab_bytes);        // [n_ref]: staged block refs, kBad = none
+    float* red = (float*)(sref + ((n_ref + 3) & ~3u));    // [NW][NR]
+    // q_latent values of atom `at` (RC of them) and its bin of row pair pp.
+    auto qrow = [&](uint32_t at) -> const QT* {
+        if constexpr (REC) return (const QT*)(smem + at * kColdRec + 16u);
+        else return qtab + at * RC;
+    };
+    auto binp = [&](uint32_t at, int pp) -> uint64_t* {
+        if constexpr (REC) return (uint64_t*)(smem + at * kColdRec + 8u * (uint32_t)pp);
+        else return bins + (uint32_t)pp * A + at;
+    };
 
     const uint4_t* cold = a.cold + (uint64_t)l * a.cold_layer;
     const uint64_t blk_codes = (uint64_t)kBlockTokens * a.kv_heads;
     const uint32_t* grefs = a.refs + (uint64_t)l * a.refs_layer + (uint64_t)(lb % a.batch) * a.refs_stride +
                             a.hot_count + t_begin / 16;
     const float sl = a.scale_log2;
-
-    // Token of lane `lane`, slot kk of wave tile `tile`.
-    auto tok = [&](uint32_t tile, int kk) { return t_begin + tile * WT + (uint32_t)kk * 64u + (uint32_t)lane; };
-    // Refs of a wave tile from LDS (~0 past the split or behind a bad ref).
-    auto tile_refs = [&](uint32_t tile, uint32_t (&rb)[CPT]) {
-#pragma unroll
-        for (int kk = 0; kk < CPT; ++kk) {
-            const uint32_t t = tok(tile, kk);
-            rb[kk] = t < t_end ? sref[(t - t_begin) >> 4] : ~0u;
+    // Token slot of this lane inside its block: wave tiles start on block boundaries.
+    const uint32_t lane_tok = (uint32_t)lane & 15u;
+    const uint32_t lane_off = BUF ? lane_tok * a.s_tok * 16u : 0u;
+    __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)0, (short)0, 0, (int)kBufferWord3);
+    if constexpr (BUF) {
+        const uint64_t head0 = (uint64_t)g * a.s_head; // codes before this kv head's first code
+        const uint64_t span = a.cold_blocks * blk_codes * 16u - head0 * 16u;
+        rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)(cold + head0), (short)0, (int)(uint32_t)min(span, kColdWindow),
+                                                 (int)kBufferWord3);
+    }
+    // Staged entry of block ref `ref` (kBad when outside the pool).
+    auto stage_ref = [&](uint32_t ref) -> uint32_t {
+        ref &= kRefMask;
+        if (ref >= a.cold_blocks) return kBad;
+        return BUF ? ref * (uint32_t)(blk_codes * 16u) : ref;
+    };
+    // The code of this lane's token in the block of staged entry e.
+    auto code_at = [&](uint32_t e) -> uint4_t {
+        if constexpr (BUF) {
+            return __builtin_amdgcn_raw_buffer_load_b128(rsrc, (int)(e + lane_off), 0, 0);
+        } else {
+            const uint4_t* p = e != ~0u ? cold + (uint64_t)e * blk_codes + lane_tok * a.s_tok + (uint64_t)g * a.s_head
+                                        : &g_zero_code;
+            return *p;
         }
     };
-    // Codes of a wave tile for this kv head; invalid tokens read the zero code.
-    // The load itself is unconditional.
-    auto tile_codes = [&](uint32_t tile, const uint32_t (&rb)[CPT], uint4_t (&buf)[CPT], bool (&ok)[CPT]) {
+    // Staged entries of wave tile `tile` (< n_wt) from LDS, and their codes.
+    auto tile_refs = [&](uint32_t tile, uint32_t (&rb)[CPT]) {
+        const uint32_t* sp = sref + tile * RPT + ((uint32_t)lane >> 4);
 #pragma unroll
-        for (int kk = 0; kk < CPT; ++kk) {
-            ok[kk] = rb[kk] != ~0u;
-            const uint4_t* p = ok[kk] ? cold + (uint64_t)rb[kk] * blk_codes + (tok(tile, kk) & 15u) * a.s_tok + g * a.s_head
-                                      : &g_zero_code;
-            buf[kk] = *p;
-        }
+        for (int kk = 0; kk < CPT; ++kk) rb[kk] = sp[4 * kk];
+    };
+    auto tile_codes = [&](const uint32_t (&rb)[CPT], uint4_t (&buf)[CPT]) {
+#pragma unroll
+        for (int kk = 0; kk < CPT; ++kk) buf[kk] = code_at(rb[kk]);
     };
     auto load_tile = [&](uint32_t tile, uint4_t (&buf)[CPT], bool (&ok)[CPT]) {
         uint32_t rb[CPT];
-        tile_refs(tile, rb);
-        tile_codes(tile, rb, buf, ok);
+        tile_refs(min(tile, n_wt - 1u), rb);
+        tile_codes(rb, buf);
+#pragma unroll
+        for (int kk = 0; kk < CPT; ++kk) ok[kk] = tile < n_wt && rb[kk] != kBad;
     };
     // Atom indices of a code word, always inside the tables: a power-of-two
     // dictionary masks them (any bit outside the mask is recorded in `oob`),
     // others are clamped (recorded when clamping changed them).
     auto atoms = [&](const uint4_t cw, uint32_t (&ia)[4], uint32_t& oob) {
         if constexpr (POW2) {
-            ia[0] = cw[0] & (A - 1u);
-            ia[1] = (cw[0] >> 16) & (A - 1u);
-            ia[2] = cw[1] & (A - 1u);
-            ia[3] = (cw[1] >> 16) & (A - 1u);
+            const uint32_t am = (A - 1u) & 0xFFFFu; // A <= 65536: indices stay 16-bit (24-bit products)
+            ia[0] = cw[0] & am;
+            ia[1] = (cw[0] >> 16) & am;
+            ia[2] = cw[1] & am;
+            ia[3] = (cw[1] >> 16) & am;
             oob |= cw[0] | cw[1];
         } else {
             const uint32_t r0 = cw[0] & 0xFFFFu, r1 = cw[0] >> 16, r2 = cw[1] & 0xFFFFu, r3 = cw[1] >> 16;
@@ -723,7 +777,7 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const float cj = (float)coef(cw, j);
-            const QT* qp = qtab + ia[j] * RC;
+            const QT* qp = qrow(ia[j]);
             if constexpr (RC == 4 && QF32) {
                 const float4_t qv = *(const float4_t*)qp;
 #pragma unroll
@@ -781,7 +835,7 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
                             : 0;
     }
     // Atom-contiguous rows (s_a == 1, q_latent's layout) load as 16-byte pieces of
-    // 8 f16 (or 4 fp32) atoms per row, interleaved into [A][RC] in registers.
+    // 8 f16 (or 4 fp32) atoms per row, interleaved into the table in registers.
     const bool qvec = QF32 || (a.s_a == 1 && (A % 8) == 0 && ((uintptr_t)a.ql & 15u) == 0);
     constexpr uint32_t QPA = QF32 ? 4u : 8u; // atoms per 16-byte piece
     uint4_t qw[RC];
@@ -821,7 +875,7 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
                 (void)hv; // the f16 table only
             } else if constexpr (RC == 4) {
                 half4_t v4 = {hv[0], hv[1], hv[2], hv[3]};
-                *(half4_t*)(qtab + (a8 * 8 + e) * 4) = v4;
+                *(half4_t*)qrow(a8 * 8 + e) = v4;
             } else {
 #pragma unroll
                 for (int rr = 0; rr < RC; ++rr) qtab[(a8 * 8 + e) * RC + rr] = hv[rr];
@@ -830,8 +884,10 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
     };
 
     // Ring of PD wave tiles of codes in flight per wave; slot d holds tile tl[d].
+    // The first fill takes its refs from global memory (the LDS copy is staged
+    // below); slot 0's validity feeds the plan.
     uint4_t ring[PD][CPT];
-    bool rv[PD][CPT];
+    bool rv0[CPT];
     uint32_t tl[PD];
     {
         uint32_t rg[PD][CPT];
@@ -839,17 +895,21 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
         for (int d = 0; d < PD; ++d) {
             tl[d] = (uint32_t)(wave + d * NW);
 #pragma unroll
-            for (int kk = 0; kk < CPT; ++kk) rg[d][kk] = grefs[min((tok(tl[d], kk) - t_begin) >> 4, n_blk - 1)];
+            for (int kk = 0; kk < CPT; ++kk) {
+                const uint32_t t = t_begin + tl[d] * WT + (uint32_t)kk * 64u + (uint32_t)lane;
+                rg[d][kk] = grefs[min((t - t_begin) >> 4, n_blk - 1)];
+            }
         }
 #pragma unroll
         for (int d = 0; d < PD; ++d) {
             uint32_t rb[CPT];
 #pragma unroll
             for (int kk = 0; kk < CPT; ++kk) {
-                const uint32_t ref = rg[d][kk] & kRefMask;
-                rb[kk] = (tok(tl[d], kk) < t_end && ref < a.cold_blocks) ? ref : ~0u;
+                const uint32_t t = t_begin + tl[d] * WT + (uint32_t)kk * 64u + (uint32_t)lane;
+                rb[kk] = t < t_end ? stage_ref(rg[d][kk]) : kBad;
+                if (d == 0) rv0[kk] = rb[kk] != kBad;
             }
-            tile_codes(tl[d], rb, ring[d], rv[d]);
+            tile_codes(rb, ring[d]);
         }
     }
     // Tables into LDS: q_latent rows of this chunk (rows past R are zero) and the
@@ -871,32 +931,46 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
             put_q(a8, w);
         }
     } else {
-        for (uint32_t at = tid; at < A; at += NT)
+        for (uint32_t at = tid; at < A; at += NT) {
+            _Float16 hv[RC];
 #pragma unroll
             for (int rr = 0; rr < RC; ++rr)
-                qtab[at * RC + rr] =
-                    __builtin_bit_cast(_Float16, rok[rr] ? a.ql[rbase[rr] + (uint64_t)at * a.s_a] : (uint16_t)0);
-    }
-    auto put_ref = [&](uint32_t i, uint32_t ref) {
-        ref &= kRefMask;
-        if (ref >= a.cold_blocks) {
-            flag_error(a.err, kErrColdRef);
-            ref = ~0u;
+                hv[rr] = __builtin_bit_cast(_Float16, rok[rr] ? a.ql[rbase[rr] + (uint64_t)at * a.s_a] : (uint16_t)0);
+            if constexpr (REC) {
+                *(half4_t*)qrow(at) = (half4_t){hv[0], hv[1], hv[2], hv[3]};
+            } else {
+#pragma unroll
+                for (int rr = 0; rr < RC; ++rr) qtab[at * RC + rr] = hv[rr];
+            }
         }
-        sref[i] = ref;
+    }
+    bool bad = false; // a bad ref in the split (recorded, and its tokens masked)
+    auto put_ref = [&](uint32_t i, uint32_t ref) {
+        uint32_t e = kBad;
+        if (i < n_blk) {
+            e = stage_ref(ref);
+            if (e == kBad) {
+                flag_error(a.err, kErrColdRef);
+                bad = true;
+            }
+        }
+        sref[i] = e;
     };
 #pragma unroll
     for (int j = 0; j < SR; ++j)
-        if (tid + (uint32_t)j * NT < n_blk) put_ref(tid + j * NT, srg[j]);
-    for (uint32_t i = tid + SR * NT; i < n_blk; i += NT) put_ref(i, grefs[i]);
-    for (uint32_t i = tid; i < A * NP; i += NT) bins[i] = 0ull;
-    __syncthreads(); // qtab, sref and bins ready
+        if (tid + (uint32_t)j * NT < n_ref) put_ref(tid + j * NT, srg[j]);
+    for (uint32_t i = tid + SR * NT; i < n_ref; i += NT) put_ref(i, i < n_blk ? grefs[i] : 0u);
+    for (uint32_t at = tid; at < A; at += NT)
+#pragma unroll
+        for (int pp = 0; pp < NP; ++pp) *binp(at, pp) = 0ull;
+    __syncthreads(); // tables, refs and bins ready
 
     // Plan from the first NW tiles (the ring's slot 0 of every wave): per row the
     // pair (max scaled score m, sum over tokens of 4*max|c|*2^(s - m)), combined
     // over lanes and waves like log-sum-exp partials, plus max |c|.
     float ref[RC];
     int F = 0;
+    bool any_bad = false;
     {
         const uint32_t n_tiles = (t_end - t_begin + NT * CPT - 1) / (NT * CPT); // plan tiles of NT*CPT tokens
         float scs[CPT][RC], cm[CPT];
@@ -909,25 +983,26 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
             uint32_t dummy = 0;
             atoms(ring[0][kk], ia, dummy);
             score(ring[0][kk], ia, scs[kk]);
-            cm[kk] = rv[0][kk] ? cmax_f(ring[0][kk]) : 0.0f;
+            cm[kk] = rv0[kk] ? cmax_f(ring[0][kk]) : 0.0f;
             cmw = fmaxf(cmw, cm[kk]);
 #pragma unroll
             for (int rr = 0; rr < RC; ++rr) {
                 scs[kk][rr] *= sl;
-                if (rv[0][kk]) m[rr] = fmaxf(m[rr], scs[kk][rr]);
+                if (rv0[kk]) m[rr] = fmaxf(m[rr], scs[kk][rr]);
             }
         }
 #pragma unroll
         for (int rr = 0; rr < RC; ++rr) {
             float acc = 0.0f;
 #pragma unroll
-            for (int kk = 0; kk < CPT; ++kk) acc += cm[kk] * fast_exp2(scs[kk][rr] - (rv[0][kk] ? m[rr] : scs[kk][rr]));
+            for (int kk = 0; kk < CPT; ++kk) acc += cm[kk] * fast_exp2(scs[kk][rr] - (rv0[kk] ? m[rr] : scs[kk][rr]));
             // Onto the wave's maximum.
             const float mw = wave_max(m[rr]);
             w[rr] = wave_sum(m[rr] == -INFINITY ? 0.0f : 4.0f * acc * fast_exp2(m[rr] - mw));
             m[rr] = mw;
         }
         cmw = wave_max(cmw);
+        const bool wave_bad = __builtin_amdgcn_ballot_w64(bad) != 0ull;
         if (lane == 0) {
 #pragma unroll
             for (int rr = 0; rr < RC; ++rr) {
@@ -935,6 +1010,7 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
                 red[wave * NR + 2 * rr + 1] = w[rr];
             }
             red[wave * NR + 2 * RC] = cmw;
+            red[wave * NR + 2 * RC + 1] = wave_bad ? 1.0f : 0.0f;
         }
         __syncthreads();
         float plan = 0.0f, cmax0 = 0.0f;
@@ -950,23 +1026,31 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
             }
             plan += L;
         }
-        for (int v = 0; v < NW; ++v) cmax0 = fmaxf(cmax0, red[v * NR + 2 * RC]);
+        for (int v = 0; v < NW; ++v) {
+            cmax0 = fmaxf(cmax0, red[v * NR + 2 * RC]);
+            any_bad |= red[v * NR + 2 * RC + 1] != 0.0f;
+        }
         plan *= (float)n_tiles; // bound on sum |p*c| over the split, if tiles are alike
         const int Fs = plan > 0.0f ? 28 - exp_of(plan) : 100;
         const int Fm = cmax0 > 0.0f ? 18 - exp_of(cmax0) : 100; // p <= 1 in the first tile
         F = min(100, max(-100, min(Fs, Fm)));
     }
+    // Wave tiles below n_full hold only tokens with codes.
+    const uint32_t n_full = any_bad ? 0u : (t_end - t_begin) / WT;
 
     float lpart[RC];
     uint32_t oob = 0;
     bool exact = false;
     for (int attempt = 0; attempt < 2; ++attempt) {
         if (attempt) {
-            for (uint32_t i = tid; i < A * NP; i += NT) bins[i] = 0ull;
+            for (uint32_t at = tid; at < A; at += NT)
+#pragma unroll
+                for (int pp = 0; pp < NP; ++pp) *binp(at, pp) = 0ull;
 #pragma unroll
             for (int d = 0; d < PD; ++d) {
                 tl[d] = (uint32_t)(wave + d * NW);
-                load_tile(tl[d], ring[d], rv[d]);
+                bool okd[CPT];
+                load_tile(tl[d], ring[d], okd);
             }
             __syncthreads(); // bins zeroed before any wave adds
         }
@@ -980,52 +1064,75 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
             lpart[rr] = 0.0f;
             rf[rr] = Ff - ref[rr];
         }
-        uint32_t cmx_bits = 0;
+        // max |c| as two packed accumulators of f16 bit patterns: the unsigned
+        // maximum holds the largest negative pattern if any (else the largest
+        // positive), the signed maximum the largest positive (else the largest
+        // negative); their magnitudes' maximum is max |c|.
+        ushort2_t cmu = (ushort2_t)(uint16_t)0;
+        short2_t cmi = (short2_t)(int16_t)0x8000;
         float pmx = 0.0f;
+        // One code: scores, p (zero for a token without a code when MASKED), bins.
+        auto consume = [&](const uint4_t cw, const bool ok, auto masked) {
+            constexpr bool MASKED = decltype(masked)::value;
+            uint32_t ia[4];
+            atoms(cw, ia, oob);
+            float sc[RC];
+            score(cw, ia, sc);
+            // Coefficient words copied out first: this compiler's __builtin_bit_cast
+            // of a vector element reads element 0.
+            const uint32_t w2 = cw[2], w3 = cw[3];
+            cmu = __builtin_elementwise_max(cmu, __builtin_elementwise_max(__builtin_bit_cast(ushort2_t, w2),
+                                                                           __builtin_bit_cast(ushort2_t, w3)));
+            cmi = __builtin_elementwise_max(cmi, __builtin_elementwise_max(__builtin_bit_cast(short2_t, w2),
+                                                                           __builtin_bit_cast(short2_t, w3)));
+            float ps[RC]; // p * 2^F
+#pragma unroll
+            for (int rr = 0; rr < RC; ++rr) {
+                const float p = fast_exp2(fmaf(sc[rr], sl, rf[rr]));
+                ps[rr] = (!MASKED || ok) ? p : 0.0f;
+                lpart[rr] += ps[rr];
+            }
+            if constexpr (RC == 4) pmx = fmaxf(pmx, fmaxf(fmaxf(ps[0], ps[1]), fmaxf(ps[2], ps[3])));
+            else if constexpr (RC == 2) pmx = fmaxf(pmx, fmaxf(ps[0], ps[1]));
+            else pmx = fmaxf(pmx, ps[0]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float cj = (float)coef(cw, j);
+#pragma unroll
+                for (int pp = 0; pp < NP; ++pp) {
+                    const uint32_t b0 = __builtin_bit_cast(uint32_t, fmaf(ps[2 * pp], cj, kMagic));
+                    const uint32_t b1 =
+                        (2 * pp + 1 < RC) ? __builtin_bit_cast(uint32_t, fmaf(ps[min(2 * pp + 1, RC - 1)], cj, kMagic))
+                                          : 0x4B400000u;
+                    const uint64_t wv = (((uint64_t)b1 << 32) | b0) - kMagic2;
+                    __hip_atomic_fetch_add(binp(ia[j], pp), wv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                }
+            }
+        };
         while (tl[0] < n_wt) {
 #pragma unroll
             for (int d = 0; d < PD; ++d) {
                 const uint32_t nt = tl[d] + (uint32_t)(PD * NW);
                 uint32_t rnext[CPT]; // refs of the slot's next tile, read before this slot's atomics
-                tile_refs(nt, rnext);
-                if (tl[d] < n_wt) { // uniform; no global loads inside
+                tile_refs(min(nt, n_wt - 1u), rnext);
+                if (tl[d] < n_full) { // uniform; no global loads inside
 #pragma unroll
-                    for (int kk = 0; kk < CPT; ++kk) {
-                        const uint4_t cw = ring[d][kk];
-                        uint32_t ia[4];
-                        atoms(cw, ia, oob);
-                        float sc[RC];
-                        score(cw, ia, sc);
-                        cmx_bits = max(cmx_bits, cmax_bits(cw));
-                        float ps[RC]; // p * 2^F, zero for invalid tokens
+                    for (int kk = 0; kk < CPT; ++kk) consume(ring[d][kk], true, std::false_type{});
+                } else if (tl[d] < n_wt) {
+                    uint32_t rcur[CPT];
+                    tile_refs(tl[d], rcur);
 #pragma unroll
-                        for (int rr = 0; rr < RC; ++rr) {
-                            const float p = fast_exp2(fmaf(sc[rr], sl, rf[rr]));
-                            ps[rr] = rv[d][kk] ? p : 0.0f;
-                            lpart[rr] += ps[rr];
-                        }
-                        if constexpr (RC == 4) pmx = fmaxf(pmx, fmaxf(fmaxf(ps[0], ps[1]), fmaxf(ps[2], ps[3])));
-                        else if constexpr (RC == 2) pmx = fmaxf(pmx, fmaxf(ps[0], ps[1]));
-                        else pmx = fmaxf(pmx, ps[0]);
-#pragma unroll
-                        for (int j = 0; j < 4; ++j) {
-                            uint64_t* bp = bins + ia[j]; // plane pp at bp + pp * A
-                            const float cj = (float)coef(cw, j);
-#pragma unroll
-                            for (int pp = 0; pp < NP; ++pp) {
-                                const uint32_t b0 = __builtin_bit_cast(uint32_t, fmaf(ps[2 * pp], cj, kMagic));
-                                const uint32_t b1 =
-                                    (2 * pp + 1 < RC) ? __builtin_bit_cast(uint32_t, fmaf(ps[min(2 * pp + 1, RC - 1)], cj, kMagic))
-                                                      : 0x4B400000u;
-                                const uint64_t wv = (((uint64_t)b1 << 32) | b0) - kMagic2;
-                                __hip_atomic_fetch_add(bp + pp * A, wv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-                            }
-                        }
-                    }
+                    for (int kk = 0; kk < CPT; ++kk) consume(ring[d][kk], rcur[kk] != kBad, std::true_type{});
                 }
-                tile_codes(nt, rnext, ring[d], rv[d]); // unconditional: past the end they read the zero code
+                tile_codes(rnext, ring[d]); // unconditional: past the end they re-read the last tile
                 tl[d] = nt;
             }
+        }
+        uint32_t cmx_bits;
+        {
+            const uint32_t mi = max((uint32_t)(uint16_t)cmi.x & 0x7FFFu, (uint32_t)(uint16_t)cmi.y & 0x7FFFu);
+            const uint32_t mu = max((uint32_t)cmu.x & 0x7FFFu, (uint32_t)cmu.y & 0x7FFFu);
+            cmx_bits = max(mu, mi);
         }
         const float cmx = (float)__builtin_bit_cast(_Float16, (uint16_t)cmx_bits);
         // Overflow proof: every |bin| <= sum over contributions |p*c|*2^F <= 4*max|c|*sum_r sum_t p*2^F,
@@ -1128,10 +1235,10 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
     }
     // Atom indices outside the dictionary: recorded (their terms went to a clamped atom).
     {
-        bool bad;
-        if constexpr (POW2) bad = (oob & ~((A - 1u) | ((A - 1u) << 16))) != 0u;
-        else bad = oob >= A;
-        if (bad) flag_error(a.err, kErrAtom);
+        bool badat;
+        if constexpr (POW2) badat = (oob & ~((A - 1u) | ((A - 1u) << 16))) != 0u;
+        else badat = oob >= A;
+        if (badat) flag_error(a.err, kErrAtom);
     }
     // Bins out as float rows [r][A]; track max |bin| per row for the f16 split of the finish.
     const float inv = pow2f(-F);
@@ -1141,7 +1248,7 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
     for (uint32_t at = tid; at < A; at += NT) {
 #pragma unroll
         for (int pp = 0; pp < NP; ++pp) {
-            const uint64_t wv = bins[pp * A + at];
+            const uint64_t wv = *binp(at, pp);
             const int32_t v0 = (int32_t)(uint32_t)wv;
             const int32_t v1 = (int32_t)((uint32_t)(wv >> 32) + (v0 < 0 ? 1u : 0u));
 #pragma unroll
@@ -1176,10 +1283,10 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
 // Persistent: work-group i takes work items i, i + gridDim.x, ... (gridDim.x a
 // multiple of 8, so each keeps its XCD), so the grid is one resident round and
 // the hot kernel can run beside it in the resources it leaves free.
-template <int RC, int CPT, int PD, bool POW2, bool QF32>
+template <int RC, int CPT, int PD, bool POW2, bool QF32, bool BUF>
 __global__ __launch_bounds__(kColdThreads) void cold_kernel(ColdArgs a) {
     for (uint32_t wg = blockIdx.x; wg < a.n_wg; wg += gridDim.x) {
-        cold_unit<RC, CPT, PD, POW2, QF32>(a, wg);
+        cold_unit<RC, CPT, PD, POW2, QF32, BUF>(a, wg);
         __syncthreads(); // the next item rewrites the LDS tables
     }
 }
@@ -1189,8 +1296,9 @@ __global__ __launch_bounds__(kColdThreads) void cold_kernel(ColdArgs a) {
 inline size_t cold_smem_bytes(uint32_t A, int RC, uint32_t tokens_per_split, uint32_t qbytes) {
     const size_t qtab = ((size_t)A * RC * qbytes + 15) & ~(size_t)15;
     const int NW = kColdThreads / 64, NP = (RC + 1) / 2;
-    const size_t n_blk = ((size_t)(tokens_per_split + 15) / 16 + 3) & ~(size_t)3;
-    return qtab + (size_t)A * NP * 8 + n_blk * 4 + (size_t)NW * (2 * RC + 2) * 4;
+    const size_t tables = (RC == 4 && qbytes == 2) ? (size_t)A * kColdRec : qtab + (size_t)A * NP * 8;
+    const size_t n_ref = ((size_t)(tokens_per_split + 15) / 16 + kColdRefPad - 1) / kColdRefPad * kColdRefPad;
+    return tables + n_ref * 4 + (size_t)NW * (2 * RC + 3) * 4;
 }
 
 // ----------------------------------------------- per-row merge factors
@@ -2079,7 +2187,9 @@ __global__ __launch_bounds__(kEncMThreads) void encode_mfma_kernel(EncodeArgs a,
                 for (int ks = 0; ks < KS; ++ks) ad[ks] = *(const half8_t*)(&sd[cur][(at * 16 + li) * P + 32 * ks + 8 * lg]);
                 // The lane's 4 atoms: bad atoms (always candidates) stay out of the bound.
                 const uint4_t gs = s_gs[cur][at * 4 + lg];
-                const float l2m = __builtin_bit_cast(float, gs[0]), l1m = __builtin_bit_cast(float, gs[1]);
+                // Words copied out first: __builtin_bit_cast of a vector element reads element 0 here.
+                const uint32_t g0 = gs[0], g1 = gs[1];
+                const float l2m = __builtin_bit_cast(float, g0), l1m = __builtin_bit_cast(float, g1);
                 const uint32_t sub = gs[2], badm = gs[3];
                 float4_t acc[NTT];
                 float E[NTT];
