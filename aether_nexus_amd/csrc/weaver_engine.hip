@@ -102,6 +102,7 @@ struct Layout {
     uint32_t rc = 4;       // cold rows per work-group
     uint32_t n_chunks = 1; // ceil(R / rc)
     uint32_t n_ar = 1;     // atom ranges of the finish
+    bool fin_rows = false; // finish_rows_kernel (16-row tiles, waves over atoms) instead of finish_kernel
     uint32_t atoms_per_range = 0;
     uint32_t tiles_per_group = 0, rows_per_group = 0, n_groups = 0;
     bool qf32 = false;     // q_latent computed on the device, kept in fp32
@@ -199,6 +200,9 @@ int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, const uint32_t 
         uint32_t wpc = hot_waves_per_cu[R <= 16 ? 0 : (R <= 32 ? 1 : 2)];
         if (d->cold_count > 0) wpc = std::min(wpc, 4u);
         uint64_t want = cdiv((uint64_t)n_cu * std::max(1u, wpc), n_lbg);
+        // Beside the cold kernel, splits of at most ~512 tokens (B = 64 sweep: 4 splits of
+        // 512 tokens 0.159 ms, 2 of 1024 0.164 ms; B = 32: 4 of 512 0.089 ms, 8 of 256 0.092 ms).
+        if (d->cold_count > 0) want = std::max<uint64_t>(want, cdiv(n_tok, 512));
         // >= 128 tokens per wave beside the cold kernel (64: B <= 4 steps 1-3% slower);
         // >= 64 alone (one-sequence attention 11.9 -> 11.1 us per layer against 128).
         uint64_t cap = std::max<uint64_t>(1, cdiv(n_tok, d->cold_count > 0 ? 128 : 64));
@@ -267,6 +271,14 @@ int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, const uint32_t 
         const uint64_t tiles = (uint64_t)o.tiles_per_group * o.n_groups;
         uint32_t n_ar = 1;
         if (tiles < (uint64_t)n_cu) n_ar = (uint32_t)std::min<uint64_t>(cdiv((uint64_t)n_cu, tiles), std::max(1u, A / 64));
+        // One cold split per row and at least a quarter of a work-group per CU of
+        // 16-row tiles: finish_rows_kernel, 16 rows per work-group over an atom
+        // range, as many ranges as fill the CUs once.
+        const uint64_t tiles16 = (uint64_t)cdiv(o.rows_per_group, 16u) * o.n_groups;
+        if (o.info.cold_splits == 1 && A % 32 == 0 && tiles16 * 4 >= (uint64_t)n_cu) {
+            o.fin_rows = true;
+            n_ar = (uint32_t)std::min<uint64_t>(cdiv((uint64_t)n_cu, tiles16), std::max(1u, A / 256));
+        }
         o.atoms_per_range = (uint32_t)align_up(cdiv(A, n_ar), 32);
         o.n_ar = cdiv(A, o.atoms_per_range);
     }
@@ -291,7 +303,9 @@ int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, const uint32_t 
         o.off_cm = take(n * 4);
         o.off_cl = take(n * 4);
         o.off_ca = take(n * 4);
-        o.off_cw = take(n * w_pitch(A) * 4);
+        // Tiled for finish_rows_kernel: whole 16-row tiles of each dictionary group.
+        const uint64_t tiled = (uint64_t)o.n_groups * cdiv(o.rows_per_group, 16u) * 16 * A;
+        o.off_cw = take((o.fin_rows ? tiled : n * w_pitch(A)) * 4);
         if (o.n_ar > 1) o.off_ocp = take(n_lbg * R * o.n_ar * HD * 4);
     }
     o.info.workspace_bytes = off;
@@ -441,6 +455,7 @@ int launch_project(aw_engine* e, const aw_decode_desc* d, const Layout& o, char*
     a.qlf = o.qf32 ? (float*)(ws + o.off_ql) : nullptr;
     a.dt = (uint16_t*)(ws + o.off_dt);
     a.dt_pitch = dt_pitch(d->dict_size);
+    a.dt_tiled = o.fin_rows ? 1u : 0u;
     a.batch = d->batch;
     a.queries = d->queries;
     a.q_heads = d->q_heads;
@@ -579,6 +594,9 @@ int launch_cold(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* ws
     a.n_chunks = o.n_chunks;
     a.n_units = (uint32_t)((uint64_t)d->layers * d->batch * o.n_chunks * a.splits);
     a.scale_log2 = d->scale * aw::kLog2e;
+    a.w_tiled = o.fin_rows ? 1u : 0u;
+    a.w_rows_per_group = o.rows_per_group;
+    a.w_dict_heads = d->dict_heads;
     a.cold_blocks = d->cold_blocks;
     a.cold_layer = d->cold_blocks * kBlock * d->kv_heads;
     const bool head_blocked = (d->flags & AW_F_COLD_HEAD_BLOCKED) != 0;
@@ -649,6 +667,14 @@ int launch_finish(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* 
     const uint64_t gx = (uint64_t)o.tiles_per_group * o.n_groups;
     if (gx > 0x7FFFFFFFull) return fail(e, AW_E_UNSUPPORTED, "finish grid too large");
     StageTimer t(e, AW_STAGE_FINISH, st);
+    if (o.fin_rows) {
+        const uint64_t gr = (uint64_t)cdiv(o.rows_per_group, 16u) * o.n_groups;
+        if (gr > 0x7FFFFFFFull) return fail(e, AW_E_UNSUPPORTED, "finish grid too large");
+        hipLaunchKernelGGL((aw::finish_rows_kernel<HD>), dim3((uint32_t)gr, o.n_ar), dim3(aw::kFinRowsWaves * 64),
+                           aw::finish_rows_smem_bytes(HD), st, a);
+        AW_HIP(e, hipGetLastError());
+        return AW_OK;
+    }
     const bool fused = o.n_ar == 1 && a.hot_splits > 0;
     const uint32_t sneed = std::max(a.cold_splits, fused ? a.hot_splits : 1u);
     uint32_t sf = 1;
@@ -982,6 +1008,9 @@ int aw_engine_create(int device, aw_engine** out) {
         const void* fin[] = {(const void*)aw::finish_kernel<128, true>, (const void*)aw::finish_kernel<128, false>,
                              (const void*)aw::finish_kernel<64, true>, (const void*)aw::finish_kernel<64, false>};
         for (const void* f : fin)
+            (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)e->max_lds);
+        const void* finr[] = {(const void*)aw::finish_rows_kernel<128>, (const void*)aw::finish_rows_kernel<64>};
+        for (const void* f : finr)
             (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)e->max_lds);
         const void* proj[] = {(const void*)aw::project_kernel<128, 32, 64, 2>, (const void*)aw::project_kernel<128, 128, 256, 2>,
                               (const void*)aw::project_kernel<128, 128, 128, 4>, (const void*)aw::project_kernel<128, 128, 64, 8>,
@@ -1441,3 +1470,4 @@ int fail(aw_engine* e, int code, const char* fmt, ...) {
 }
 
 } // namespace aw_engine_internal
+

@@ -49,6 +49,7 @@ constexpr int kColdThreads = 512;
 constexpr int kMaxSplits = 64;              // splits per row: the merges combine them lane = split
 constexpr uint32_t kMaxHotSplitBlocks = 4096; // hot blocks per split (16 KiB of LDS refs): 4 Mi tokens per sequence
 
+
 // Error bits written to the engine's device error word.
 constexpr uint32_t kErrHotRef = 1u, kErrColdRef = 2u, kErrAtom = 4u;
 
@@ -108,8 +109,9 @@ struct ProjArgs {
     const uint16_t* dict; // [L][dict_heads][A][HD]
     uint16_t* ql;         // [L][B][Q][Hq][A] f16, or null
     float* qlf;           // [L][B][Q][Hq][A] fp32, or null (both null: transpose only)
-    uint16_t* dt;         // [L][dict_heads][HD][dt_pitch] f16: D^T for the finish
+    uint16_t* dt;         // [L][dict_heads][HD][dt_pitch] f16: D^T for the finish (or tiled, below)
     uint32_t dt_pitch;    // A + padding: rows of D^T do not alias one L2 channel
+    uint32_t dt_tiled;    // D^T as [group][A/32][HD/16][64 lanes][8 atoms] (finish_rows_kernel's A operand)
     uint32_t batch, queries, q_heads, kv_heads, gqa, rows_r;
     uint32_t dict_size, dict_heads;
     uint32_t rows_per_group; // B*Q*(dict_heads==1 ? Hq : G)
@@ -152,6 +154,9 @@ struct ColdArgs {
     uint32_t s_tok, s_head; // code (block b, token j, kv head g) = cold[b*16*kv_heads + j*s_tok + g*s_head]
     uint32_t splits, tokens_per_split, n_chunks, n_units;
     uint32_t n_wg; // work items (8 XCD slots x kv heads x unit groups)
+    // Bins tiled for finish_rows_kernel: [group][row tile of 16][A/32][2][64 lanes][4],
+    // group and group row as the finish numbers them (one split only).
+    uint32_t w_tiled, w_rows_per_group, w_dict_heads;
     float scale_log2;
     uint64_t cold_blocks, cold_layer, refs_layer;
     // q_latent element (lb, g, q, j, a) = ql[lb*s_lb + g*s_g + q*s_q + j*s_j + a*s_a]
@@ -294,7 +299,7 @@ __global__ __launch_bounds__(kProjThreads) void project_kernel(ProjArgs a) {
         const uint32_t nrb = gridDim.y, y = blockIdx.y;
         const int d0 = (int)((y * (uint32_t)HD) / nrb), nd = (int)(((y + 1) * (uint32_t)HD) / nrb) - d0;
         const int TP = nd * (TA / 8);
-        uint16_t* dt = a.dt + (uint64_t)group * HD * a.dt_pitch;
+        uint16_t* dt = a.dt + (uint64_t)group * HD * (a.dt_tiled ? A : a.dt_pitch);
         for (int p = tid; p < TP; p += kProjThreads) {
             const int d = d0 + p % nd, ag = p / nd;
             const uint32_t at = atom0 + 8 * ag;
@@ -304,7 +309,11 @@ __global__ __launch_bounds__(kProjThreads) void project_kernel(ProjArgs a) {
             for (int e = 0; e < 4; ++e)
                 w[e] = (uint32_t)__builtin_bit_cast(uint16_t, sd[(8 * ag + 2 * e) * P + d]) |
                        ((uint32_t)__builtin_bit_cast(uint16_t, sd[(8 * ag + 2 * e + 1) * P + d]) << 16);
-            *(uint4_t*)(dt + (uint64_t)d * a.dt_pitch + at) = (uint4_t){w[0], w[1], w[2], w[3]};
+            // Tiled: the piece of lane (li = d % 16, lg = (at % 32) / 8) of k-step at / 32, dim block d / 16.
+            const uint64_t off = a.dt_tiled ? (((uint64_t)(at / 32) * (HD / 16) + (uint32_t)d / 16) * 64 +
+                                               ((at % 32) / 8) * 16 + (uint32_t)d % 16) * 8
+                                            : (uint64_t)d * a.dt_pitch + at;
+            *(uint4_t*)(dt + off) = (uint4_t){w[0], w[1], w[2], w[3]};
         }
     }
     if (a.qlf != nullptr) {
@@ -1240,11 +1249,38 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
         else badat = oob >= A;
         if (badat) flag_error(a.err, kErrAtom);
     }
-    // Bins out as float rows [r][A]; track max |bin| per row for the f16 split of the finish.
+    // Bins out as float rows [r][A] (or tiled); track max |bin| per row for the f16 split of the finish.
     const float inv = pow2f(-F);
     float amax[RC];
 #pragma unroll
     for (int rr = 0; rr < RC; ++rr) amax[rr] = 0.0f;
+    // The bin of row rr at atom `at` as a float.
+    auto bin_value = [&](uint32_t at, int rr) -> float {
+        const uint64_t wv = *binp(at, rr / 2);
+        const int32_t v0 = (int32_t)(uint32_t)wv;
+        const int32_t v1 = (int32_t)((uint32_t)(wv >> 32) + (v0 < 0 ? 1u : 0u));
+        return (float)((rr & 1) ? v1 : v0) * inv;
+    };
+    if (a.w_tiled) {
+        // Thread -> (group of 4 atoms, row): 16-byte pieces, the rows of one piece
+        // position adjacent in the tile (64-byte runs for 4 rows).
+        const uint32_t l_in = lb / a.batch, b_in = lb % a.batch;
+        const uint32_t grp = a.w_dict_heads == 1 ? l_in : l_in * a.kv_heads + g;
+        const uint32_t tiles = (a.w_rows_per_group + 15) / 16, nk = A / 32;
+        for (uint32_t i = tid; i < (A / 4) * RC; i += NT) {
+            const int rr = (int)(i % RC);
+            const uint32_t a4 = i / RC, r = c * RC + (uint32_t)rr;
+            float4_t v;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = bin_value(4 * a4 + e, rr);
+            amax[rr] = fmaxf(amax[rr], fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+            if (r >= R) continue;
+            const uint32_t grow = a.w_dict_heads == 1 ? (b_in * a.kv_heads + g) * R + r : b_in * R + r;
+            const uint32_t at = 4 * a4, kk = at / 32, lgv = (at % 32) / 8, h = (at % 8) / 4;
+            const uint64_t off = ((((uint64_t)grp * tiles + grow / 16) * nk + kk) * 2 + h) * 64 + lgv * 16 + grow % 16;
+            *(float4_t*)(a.part_w + off * 4) = v;
+        }
+    } else
     for (uint32_t at = tid; at < A; at += NT) {
 #pragma unroll
         for (int pp = 0; pp < NP; ++pp) {
@@ -1645,6 +1681,175 @@ __global__ __launch_bounds__(kFinishWaves * 64) void finish_kernel(FinishArgs a)
             v[e] = (_Float16)merge_value(oh[nb][e], Mh, Lh, acc[nb][e] * inv_scl, Mc, Lc);
         *(half4_t*)(o + 16 * nb + 4 * lg) = v;
     }
+}
+
+// ---------------------------------------- bins . D by row tiles (MFMA)
+//
+// For many rows with one cold split each.  Work-group = 16 rows sharing one
+// dictionary x one atom range; its 8 waves split the range into 8 stretches of
+// whole 32-atom k-steps and each streams its stretch of D^T and of the rows'
+// bins straight from memory, kFinRowsPD k-steps of loads ahead, with no LDS
+// staging and no barrier: per k-step
+//   A = D^T (lane: dim 16*nb + li, atoms 8*lg .. +7: one 16-byte load per dim block)
+//   B = W^T (lane: row li, the same 8 atoms) times the row's cold factor, split
+//       into hi + lo f16 terms -> two MFMAs per dim block.
+// The projection writes D^T and the cold kernel the bins in these lane orders
+// (ProjArgs::dt_tiled, ColdArgs::w_tiled), so every load instruction reads 1 KB
+// contiguous: on gfx950 a CU reads L2-resident data at ~135 GB/s that way and at
+// ~37 GB/s when a load spans 16 rows of 64 bytes (measured).
+// Every wave reads a different stretch of D^T, so no operand is shared through
+// LDS; the 16 rows fill the MFMA's 16 columns.  The 8 waves' O^T partials are
+// then summed in LDS in wave order, and each thread finishes 4 dims of one row:
+// with one atom range the row is merged with its hot partials and written as
+// f16, otherwise the range partial goes to `ocp` for merge_kernel.
+constexpr int kFinRowsWaves = 8;
+constexpr int kFinRowsPD = 4; // k-steps of loads in flight per wave
+
+inline size_t finish_rows_smem_bytes(int HD) { return (size_t)kFinRowsWaves * (HD / 16) * 64 * 16; }
+
+template <int HD>
+__global__ __launch_bounds__(kFinRowsWaves * 64) void finish_rows_kernel(FinishArgs a) {
+    constexpr int NB = HD / 16;
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    float4_t* s_part = (float4_t*)smem; // [wave][nb][lane]
+    const int tid = threadIdx.x, lane = tid & 63, li = lane & 15, lg = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t tiles = (a.rows_per_group + 15) / 16;
+    const uint32_t group = blockIdx.x / tiles, tile = blockIdx.x % tiles;
+    const uint32_t ar = blockIdx.y;
+    const uint32_t l = group / a.dict_heads, dg = group % a.dict_heads;
+    const uint32_t R = a.rows_r, A = a.dict_size;
+
+    // Row (lbg, r) of group row `row` (clamped into the group).
+    auto row_id = [&](uint32_t row, uint64_t& lbg, uint32_t& r) {
+        row = min(row, a.rows_per_group - 1u);
+        if (a.dict_heads == 1) lbg = (uint64_t)l * a.batch * a.kv_heads + row / R; // row = (b*Hkv + g)*R + r
+        else lbg = ((uint64_t)l * a.batch + row / R) * a.kv_heads + dg;            // row = b*R + r
+        r = row % R;
+    };
+
+    // This lane's B-operand row and its cold factor (one split: the bins' own scale).
+    const uint32_t my_raw = tile * 16 + li;
+    uint64_t lbg_b;
+    uint32_t r_b;
+    row_id(my_raw, lbg_b, r_b);
+    const uint64_t cb_b = lbg_b * R + r_b;
+    const float lc_b = a.cold_l[cb_b], ca_b = a.cold_amax[cb_b];
+    const float f_b = my_raw < a.rows_per_group && lc_b > 0.0f ? bin_scale(ca_b, lc_b) / lc_b : 0.0f;
+
+    // This wave's stretch of the range, in k-steps of 32 atoms.
+    const uint32_t a_begin = ar * a.atoms_per_range;
+    const uint32_t a_end = min(a_begin + a.atoms_per_range, A);
+    const uint32_t n_k = (a_end - a_begin + 31) / 32;
+    const uint32_t k_per = (n_k + kFinRowsWaves - 1) / kFinRowsWaves;
+    const uint32_t k0 = min(n_k, (uint32_t)wave * k_per), k1 = min(n_k, k0 + k_per);
+    // Both operands tiled so that each load instruction reads 1 KB contiguous (64
+    // lanes x 16 bytes): D^T as [A/32][NB][lane][8 atoms], the bins of this row
+    // tile as [A/32][2][lane][4].
+    const uint32_t kbase = a_begin / 32;
+    const uint16_t* dt = a.dt + (uint64_t)group * HD * A + (uint64_t)lane * 8;
+    const float* wt = a.cold_w + ((uint64_t)blockIdx.x * (A / 32) * 2 * 64 + (uint64_t)lane) * 4;
+
+    struct KLoads {
+        uint4_t d[NB];
+        float4_t w[2];
+    };
+    auto load_k = [&](uint32_t k, KLoads& v) {
+        const uint64_t kk = kbase + k;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) v.d[nb] = *(const uint4_t*)(dt + (kk * NB + nb) * 64 * 8);
+        v.w[0] = *(const float4_t*)(wt + kk * 2 * 64 * 4);
+        v.w[1] = *(const float4_t*)(wt + (kk * 2 + 1) * 64 * 4);
+    };
+    float4_t acc[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[nb] = (float4_t)0.0f;
+    auto compute_k = [&](uint32_t k, const KLoads& v) {
+        // This lane's 8 atoms count (inside the wave's stretch and the range); a row
+        // without cold tokens has no bins (never read).
+        const bool in = k < k1 && a_begin + 32u * k + 8u * (uint32_t)lg < a_end && f_b != 0.0f;
+        half8_t hi, lo;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float x = in ? f_b * v.w[e / 4][e % 4] : 0.0f;
+            hi[e] = (_Float16)x;
+            lo[e] = (_Float16)(x - (float)hi[e]);
+        }
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+            acc[nb] = mfma16x16x32(as_h8(v.d[nb]), hi, acc[nb]);
+            acc[nb] = mfma16x16x32(as_h8(v.d[nb]), lo, acc[nb]);
+        }
+    };
+    // Ring of kFinRowsPD k-steps in flight; every load is unconditional (clamped).
+    KLoads ring[kFinRowsPD];
+#pragma unroll
+    for (int j = 0; j < kFinRowsPD; ++j) {
+        // Issued in ring order (oldest first), as the loop below refills it.
+        load_k(min(k0 + (uint32_t)j, n_k - 1u), ring[j]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // Whole rounds of kFinRowsPD k-steps (past the stretch, masked to zero): no
+    // branch inside a round, so the waits count the loads in flight exactly.
+    for (uint32_t k = k0; k < k1; k += kFinRowsPD) {
+#pragma unroll
+        for (int j = 0; j < kFinRowsPD; ++j) {
+            compute_k(k + j, ring[j]);
+            // The refill stays below this k-step's MFMAs: hoisted above them it would
+            // take fresh registers and make the MFMAs wait for every load in flight.
+            __builtin_amdgcn_sched_barrier(0);
+            load_k(min(k + j + kFinRowsPD, n_k - 1u), ring[j]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    // Sum the waves' partials in wave order.
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) s_part[(wave * NB + nb) * 64 + lane] = acc[nb];
+    __syncthreads();
+    // Thread t: dim block nb = t / 64, lane position p = t % 64 -> row p % 16,
+    // dims 16*nb + 4*(p / 16) .. +3.
+    static_assert(NB * 64 <= kFinRowsWaves * 64, "one float4 of O^T per thread");
+    if (tid >= NB * 64) return;
+    const int nb = tid / 64, p = tid % 64, pr = p & 15, pd = 16 * nb + 4 * (p >> 4);
+    float4_t o = s_part[nb * 64 + p];
+#pragma unroll
+    for (int w = 1; w < kFinRowsWaves; ++w) o += s_part[(w * NB + nb) * 64 + p];
+    const uint32_t row_raw = tile * 16 + pr;
+    if (row_raw >= a.rows_per_group) return;
+    uint64_t lbg;
+    uint32_t r;
+    row_id(row_raw, lbg, r);
+    const uint64_t cb = lbg * R + r;
+    const float Mc = a.cold_m[cb], Lc = a.cold_l[cb];
+    const float inv_scl = Lc > 0.0f ? 1.0f / bin_scale(a.cold_amax[cb], Lc) : 1.0f;
+    const uint64_t rowid = lbg * R + r;
+    if (a.n_ar > 1) {
+        *(float4_t*)(a.ocp + (rowid * a.n_ar + ar) * HD + pd) = o * inv_scl;
+        return;
+    }
+    // Merge with the row's hot splits (log-sum-exp over splits, then over hot / cold).
+    float Mh = -INFINITY;
+    for (uint32_t s = 0; s < a.hot_splits; ++s) {
+        const uint64_t hb = (lbg * a.hot_splits + s) * R + r;
+        if (a.hot_l[hb] > 0.0f) Mh = fmaxf(Mh, a.hot_m[hb]);
+    }
+    float Lh = 0.0f;
+    float4_t oh = (float4_t)0.0f;
+    for (uint32_t s = 0; s < a.hot_splits; ++s) {
+        const uint64_t hb = (lbg * a.hot_splits + s) * R + r;
+        const float hl = a.hot_l[hb];
+        if (!(hl > 0.0f)) continue;
+        const float f = fast_exp2(a.hot_m[hb] - Mh);
+        Lh += f * hl;
+        oh += f * *(const float4_t*)(a.hot_o + hb * HD + pd);
+    }
+    const uint64_t lb = lbg / a.kv_heads, g = lbg % a.kv_heads;
+    const uint64_t q = r / a.gqa, h = g * a.gqa + r % a.gqa;
+    uint16_t* dst = a.out + ((lb * a.queries + q) * a.q_heads + h) * HD + pd;
+    half4_t v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = (_Float16)merge_value(oh[e], Mh, Lh, o[e] * inv_scl, Mc, Lc);
+    *(half4_t*)dst = v;
 }
 
 // --------------------------------------------------- log-sum-exp merge
