@@ -214,6 +214,7 @@ def test_views_dirty_and_checkpoints(genesis):
     force_checkpoint always flushes; the writes reach the file."""
     r = FO.compute_regions(SMALL)
     fab = F.Fabric(genesis, dims(SMALL))
+    booted = time.monotonic()
     hot = fab.hot_pool()
     assert hot.size == r["hot_pool_size"] and not hot.flags.writeable
     assert fab.hot_pool_blocks().shape == (8192, 16, 2, 64)
@@ -226,7 +227,8 @@ def test_views_dirty_and_checkpoints(genesis):
     assert fab.dirty
     cold[:16] = 7
     fab.checkpoint()  # < 300 ms since boot: nothing flushed
-    assert fab.dirty
+    if time.monotonic() - booted < 0.2:  # a loaded host can take longer to get here
+        assert fab.dirty
     time.sleep(0.35)
     fab.checkpoint()
     assert not fab.dirty
