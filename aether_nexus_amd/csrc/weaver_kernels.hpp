@@ -636,6 +636,18 @@ constexpr uint64_t kColdWindow = kBadCodeOff;         // largest layer pool (byt
 constexpr uint32_t kColdRefPad = 16;                  // staged refs are padded to whole wave tiles
 constexpr uint32_t kBufferWord3 = 0x00020000u;        // gfx9 buffer resource word 3 (32-bit data format)
 constexpr uint32_t kColdRec = 24;                     // bytes of an RC = 4 f16 atom record
+constexpr uint32_t kNoHot = ~0u;                      // no atom hot enough for private bins
+constexpr uint32_t kHotMin = 64;                      // plan samples (of 4096) that make an atom hot
+
+// LDS of the plan histogram / the hot atom's private bins, and its offset after
+// the tables (tab bytes), the staged refs (n_ref) and the reduction slots (nred floats).
+__host__ __device__ constexpr size_t cold_hp_bytes(uint32_t A, int NP) {
+    return (((size_t)A * 2 > (size_t)kColdThreads * NP * 8 ? (size_t)A * 2 : (size_t)kColdThreads * NP * 8) + 15) &
+           ~(size_t)15;
+}
+__host__ __device__ constexpr size_t cold_hp_offset(size_t tab, uint32_t n_ref, uint32_t nred) {
+    return (tab + (((size_t)n_ref + 3) & ~(size_t)3) * 4 + (size_t)nred * 4 + 15) & ~(size_t)15;
+}
 
 typedef uint16_t ushort2_t __attribute__((ext_vector_type(2)));
 typedef int16_t short2_t __attribute__((ext_vector_type(2)));
@@ -652,7 +664,7 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
     using QT = std::conditional_t<QF32, float, _Float16>; // q_latent table element
     constexpr int NT = kColdThreads, NW = NT / 64, NP = (RC + 1) / 2;
     constexpr int NB = RC + 2;      // values of the end-of-split reductions
-    constexpr int NR = 2 * RC + 3;  // LDS slots per wave: the plan's (max, sum) pairs, max|c|, bad refs
+    constexpr int NR = 2 * RC + 4;  // LDS slots per wave: the plan's (max, sum) pairs, max|c|, bad refs, hot key
     constexpr uint32_t WT = 64u * CPT; // tokens of one wave tile
     constexpr uint32_t RPT = WT / 16;  // block refs of one wave tile
     static_assert(kColdRefPad % RPT == 0, "ref padding");
@@ -698,6 +710,10 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
     uint64_t* bins = (uint64_t*)(smem + qtab_bytes);       // [NP][A] (not REC)
     uint32_t* sref = (uint32_t*)(smem + tab_bytes);        // [n_ref]: staged block refs, kBad = none
     float* red = (float*)(sref + ((n_ref + 3) & ~3u));    // [NW][NR]
+    // Plan histogram of atom indices (two 16-bit counters per word), then each
+    // lane's private bins of the split's hottest atom ([lane][NP] u64).
+    uint32_t* hp = (uint32_t*)(smem + cold_hp_offset(tab_bytes, n_ref, NW * NR));
+    const uint32_t hp_words = cold_hp_bytes(A, NP) / 4;
     // q_latent values of atom `at` (RC of them) and its bin of row pair pp.
     auto qrow = [&](uint32_t at) -> const QT* {
         if constexpr (REC) return (const QT*)(smem + at * kColdRec + 16u);
@@ -972,7 +988,8 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
     for (uint32_t at = tid; at < A; at += NT)
 #pragma unroll
         for (int pp = 0; pp < NP; ++pp) *binp(at, pp) = 0ull;
-    __syncthreads(); // tables, refs and bins ready
+    for (uint32_t i = tid; i < hp_words; i += NT) hp[i] = 0u;
+    __syncthreads(); // tables, refs, bins and the histogram ready
 
     // Plan from the first NW tiles (the ring's slot 0 of every wave): per row the
     // pair (max scaled score m, sum over tokens of 4*max|c|*2^(s - m)), combined
@@ -980,18 +997,32 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
     float ref[RC];
     int F = 0;
     bool any_bad = false;
+    // The split's hottest atom (REC layout only): its adds go to per-lane private
+    // bins instead of one LDS address, then one add per wave.  Integer sums, so
+    // the bins are the same bits either way.
+    uint32_t hot = kNoHot;
     {
         const uint32_t n_tiles = (t_end - t_begin + NT * CPT - 1) / (NT * CPT); // plan tiles of NT*CPT tokens
         float scs[CPT][RC], cm[CPT];
         float m[RC], w[RC], cmw = 0.0f;
 #pragma unroll
         for (int rr = 0; rr < RC; ++rr) m[rr] = -INFINITY;
+        uint32_t hkey = 0; // (largest plan count of an atom) << 16 | that atom
 #pragma unroll
         for (int kk = 0; kk < CPT; ++kk) {
             uint32_t ia[4];
             uint32_t dummy = 0;
             atoms(ring[0][kk], ia, dummy);
             score(ring[0][kk], ia, scs[kk]);
+            if (rv0[kk])
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    // The last add to an atom returns its final count - 1.
+                    const uint32_t sh = 16u * (ia[j] & 1u);
+                    const uint32_t old = __hip_atomic_fetch_add(hp + (ia[j] >> 1), 1u << sh, __ATOMIC_RELAXED,
+                                                                __HIP_MEMORY_SCOPE_WORKGROUP);
+                    hkey = max(hkey, ((((old >> sh) & 0xFFFFu) + 1u) << 16) | ia[j]);
+                }
             cm[kk] = rv0[kk] ? cmax_f(ring[0][kk]) : 0.0f;
             cmw = fmaxf(cmw, cm[kk]);
 #pragma unroll
@@ -1011,6 +1042,8 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
             m[rr] = mw;
         }
         cmw = wave_max(cmw);
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) hkey = max(hkey, (uint32_t)__shfl_xor((int)hkey, o));
         const bool wave_bad = __builtin_amdgcn_ballot_w64(bad) != 0ull;
         if (lane == 0) {
 #pragma unroll
@@ -1020,6 +1053,7 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
             }
             red[wave * NR + 2 * RC] = cmw;
             red[wave * NR + 2 * RC + 1] = wave_bad ? 1.0f : 0.0f;
+            ((uint32_t*)red)[wave * NR + 2 * RC + 2] = hkey;
         }
         __syncthreads();
         float plan = 0.0f, cmax0 = 0.0f;
@@ -1035,10 +1069,13 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
             }
             plan += L;
         }
+        uint32_t hk = 0;
         for (int v = 0; v < NW; ++v) {
             cmax0 = fmaxf(cmax0, red[v * NR + 2 * RC]);
             any_bad |= red[v * NR + 2 * RC + 1] != 0.0f;
+            hk = max(hk, ((const uint32_t*)red)[v * NR + 2 * RC + 2]);
         }
+        if (REC && (hk >> 16) >= kHotMin) hot = hk & 0xFFFFu;
         plan *= (float)n_tiles; // bound on sum |p*c| over the split, if tiles are alike
         const int Fs = plan > 0.0f ? 28 - exp_of(plan) : 100;
         const int Fm = cmax0 > 0.0f ? 18 - exp_of(cmax0) : 100; // p <= 1 in the first tile
@@ -1080,7 +1117,13 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
         ushort2_t cmu = (ushort2_t)(uint16_t)0;
         short2_t cmi = (short2_t)(int16_t)0x8000;
         float pmx = 0.0f;
-        // One code: scores, p (zero for a token without a code when MASKED), bins.
+        // This lane's private bins of the hot atom (its own [NP] u64; only it touches them).
+        uint64_t* priv_me = (uint64_t*)hp + (uint32_t)tid * NP;
+        if (hot != kNoHot)
+#pragma unroll
+            for (int pp = 0; pp < NP; ++pp) priv_me[pp] = 0ull;
+        // One code: scores, p (zero for a token without a code when MASKED), bins
+        // (the hot atom's go to this lane's private bins; kNoHot matches no atom).
         auto consume = [&](const uint4_t cw, const bool ok, auto masked) {
             constexpr bool MASKED = decltype(masked)::value;
             uint32_t ia[4];
@@ -1107,6 +1150,8 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const float cj = (float)coef(cw, j);
+                uint64_t* bb = binp(ia[j], 0); // plane pp at bb + pp (REC) in both cases
+                if constexpr (REC) bb = ia[j] == hot ? priv_me : bb;
 #pragma unroll
                 for (int pp = 0; pp < NP; ++pp) {
                     const uint32_t b0 = __builtin_bit_cast(uint32_t, fmaf(ps[2 * pp], cj, kMagic));
@@ -1114,27 +1159,40 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
                         (2 * pp + 1 < RC) ? __builtin_bit_cast(uint32_t, fmaf(ps[min(2 * pp + 1, RC - 1)], cj, kMagic))
                                           : 0x4B400000u;
                     const uint64_t wv = (((uint64_t)b1 << 32) | b0) - kMagic2;
-                    __hip_atomic_fetch_add(binp(ia[j], pp), wv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                    __hip_atomic_fetch_add(REC ? bb + pp : binp(ia[j], pp), wv, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_WORKGROUP);
                 }
             }
         };
-        while (tl[0] < n_wt) {
+        {
+            while (tl[0] < n_wt) {
 #pragma unroll
-            for (int d = 0; d < PD; ++d) {
-                const uint32_t nt = tl[d] + (uint32_t)(PD * NW);
-                uint32_t rnext[CPT]; // refs of the slot's next tile, read before this slot's atomics
-                tile_refs(min(nt, n_wt - 1u), rnext);
-                if (tl[d] < n_full) { // uniform; no global loads inside
+                for (int d = 0; d < PD; ++d) {
+                    const uint32_t nt = tl[d] + (uint32_t)(PD * NW);
+                    uint32_t rnext[CPT]; // refs of the slot's next tile, read before this slot's atomics
+                    tile_refs(min(nt, n_wt - 1u), rnext);
+                    if (tl[d] < n_full) { // uniform; no global loads inside
 #pragma unroll
-                    for (int kk = 0; kk < CPT; ++kk) consume(ring[d][kk], true, std::false_type{});
-                } else if (tl[d] < n_wt) {
-                    uint32_t rcur[CPT];
-                    tile_refs(tl[d], rcur);
+                        for (int kk = 0; kk < CPT; ++kk) consume(ring[d][kk], true, std::false_type{});
+                    } else if (tl[d] < n_wt) {
+                        uint32_t rcur[CPT];
+                        tile_refs(tl[d], rcur);
 #pragma unroll
-                    for (int kk = 0; kk < CPT; ++kk) consume(ring[d][kk], rcur[kk] != kBad, std::true_type{});
+                        for (int kk = 0; kk < CPT; ++kk) consume(ring[d][kk], rcur[kk] != kBad, std::true_type{});
+                    }
+                    tile_codes(rnext, ring[d]); // unconditional: past the end they re-read the last tile
+                    tl[d] = nt;
                 }
-                tile_codes(rnext, ring[d]); // unconditional: past the end they re-read the last tile
-                tl[d] = nt;
+            }
+        }
+        if (REC && hot != kNoHot) {
+            // The private bins into the hot atom's bins: one add per wave.
+#pragma unroll
+            for (int pp = 0; pp < NP; ++pp) {
+                uint64_t s = priv_me[pp];
+#pragma unroll
+                for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+                if (lane == 0) __hip_atomic_fetch_add(binp(hot, pp), s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             }
         }
         uint32_t cmx_bits;
@@ -1334,7 +1392,7 @@ inline size_t cold_smem_bytes(uint32_t A, int RC, uint32_t tokens_per_split, uin
     const int NW = kColdThreads / 64, NP = (RC + 1) / 2;
     const size_t tables = (RC == 4 && qbytes == 2) ? (size_t)A * kColdRec : qtab + (size_t)A * NP * 8;
     const size_t n_ref = ((size_t)(tokens_per_split + 15) / 16 + kColdRefPad - 1) / kColdRefPad * kColdRefPad;
-    return tables + n_ref * 4 + (size_t)NW * (2 * RC + 3) * 4;
+    return cold_hp_offset(tables, (uint32_t)n_ref, (uint32_t)(NW * (2 * RC + 4))) + cold_hp_bytes(A, NP);
 }
 
 // ----------------------------------------------- per-row merge factors
