@@ -513,6 +513,9 @@ int launch_hot(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* ws,
     a.splits = o.info.hot_splits;
     a.tokens_per_split = o.info.hot_tokens_per_split;
     a.refs_cap = (uint32_t)align_up(cdiv(a.tokens_per_split, kBlock), 4);
+    // The engine's identity table (contiguous caches, one sequence): the kernel
+    // computes the block instead of reading it.
+    a.refs_identity = (d->refs == (const uint32_t*)e->iota.ptr && d->batch == 1 && d->layers == 1) ? 1u : 0u;
     a.causal = (d->flags & AW_F_CAUSAL) ? 1u : 0u;
     a.n_tok_max = d->hot_tokens ? d->hot_tokens : d->hot_count * kBlock;
     a.seq_tokens = (d->flags & AW_F_SEQ_HOT_TOKENS) ? 1u : 0u;
@@ -524,7 +527,7 @@ int launch_hot(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* ws,
     if (grid > 0x7FFFFFFFull) return fail(e, AW_E_UNSUPPORTED, "hot grid too large");
     StageTimer t(e, AW_STAGE_HOT, st);
     const uint32_t R = a.rows_r;
-    const size_t smem = (size_t)a.refs_cap * 4; // the split's block refs
+    const size_t smem = a.refs_identity ? 0 : (size_t)a.refs_cap * 4; // the split's block refs
 #define AW_LAUNCH_HOT(RTV, SV) hipLaunchKernelGGL((aw::hot_kernel<HD, RTV, SV>), dim3((uint32_t)grid), dim3(64), smem, st, a)
     const bool sepv = a.hot_v != nullptr;
     if (R <= 16) {

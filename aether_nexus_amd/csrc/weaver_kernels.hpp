@@ -131,6 +131,7 @@ struct HotArgs {
     uint32_t batch, queries, q_heads, kv_heads, gqa, rows_r;
     uint32_t hot_count, refs_stride, splits, tokens_per_split, causal;
     uint32_t refs_cap;   // block refs the launch's LDS holds per split (>= tokens_per_split / 16)
+    uint32_t refs_identity; // refs[i] == i for every sequence (a contiguous cache): refs are not read
     uint32_t n_tok_max;  // hot tokens of a sequence (hot_count * 16 unless the request gives fewer)
     uint32_t seq_tokens; // seq_hot counts tokens rather than blocks
     float scale_log2;
@@ -385,18 +386,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu((RT == 1 && 
     const uint32_t t_end = min(t_begin + a.tokens_per_split, n_tok);
     const uint32_t R = a.rows_r;
 
-    // Block refs of this split (at most refs_cap = tokens_per_split / 16 blocks,
-    // dynamic LDS sized by the launch), staged once: the loop reads them with LDS
-    // loads, which never wait behind the K loads.
-    extern __shared__ uint32_t s_refs[];
-    const uint32_t blk0 = t_begin / kBlockTokens;
-    const uint32_t n_blk = t_end > t_begin ? (t_end - t_begin + kBlockTokens - 1) / kBlockTokens : 0u;
-    {
-        const uint32_t* refs = a.refs + (uint64_t)l * a.refs_layer + (uint64_t)(lb % a.batch) * a.refs_stride;
-        for (uint32_t i = (uint32_t)lane; i < n_blk; i += 64u) s_refs[i] = refs[blk0 + i] & kRefMask;
-        __syncthreads();
-    }
-
+    // The query rows first: their loads then overlap the block refs' below.
     half8_t qop[RT][KS];
     int lim[RT];
 #pragma unroll
@@ -407,6 +397,19 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu((RT == 1 && 
 #pragma unroll
         for (int j = 0; j < KS; ++j) qop[rt][j] = as_h8(*(const uint4_t*)(p + 32 * j + 8 * lg));
         lim[rt] = 16u * rt + li < R ? (a.causal ? (int)n_tok - (int)a.queries + 1 + (int)q : (int)n_tok) : 0;
+    }
+
+    // Block refs of this split (at most refs_cap = tokens_per_split / 16 blocks,
+    // dynamic LDS sized by the launch), staged once: the loop reads them with LDS
+    // loads, which never wait behind the K loads.  An identity table (a
+    // contiguous cache) is not read at all: block i of the sequence is block i.
+    extern __shared__ uint32_t s_refs[];
+    const uint32_t blk0 = t_begin / kBlockTokens;
+    const uint32_t n_blk = t_end > t_begin ? (t_end - t_begin + kBlockTokens - 1) / kBlockTokens : 0u;
+    if (!a.refs_identity) {
+        const uint32_t* refs = a.refs + (uint64_t)l * a.refs_layer + (uint64_t)(lb % a.batch) * a.refs_stride;
+        for (uint32_t i = (uint32_t)lane; i < n_blk; i += 64u) s_refs[i] = refs[blk0 + i] & kRefMask;
+        __syncthreads();
     }
 
     float m_run[RT], l_run[RT];
@@ -429,7 +432,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu((RT == 1 && 
         for (int tb = 0; tb < 2; ++tb) {
             const uint32_t bi = (c0 - t_begin) / kBlockTokens + tb;
             const bool in = c0 + 16 * tb < t_end;
-            const uint32_t ref = s_refs[min(bi, a.refs_cap - 1u)]; // entries past n_blk: `in` is false
+            // entries past n_blk: `in` is false
+            const uint32_t ref = a.refs_identity ? blk0 + bi : s_refs[min(bi, a.refs_cap - 1u)];
             ok[tb] = in && ref < a.hot_blocks;
             bad |= in && !ok[tb];
             const uint32_t pr = ok[tb] ? ref : 0u;
@@ -595,20 +599,29 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu((RT == 1 && 
 // v1*2^32 + v0 (v0 sign-extended); sums of such words are exact and decode back
 // to (sum v0, sum v1) while each row sum stays inside int32.
 //
-// Each contribution p*c*2^F is rounded to the nearest integer (ties to even)
-// by one FMA with 1.5*2^23: for |x| < 2^22 the sum's bit pattern is
-// 0x4B400000 + round(x).  The two patterns of a row pair, read as one 64-bit
-// word, minus 0x4B4000004B400000 give exactly v1*2^32 + v0.
+// Each row r has its own scale 2^F_r, so a peaked row is not quantised on the
+// scale of a flat row in the same chunk.  A contribution x = p*c*2^F_r is
+// rounded to an integer in one of two ways, chosen per split:
+//   narrow (every row's largest planned contribution below 2^18): one FMA with
+//     1.5*2^23 rounds to nearest even; for |x| < 2^22 the sum's bit pattern is
+//     0x4B400000 + round(x), and the two patterns of a row pair, read as one
+//     64-bit word, minus 0x4B4000004B400000 give exactly v1*2^32 + v0;
+//   wide (a peaked row, whose largest contributions would otherwise be capped
+//     near 2^18, about 18 significant bits): floor(x + 1/2) by
+//     v_cvt_flr_i32_f32, exact for any |x| < 2^31, and the word v1*2^32 + v0
+//     from the sign of v0; three more VALU operations per row pair.
 //
-// p = 2^(s - ref_r).  ref_r (integral, log2 units) and F come from the split's
-// first tile: ref_r = ceil(max score of the tile); F keeps the planned bound on
-// sum |p*c| over the whole split near 2^28 and the tile's largest contribution
-// below 2^18.  The work-group then streams every tile with no further
-// synchronisation.  At the end two conservative bounds, 4 * max|c| *
-// sum_t sum_r p < 2^31 and max p * max|c| < 2^22, prove the bins exact; when
-// they fail (scores far above the first tile's, coefficients far larger), the
-// split is recomputed exactly: a pass for the per-row maxima, a pass for the
-// exact bound, a pass for the bins.
+// p = 2^(s - ref_r).  ref_r (integral, log2 units) and F_r come from the
+// split's first tile: ref_r = ceil(max score of the tile); F_r keeps the
+// planned bound on row r's sum |p*c| over the whole split near 2^28 and the
+// tile's largest contribution below 2^18 (narrow) or 2^26 (wide).  The
+// work-group then streams every tile with no further synchronisation.  At the
+// end, per row, 4 * max|c| * sum_t p + 2 * tokens < 2^31 - 2^27 (the last term
+// covers the rounding of each contribution) bounds every bin and every single
+// contribution, and a narrow split also needs max p * max|c| < 2^22; together
+// they prove the bins exact.  When they fail (scores far above the first
+// tile's, coefficients far larger), the split is recomputed exactly and wide:
+// a pass for the per-row maxima, a pass for the exact bounds, a pass for the bins.
 //
 // Code loads.  BUF (a layer's pool of at most kColdWindow bytes): buffer loads
 // through a resource whose base is the item's kv head in the layer's pool; the
@@ -629,8 +642,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu((RT == 1 && 
 // global (not constant) memory, so every code load stays a global load.
 __device__ __attribute__((aligned(16))) uint4_t g_zero_code = {0u, 0u, 0u, 0u};
 
-constexpr float kMagic = 12582912.0f;                 // 1.5 * 2^23
-constexpr uint64_t kMagic2 = 0x4B4000004B400000ull;   // two magic patterns
 constexpr uint32_t kBadCodeOff = 0xFFFF0000u;         // staged offset of a token without a code
 constexpr uint64_t kColdWindow = kBadCodeOff;         // largest layer pool (bytes) the buffer loads cover
 constexpr uint32_t kColdRefPad = 16;                  // staged refs are padded to whole wave tiles
@@ -651,6 +662,20 @@ __host__ __device__ constexpr size_t cold_hp_offset(size_t tab, uint32_t n_ref, 
 
 typedef uint16_t ushort2_t __attribute__((ext_vector_type(2)));
 typedef int16_t short2_t __attribute__((ext_vector_type(2)));
+
+constexpr float kMagic = 12582912.0f;                 // 1.5 * 2^23
+constexpr uint64_t kMagic2 = 0x4B4000004B400000ull;   // two magic patterns
+
+// floor(x) as an int32 in one instruction (the compiler emits v_floor_f32 +
+// v_cvt_i32_f32 for the same expression).  Saturates outside int32.
+__device__ __forceinline__ int32_t cvt_flr_i32(float x) {
+    int32_t r;
+    asm("v_cvt_flr_i32_f32 %0, %1" : "=v"(r) : "v"(x));
+    return r;
+}
+// The bins' bound: no bin of a row may reach it (2^31 - 2^27, slack for the
+// float arithmetic of the bound itself).
+constexpr float kBinLimit = 2013265920.0f;
 
 // One work item `wg` (its index in the full grid of work items; the kernel below
 // walks them persistently, one work-group per CU slot).
@@ -995,7 +1020,8 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
     // pair (max scaled score m, sum over tokens of 4*max|c|*2^(s - m)), combined
     // over lanes and waves like log-sum-exp partials, plus max |c|.
     float ref[RC];
-    int F = 0;
+    int F[RC]; // per-row fixed-point scale 2^F_r
+    bool wide = false; // contributions rounded by v_cvt_flr_i32_f32 instead of the 2^22-range FMA
     bool any_bad = false;
     // The split's hottest atom (REC layout only): its adds go to per-lane private
     // bins instead of one LDS address, then one add per wave.  Integer sums, so
@@ -1056,7 +1082,7 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
             ((uint32_t*)red)[wave * NR + 2 * RC + 2] = hkey;
         }
         __syncthreads();
-        float plan = 0.0f, cmax0 = 0.0f;
+        float plan[RC], cmax0 = 0.0f;
 #pragma unroll
         for (int rr = 0; rr < RC; ++rr) {
             float M = -INFINITY;
@@ -1067,7 +1093,7 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
                 const float mv = red[v * NR + 2 * rr];
                 L += mv == -INFINITY ? 0.0f : red[v * NR + 2 * rr + 1] * fast_exp2(mv - ref[rr]);
             }
-            plan += L;
+            plan[rr] = L;
         }
         uint32_t hk = 0;
         for (int v = 0; v < NW; ++v) {
@@ -1076,10 +1102,18 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
             hk = max(hk, ((const uint32_t*)red)[v * NR + 2 * RC + 2]);
         }
         if (REC && (hk >> 16) >= kHotMin) hot = hk & 0xFFFFu;
-        plan *= (float)n_tiles; // bound on sum |p*c| over the split, if tiles are alike
-        const int Fs = plan > 0.0f ? 28 - exp_of(plan) : 100;
-        const int Fm = cmax0 > 0.0f ? 18 - exp_of(cmax0) : 100; // p <= 1 in the first tile
-        F = min(100, max(-100, min(Fs, Fm)));
+        // p <= 1 in the first tile: its contributions stay below 2^18 (narrow) or 2^26 (wide).
+        const int Fm = cmax0 > 0.0f ? 18 - exp_of(cmax0) : 100;
+        int Fs[RC];
+#pragma unroll
+        for (int rr = 0; rr < RC; ++rr) {
+            // Bound on row rr's sum |p*c| over the split, if tiles are alike.
+            const float pl = plan[rr] * (float)n_tiles;
+            Fs[rr] = pl > 0.0f ? 28 - exp_of(pl) : 100;
+            wide |= Fs[rr] > Fm;
+        }
+#pragma unroll
+        for (int rr = 0; rr < RC; ++rr) F[rr] = min(100, max(-100, min(Fs[rr], wide ? Fm + 8 : Fm)));
     }
     // Wave tiles below n_full hold only tokens with codes.
     const uint32_t n_full = any_bad ? 0u : (t_end - t_begin) / WT;
@@ -1087,28 +1121,27 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
     float lpart[RC];
     uint32_t oob = 0;
     bool exact = false;
+    // Attempt 0 streams narrow with the prefetching ring, unless the plan found a
+    // peaked row (wide), which goes straight to attempt 1: the exact recompute,
+    // streamed wide.  Unrolled, so each attempt holds one streaming loop and the
+    // ring's registers are dead in attempt 1.
+#pragma unroll
     for (int attempt = 0; attempt < 2; ++attempt) {
         if (attempt) {
             for (uint32_t at = tid; at < A; at += NT)
 #pragma unroll
                 for (int pp = 0; pp < NP; ++pp) *binp(at, pp) = 0ull;
-#pragma unroll
-            for (int d = 0; d < PD; ++d) {
-                tl[d] = (uint32_t)(wave + d * NW);
-                bool okd[CPT];
-                load_tile(tl[d], ring[d], okd);
-            }
             __syncthreads(); // bins zeroed before any wave adds
         }
+        if (attempt > 0 || !wide) {
         // Stream the split into the bins.  Each slot, once consumed, is refilled
         // with the wave's tile PD*NW further on; slot 0 always holds the wave's
         // earliest tile, so once it is past the end the wave is done.
-        const float Ff = (float)F;
         float rf[RC];
 #pragma unroll
         for (int rr = 0; rr < RC; ++rr) {
             lpart[rr] = 0.0f;
-            rf[rr] = Ff - ref[rr];
+            rf[rr] = (float)F[rr] - ref[rr];
         }
         // max |c| as two packed accumulators of f16 bit patterns: the unsigned
         // maximum holds the largest negative pattern if any (else the largest
@@ -1116,7 +1149,8 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
         // negative); their magnitudes' maximum is max |c|.
         ushort2_t cmu = (ushort2_t)(uint16_t)0;
         short2_t cmi = (short2_t)(int16_t)0x8000;
-        float pmx = 0.0f;
+        float pmx = 0.0f; // largest p * 2^F_r (narrow splits)
+        const bool wide_run = attempt > 0;
         // This lane's private bins of the hot atom (its own [NP] u64; only it touches them).
         uint64_t* priv_me = (uint64_t*)hp + (uint32_t)tid * NP;
         if (hot != kNoHot)
@@ -1124,8 +1158,9 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
             for (int pp = 0; pp < NP; ++pp) priv_me[pp] = 0ull;
         // One code: scores, p (zero for a token without a code when MASKED), bins
         // (the hot atom's go to this lane's private bins; kNoHot matches no atom).
-        auto consume = [&](const uint4_t cw, const bool ok, auto masked) {
+        auto consume = [&](const uint4_t cw, const bool ok, auto masked, auto wide_t) {
             constexpr bool MASKED = decltype(masked)::value;
+            constexpr bool WIDE = decltype(wide_t)::value;
             uint32_t ia[4];
             atoms(cw, ia, oob);
             float sc[RC];
@@ -1137,16 +1172,18 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
                                                                            __builtin_bit_cast(ushort2_t, w3)));
             cmi = __builtin_elementwise_max(cmi, __builtin_elementwise_max(__builtin_bit_cast(short2_t, w2),
                                                                            __builtin_bit_cast(short2_t, w3)));
-            float ps[RC]; // p * 2^F
+            float ps[RC]; // p * 2^F_r
 #pragma unroll
             for (int rr = 0; rr < RC; ++rr) {
                 const float p = fast_exp2(fmaf(sc[rr], sl, rf[rr]));
                 ps[rr] = (!MASKED || ok) ? p : 0.0f;
                 lpart[rr] += ps[rr];
             }
-            if constexpr (RC == 4) pmx = fmaxf(pmx, fmaxf(fmaxf(ps[0], ps[1]), fmaxf(ps[2], ps[3])));
-            else if constexpr (RC == 2) pmx = fmaxf(pmx, fmaxf(ps[0], ps[1]));
-            else pmx = fmaxf(pmx, ps[0]);
+            if constexpr (!WIDE) {
+                if constexpr (RC == 4) pmx = fmaxf(pmx, fmaxf(fmaxf(ps[0], ps[1]), fmaxf(ps[2], ps[3])));
+                else if constexpr (RC == 2) pmx = fmaxf(pmx, fmaxf(ps[0], ps[1]));
+                else pmx = fmaxf(pmx, ps[0]);
+            }
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const float cj = (float)coef(cw, j);
@@ -1154,17 +1191,25 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
                 if constexpr (REC) bb = ia[j] == hot ? priv_me : bb;
 #pragma unroll
                 for (int pp = 0; pp < NP; ++pp) {
-                    const uint32_t b0 = __builtin_bit_cast(uint32_t, fmaf(ps[2 * pp], cj, kMagic));
-                    const uint32_t b1 =
-                        (2 * pp + 1 < RC) ? __builtin_bit_cast(uint32_t, fmaf(ps[min(2 * pp + 1, RC - 1)], cj, kMagic))
-                                          : 0x4B400000u;
-                    const uint64_t wv = (((uint64_t)b1 << 32) | b0) - kMagic2;
+                    uint64_t wv;
+                    if constexpr (WIDE) {
+                        const int32_t v0 = cvt_flr_i32(fmaf(ps[2 * pp], cj, 0.5f));
+                        const int32_t v1 =
+                            (2 * pp + 1 < RC) ? cvt_flr_i32(fmaf(ps[min(2 * pp + 1, RC - 1)], cj, 0.5f)) : 0;
+                        wv = ((uint64_t)(uint32_t)(v1 + (v0 >> 31)) << 32) | (uint32_t)v0;
+                    } else {
+                        const uint32_t b0 = __builtin_bit_cast(uint32_t, fmaf(ps[2 * pp], cj, kMagic));
+                        const uint32_t b1 = (2 * pp + 1 < RC)
+                                                ? __builtin_bit_cast(uint32_t, fmaf(ps[min(2 * pp + 1, RC - 1)], cj, kMagic))
+                                                : 0x4B400000u;
+                        wv = (((uint64_t)b1 << 32) | b0) - kMagic2;
+                    }
                     __hip_atomic_fetch_add(REC ? bb + pp : binp(ia[j], pp), wv, __ATOMIC_RELAXED,
                                            __HIP_MEMORY_SCOPE_WORKGROUP);
                 }
             }
         };
-        {
+        if (!wide_run) {
             while (tl[0] < n_wt) {
 #pragma unroll
                 for (int d = 0; d < PD; ++d) {
@@ -1173,16 +1218,29 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
                     tile_refs(min(nt, n_wt - 1u), rnext);
                     if (tl[d] < n_full) { // uniform; no global loads inside
 #pragma unroll
-                        for (int kk = 0; kk < CPT; ++kk) consume(ring[d][kk], true, std::false_type{});
+                        for (int kk = 0; kk < CPT; ++kk)
+                            consume(ring[d][kk], true, std::false_type{}, std::false_type{});
                     } else if (tl[d] < n_wt) {
                         uint32_t rcur[CPT];
                         tile_refs(tl[d], rcur);
 #pragma unroll
-                        for (int kk = 0; kk < CPT; ++kk) consume(ring[d][kk], rcur[kk] != kBad, std::true_type{});
+                        for (int kk = 0; kk < CPT; ++kk)
+                            consume(ring[d][kk], rcur[kk] != kBad, std::true_type{}, std::false_type{});
                     }
                     tile_codes(rnext, ring[d]); // unconditional: past the end they re-read the last tile
                     tl[d] = nt;
                 }
+            }
+        } else {
+            // Wide splits (peaked rows, or the exact recompute): a plain tile loop
+            // with one tile in flight, so that its registers stay within those of
+            // the prefetching loop above.
+            for (uint32_t tile = wave; tile < n_wt; tile += NW) {
+                uint4_t cur[CPT];
+                bool curv[CPT];
+                load_tile(tile, cur, curv);
+#pragma unroll
+                for (int kk = 0; kk < CPT; ++kk) consume(cur[kk], curv[kk], std::true_type{}, std::true_type{});
             }
         }
         if (REC && hot != kNoHot) {
@@ -1202,8 +1260,9 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
             cmx_bits = max(mu, mi);
         }
         const float cmx = (float)__builtin_bit_cast(_Float16, (uint16_t)cmx_bits);
-        // Overflow proof: every |bin| <= sum over contributions |p*c|*2^F <= 4*max|c|*sum_r sum_t p*2^F,
-        // and every contribution |p*c|*2^F <= max p*2^F * max|c| stays inside the rounding trick.
+        // Overflow proof, per row: every |bin| <= sum over its contributions (|p*c|*2^F_r + 1/2)
+        // <= 4*max|c|*sum_t p*2^F_r + 2*tokens, and so is every single contribution; a narrow
+        // split's contributions |p*c|*2^F_r <= max p*2^F_r * max|c| stay inside the FMA's 2^22.
         float v[NB];
         bool is_max[NB];
 #pragma unroll
@@ -1218,20 +1277,19 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
         v[RC + 1] = pmx;
         is_max[RC + 1] = true;
         wg_reduce(v, is_max);
-        float psum = 0.0f;
+        float lmax = 0.0f;
 #pragma unroll
         for (int rr = 0; rr < RC; ++rr) {
             lpart[rr] = v[rr];
-            psum += v[rr];
+            lmax = fmaxf(lmax, v[rr]);
         }
-        const float bound = 4.0f * v[RC] * psum; // already in units of 2^-F
-        const float cbound = v[RC + 1] * v[RC];
-        if (exact || (bound < 2147483648.0f && cbound < 4194304.0f)) break;
+        const float bound = 4.0f * v[RC] * lmax + 2.0f * (float)(t_end - t_begin); // units of 2^-F_r
+        if (exact || (bound < kBinLimit && v[RC + 1] * v[RC] < 4194304.0f)) break;
+        }
 
         // Exact path: per-row maxima, then the exact bound, then the bins.
         exact = true;
         float mx[RC];
-        float cm2 = 0.0f;
 #pragma unroll
         for (int rr = 0; rr < RC; ++rr) mx[rr] = -INFINITY;
         for (uint32_t tile = wave; tile < n_wt; tile += NW) {
@@ -1278,7 +1336,6 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
                     float ca = 0.0f;
 #pragma unroll
                     for (int j = 0; j < 4; ++j) ca += fabsf((float)coef(cur[kk], j));
-                    cm2 = fmaxf(cm2, cmax_f(cur[kk]));
 #pragma unroll
                     for (int rr = 0; rr < RC; ++rr) ebr[rr] += fast_exp2(sc[rr] * sl - ref[rr]) * ca;
                 }
@@ -1288,16 +1345,11 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
             m2[i] = i < RC ? ebr[i] : 0.0f;
             im2[i] = false;
         }
-        m2[RC] = cm2;
-        im2[RC] = true;
         wg_reduce(m2, im2);
-        float eb = 0.0f; // exact sum over contributions of |p*c|, maximised over rows
+        // Row rr's exact sum over contributions of |p*c|: its bins stay within
+        // 2^29 * (1 + float rounding) + 2 * tokens.
 #pragma unroll
-        for (int rr = 0; rr < RC; ++rr) eb = fmaxf(eb, m2[rr]);
-        // p <= 1 now: contributions are at most max|c| * 2^F.
-        const int Fs = eb > 0.0f ? 29 - exp_of(eb) : 100;
-        const int Fm = m2[RC] > 0.0f ? 21 - exp_of(m2[RC]) : 100;
-        F = min(100, max(-100, min(Fs, Fm)));
+        for (int rr = 0; rr < RC; ++rr) F[rr] = m2[rr] > 0.0f ? min(100, max(-100, 29 - exp_of(m2[rr]))) : 100;
         __syncthreads(); // every wave is done with the bins
     }
     // Atom indices outside the dictionary: recorded (their terms went to a clamped atom).
@@ -1308,7 +1360,17 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
         if (badat) flag_error(a.err, kErrAtom);
     }
     // Bins out as float rows [r][A] (or tiled); track max |bin| per row for the f16 split of the finish.
-    const float inv = pow2f(-F);
+    float inv[RC];
+#pragma unroll
+    for (int rr = 0; rr < RC; ++rr) inv[rr] = pow2f(-F[rr]);
+    // 2^-F_rr for a row index known only at run time, by arithmetic: selects over
+    // the array would be folded into an indexed load from scratch memory.
+    auto inv_of = [&](int rr) -> float {
+        int f = 0;
+#pragma unroll
+        for (int k = 0; k < RC; ++k) f += F[k] * (int)(rr == k);
+        return pow2f(-f);
+    };
     float amax[RC];
 #pragma unroll
     for (int rr = 0; rr < RC; ++rr) amax[rr] = 0.0f;
@@ -1317,7 +1379,7 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
         const uint64_t wv = *binp(at, rr / 2);
         const int32_t v0 = (int32_t)(uint32_t)wv;
         const int32_t v1 = (int32_t)((uint32_t)(wv >> 32) + (v0 < 0 ? 1u : 0u));
-        return (float)((rr & 1) ? v1 : v0) * inv;
+        return (float)((rr & 1) ? v1 : v0) * inv_of(rr);
     };
     if (a.w_tiled) {
         // Thread -> (group of 4 atoms, row): 16-byte pieces, the rows of one piece
@@ -1349,7 +1411,7 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
             for (int h = 0; h < 2; ++h) {
                 const int rr = 2 * pp + h;
                 if (rr >= RC) continue;
-                const float v = (float)(h ? v1 : v0) * inv;
+                const float v = (float)(h ? v1 : v0) * inv[rr];
                 amax[rr] = fmaxf(amax[rr], fabsf(v));
                 const uint32_t r = c * RC + rr;
                 if (r < R) a.part_w[(pbase + r) * a.w_pitch + at] = v;
@@ -1364,14 +1426,16 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
         is_max[i] = true;
     }
     wg_reduce(v, is_max);
-    if (tid < RC) {
-        const uint32_t r = c * RC + tid;
-        if (r < R) {
-            a.part_m[pbase + r] = ref[tid];
-            a.part_l[pbase + r] = lpart[tid] * inv; // sum of p, back from units of 2^-F
-            a.part_amax[pbase + r] = v[tid];
+#pragma unroll
+    for (int rr = 0; rr < RC; ++rr) // static indices: no register array indexed at run time
+        if (tid == rr) {
+            const uint32_t r = c * RC + rr;
+            if (r < R) {
+                a.part_m[pbase + r] = ref[rr];
+                a.part_l[pbase + r] = lpart[rr] * inv[rr]; // sum of p, back from units of 2^-F_r
+                a.part_amax[pbase + r] = v[rr];
+            }
         }
-    }
 }
 
 // Persistent: work-group i takes work items i, i + gridDim.x, ... (gridDim.x a

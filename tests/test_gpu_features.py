@@ -168,10 +168,12 @@ def full_size(engine, stream, geom, seed, n_rows, what):
 
 
 @pytest.mark.parametrize("geom", [W.sweep(8), W.hot_cold(hot_count=3, cold_count=40, dict_size=256, batch=3),
-                                  W.tiny(q_heads=4, kv_heads=2, dict_heads=2)], ids=["sweep_b8", "ragged", "perhead"])
+                                  W.tiny(q_heads=4, kv_heads=2, dict_heads=2), W.sweep(16, zipf=1.1)],
+                         ids=["sweep_b8", "ragged", "perhead", "sweep_b16_zipf"])
 def test_cold_head_blocked_layout_bit_identical(engine, stream, geom):
     """AW_F_COLD_HEAD_BLOCKED: the same codes laid out [blocks][kv_heads][16] give
-    the same output bits as the reference layout [blocks][16][kv_heads]."""
+    the same output bits as the reference layout [blocks][16][kv_heads].  The
+    Zipf case runs the hot-atom private bins (4-row chunks, 2 splits)."""
     wl = W.generate(geom, seed=55, device="cuda:0")
     ref = torch.empty(wl.out_shape(), dtype=torch.float16, device="cuda:0")
     engine.decode_device(W.device_desc(wl, ref), stream=stream)
@@ -182,10 +184,12 @@ def test_cold_head_blocked_layout_bit_identical(engine, stream, geom):
     assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
 
 
-def test_repeat_calls_bit_identical(engine, stream):
+@pytest.mark.parametrize("zipf", [None, 1.1], ids=["uniform", "zipf"])
+def test_repeat_calls_bit_identical(engine, stream, zipf):
     """The same inputs give the same output bits on every call (fixed
-    reduction orders; integer bins), also after other decodes ran in between."""
-    geom = W.sweep(16)
+    reduction orders; integer bins, also the hot atom's private bins under
+    Zipf), also after other decodes ran in between."""
+    geom = W.sweep(16, zipf=zipf)
     wl = W.generate(geom, seed=53, device="cuda:0")
     outs = []
     for i in range(3):
