@@ -1825,7 +1825,9 @@ __global__ __launch_bounds__(kFinishWaves * 64) void finish_kernel(FinishArgs a)
 // with one atom range the row is merged with its hot partials and written as
 // f16, otherwise the range partial goes to `ocp` for merge_kernel.
 constexpr int kFinRowsWaves = 8;
-constexpr int kFinRowsPD = 4; // k-steps of loads in flight per wave
+// k-steps of loads in flight per wave: 2 measured faster than 3 or 4 (B = 64 finish 15.0 against
+// 16.9 and 16.8 us: deeper rings issue more than the CU's memory pipeline drains).
+constexpr int kFinRowsPD = 2;
 
 inline size_t finish_rows_smem_bytes(int HD) { return (size_t)kFinRowsWaves * (HD / 16) * 64 * 16; }
 
