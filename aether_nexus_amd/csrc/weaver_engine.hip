@@ -1000,27 +1000,37 @@ int aw_engine_create(int device, aw_engine** out) {
                 e->hot_wpc[i] = (uint32_t)nb;
         }
     }
-    // Let the cold, finish and projection kernels use the device's full LDS.
+    // Let the cold, finish and projection kernels use the device's full LDS.  A
+    // refusal (a kernel whose static LDS leaves less than that) fails the
+    // engine here, and its error is cleared so that it does not surface at the
+    // caller's next HIP call.
+    bool attr_ok = true;
+    auto set_lds = [&](const void* f) {
+        if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)e->max_lds) != hipSuccess) {
+            attr_ok = false;
+            (void)hipGetLastError();
+        }
+    };
     {
         for (uint32_t rcv : {1u, 2u, 4u})
             for (bool p2 : {false, true})
                 for (bool qf : {false, true})
                     for (bool bf : {false, true})
-                        (void)hipFuncSetAttribute(cold_kernel_fn(rcv, p2, qf, bf),
-                                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)e->max_lds);
+                        set_lds(cold_kernel_fn(rcv, p2, qf, bf));
         const void* fin[] = {(const void*)aw::finish_kernel<128, true>, (const void*)aw::finish_kernel<128, false>,
                              (const void*)aw::finish_kernel<64, true>, (const void*)aw::finish_kernel<64, false>};
-        for (const void* f : fin)
-            (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)e->max_lds);
+        for (const void* f : fin) set_lds(f);
         const void* finr[] = {(const void*)aw::finish_rows_kernel<128>, (const void*)aw::finish_rows_kernel<64>};
-        for (const void* f : finr)
-            (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)e->max_lds);
+        for (const void* f : finr) set_lds(f);
         const void* proj[] = {(const void*)aw::project_kernel<128, 32, 64, 2>, (const void*)aw::project_kernel<128, 128, 256, 2>,
                               (const void*)aw::project_kernel<128, 128, 128, 4>, (const void*)aw::project_kernel<128, 128, 64, 8>,
                               (const void*)aw::project_kernel<64, 32, 64, 2>, (const void*)aw::project_kernel<64, 128, 256, 2>,
                               (const void*)aw::project_kernel<64, 128, 128, 4>, (const void*)aw::project_kernel<64, 128, 64, 8>};
-        for (const void* f : proj)
-            (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)e->max_lds);
+        for (const void* f : proj) set_lds(f);
+    }
+    if (!attr_ok) {
+        aw_engine_destroy(e);
+        return AW_E_HIP;
     }
     if (hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking) != hipSuccess ||
         hipStreamCreateWithFlags(&e->side, hipStreamNonBlocking) != hipSuccess ||
