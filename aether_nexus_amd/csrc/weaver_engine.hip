@@ -1438,6 +1438,46 @@ int aw_debug_read_stream(aw_engine* e, const void* buf, uint64_t bytes, uint32_t
     return AW_OK;
 }
 
+int aw_debug_read_pools(aw_engine* e, const aw_decode_desc* d, uint32_t* sink, void* stream) {
+    if (!e) return AW_E_INVALID_ARG;
+    if (!d || !sink) return fail(e, AW_E_INVALID_ARG, "desc and sink are required");
+    if (d->layers == 0 || d->batch == 0 || d->kv_heads == 0 || (d->head_dim != 64 && d->head_dim != 128))
+        return fail(e, AW_E_INVALID_ARG, "layers, batch, kv_heads >= 1 and head_dim 64 or 128 are required");
+    if (d->refs_stride < d->hot_count + d->cold_count) return fail(e, AW_E_INVALID_ARG, "refs_stride too small");
+    if ((d->hot_count && (!d->hot_k || !d->hot_blocks)) || (d->cold_count && (!d->cold || !d->cold_blocks)) ||
+        ((d->hot_count || d->cold_count) && !d->refs))
+        return fail(e, AW_E_INVALID_ARG, "pools, capacities and refs are required for the blocks asked for");
+    if (((uintptr_t)d->hot_k | (uintptr_t)d->hot_v | (uintptr_t)d->cold) & 15u)
+        return fail(e, AW_E_ALIGN, "pools must be 16-byte aligned");
+    AW_HIP(e, hipSetDevice(e->device));
+    aw::GatherArgs a{};
+    a.hot_k = (const aw::uint4_t*)d->hot_k;
+    a.hot_v = (const aw::uint4_t*)d->hot_v;
+    a.cold = (const aw::uint4_t*)d->cold;
+    a.refs = d->refs;
+    a.sink = sink;
+    a.batch = d->batch;
+    a.kv_heads = d->kv_heads;
+    a.hd16 = d->head_dim / 8;
+    a.hot_count = d->hot_count;
+    a.cold_count = d->cold_count;
+    a.refs_stride = d->refs_stride;
+    a.cold_head_blocked = (d->flags & AW_F_COLD_HEAD_BLOCKED) ? 1u : 0u;
+    a.hot_units = (uint32_t)cdiv(d->hot_count, aw::kGatherHotBlocks);
+    a.cold_units = (uint32_t)cdiv(d->cold_count, aw::kGatherColdBlocks);
+    a.hot_blocks = d->hot_blocks;
+    a.cold_blocks = d->cold_blocks;
+    a.hot_layer16 = d->hot_blocks * kBlock * d->kv_heads * a.hd16;
+    a.cold_layer16 = d->cold_blocks * kBlock * d->kv_heads;
+    a.refs_layer = (uint64_t)d->batch * d->refs_stride;
+    const uint64_t grid = (uint64_t)d->layers * d->batch * d->kv_heads * (a.hot_units + a.cold_units);
+    if (grid == 0) return AW_OK;
+    if (grid > 0x7FFFFFFFull) return fail(e, AW_E_UNSUPPORTED, "gather grid too large");
+    hipLaunchKernelGGL(aw::gather_read_kernel<8>, dim3((uint32_t)grid), dim3(64), 0, (hipStream_t)stream, a);
+    AW_HIP(e, hipGetLastError());
+    return AW_OK;
+}
+
 int aw_engine_set_profiling(aw_engine* e, int enable) {
     if (!e) return AW_E_INVALID_ARG;
     if (enable < AW_PROFILE_OFF || enable > AW_PROFILE_SERIAL) return fail(e, AW_E_INVALID_ARG, "profiling mode %d", enable);

@@ -2196,6 +2196,95 @@ __global__ __launch_bounds__(256) void read_stream_kernel(const uint4_t* p, uint
     if (x == kReadSinkMagic) sink[threadIdx.x & 63u] = x; // lane-indexed: a vector store
 }
 
+// ------------------------------------------------ pool gather (read only)
+//
+// The attainable rate of the decode's own pool reads: every hot K (and V) row
+// and every cold code of a request, through its block table, in the pools'
+// layouts, with nothing computed and (almost) nothing written.  One wave per
+// unit: a (layer, sequence, kv head) and a stretch of kGatherHotBlocks hot
+// blocks (16 rows of HD halves each) or kGatherColdBlocks cold blocks (16
+// codes each); the unit's block refs are staged in LDS first (as the decode
+// kernels stage theirs), then every lane keeps U 16-byte loads in flight.
+// A wave's XOR fold is written to `sink` only when it equals kReadSinkMagic.
+constexpr uint32_t kGatherHotBlocks = 32;   // 512 tokens: the hot kernel's split at B = 64
+constexpr uint32_t kGatherColdBlocks = 256; // 4096 tokens
+
+struct GatherArgs {
+    const uint4_t* hot_k;
+    const uint4_t* hot_v; // may be null
+    const uint4_t* cold;
+    const uint32_t* refs;
+    uint32_t* sink;
+    uint32_t batch, kv_heads, hd16; // hd16: 16-byte pieces per row (HD / 8)
+    uint32_t hot_count, cold_count, refs_stride, cold_head_blocked;
+    uint32_t hot_units, cold_units; // per (layer, sequence, kv head)
+    uint64_t hot_blocks, cold_blocks, hot_layer16, cold_layer16, refs_layer;
+};
+
+template <int U>
+__global__ __launch_bounds__(64) void gather_read_kernel(GatherArgs a) {
+    __shared__ uint32_t s_ref[kGatherColdBlocks];
+    const uint32_t lane = threadIdx.x;
+    const uint32_t per = a.hot_units + a.cold_units;
+    const uint32_t unit = blockIdx.x % per, lbg = blockIdx.x / per;
+    const uint32_t g = lbg % a.kv_heads, lb = lbg / a.kv_heads, l = lb / a.batch;
+    const uint32_t* refs = a.refs + (uint64_t)l * a.refs_layer + (uint64_t)(lb % a.batch) * a.refs_stride;
+    const bool hot = unit < a.hot_units;
+    const uint32_t nblk_all = hot ? a.hot_count : a.cold_count;
+    const uint32_t per_unit = hot ? kGatherHotBlocks : kGatherColdBlocks;
+    const uint32_t b0 = (hot ? unit : unit - a.hot_units) * per_unit;
+    const uint32_t nb = b0 < nblk_all ? min(per_unit, nblk_all - b0) : 0u;
+    const uint64_t cap = hot ? a.hot_blocks : a.cold_blocks;
+    for (uint32_t i = lane; i < nb; i += 64u) {
+        const uint32_t r = refs[(hot ? 0u : a.hot_count) + b0 + i] & 0x7FFFFFFFu;
+        s_ref[i] = r < cap ? r : 0u;
+    }
+    __syncthreads();
+    uint4_t acc = (uint4_t)0u;
+    if (hot) {
+        // Row (block i, token t): hd16 pieces; a load instruction covers 64 / hd16 rows.
+        const uint32_t rows = nb * 16u, pieces = rows * a.hd16;
+        const uint4_t* kb = a.hot_k + (uint64_t)l * a.hot_layer16;
+        const uint4_t* vb = a.hot_v ? a.hot_v + (uint64_t)l * a.hot_layer16 : nullptr;
+        auto addr = [&](uint32_t pc) -> uint64_t {
+            const uint32_t row = pc / a.hd16, q = pc % a.hd16;
+            return (((uint64_t)s_ref[row / 16u] * 16u + row % 16u) * a.kv_heads + g) * a.hd16 + q;
+        };
+        for (uint32_t p0 = 0; p0 < pieces; p0 += 64u * U) {
+            uint4_t v[U], w[U];
+#pragma unroll
+            for (int j = 0; j < U; ++j) {
+                const uint32_t pc = min(p0 + (uint32_t)j * 64u + lane, pieces - 1u);
+                v[j] = kb[addr(pc)];
+                if (vb) w[j] = vb[addr(pc)];
+            }
+#pragma unroll
+            for (int j = 0; j < U; ++j) {
+                acc ^= v[j];
+                if (vb) acc ^= w[j];
+            }
+        }
+    } else {
+        const uint32_t codes = nb * 16u;
+        const uint4_t* cb = a.cold + (uint64_t)l * a.cold_layer16;
+        for (uint32_t c0 = 0; c0 < codes; c0 += 64u * U) {
+            uint4_t v[U];
+#pragma unroll
+            for (int j = 0; j < U; ++j) {
+                const uint32_t c = min(c0 + (uint32_t)j * 64u + lane, codes - 1u);
+                const uint64_t blk = s_ref[c / 16u], t = c % 16u;
+                v[j] = cb[a.cold_head_blocked ? (blk * a.kv_heads + g) * 16u + t : (blk * 16u + t) * a.kv_heads + g];
+            }
+#pragma unroll
+            for (int j = 0; j < U; ++j) acc ^= v[j];
+        }
+    }
+    uint32_t x = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x ^= (uint32_t)__shfl_xor((int)x, o);
+    if (x == kReadSinkMagic) a.sink[lane] = x; // lane-indexed: a vector store
+}
+
 // ------------------------------------------------ codec check (bit-exact)
 __global__ void gather_codes_kernel(const uint4_t* codes, uint64_t n, const uint16_t* dict, uint32_t A,
                                     uint32_t HD, uint32_t* idx, float* coef, uint16_t* atoms, uint32_t* err) {

@@ -207,6 +207,12 @@ class WeaverEngine:
         rc = self._lib.aw_debug_read_stream(self._h, _ptr(buf), nbytes, waves_per_cu, _ptr(sink), _stream(stream))
         self._check(rc, "read_stream")
 
+    def read_pools(self, desc: DecodeDesc, sink, stream: Optional[int] = None) -> None:
+        """Enqueue a read of every hot row and cold code of ``desc`` through its block
+        table, nothing computed (the attainable rate of the decode's pool reads)."""
+        rc = self._lib.aw_debug_read_pools(self._h, ctypes.byref(desc), _ptr(sink), _stream(stream))
+        self._check(rc, "read_pools")
+
     def decode_device_noalloc(self, desc: DecodeDesc, stream: Optional[int] = None) -> None:
         """``decode_device`` with its scratch in the library's fixed per-GPU array
         (AW_NOALLOC_SCRATCH_BYTES): allocates nothing; larger requests raise."""

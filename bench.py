@@ -271,6 +271,38 @@ def hbm_read_peak(engine, mib: int = 2048, reps: int = 10) -> dict:
             "read": f"aw_debug_read_stream over {mib} MiB, {reps} passes, bytes read counted"}
 
 
+def pool_gather_rate(engine, runner, reps: int = 20) -> dict:
+    """The attainable rate of the decode's own pool reads (aw_debug_read_pools):
+    every hot row and cold code of the runner's request through its block table,
+    in the pools' layouts, nothing computed, rotating over the same pool copies
+    as the timed steps.  Bytes counted: the hot rows, the codes and the block
+    refs of both pools."""
+    import torch
+    from aether_nexus_amd.types import BLOCK_SIZE
+    g = runner.geom
+    B, Hkv, D = g.batch * g.layers, g.kv_heads, g.head_dim
+    nbytes = B * Hkv * (g.hot_count * BLOCK_SIZE * D * 2 + g.cold_count * BLOCK_SIZE * 16) + \
+        B * (g.hot_count + g.cold_count) * 4
+    sink = torch.zeros(64, dtype=torch.int32, device="cuda:0")
+    s = runner.stream
+    with torch.cuda.stream(s):
+        for d in runner.descs:
+            engine.read_pools(d, sink, stream=s.cuda_stream)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(s)
+        for i in range(reps):
+            engine.read_pools(runner.descs[i % len(runner.descs)], sink, stream=s.cuda_stream)
+        b.record(s)
+    torch.cuda.synchronize()
+    us = a.elapsed_time(b) * 1e3 / reps
+    gbps = nbytes / (us * 1e-6) / 1e9
+    return {"gbps": round(gbps, 1), "frac_of_nominal": round(gbps / PEAK_HBM_GBPS, 4), "us": round(us, 2),
+            "bytes": int(nbytes),
+            "read": f"aw_debug_read_pools over the B={g.batch} request's hot rows, codes and block refs "
+                    f"({'head-blocked' if runner.cold_hb is not None else 'reference-order'} cold pool, "
+                    f"{len(runner.descs)} pool copies), {reps} passes"}
+
+
 # BASELINE configurations timed beside the sweep (config 3 is the sweep at B = 1).
 CONFIGS = {
     "2": "hot-only exact f16 decode, 32q/8kv heads, head_dim 128, hot 4096 tokens, no cold pool, B=1, "
@@ -1083,6 +1115,11 @@ def main():
     copy_peak = hbm_copy_peak()
     read_peak = hbm_read_peak(engine)
     log(json.dumps({"hbm_read_peak": read_peak}))
+    gather_peak = pool_gather_rate(engine, r)
+    log(json.dumps({"hbm_gather_peak": gather_peak}))
+    if "hot_cold_phase" in roofline:
+        ph = roofline["hot_cold_phase"]
+        ph["frac_of_gather_peak"] = round(ph["achieved"] / gather_peak["gbps"], 4)
     # The same workload with the cold pool in the other order (by default the
     # reference's file order [blocks][16][kv_heads], where one kv head's code is
     # 16 bytes of every 128-byte token line): output bits must be identical.
@@ -1154,6 +1191,7 @@ def main():
         "roofline": roofline,
         "hbm_copy_peak": copy_peak,
         "hbm_read_peak": read_peak,
+        "hbm_gather_peak": gather_peak,
         "configs": configs,
         "mfma_kernels": mfma,
         "other_cold_layout": alt,

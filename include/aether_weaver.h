@@ -399,6 +399,17 @@ int aw_block_entropy_device(aw_engine* engine, const uint16_t* hot, uint64_t hot
 int aw_debug_read_stream(aw_engine* engine, const void* buf, uint64_t bytes, uint32_t waves_per_cu,
                          uint32_t* sink, void* hip_stream);
 
+/* No reference counterpart: the attainable HBM rate of a decode's own pool
+ * reads.  Reads every hot K (and V) row and every cold code of the request
+ * `desc` describes (its pools, block refs, counts and cold order; q, dict and
+ * out are not used), through the block table, in the pools' layouts, one wave
+ * per stretch of 32 hot or 256 cold blocks of a (layer, sequence, kv head),
+ * nothing computed; a wave writes its XOR fold into `sink` (64 u32, device)
+ * only when it equals 0xA5A5A5A5.  Per-sequence counts (seq_hot, seq_cold) are
+ * ignored: every sequence's hot_count and cold_count blocks are read.
+ * Asynchronous on `hip_stream`. */
+int aw_debug_read_pools(aw_engine* engine, const aw_decode_desc* desc, uint32_t* sink, void* hip_stream);
+
 /* Per-stage kernel timing with HIP events recorded on the stream each kernel
  * runs on: every launch is bracketed by a pair of events.  AW_PROFILE_ON keeps
  * the pipeline as it runs unprofiled (the hot kernel on the engine's side

@@ -232,6 +232,41 @@ def test_full_size_spec_verify(engine, stream):
     torch.cuda.empty_cache()
 
 
+@pytest.mark.parametrize("head_blocked", [False, True], ids=["reference_order", "head_blocked"])
+def test_read_pools_reads_through_the_block_table(engine, stream, head_blocked):
+    """aw_debug_read_pools (the attainable rate of the decode's pool reads): zero
+    pools leave the sink untouched; one 16-byte piece set to the sink value at the
+    physical block that a sequence's block table points to (its first hot row,
+    then its first cold code of kv head 0) makes the wave that reads it write the
+    sink, so the probe reads through the refs and in the pool's order."""
+    geom = W.hot_cold(batch=3, hot_count=5, cold_count=40)
+    wl = W.generate(geom, seed=61, device="cuda:0")
+    wl.hot_k.zero_()
+    wl.cold.zero_()
+    magic = int(np.array([0xA5A5A5A5], dtype=np.uint32).view(np.int32)[0])
+    out = torch.empty(wl.out_shape(), dtype=torch.float16, device="cuda:0")
+    sink = torch.zeros(64, dtype=torch.int32, device="cuda:0")
+    hb = W.head_blocked(wl.cold) if head_blocked else None
+    engine.read_pools(W.device_desc(wl, out, cold_head_blocked=hb), sink, stream=stream)
+    torch.cuda.synchronize()
+    assert int(sink.abs().sum()) == 0
+    refs = wl.refs[0].view(torch.int32).cpu().numpy().reshape(geom.layers, geom.batch, -1) & 0x7FFFFFFF
+    b = 1
+    hot_blk = int(refs[0, b, 0])
+    wl.hot_k.view(torch.int32)[0, hot_blk, 0, 0, 0] = magic  # [L][blocks][16][Hkv][d] f16 -> first 4 bytes
+    engine.read_pools(W.device_desc(wl, out, cold_head_blocked=hb), sink, stream=stream)
+    torch.cuda.synchronize()
+    assert bool((sink == magic).all())
+    wl.hot_k.zero_()
+    sink.zero_()
+    cold_blk = int(refs[0, b, geom.hot_count])
+    cold = hb if head_blocked else wl.cold
+    cold.view(torch.int32).view(geom.layers, geom.cold_blocks, -1)[0, cold_blk, 0] = magic  # first code of the block, kv head 0
+    engine.read_pools(W.device_desc(wl, out, cold_head_blocked=hb), sink, stream=stream)
+    torch.cuda.synchronize()
+    assert bool((sink == magic).all())
+
+
 def test_read_stream_reads_the_buffer(engine, stream):
     """aw_debug_read_stream (the attainable-read-rate probe): a zero buffer leaves
     the sink untouched; one word set to the sink value makes the wave that reads
