@@ -39,6 +39,7 @@ SIGNATURES = {
     "aw_decode_device_noalloc": (_c_int, [_vp, _vp, _vp]),
     "aw_debug_read_stream": (_c_int, [_vp, _vp, ctypes.c_uint64, ctypes.c_uint32, _vp, _vp]),
     "aw_debug_read_pools": (_c_int, [_vp, _vp, _vp, _vp]),
+    "aw_debug_project": (_c_int, [_vp, _vp, _vp, _vp]),
     "aw_multihead_attention_device": (_c_int, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u64, _vp]),
     "aw_engine_check_device_errors": (_c_int, [_vp, _vp]),
     "aw_debug_gather_codes": (_c_int, [_vp, _vp, _sz, _vp, _u32, _u32, _vp, _vp, _vp, _vp]),

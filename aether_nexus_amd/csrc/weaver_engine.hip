@@ -1438,6 +1438,27 @@ int aw_debug_read_stream(aw_engine* e, const void* buf, uint64_t bytes, uint32_t
     return AW_OK;
 }
 
+int aw_debug_project(aw_engine* e, const aw_decode_desc* d, void* q_latent, void* stream) {
+    if (!e) return AW_E_INVALID_ARG;
+    if (!d || !q_latent) return fail(e, AW_E_INVALID_ARG, "desc and q_latent are required");
+    Layout o;
+    char msg[256] = {0};
+    int rc = plan(d, e->max_lds, e->n_cu, e->hot_wpc, &o, msg, sizeof msg);
+    if (rc) return fail(e, rc, "%s", msg);
+    if (!o.info.computes_q_latent)
+        return fail(e, AW_E_INVALID_ARG, "the request does not compute q_latent (it needs a cold pool and q_latent NULL)");
+    if (!d->q || !d->dict) return fail(e, AW_E_INVALID_ARG, "q and dict are required");
+    AW_HIP(e, hipSetDevice(e->device));
+    hipStream_t st = (hipStream_t)stream; // NULL is HIP's null stream
+    if ((rc = ensure_keep(e->ws, o.info.workspace_bytes, e->retired_ws, e->last_error, st))) return rc;
+    char* ws = (char*)e->ws.ptr;
+    rc = d->head_dim == 64 ? launch_project<64>(e, d, o, ws, st) : launch_project<128>(e, d, o, ws, st);
+    if (rc) return rc;
+    const size_t bytes = (size_t)d->layers * d->batch * d->queries * d->q_heads * d->dict_size * (o.qf32 ? 4 : 2);
+    AW_HIP(e, hipMemcpyAsync(q_latent, ws + o.off_ql, bytes, hipMemcpyDeviceToDevice, st));
+    return AW_OK;
+}
+
 int aw_debug_read_pools(aw_engine* e, const aw_decode_desc* d, uint32_t* sink, void* stream) {
     if (!e) return AW_E_INVALID_ARG;
     if (!d || !sink) return fail(e, AW_E_INVALID_ARG, "desc and sink are required");

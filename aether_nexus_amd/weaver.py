@@ -207,6 +207,12 @@ class WeaverEngine:
         rc = self._lib.aw_debug_read_stream(self._h, _ptr(buf), nbytes, waves_per_cu, _ptr(sink), _stream(stream))
         self._check(rc, "read_stream")
 
+    def project(self, desc: DecodeDesc, q_latent, stream: Optional[int] = None) -> None:
+        """Run the request's q_latent = q . D^T projection alone into ``q_latent``
+        (device, [L][B][Q][Hq][A], f16 or fp32 with AW_F_QLATENT_F32)."""
+        rc = self._lib.aw_debug_project(self._h, ctypes.byref(desc), _ptr(q_latent), _stream(stream))
+        self._check(rc, "project")
+
     def read_pools(self, desc: DecodeDesc, sink, stream: Optional[int] = None) -> None:
         """Enqueue a read of every hot row and cold code of ``desc`` through its block
         table, nothing computed (the attainable rate of the decode's pool reads)."""

@@ -399,6 +399,14 @@ int aw_block_entropy_device(aw_engine* engine, const uint16_t* hot, uint64_t hot
 int aw_debug_read_stream(aw_engine* engine, const void* buf, uint64_t bytes, uint32_t waves_per_cu,
                          uint32_t* sink, void* hip_stream);
 
+/* No reference counterpart: the q_latent = q . D^T projection of a request on
+ * its own, for checking it directly.  `desc` is a request that computes
+ * q_latent (a cold pool and q_latent NULL); the projection runs as in
+ * aw_decode_device and its result, [L][B][Q][Hq][A] f16 (fp32 with
+ * AW_F_QLATENT_F32), is copied into `q_latent` (device).  Asynchronous on
+ * `hip_stream`; may grow the engine workspace. */
+int aw_debug_project(aw_engine* engine, const aw_decode_desc* desc, void* q_latent, void* hip_stream);
+
 /* No reference counterpart: the attainable HBM rate of a decode's own pool
  * reads.  Reads every hot K (and V) row and every cold code of the request
  * `desc` describes (its pools, block refs, counts and cold order; q, dict and

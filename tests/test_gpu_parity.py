@@ -144,6 +144,58 @@ def test_cold_only_large_coefficients(engine, stream):
     assert_close(got, oracle.decode_f64(geom, a), "cold-only, coef std 6, f16 q_latent given")
 
 
+PROJECTIONS = {
+    # name: (geometry, fp32 q_latent)
+    "b1_small_tiles": (W.hot_cold(batch=1, hot_count=2, cold_count=4), False),
+    "b64_large_tiles": (W.hot_cold(batch=64, hot_count=1, cold_count=2), False),
+    "b8_per_head_q4_l2": (W.Geometry(layers=2, batch=8, queries=4, hot_count=1, cold_count=2, dict_size=1008,
+                                     dict_heads=8, causal=True, scale=0.1), False),
+    "b16_d64": (W.hot_cold(batch=16, head_dim=64, hot_count=1, cold_count=2, dict_size=512), False),
+    "b64_fp32": (W.hot_cold(batch=64, hot_count=1, cold_count=2), True),
+}
+
+
+@pytest.mark.parametrize("name", list(PROJECTIONS))
+def test_projection_q_latent_direct(engine, stream, name):
+    """q_latent = q . D^T on the device (project_kernel, MFMA f16 x f16 -> fp32),
+    checked directly against the float64 projection: the f16 result is the
+    float64 value rounded to f16 for all but entries within the fp32
+    accumulation error of a rounding boundary (those are one f16 ulp off); the
+    fp32 result (AW_F_QLATENT_F32) is within HD * 2^-23 * sum_j |q_j d_j|.
+    Shapes: the small-tile (<= 32 rows) and large-tile launches, a per-kv-head
+    dictionary with 4 queries over 2 layers and a dictionary size (1008) that is
+    not a multiple of the atom tile, head_dim 64."""
+    import torch
+    geom, f32 = PROJECTIONS[name]
+    wl = W.generate(geom, seed=71)
+    a = W.host_arrays(wl)
+    ref = oracle.qlatent_f64(geom, a)
+    dev = wl.to("cuda:0")
+    out = torch.empty(dev.out_shape(), dtype=torch.float16, device="cuda:0")
+    desc = W.device_desc(dev, out, q_latent_f32=f32)
+    ql = torch.empty(ref.shape, dtype=torch.float32 if f32 else torch.float16, device="cuda:0")
+    engine.project(desc, ql, stream=stream)
+    torch.cuda.synchronize()
+    got = ql.cpu().numpy().astype(np.float64)
+    q = oracle.h2f(a["q"]).astype(np.float64).reshape(geom.layers, geom.batch, geom.queries, geom.q_heads, -1)
+    dic = oracle.h2f(a["dictionary"]).astype(np.float64).reshape(geom.layers, geom.dict_heads, geom.dict_size, -1)
+    G = geom.q_heads // geom.kv_heads
+    heads = np.arange(geom.q_heads) // G if geom.dict_heads > 1 else np.zeros(geom.q_heads, dtype=np.int64)
+    absum = np.einsum("lbqhd,lhad->lbqha", np.abs(q), np.abs(dic[:, heads]))
+    print(f"projection {name}: {got.size} entries, max |dev - f64| {np.abs(got - ref).max():.3e}", flush=True)
+    if f32:
+        assert np.all(np.abs(got - ref) <= geom.head_dim * 2.0 ** -23 * absum + 1e-30)
+        return
+    # Every entry: the float64 value within the fp32 accumulation error, then
+    # rounded to f16 (half an f16 ulp of the stored value).
+    acc = geom.head_dim * 2.0 ** -23 * absum
+    half = np.spacing(np.abs(got).astype(np.float16)).astype(np.float64) / 2
+    assert np.all(np.abs(got - ref) <= half + acc), f"{name}: an entry is off by more than rounding allows"
+    # And nearly all of them are exactly the float64 value rounded to f16.
+    off = got != ref.astype(np.float16).astype(np.float64)
+    assert off.mean() <= 1e-3, f"{name}: {off.mean():.2e} of entries differ from the rounded float64 value"
+
+
 @pytest.mark.parametrize("zipf", [None, 1.1], ids=["uniform", "zipf"])
 def test_peaked_softmax_row_chunks(engine, stream, zipf):
     """The peaked softmax (coefficient std 6, q std 2) in 4-row chunks (B = 32, one
