@@ -554,7 +554,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu((RT == 1 && 
         load_chunk(min(c0 + 32, last), kb[1], vb[1], okb[1]); // the last chunk reloads itself
         process(c0, kb[0], vb[0], okb[0]);
         if (c0 + 32 >= t_end) break;
-        load_chunk(min(c0 + 64, last), kb[0], vb[0], okb[0]);
+        // No reload of the last chunk here: with a split of two chunks (one-sequence
+        // attention) it was a third of the split's loads (10.77 -> 10.53 us per layer).
+        if (c0 + 64 < t_end) load_chunk(c0 + 64, kb[0], vb[0], okb[0]);
         process(c0 + 32, kb[1], vb[1], okb[1]);
     }
     if (bad) flag_error(a.err, kErrHotRef);
