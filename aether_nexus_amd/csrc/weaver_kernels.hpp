@@ -1831,7 +1831,8 @@ constexpr int kFinRowsWaves = 8;
 // 16.9 and 16.8 us: deeper rings issue more than the CU's memory pipeline drains).
 constexpr int kFinRowsPD = 2;
 
-inline size_t finish_rows_smem_bytes(int HD) { return (size_t)kFinRowsWaves * (HD / 16) * 64 * 16; }
+// The waves' partials, then (Mc, Lc, 1/scale) of the tile's 16 rows.
+inline size_t finish_rows_smem_bytes(int HD) { return (size_t)kFinRowsWaves * (HD / 16) * 64 * 16 + 16 * 16; }
 
 template <int HD>
 __global__ __launch_bounds__(kFinRowsWaves * 64) void finish_rows_kernel(FinishArgs a) {
@@ -1860,8 +1861,19 @@ __global__ __launch_bounds__(kFinRowsWaves * 64) void finish_rows_kernel(FinishA
     uint32_t r_b;
     row_id(my_raw, lbg_b, r_b);
     const uint64_t cb_b = lbg_b * R + r_b;
-    const float lc_b = a.cold_l[cb_b], ca_b = a.cold_amax[cb_b];
+    const float mc_b = a.cold_m[cb_b], lc_b = a.cold_l[cb_b], ca_b = a.cold_amax[cb_b];
     const float f_b = my_raw < a.rows_per_group && lc_b > 0.0f ? bin_scale(ca_b, lc_b) / lc_b : 0.0f;
+    // The row's factors for the end, kept in LDS so that no thread reloads them
+    // from memory after the wave reduction (published by its barrier).
+    float4_t* s_rowf = (float4_t*)(smem + (size_t)kFinRowsWaves * NB * 64 * 16); // [16]
+    if (wave == 0 && lg == 0) {
+        float4_t rf;
+        rf[0] = mc_b;
+        rf[1] = lc_b;
+        rf[2] = lc_b > 0.0f ? 1.0f / bin_scale(ca_b, lc_b) : 1.0f;
+        rf[3] = 0.0f;
+        s_rowf[li] = rf;
+    }
 
     // This wave's stretch of the range, in k-steps of 32 atoms.
     const uint32_t a_begin = ar * a.atoms_per_range;
@@ -1946,9 +1958,8 @@ __global__ __launch_bounds__(kFinRowsWaves * 64) void finish_rows_kernel(FinishA
     uint64_t lbg;
     uint32_t r;
     row_id(row_raw, lbg, r);
-    const uint64_t cb = lbg * R + r;
-    const float Mc = a.cold_m[cb], Lc = a.cold_l[cb];
-    const float inv_scl = Lc > 0.0f ? 1.0f / bin_scale(a.cold_amax[cb], Lc) : 1.0f;
+    const float4_t rf = s_rowf[pr];
+    const float Mc = rf[0], Lc = rf[1], inv_scl = rf[2];
     const uint64_t rowid = lbg * R + r;
     if (a.n_ar > 1) {
         *(float4_t*)(a.ocp + (rowid * a.n_ar + ar) * HD + pd) = o * inv_scl;
