@@ -1919,7 +1919,8 @@ __global__ __launch_bounds__(kFinRowsWaves * 64) void finish_rows_kernel(FinishA
             acc[nb] = mfma16x16x32(as_h8(v.d[nb]), lo, acc[nb]);
         }
     };
-    // Ring of kFinRowsPD k-steps in flight; every load is unconditional (clamped).
+    // Ring of kFinRowsPD k-steps in flight; its first loads are clamped into the
+    // range (a stretch may be shorter than the ring), its refills stay inside the stretch.
     KLoads ring[kFinRowsPD];
 #pragma unroll
     for (int j = 0; j < kFinRowsPD; ++j) {

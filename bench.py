@@ -911,13 +911,18 @@ def traffic_file(layout: str) -> Path:
 def sources_digest() -> str:
     """sha256 over the decode path's HIP sources (the kernels and their
     launches), so a traffic profile is only used for the kernels it was
-    measured on."""
+    measured on.  Comments, trailing blanks and blank lines are left out, so a
+    comment edit keeps a profile's digest; these sources hold no string
+    literal with `//` or `/*` in it."""
     import hashlib
+    import re
     h = hashlib.sha256()
     for name in ("weaver_engine.hip", "weaver_kernels.hpp"):
         f = ROOT / "aether_nexus_amd" / "csrc" / name
+        code = re.sub(r"/\*.*?\*/", "", f.read_text(), flags=re.S)
+        lines = (re.sub(r"//.*", "", ln).rstrip() for ln in code.splitlines())
         h.update(f.name.encode())
-        h.update(f.read_bytes())
+        h.update("\n".join(ln for ln in lines if ln).encode())
     return h.hexdigest()[:16]
 
 
