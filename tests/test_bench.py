@@ -59,3 +59,25 @@ def test_traffic_reader_checks_layout_and_sources(tmp_path, monkeypatch):
     fake("head_blocked").write_text("\n".join(lines).replace(bench.sources_digest(), "0123456789abcdef") + "\n")
     v, why = bench.read_traffic("cold_kernel", "head_blocked")
     assert v is None and "other kernel sources" in why
+
+
+def test_sources_digest_ignores_comments_but_not_code(tmp_path, monkeypatch):
+    """A comment or blank-line edit of the kernel sources keeps the digest (a
+    traffic profile stays valid for the same code); a code edit changes it."""
+    csrc = tmp_path / "aether_nexus_amd" / "csrc"
+    csrc.mkdir(parents=True)
+    names = ("weaver_engine.hip", "weaver_kernels.hpp")
+    for n in names:
+        (csrc / n).write_text((ROOT / "aether_nexus_amd" / "csrc" / n).read_text())
+    monkeypatch.setattr(bench, "ROOT", tmp_path)
+    base = bench.sources_digest()
+    assert base == bench.sources_digest()
+    k = csrc / "weaver_kernels.hpp"
+    src = k.read_text()
+    k.write_text("// a new comment line\n\n" + src.replace("\n", "  // trailing note\n", 1) + "/* block\ncomment */\n")
+    assert bench.sources_digest() == base
+    k.write_text(src + "constexpr int kDigestProbe = 1;\n")
+    assert bench.sources_digest() != base
+    k.write_text(src)
+    (csrc / "weaver_engine.hip").write_text((csrc / "weaver_engine.hip").read_text().replace("AW_OK", "AW_OK ", 1) + "int x;\n")
+    assert bench.sources_digest() != base
