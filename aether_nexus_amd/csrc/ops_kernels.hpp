@@ -153,9 +153,15 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const uint16_t* in, const
             }
         }
     } else {
-        for (uint32_t i = tid; i < H; i += 256) {
-            const float f = h2f(x[i]);
-            acc += f * f;
+        // The VEC path's assignment and order (8 consecutive elements per thread
+        // and chunk), so an aligned and an unaligned row give the same bits.
+        for (uint32_t c = tid; c < (H + 7) / 8; c += 256) {
+#pragma unroll
+            for (uint32_t e = 0; e < 8; ++e) {
+                const uint32_t i = 8 * c + e;
+                const float f = i < H ? h2f(x[i]) : 0.0f;
+                acc += f * f;
+            }
         }
     }
     for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);

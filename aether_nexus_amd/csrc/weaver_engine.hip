@@ -102,6 +102,7 @@ struct Layout {
     uint32_t rc = 4;       // cold rows per work-group
     uint32_t n_chunks = 1; // ceil(R / rc)
     uint32_t n_ar = 1;     // atom ranges of the finish
+    bool sep_merge = false; // a merge kernel after the finish even with one atom range
     bool fin_rows = false; // finish_rows_kernel (16-row tiles, waves over atoms) instead of finish_kernel
     uint32_t atoms_per_range = 0;
     uint32_t tiles_per_group = 0, rows_per_group = 0, n_groups = 0;
@@ -111,6 +112,10 @@ struct Layout {
 };
 
 bool supported_head_dim(uint32_t d) { return d == 64 || d == 128; }
+
+// Query rows per kv head from which the merge runs as its own kernel after the
+// finish, whatever the finish's atom ranges.
+constexpr uint32_t kSepMergeRows = 16;
 
 // Row pitches of D^T (halves) and of the cold bins W (floats): one 128-byte line
 // of padding, so rows whose natural stride is a power of two (8 or 16 KiB at
@@ -281,6 +286,10 @@ int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, const uint32_t 
         }
         o.atoms_per_range = (uint32_t)align_up(cdiv(A, n_ar), 32);
         o.n_ar = cdiv(A, o.atoms_per_range);
+        // Many rows per kv head: the hot kernel, starved of LDS beside the cold
+        // kernel, ends after it (32-layer verify, R = 32: 4.97 against 4.70 ms), so
+        // the finish does not merge and wait for it; a merge kernel follows.
+        o.sep_merge = o.n_ar > 1 || (R >= kSepMergeRows && o.info.hot_splits > 0);
     }
 
     // Workspace layout.
@@ -306,7 +315,7 @@ int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, const uint32_t 
         // Tiled for finish_rows_kernel: whole 16-row tiles of each dictionary group.
         const uint64_t tiled = (uint64_t)o.n_groups * cdiv(o.rows_per_group, 16u) * 16 * A;
         o.off_cw = take((o.fin_rows ? tiled : n * w_pitch(A)) * 4);
-        if (o.n_ar > 1) o.off_ocp = take(n_lbg * R * o.n_ar * HD * 4);
+        if (o.sep_merge) o.off_ocp = take(n_lbg * R * o.n_ar * HD * 4);
     }
     o.info.workspace_bytes = off;
     return AW_OK;
@@ -595,14 +604,21 @@ int launch_cold(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* ws
     a.splits = o.info.cold_splits;
     a.tokens_per_split = o.info.cold_tokens_per_split;
     a.n_chunks = o.n_chunks;
-    a.n_units = (uint32_t)((uint64_t)d->layers * d->batch * o.n_chunks * a.splits);
+    const bool head_blocked = (d->flags & AW_F_COLD_HEAD_BLOCKED) != 0;
+    // Sharers on one XCD: the row chunks of a kv head in the head-blocked order
+    // (they read the same 256-byte runs), else the kv heads of a chunk (their codes
+    // share lines in the reference order).
+    a.chunk_xcd = (head_blocked && o.n_chunks > 1) ? 1u : 0u;
+    const uint64_t n_units = a.chunk_xcd ? (uint64_t)d->layers * d->batch * a.splits * d->kv_heads
+                                         : (uint64_t)d->layers * d->batch * o.n_chunks * a.splits;
+    if (n_units > 0xFFFFFFFFull) return fail(e, AW_E_UNSUPPORTED, "cold grid too large");
+    a.n_units = (uint32_t)n_units;
     a.scale_log2 = d->scale * aw::kLog2e;
     a.w_tiled = o.fin_rows ? 1u : 0u;
     a.w_rows_per_group = o.rows_per_group;
     a.w_dict_heads = d->dict_heads;
     a.cold_blocks = d->cold_blocks;
     a.cold_layer = d->cold_blocks * kBlock * d->kv_heads;
-    const bool head_blocked = (d->flags & AW_F_COLD_HEAD_BLOCKED) != 0;
     a.s_tok = head_blocked ? 1u : d->kv_heads;
     a.s_head = head_blocked ? kBlock : 1u;
     a.refs_layer = (uint64_t)d->batch * d->refs_stride;
@@ -616,7 +632,7 @@ int launch_cold(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* ws
     a.s_j = A;
     a.s_a = 1;
     (void)HD;
-    const uint64_t n_wg = (uint64_t)cdiv(a.n_units, 8) * 8 * d->kv_heads;
+    const uint64_t n_wg = (uint64_t)cdiv(a.n_units, 8) * 8 * (a.chunk_xcd ? o.n_chunks : d->kv_heads);
     if (n_wg > 0x7FFFFFFFull) return fail(e, AW_E_UNSUPPORTED, "cold grid too large");
     a.n_wg = (uint32_t)n_wg;
     const size_t smem = aw::cold_smem_bytes(A, (int)o.rc, a.tokens_per_split, o.qf32 ? 4u : 2u);
@@ -650,7 +666,8 @@ int launch_finish(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* 
         a.hot_l = (const float*)(ws + o.off_hl);
         a.hot_o = (const float*)(ws + o.off_ho);
     }
-    a.ocp = o.n_ar > 1 ? (float*)(ws + o.off_ocp) : nullptr;
+    a.ocp = o.sep_merge ? (float*)(ws + o.off_ocp) : nullptr;
+    a.sep_merge = o.sep_merge ? 1u : 0u;
     a.out = d->out;
     a.batch = d->batch;
     a.queries = d->queries;
@@ -678,7 +695,7 @@ int launch_finish(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* 
         AW_HIP(e, hipGetLastError());
         return AW_OK;
     }
-    const bool fused = o.n_ar == 1 && a.hot_splits > 0;
+    const bool fused = !o.sep_merge && a.hot_splits > 0;
     const uint32_t sneed = std::max(a.cold_splits, fused ? a.hot_splits : 1u);
     uint32_t sf = 1;
     while (sf < sneed) sf *= 2;
@@ -763,7 +780,7 @@ int run_pipeline(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* w
         if ((rc = launch_hot<HD>(e, d, o, ws, e->side))) return rc;
         AW_HIP(e, hipEventRecord(e->ev_join, e->side));
     }
-    const bool merge = o.n_ar > 1; // otherwise the finish merges
+    const bool merge = o.sep_merge; // otherwise the finish merges
     if (fork && !merge) AW_HIP(e, hipStreamWaitEvent(st, e->ev_join, 0));
     if ((rc = launch_finish<HD>(e, d, o, ws, st))) return rc;
     if (merge) {

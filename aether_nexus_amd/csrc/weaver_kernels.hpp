@@ -155,6 +155,11 @@ struct ColdArgs {
     uint32_t s_tok, s_head; // code (block b, token j, kv head g) = cold[b*16*kv_heads + j*s_tok + g*s_head]
     uint32_t splits, tokens_per_split, n_chunks, n_units;
     uint32_t n_wg; // work items (8 XCD slots x kv heads x unit groups)
+    // Which items share an XCD: 0 = the kv heads of one (sequence, chunk, split)
+    // (the reference order interleaves their codes in one line); 1 = the row
+    // chunks of one (sequence, split, kv head) (head-blocked order: they read the
+    // same lines).
+    uint32_t chunk_xcd;
     // Bins tiled for finish_rows_kernel: [group][row tile of 16][A/32][2][64 lanes][4],
     // group and group row as the finish numbers them (one split only).
     uint32_t w_tiled, w_rows_per_group, w_dict_heads;
@@ -174,11 +179,14 @@ struct FinishArgs {
     const float* hot_m;
     const float* hot_l;
     const float* hot_o;
-    float* ocp; // [lbg*R + r][n_ar][HD] when n_ar > 1
+    float* ocp; // [lbg*R + r][n_ar][HD] when n_ar > 1 or sep_merge
     uint16_t* out;
     uint32_t batch, queries, q_heads, kv_heads, gqa, rows_r;
     uint32_t dict_size, dict_heads, rows_per_group, tiles_per_group;
     uint32_t cold_splits, hot_splits, n_ar, atoms_per_range;
+    // 1: the cold output goes to `ocp` for merge_kernel even with one atom range
+    // (the finish then does not wait for the hot kernel).
+    uint32_t sep_merge;
     uint64_t dict_layer;
 };
 
@@ -637,9 +645,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu((RT == 1 && 
 // without per-token masks; the split's last partial tile masks p to zero for
 // tokens that read the zero code.
 //
-// The kv heads of one (sequence, chunk, split) run on one XCD (work-groups are
-// dealt round-robin over the 8 XCDs), so the 128-byte lines interleaving their
-// 16-byte codes come from HBM once per XCD L2.
+// Items that read the same lines run on one XCD (work-groups are dealt
+// round-robin over the 8 XCDs), so each line comes from HBM once per XCD L2: in
+// the reference order the kv heads of one (sequence, chunk, split), whose
+// 16-byte codes interleave in 128-byte lines; in the head-blocked order the row
+// chunks of one (sequence, split, kv head), which read the same codes.
 // All-zero code read by tokens behind a bad ref on the 64-bit address path;
 // global (not constant) memory, so every code load stays a global load.
 __device__ __attribute__((aligned(16))) uint4_t g_zero_code = {0u, 0u, 0u, 0u};
@@ -700,12 +710,29 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6); // uniform, so tile branches stay scalar
+    // Work-groups are dealt round-robin over the 8 XCDs (x = wg % 8); the items
+    // that read the same code lines get one x and consecutive slots k, so they run
+    // on one XCD at about the same time and its L2 fetches each line once.
     const uint32_t x = wg % 8u, k = wg / 8u;
-    const uint32_t g = k % a.kv_heads;
-    const uint32_t u = (k / a.kv_heads) * 8u + x;
-    if (u >= a.n_units) return;
-    const uint32_t s = u % a.splits, uc = u / a.splits;
-    const uint32_t c = uc % a.n_chunks, lb = uc / a.n_chunks;
+    uint32_t g, s, c, lb;
+    if (a.chunk_xcd) {
+        // p = (sequence, split, kv head): its n_chunks row chunks share XCD p % 8.
+        c = k % a.n_chunks;
+        const uint32_t p = (k / a.n_chunks) * 8u + x;
+        if (p >= a.n_units) return; // n_units counts (sequence, split, kv head) here
+        g = p % a.kv_heads;
+        const uint32_t ls = p / a.kv_heads;
+        s = ls % a.splits;
+        lb = ls / a.splits;
+    } else {
+        g = k % a.kv_heads;
+        const uint32_t u = (k / a.kv_heads) * 8u + x;
+        if (u >= a.n_units) return;
+        s = u % a.splits;
+        const uint32_t uc = u / a.splits;
+        c = uc % a.n_chunks;
+        lb = uc / a.n_chunks;
+    }
     const uint32_t l = lb / a.batch;
     const uint64_t lbg = (uint64_t)lb * a.kv_heads + g;
     const uint32_t A = a.dict_size, R = a.rows_r;
@@ -1544,7 +1571,7 @@ __global__ __launch_bounds__(kFinishWaves * 64) void finish_kernel(FinishArgs a)
     const uint32_t ar = blockIdx.y;
     const uint32_t l = group / a.dict_heads, dg = group % a.dict_heads;
     const uint32_t R = a.rows_r, A = a.dict_size;
-    const bool fused = a.n_ar == 1 && a.hot_splits > 0;
+    const bool fused = a.n_ar == 1 && a.hot_splits > 0 && !a.sep_merge;
     const uint32_t sneed = max(a.cold_splits, fused ? a.hot_splits : 1u);
     const uint32_t lpr = sneed <= 1 ? 1u : 1u << (32 - __builtin_clz(sneed - 1u)); // factors per row
     _Float16* sd = (_Float16*)smem;                           // [2][HD][DP]
@@ -1776,7 +1803,7 @@ __global__ __launch_bounds__(kFinishWaves * 64) void finish_kernel(FinishArgs a)
     const float* rf = s_rf + myr * 5;
     const float Mc = rf[0], Lc = rf[1], inv_scl = rf[2], Mh = rf[3], Lh = rf[4];
     const uint64_t rowid = lbg_me * R + r_me;
-    if (!fused && a.n_ar > 1) {
+    if (!fused && (a.n_ar > 1 || a.sep_merge)) {
         float* dst = a.ocp + (rowid * a.n_ar + ar) * HD;
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) *(float4_t*)(dst + 16 * nb + 4 * lg) = acc[nb] * inv_scl;
@@ -1962,7 +1989,7 @@ __global__ __launch_bounds__(kFinRowsWaves * 64) void finish_rows_kernel(FinishA
     const float4_t rf = s_rowf[pr];
     const float Mc = rf[0], Lc = rf[1], inv_scl = rf[2];
     const uint64_t rowid = lbg * R + r;
-    if (a.n_ar > 1) {
+    if (a.n_ar > 1 || a.sep_merge) {
         *(float4_t*)(a.ocp + (rowid * a.n_ar + ar) * HD + pd) = o * inv_scl;
         return;
     }

@@ -83,6 +83,8 @@ class OpsEngine:
         s = _stream(stream)
         if s is None:
             torch.cuda.synchronize()
+        elif s == 0:  # the null stream (torch.cuda.ExternalStream(0) would make a stream of its own)
+            torch.cuda.default_stream().synchronize()
         else:
             torch.cuda.ExternalStream(s).synchronize()
 

@@ -82,6 +82,9 @@ def parse():
     p.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DB", "WRITE_DB"),
                    help="print HBM traffic per launch from a FETCH_SIZE and a WRITE_SIZE rocprofv3 database and exit")
     p.add_argument("--traffic-command", default="", help="command line recorded in --traffic-summary output")
+    p.add_argument("--traffic-title", default="", help="workload named in --traffic-summary output")
+    p.add_argument("--only-attention", action="store_true",
+                   help="time only the inference attention (dense and tiered caches) and print it")
     return p.parse_args()
 
 
@@ -959,7 +962,8 @@ def _counters(db: str) -> dict:
     return {k: {cn: v / len(nd[k]) for cn, v in d.items()} for k, d in per.items()}
 
 
-def traffic_summary(fetch_db: str, write_db: str, copy_mib: int, command: str, layout: str) -> str:
+def traffic_summary(fetch_db: str, write_db: str, copy_mib: int, command: str, layout: str,
+                    title: str = "hot 2048 + cold 32768 per kv head, B = 64 (32q/8kv, d128, 4096 atoms)") -> str:
     """HBM bytes per launch of each aw:: kernel (largest grid = the B = 64 launch)
     from a FETCH_SIZE and a WRITE_SIZE pass, each scaled by what the counter
     reads for the calibration copy of `copy_mib` MiB in the same pass."""
@@ -973,7 +977,7 @@ def traffic_summary(fetch_db: str, write_db: str, copy_mib: int, command: str, l
         return max(cands, key=lambda kv: kv[0][1])  # the largest grid: the calibration copy
     (ck_f, cf), (ck_w, cw) = copy_kib(f, "FETCH_SIZE"), copy_kib(w, "WRITE_SIZE")
     ff, fw = copy_bytes / (cf * 1024), copy_bytes / (cw * 1024)
-    lines = ["# HBM traffic per launch, hot 2048 + cold 32768 per kv head, B = 64 (32q/8kv, d128, 4096 atoms)",
+    lines = [f"# HBM traffic per launch, {title}",
              f"# command: {command}",
              f"# cold_layout: {layout}",
              f"# sources: {sources_digest()}",
@@ -1019,8 +1023,9 @@ def main():
         print(rocpd_summary(args.rocpd_summary, args.kernel_filter))
         return 0
     if args.traffic_summary:
+        extra = {"title": args.traffic_title} if args.traffic_title else {}
         print(traffic_summary(args.traffic_summary[0], args.traffic_summary[1], args.copy_calibration or 256,
-                              args.traffic_command, args.cold_layout))
+                              args.traffic_command, args.cold_layout, **extra))
         return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
@@ -1039,6 +1044,8 @@ def main():
         if k not in CONFIGS:
             print(f"unknown config {k} (choose from {', '.join(CONFIGS)})", file=sys.stderr)
             return 2
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
     if args.only_configs:
         rows = []
         for k in config_keys:
@@ -1047,14 +1054,17 @@ def main():
         engine.close()
         print(json.dumps({"configs": rows}), flush=True)
         return 0
+    if args.only_attention:
+        out = attention_bench(engine, args.seed, 20, 0.5 if args.no_cpu else 3.0)
+        engine.close()
+        print(json.dumps({"inference_attention": out}), flush=True)
+        return 0
     if args.only_ops:
         rp = hbm_read_peak(engine)
         out = ops_bench(engine, args.seed, rp["gbps"])
         engine.close()
         print(json.dumps({"hbm_read_peak": rp, "dense_ops": out}), flush=True)
         return 0
-    if args.copy_calibration:
-        copy_calibration(args.copy_calibration)
     sweep = []
     head = None
     for B in batches:

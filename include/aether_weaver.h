@@ -268,8 +268,8 @@ int aw_decode_device(aw_engine* engine, const aw_decode_desc* desc, void* hip_st
  * process ends (its address is looked up once per device, at
  * aw_engine_create).  A request whose scratch (aw_decode_plan_info.
  * workspace_bytes) exceeds it returns AW_E_UNSUPPORTED: 96 MiB covers a
- * one-layer decode of 64 sequences at hot 2048 + cold 32768 tokens (67 MiB),
- * not a 32-layer call in one piece.  Stage timing (aw_engine_set_profiling) is
+ * one-layer decode of 64 sequences at hot 2048 + cold 32768 tokens (55.1 MiB),
+ * not two such layers in one call (106.2 MiB) nor a 32-layer call.  Stage timing (aw_engine_set_profiling) is
  * not recorded for these calls.  Every call on one GPU, from any engine,
  * shares that GPU's array and leaves its contents behind: calls (and graph
  * replays) that overlap on one GPU race; order them on one stream or

@@ -2,7 +2,7 @@
 # The CPU test suite (pytest -m "not gpu") under AddressSanitizer and
 # UndefinedBehaviorSanitizer.  Instrumented: the host code of libaether_weaver.so
 # (planner, parameter validation, the .aether fabric's file, loom and checkpoint
-# code; the gfx950 device code is not) and the CPU oracle, both built with ROCm's
+# code, the dense ops' argument checks; the gfx950 device code is not) and the CPU oracle, both built with ROCm's
 # clang into a scratch directory and loaded through AETHER_WEAVER_LIB and
 # WEAVER_ORACLE_LIB.  Usage: tests/run_sanitized.sh [scratch-dir]
 set -euo pipefail
@@ -16,7 +16,8 @@ echo "building the host-instrumented library into $OUT/lib"
 /opt/rocm/bin/hipcc --offload-arch=gfx950 -O1 -g -std=c++17 -fPIC -shared \
     -Xclang -target-feature -Xclang -packed-fp32-ops $SAN_HOST -shared-libsan -Wl,-rpath,"$RTDIR" \
     -I "$ROOT/include" -o "$OUT/lib/libaether_weaver.so" \
-    "$ROOT/aether_nexus_amd/csrc/weaver_engine.hip" "$ROOT/aether_nexus_amd/csrc/fabric.hip" 2>&1 |
+    "$ROOT/aether_nexus_amd/csrc/weaver_engine.hip" "$ROOT/aether_nexus_amd/csrc/fabric.hip" \
+    "$ROOT/aether_nexus_amd/csrc/ops.hip" 2>&1 |
     { grep -v "packed-fp32-ops\|argument unused" || true; }
 echo "building the instrumented oracle"
 /opt/rocm/llvm/bin/clang -O1 -g -std=c11 -ffp-contract=off -march=x86-64-v3 -fPIC -shared \

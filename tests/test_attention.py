@@ -171,7 +171,7 @@ def test_weaver_kv_cache_tiers():
     cold tier, the hot ring keeps the window, distill moves whole blocks by age,
     the block table lists hot ring slots oldest first then cold blocks, and
     rollback stays inside the hot tier."""
-    from aether_nexus_amd.types import AW_F_CAUSAL, AW_F_COLD_HEAD_BLOCKED
+    from aether_nexus_amd.types import AW_F_CAUSAL, AW_F_COLD_HEAD_BLOCKED, AW_F_QLATENT_F32
     layers, hkv, d, win = 2, 2, 8, 32
     dicts = torch.zeros((layers, 1, 64, d), dtype=torch.float16)
     c = I.WeaverKvCache(layers, hkv, d, dicts, hot_window=win, max_seq_len=400, max_batch=4, device="cpu")
@@ -191,8 +191,9 @@ def test_weaver_kv_cache_tiers():
         c.append(layer, ks[layer][:4], vs[layer][:4])
         c.attend(eng, layer, q, torch.empty_like(q))
     got = eng.decodes[-1]
+    # q_latent stays fp32 by default (AW_F_QLATENT_F32).
     assert got == {"queries": 4, "hot_count": 3, "cold_count": 4, "refs_stride": 7, "hot_tokens": 40,
-                   "flags": AW_F_CAUSAL | AW_F_COLD_HEAD_BLOCKED, "hot_blocks": c.hot_capacity,
+                   "flags": AW_F_CAUSAL | AW_F_COLD_HEAD_BLOCKED | AW_F_QLATENT_F32, "hot_blocks": c.hot_capacity,
                    "cold_blocks": c.cold_capacity}
     assert c.refs(3)[:7].tolist() == [0, 1, 2, 0, 1, 2, 3]
     saved = c.push_loom()
@@ -217,3 +218,13 @@ def test_weaver_kv_cache_tiers():
         I.WeaverKvCache(layers, hkv, d, dicts[:1], hot_window=win, device="cpu")
     c.reset()
     assert (c.position, c.cold_blocks, c.hot_first) == (0, 0, 0)
+    # The reference's f16 q_latent on request; a background distill needs the GPU.
+    c16 = I.WeaverKvCache(layers, hkv, d, dicts, hot_window=win, max_seq_len=400, max_batch=4, device="cpu",
+                          q_latent_f32=False)
+    c16.extend(eng, ks, vs)
+    c16.append(0, ks[0][:1], vs[0][:1])
+    c16.attend(eng, 0, q[:1], torch.empty_like(q[:1]))
+    assert eng.decodes[-1]["flags"] == AW_F_CAUSAL | AW_F_COLD_HEAD_BLOCKED
+    assert c16.distilling == 0 and not c16.commit()
+    with pytest.raises(I.KvCacheError, match="GPU"):
+        c16.distill(eng, side_stream=1)

@@ -267,3 +267,165 @@ def test_weaver_kv_cache_verify_step(engine, stream):
     assert cache.position == p0 + 2 and cache.cold_tokens == 32768
     del ks, vs
     torch.cuda.empty_cache()
+
+
+
+def _tiered_cache(engine, stream, gen, layers, n, q_latent_f32=True, max_seq_len=None):
+    """A WeaverKvCache at Llama-3.1-8B heads with 512-atom per-kv-head unit-norm
+    dictionaries, loaded with an n-token prompt (2048 stay hot) on `stream`."""
+    hkv, d, A = 8, 128, 512
+    dd = torch.randn((layers, hkv, A, d), generator=gen, device="cuda:0", dtype=torch.float64)
+    dicts = (dd / dd.norm(dim=-1, keepdim=True)).to(torch.float16)
+    cache = I.WeaverKvCache(layers, hkv, d, dicts, hot_window=2048, max_seq_len=max_seq_len or n + 256,
+                            q_latent_f32=q_latent_f32)
+    ks = [torch.randn((n, hkv, d), generator=gen, device="cuda:0").to(torch.float16) for _ in range(layers)]
+    vs = [torch.randn((n, hkv, d), generator=gen, device="cuda:0").to(torch.float16) for _ in range(layers)]
+    torch.cuda.synchronize()  # the inputs, made on torch's current stream, before `stream` reads them
+    cache.extend(engine, ks, vs, stream=stream)
+    engine.check_device_errors(stream)
+    torch.cuda.synchronize()
+    return cache, dicts
+
+
+def test_weaver_kv_cache_peaked_verify_fp32_q_latent(engine, stream):
+    """A verify step (last token + 3 drafts) over WeaverKvCache on a peaked
+    softmax: cold codes with coefficient std 6 (written straight into the cold
+    tier) and q std 2, 32768 cold + 2048 hot tokens.  With q_latent kept fp32
+    (the cache's default) every output is within 2e-3 of the fp64 brute force
+    beyond its own f16 rounding (outputs reach several units, where that rounding
+    alone approaches 2e-3) and rel-L2 within 1e-3; the reference's f16 q_latent
+    (q_latent_f32=False) is measured beside it and misses by more."""
+    hq, hkv, d, A, nv, nb = 32, 8, 128, 512, 4, 2048
+    results = {}
+    for f32 in (True, False):
+        gen = torch.Generator(device="cuda:0")
+        gen.manual_seed(52)
+        cache, dicts = _tiered_cache(engine, stream, gen, 1, 2048, q_latent_f32=f32, max_seq_len=40000)
+        # 2048 cold blocks of random codes (indices uniform, coefficients ~ N(0, 36))
+        # become the oldest tokens, in front of the 2048 hot ones.
+        idx = torch.randint(0, A, (nb, hkv, 16, 4), generator=gen, device="cuda:0", dtype=torch.int32)
+        coef = (torch.randn((nb, hkv, 16, 4), generator=gen, device="cuda:0") * 6.0).to(torch.float16)
+        cache.cold[0][:nb] = torch.cat([idx.to(torch.int16), coef.view(torch.int16)], dim=-1)
+        cache.cold_blocks = nb
+        cache.position += nb * 16
+        q = (torch.randn((nv, hq, d), generator=gen, device="cuda:0") * 2.0).to(torch.float16)
+        rows = torch.randn((nv, hkv, d), generator=gen, device="cuda:0").to(torch.float16)
+        cache.append(0, rows, rows, stream=stream)
+        out = torch.full((nv, hq, d), float("nan"), dtype=torch.float16, device="cuda:0")
+        print(f"tiered peaked verify, q_latent {'fp32' if f32 else 'f16'}", flush=True)
+        cache.attend(engine, 0, q, out, stream=stream)
+        engine.check_device_errors(stream)
+        p = cache.position
+        coldr = decompress_cold(cache.cold[0][:nb], dicts[0])
+        hk, hv = hot_rows(cache, 0, cache.hot_tokens(p + nv))
+        ref = AO.multihead_attention_f64(q.float().cpu().numpy(), np.concatenate([coldr, hk]),
+                                         np.concatenate([coldr, hv]), p + nv, nv)
+        got = out.float().cpu().numpy().astype(np.float64)
+        half_ulp = np.spacing(np.abs(got).astype(np.float16)).astype(np.float64) / 2
+        excess = np.abs(got - ref) - half_ulp
+        rel = np.linalg.norm(got - ref) / np.linalg.norm(ref)
+        results[f32] = (np.abs(got - ref).max(), excess.max(), rel)
+        print(f"  max |out| {np.abs(ref).max():.2f}, max-abs {results[f32][0]:.2e}, beyond f16 rounding "
+              f"{results[f32][1]:.2e}, rel-L2 {rel:.2e}", flush=True)
+        del cache
+    assert results[True][1] <= 2e-3 and results[True][2] <= 1e-3
+    assert results[True][0] < results[False][0]
+
+
+def test_weaver_kv_cache_side_stream(engine):
+    """Every call of WeaverKvCache on a stream other than torch's current one
+    (prompt with ring writes, a distill after each forward that frees a ring slot,
+    appends that reuse it, attends), with no synchronisation in between: the
+    outputs are the bits of the same calls on the current stream."""
+    hq, d, layers, n, steps = 32, 128, 2, 2048 + 16 * 40, 40
+    outs = {}
+    for mode in ("current", "side"):
+        gen = torch.Generator(device="cuda:0")
+        gen.manual_seed(61)
+        side = torch.cuda.Stream()
+        sh = side.cuda_stream if mode == "side" else torch.cuda.current_stream().cuda_stream
+        cache, _ = _tiered_cache(engine, sh, gen, layers, n, max_seq_len=n + 16 * (steps + 1))
+        qs = [torch.randn((16, hq, d), generator=gen, device="cuda:0").to(torch.float16) for _ in range(steps)]
+        rows = [torch.randn((16, 8, d), generator=gen, device="cuda:0").to(torch.float16) for _ in range(steps)]
+        got = [torch.empty((16, hq, d), dtype=torch.float16, device="cuda:0") for _ in range(steps * layers)]
+        torch.cuda.synchronize()
+        print(f"tiered cache on the {mode} stream: {steps} forwards of 16 tokens", flush=True)
+        for i in range(steps):  # a block leaves the window after each forward
+            for layer in range(layers):
+                cache.append(layer, rows[i], rows[i], stream=sh)
+                cache.attend(engine, layer, qs[i], got[i * layers + layer], stream=sh)
+            cache.advance(16)
+            cache.distill(engine, stream=sh)
+        torch.cuda.synchronize()
+        engine.check_device_errors(sh)
+        assert cache.cold_tokens == 16 * 80
+        outs[mode] = torch.stack(got).view(torch.int16)
+        del cache
+    assert torch.equal(outs["side"], outs["current"])
+
+
+def test_weaver_kv_cache_background_distill(engine, stream):
+    """The Distiller's pass beside the decode: a block leaving the hot window is
+    encoded on a side stream (queued behind other work there, so it is still in
+    flight) while verify steps run on the main stream.  Every output is the bits
+    of a cache where no pass ran (the block still hot) or of one distilled
+    synchronously (the block cold), never anything else; while the pass is in
+    flight it is the former, and after the commit the latter."""
+    hq, d, layers, nv = 32, 128, 2, 4
+    side = torch.cuda.Stream()
+    caches = []
+    for _ in range(3):  # a: background pass; b0: never distilled; b1: distilled synchronously
+        gen = torch.Generator(device="cuda:0")
+        gen.manual_seed(71)
+        caches.append(_tiered_cache(engine, stream, gen, layers, 34816)[0])
+    a, b0, b1 = caches
+    gen = torch.Generator(device="cuda:0")
+    gen.manual_seed(72)
+    rows = [torch.randn((16, 8, d), generator=gen, device="cuda:0").to(torch.float16) for _ in range(layers)]
+    qs = [torch.randn((nv, hq, d), generator=gen, device="cuda:0").to(torch.float16) for _ in range(6)]
+    for c in caches:  # 16 more tokens: one block beyond the window
+        for layer in range(layers):
+            c.append(layer, rows[layer], rows[layer], stream=stream)
+        c.advance(16)
+    assert b1.distill(engine, stream=stream) == 1
+    torch.cuda.synchronize()
+    # Keep the side stream busy so that the pass is still queued when the decodes run.
+    x = torch.randn((4096, 4096), generator=gen, device="cuda:0")
+    x = torch.tanh(x @ x * 1e-3)  # the product's library set-up, before the timed queue
+    torch.cuda.synchronize()
+    with torch.cuda.stream(side):
+        for _ in range(40):
+            x = torch.tanh(x @ x * 1e-3)
+    print("background distill: one block per layer queued on a busy side stream", flush=True)
+    assert a.distill(engine, stream=stream, side_stream=side.cuda_stream) == 1
+    assert a.distilling == 1 and a.cold_tokens == 32768
+
+    def step(c, q):
+        outs = []
+        for layer in range(layers):
+            c.append(layer, rows[layer][:nv], rows[layer][:nv], stream=stream)
+            out = torch.empty((nv, hq, d), dtype=torch.float16, device="cuda:0")
+            c.attend(engine, layer, q, out, stream=stream)
+            outs.append(out)
+        p = c.push_loom()
+        c.advance(nv)
+        c.pop_loom(p)  # a rejected verify step
+        return [o.view(torch.int16) for o in outs]
+
+    in_flight = 0
+    for i, q in enumerate(qs):
+        if i == 3:
+            a.commit(wait=True)
+        pending = a.distilling
+        oa, o0, o1 = step(a, q), step(b0, q), step(b1, q)
+        for layer in range(layers):
+            same0, same1 = torch.equal(oa[layer], o0[layer]), torch.equal(oa[layer], o1[layer])
+            assert same0 or same1, f"step {i} layer {layer}: output of neither state"
+            if not pending:
+                assert same1, f"step {i}: committed, yet not the distilled cache's output"
+        in_flight += pending > 0 and a.distilling > 0
+    torch.cuda.synchronize()
+    engine.check_device_errors(stream)
+    print(f"background distill: {in_flight} steps ran with the pass in flight", flush=True)
+    assert in_flight >= 1 and a.distilling == 0 and a.cold_tokens == 32768 + 16
+    assert (a.cold_tokens, a.hot_first) == (b1.cold_tokens, b1.hot_first)

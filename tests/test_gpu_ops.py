@@ -145,6 +145,28 @@ def test_rms_norm(ops, hidden, tokens):
     within_one_ulp(host(t), want, "rms_norm in place")
 
 
+@pytest.mark.parametrize("hidden", [4096, 2056])
+def test_rms_norm_aligned_and_unaligned_rows_same_bits(ops, hidden):
+    """A row read through 16-byte loads (aligned pointers) and one-half loads
+    (pointers 2 bytes off) is summed in the same order: the same output bits."""
+    import torch
+    rng = np.random.default_rng(hidden)
+    tokens = 3
+    x = f16(rng, tokens, hidden, scale=3.0)
+    w = f16(rng, hidden)
+    out = dev(np.zeros((tokens, hidden), np.float16))
+    ops.rms_norm(dev(x), dev(w), out, hidden, tokens, 1e-5)
+    # The same data at an odd half offset of larger buffers: the element-wise path.
+    xb = torch.zeros(tokens * hidden + 1, dtype=torch.float16, device="cuda:0")
+    wb = torch.zeros(hidden + 1, dtype=torch.float16, device="cuda:0")
+    ob = torch.zeros(tokens * hidden + 1, dtype=torch.float16, device="cuda:0")
+    xb[1:] = dev(x).reshape(-1)
+    wb[1:] = dev(w)
+    ops.rms_norm(xb[1:], wb[1:], ob[1:], hidden, tokens, 1e-5)
+    assert xb[1:].data_ptr() % 16 != 0
+    assert np.array_equal(bits(host(ob[1:]).reshape(tokens, hidden)), bits(host(out)))
+
+
 @pytest.mark.parametrize("tokens,hq,hkv,hd,start", [(1, 32, 8, 128, 4095), (16, 32, 8, 128, 100), (3, 4, 0, 64, 0),
                                                      (5, 2, 2, 6, 7)])
 def test_rope(ops, tokens, hq, hkv, hd, start):

@@ -30,7 +30,7 @@ def decode_both(engine, stream, geom, seed):
 
 
 def test_noalloc_matches_decode_device(engine, stream):
-    # 64 sequences at hot 2048 + cold 32768 tokens (67 MiB of scratch), then a
+    # 64 sequences at hot 2048 + cold 32768 tokens (55.1 MiB of scratch), then a
     # smaller ragged request: the second call reuses the array the first left behind.
     big = W.sweep(64)
     small = W.hot_cold(batch=3, hot_count=5, cold_count=40, dict_size=256, queries=2, causal=True)
@@ -38,14 +38,58 @@ def test_noalloc_matches_decode_device(engine, stream):
     decode_both(engine, stream, small, seed=72)
 
 
-def test_noalloc_rejects_requests_beyond_its_scratch(engine, stream):
-    geom = W.sweep(64, layers=2)  # 135 MiB of scratch
+@pytest.mark.parametrize("layers", [2, 4])
+def test_noalloc_rejects_requests_beyond_its_scratch(engine, stream, layers):
+    geom = W.sweep(64, layers=layers)  # 106.2 and 212.4 MiB of scratch
     wl = W.generate(geom, seed=73, device="cuda:0")
     out = torch.full(wl.out_shape(), float("nan"), dtype=torch.float16, device="cuda:0")
     desc = W.device_desc(wl, out)
-    assert plan(desc).workspace_bytes > AW_NOALLOC_SCRATCH_BYTES
+    need = plan(desc).workspace_bytes
+    print(f"no-alloc: {layers} layers need {need / 2**20:.1f} MiB", flush=True)
+    assert need > AW_NOALLOC_SCRATCH_BYTES
     with pytest.raises(WeaverError) as e:
         engine.decode_device_noalloc(desc, stream=stream)
     assert e.value.status == AW_E_UNSUPPORTED and "scratch" in str(e.value)
     torch.cuda.synchronize()
     assert torch.isnan(out.float()).all()  # nothing ran
+
+
+def test_noalloc_graph_capture_on_a_fresh_engine():
+    """The entry point's purpose: capture into a HIP graph with no eager call first
+    (a fresh engine has no workspace, and aw_decode_device would refuse to grow
+    one under capture), the hot branch forked onto the engine's side stream
+    inside the capture.  Every replay, with eager decodes of another shape and
+    torch work in between, gives aw_decode_device's output bits."""
+    from aether_nexus_amd.weaver import WeaverEngine
+    eng = WeaverEngine()  # fresh: no workspace
+    try:
+        geom = W.hot_cold(batch=8)
+        wl = W.generate(geom, seed=74, device="cuda:0")
+        other = W.generate(W.hot_cold(batch=2, queries=2, causal=True), seed=75, device="cuda:0")
+        out = torch.full(wl.out_shape(), float("nan"), dtype=torch.float16, device="cuda:0")
+        out2 = torch.empty(other.out_shape(), dtype=torch.float16, device="cuda:0")
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        print("no-alloc: capture on a fresh engine", flush=True)
+        with torch.cuda.stream(s):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=s):
+                eng.decode_device_noalloc(W.device_desc(wl, out), stream=torch.cuda.current_stream().cuda_stream)
+            torch.cuda.synchronize()
+            assert torch.isnan(out.float()).all()  # captured, not run
+            ref = torch.empty_like(out)
+            eng.decode_device(W.device_desc(wl, ref), stream=s.cuda_stream)
+            eng.check_device_errors(s.cuda_stream)
+            for rep in range(4):
+                out.fill_(float("nan"))
+                g.replay()
+                torch.cuda.synchronize()
+                assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), f"replay {rep}"
+                eng.decode_device_noalloc(W.device_desc(other, out2), stream=s.cuda_stream)
+                _ = (out2.float() * 2).sum()
+                torch.cuda.synchronize()
+            eng.check_device_errors(s.cuda_stream)
+        del g
+    finally:
+        torch.cuda.synchronize()
+        eng.close()
