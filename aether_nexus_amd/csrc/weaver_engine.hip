@@ -116,6 +116,8 @@ bool supported_head_dim(uint32_t d) { return d == 64 || d == 128; }
 // Query rows per kv head from which the merge runs as its own kernel after the
 // finish, whatever the finish's atom ranges.
 constexpr uint32_t kSepMergeRows = 16;
+// Cold splits per row before the row chunk is halved instead.
+constexpr uint64_t kColdSplitsBeforeRc = 8;
 
 // Row pitches of D^T (halves) and of the cold bins W (floats): one 128-byte line
 // of padding, so rows whose natural stride is a power of two (8 or 16 KiB at
@@ -238,12 +240,18 @@ int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, const uint32_t 
         // Splits per (layer, sequence, kv head, row chunk) item for a chunk of rc rows:
         // >= 1024 tokens per split, and bin partials (A*rc*4 bytes per split, written here
         // and read again by the finish) at most half the code bytes of the sequence.
+        // A row with many cold splits costs the finish ~0.6 us per split (it combines
+        // their factors and bins), so while the row chunk can still shrink, at most
+        // kColdSplitsBeforeRc splits: a one-sequence decode over 512-atom per-kv-head
+        // dictionaries measured 51.6 us with rc 4 x 32 splits, 44.9 with 4 x 16,
+        // 38.1 with 2 x 8 and 35.3 with 1 x 8.
         auto splits_for = [&](uint32_t rc) {
             const uint64_t items = n_lbg * cdiv(R, rc);
             const uint64_t want = cdiv((uint64_t)n_cu, items);
             const uint64_t cap = std::max<uint64_t>(
                 1, std::min<uint64_t>(cdiv(n_tok, 1024), (n_tok * 16) / ((uint64_t)A * rc * 4 * 2)));
-            return std::max<uint64_t>(1, std::min<uint64_t>({want, cap, (uint64_t)aw::kMaxSplits}));
+            const uint64_t lim = rc > 1 ? kColdSplitsBeforeRc : (uint64_t)aw::kMaxSplits;
+            return std::max<uint64_t>(1, std::min<uint64_t>({want, cap, lim, (uint64_t)aw::kMaxSplits}));
         };
         // Too few work-groups to fill the CUs: smaller row chunks (each item then reads
         // the codes again, but does less work per token and allows more splits).

@@ -137,20 +137,25 @@ def test_out_of_range_refs_are_reported(engine, stream):
     assert torch.isfinite(out.float()).all()
 
 
-def sampled_rows(geom, n, seed):
+def sampled_rows(geom, n, seed, per_layer_head=False):
     """n random output rows, plus one q head of every kv head (a different member
     of each GQA group) in the first and last query of the first and last
-    sequence of the first and last layer.  Row id = ((l*B + b)*Q + q)*Hq + h."""
+    sequence of the first and last layer; with `per_layer_head`, also one row of
+    every (layer, kv head), its sequence, query and GQA member varying with both.
+    Row id = ((l*B + b)*Q + q)*Hq + h."""
     L, B, Q, Hq, Hkv = geom.layers, geom.batch, geom.queries, geom.q_heads, geom.kv_heads
     G = Hq // Hkv
     total = L * B * Q * Hq
     fixed = [((l * B + b) * Q + q) * Hq + g * G + (g + l + b + q) % G
              for l in {0, L - 1} for b in {0, B - 1} for q in {0, Q - 1} for g in range(Hkv)]
+    if per_layer_head:
+        fixed += [((l * B + (7 * l + g) % B) * Q + (l + 3 * g) % Q) * Hq + g * G + (l + g) % G
+                  for l in range(L) for g in range(Hkv)]
     rng = np.random.default_rng(seed)
     return np.unique(np.concatenate([fixed, rng.integers(0, total, n)])).astype(np.uint64)
 
 
-def full_size(engine, stream, geom, seed, n_rows, what):
+def full_size(engine, stream, geom, seed, n_rows, what, per_layer_head=False, every_row=False):
     wl = W.generate(geom, seed=seed, device="cuda:0")
     out = torch.full(wl.out_shape(), float("nan"), dtype=torch.float16, device="cuda:0")
     engine.decode_device(W.device_desc(wl, out), stream=stream)
@@ -162,7 +167,11 @@ def full_size(engine, stream, geom, seed, n_rows, what):
         n_nan = int(torch.isnan(got.float()).sum())
         pytest.fail(f"{what}: {int(bad.sum())} of {got.shape[0]} rows non-finite ({n_nan} NaN values), "
                     f"first rows {rows_bad[:8].tolist()}, last {rows_bad[-4:].tolist()}")
-    rows = sampled_rows(geom, n_rows, seed)
+    if every_row:
+        rows = np.arange(got.shape[0], dtype=np.uint64)
+    else:
+        rows = sampled_rows(geom, n_rows, seed, per_layer_head)
+    print(f"{what}: {rows.size} of {got.shape[0]} rows against the fp64 oracle", flush=True)
     ref = oracle.decode_f64(geom, W.host_arrays(wl), rows=rows, threads=16)
     assert_close(got[torch.from_numpy(rows.astype(np.int64)).cuda()].cpu().numpy(), ref, what)
 
@@ -211,7 +220,7 @@ def test_full_hot_region_8192_blocks(engine, stream, cold_count):
     (weaver_kernel.metal:143-168): B = 1, 32 q / 8 kv heads, d 128, 131072 hot
     tokens, alone and with 2048 cold blocks; every row against the fp64 oracle."""
     geom = W.hot_cold(hot_count=8192, cold_count=cold_count)
-    full_size(engine, stream, geom, 56 + cold_count, 64, f"hot 8192 blocks + cold {cold_count} blocks")
+    full_size(engine, stream, geom, 56 + cold_count, 0, f"hot 8192 blocks + cold {cold_count} blocks", every_row=True)
     torch.cuda.empty_cache()
 
 
@@ -227,8 +236,9 @@ def test_full_size_batched_zipf(engine, stream):
 
 def test_full_size_spec_verify(engine, stream):
     """32 layers, B = 8, 8 causal drafts, hot 2048 + cold 65536 per kv head,
-    per-layer 4096 x 128 dictionary."""
-    full_size(engine, stream, W.spec_verify(), 52, 64, "spec-verify L32 (sampled rows)")
+    per-layer 4096 x 128 dictionary: at least one row of every (layer, kv head),
+    the first and last sequence, and random rows (>= 256 rows)."""
+    full_size(engine, stream, W.spec_verify(), 52, 64, "spec-verify L32 (sampled rows)", per_layer_head=True)
     torch.cuda.empty_cache()
 
 

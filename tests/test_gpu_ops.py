@@ -211,6 +211,41 @@ def test_matmul(ops, m, n, k):
     check_product(host(out).astype(np.float64), a, b, k, f"matmul {m}x{n}x{k}")
 
 
+# The benchmarked Llama-3.1-8B products (inference.rs:518-600): gate/up at the
+# prefill-sized M = 2048 (tiled), down_proj (K = 14336) at M = 1, 16 and 2048.
+LLAMA_SHAPES = [(2048, 14336, 4096), (1, 4096, 14336), (16, 4096, 14336), (2048, 4096, 14336)]
+
+
+@pytest.mark.parametrize("m,n,k", LLAMA_SHAPES, ids=[f"{m}x{n}x{k}" for m, n, k in LLAMA_SHAPES])
+def test_matmul_llama_shapes(ops, m, n, k):
+    """Every output column, and every row up to 16 (128 spread rows of the
+    M = 2048 products), within the fp32 accumulation bound of the float64 product."""
+    rng = np.random.default_rng(m + n + k)
+    a = f16(rng, m, k)
+    b = f16(rng, n, k, scale=k ** -0.5)
+    out = dev(np.full((m, n), np.nan, np.float16))
+    print(f"matmul {m}x{n}x{k}", flush=True)
+    ops.matmul(dev(a), dev(b), out, m, n, k)
+    got = host(out).astype(np.float64)
+    rows = np.arange(m) if m <= 16 else np.unique(np.concatenate([np.arange(16), rng.integers(0, m, 112), [m - 1]]))
+    assert np.all(np.isfinite(got))
+    check_product(got[rows], a[rows], b, k, f"matmul {m}x{n}x{k} ({rows.size} rows)")
+
+
+@pytest.mark.parametrize("m", [1, 16])
+def test_lm_head_scaled_llama(ops, m):
+    """The f32 lm_head of Llama-3.1-8B (128256 x 4096, matmul_scaled) at M = 1 and 16."""
+    import torch
+    rng = np.random.default_rng(128256 + m)
+    n, k = 128256, 4096
+    a = f16(rng, m, k)
+    b = f16(rng, n, k, scale=k ** -0.5)
+    out = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda:0")
+    print(f"lm_head {m}x{n}x{k}", flush=True)
+    ops.matmul_scaled(dev(a), dev(b), out, m, n, k, 1.0)
+    check_product(host(out), a, b, k, f"lm_head {m}x{n}x{k}", f16_out=False)
+
+
 @pytest.mark.parametrize("m,n,k", [(1, 49155, 2048), (4, 1000, 4096), (100, 250, 64)])
 def test_matmul_scaled(ops, m, n, k):
     import torch
