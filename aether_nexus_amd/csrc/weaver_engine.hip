@@ -119,6 +119,18 @@ constexpr uint32_t kSepMergeRows = 16;
 // Cold splits per row before the row chunk is halved instead.
 constexpr uint64_t kColdSplitsBeforeRc = 8;
 
+// q . D^T on the vector ALUs (project_valu_kernel: kProjValuTa atoms x
+// kProjValuRb rows per work-group) for groups of at most kProjValuRows rows
+// sharing a dictionary, on MFMA (project_kernel) above.  0: MFMA at every row
+// count.  Measured (serialized, MI355X): 4 rows per group over 512 atoms 10.9
+// against 6.6 us; 16 rows 10.5 against 6.6; 32 rows over 4096 atoms 9.0 against
+// 6.5; 256 rows 11.1 against 6.7; 2048 rows 56 against 12.3.  At small row
+// counts both are a chain of one dictionary load, the products and the stores;
+// the MFMA kernel's 512-thread tiles issue more of the loads at once.
+constexpr int kProjValuRb = 8;
+constexpr int kProjValuTa = 64;
+constexpr uint32_t kProjValuRows = 0;
+
 // Row pitches of D^T (halves) and of the cold bins W (floats): one 128-byte line
 // of padding, so rows whose natural stride is a power of two (8 or 16 KiB at
 // 4096 atoms) spread over the L2 channels instead of landing on one.
@@ -198,6 +210,10 @@ int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, const uint32_t 
     // buffer, or kept in fp32 on request (workspace and the cold kernel's LDS
     // table): f16 rounding moves a score by up to 2^-11 of sum_k |c_k q_latent[idx_k]|.
     o.qf32 = o.info.computes_q_latent != 0 && (d->flags & AW_F_QLATENT_F32) != 0;
+    if (o.info.computes_q_latent) {
+        const uint32_t per_group = d->batch * d->queries * (d->dict_heads == 1 ? d->q_heads : d->q_heads / d->kv_heads);
+        o.info.projection = per_group <= kProjValuRows ? AW_PROJECT_VALU : AW_PROJECT_MFMA;
+    }
     const uint32_t qbytes = o.qf32 ? 4u : 2u;
 
     // Hot: one round of waves filling the resident capacity, splits <= kMaxSplits.
@@ -387,6 +403,7 @@ struct aw_engine {
     uint32_t iota_n = 0;                      // entries of `iota` filled
     uint32_t* err = nullptr;                  // device error word
     int profiling = 0; // AW_PROFILE_*
+    int projection = AW_PROJECT_AUTO;
     struct Pending {
         int stage;
         hipEvent_t a, b;
@@ -488,6 +505,15 @@ int launch_project(aw_engine* e, const aw_decode_desc* d, const Layout& o, char*
     const uint32_t gz = d->layers * d->dict_heads;
     const uint32_t A = d->dict_size;
     StageTimer t(e, AW_STAGE_PROJECT, st);
+    const bool valu = e->projection == AW_PROJECT_VALU ||
+                      (e->projection == AW_PROJECT_AUTO && o.info.projection == AW_PROJECT_VALU);
+    if (valu) {
+        hipLaunchKernelGGL((aw::project_valu_kernel<HD, kProjValuTa, kProjValuRb>), dim3(cdiv(A, (uint32_t)kProjValuTa),
+                           cdiv(rows, (uint32_t)kProjValuRb), gz), dim3(kProjValuTa),
+                           aw::project_valu_smem_bytes(HD, kProjValuTa, kProjValuRb), st, a);
+        AW_HIP(e, hipGetLastError());
+        return AW_OK;
+    }
     const dim3 block(aw::kProjThreads);
     // Tiles as large as keep >= one work-group per CU: fewer re-reads of D and q.
     auto wgs = [&](uint32_t tr, uint32_t ta) { return (uint64_t)cdiv(A, ta) * cdiv(rows, tr) * gz; };
@@ -1050,7 +1076,9 @@ int aw_engine_create(int device, aw_engine** out) {
         const void* proj[] = {(const void*)aw::project_kernel<128, 32, 64, 2>, (const void*)aw::project_kernel<128, 128, 256, 2>,
                               (const void*)aw::project_kernel<128, 128, 128, 4>, (const void*)aw::project_kernel<128, 128, 64, 8>,
                               (const void*)aw::project_kernel<64, 32, 64, 2>, (const void*)aw::project_kernel<64, 128, 256, 2>,
-                              (const void*)aw::project_kernel<64, 128, 128, 4>, (const void*)aw::project_kernel<64, 128, 64, 8>};
+                              (const void*)aw::project_kernel<64, 128, 128, 4>, (const void*)aw::project_kernel<64, 128, 64, 8>,
+                              (const void*)aw::project_valu_kernel<128, kProjValuTa, kProjValuRb>,
+                              (const void*)aw::project_valu_kernel<64, kProjValuTa, kProjValuRb>};
         for (const void* f : proj) set_lds(f);
     }
     if (!attr_ok) {
@@ -1521,6 +1549,13 @@ int aw_debug_read_pools(aw_engine* e, const aw_decode_desc* d, uint32_t* sink, v
     if (grid > 0x7FFFFFFFull) return fail(e, AW_E_UNSUPPORTED, "gather grid too large");
     hipLaunchKernelGGL(aw::gather_read_kernel<8>, dim3((uint32_t)grid), dim3(64), 0, (hipStream_t)stream, a);
     AW_HIP(e, hipGetLastError());
+    return AW_OK;
+}
+
+int aw_engine_set_projection(aw_engine* e, int mode) {
+    if (!e) return AW_E_INVALID_ARG;
+    if (mode < AW_PROJECT_AUTO || mode > AW_PROJECT_VALU) return fail(e, AW_E_INVALID_ARG, "projection mode %d", mode);
+    e->projection = mode;
     return AW_OK;
 }
 

@@ -38,6 +38,7 @@ namespace aw {
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t uint4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t uint2_t __attribute__((ext_vector_type(2)));
@@ -236,6 +237,34 @@ inline size_t project_smem_bytes(int HD, int TR, int TA) {
     return in > out ? in : out;
 }
 
+// D^T of a staged tile of TA atoms (rows of `sd`, pitch P halves), the dims
+// split over the grid's row blocks: pieces of 8 atoms, piece p = (atom group
+// p / nd, dim d0 + p % nd), written [HD][dt_pitch] or in the row-tile finish's
+// lane order.
+template <int HD, int TA, int NTH>
+__device__ __forceinline__ void write_dt(const ProjArgs& a, const _Float16* sd, int P, uint32_t group, uint32_t atom0) {
+    const uint32_t A = a.dict_size;
+    const uint32_t nrb = gridDim.y, y = blockIdx.y;
+    const int d0 = (int)((y * (uint32_t)HD) / nrb), nd = (int)(((y + 1) * (uint32_t)HD) / nrb) - d0;
+    const int TP = nd * (TA / 8);
+    uint16_t* dt = a.dt + (uint64_t)group * HD * (a.dt_tiled ? A : a.dt_pitch);
+    for (int p = (int)threadIdx.x; p < TP; p += NTH) {
+        const int d = d0 + p % nd, ag = p / nd;
+        const uint32_t at = atom0 + 8 * ag;
+        if (at >= A) continue;
+        uint32_t w[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            w[e] = (uint32_t)__builtin_bit_cast(uint16_t, sd[(8 * ag + 2 * e) * P + d]) |
+                   ((uint32_t)__builtin_bit_cast(uint16_t, sd[(8 * ag + 2 * e + 1) * P + d]) << 16);
+        // Tiled: the piece of lane (li = d % 16, lg = (at % 32) / 8) of k-step at / 32, dim block d / 16.
+        const uint64_t off = a.dt_tiled ? (((uint64_t)(at / 32) * (HD / 16) + (uint32_t)d / 16) * 64 +
+                                           ((at % 32) / 8) * 16 + (uint32_t)d % 16) * 8
+                                        : (uint64_t)d * a.dt_pitch + at;
+        *(uint4_t*)(dt + off) = (uint4_t){w[0], w[1], w[2], w[3]};
+    }
+}
+
 template <int HD, int TR, int TA, int WR>
 __global__ __launch_bounds__(kProjThreads) void project_kernel(ProjArgs a) {
     constexpr int NW = kProjThreads / 64, P = kProjPitch(HD), KS = HD / 32, PR = HD / 8; // 16-byte pieces per row
@@ -302,29 +331,7 @@ __global__ __launch_bounds__(kProjThreads) void project_kernel(ProjArgs a) {
             }
         }
     }
-    {
-        // D^T of the tile's atoms, the dims split over the row blocks: pieces of 8
-        // atoms, piece p = (atom group p / nd, dim d0 + p % nd).
-        const uint32_t nrb = gridDim.y, y = blockIdx.y;
-        const int d0 = (int)((y * (uint32_t)HD) / nrb), nd = (int)(((y + 1) * (uint32_t)HD) / nrb) - d0;
-        const int TP = nd * (TA / 8);
-        uint16_t* dt = a.dt + (uint64_t)group * HD * (a.dt_tiled ? A : a.dt_pitch);
-        for (int p = tid; p < TP; p += kProjThreads) {
-            const int d = d0 + p % nd, ag = p / nd;
-            const uint32_t at = atom0 + 8 * ag;
-            if (at >= A) continue;
-            uint32_t w[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-                w[e] = (uint32_t)__builtin_bit_cast(uint16_t, sd[(8 * ag + 2 * e) * P + d]) |
-                       ((uint32_t)__builtin_bit_cast(uint16_t, sd[(8 * ag + 2 * e + 1) * P + d]) << 16);
-            // Tiled: the piece of lane (li = d % 16, lg = (at % 32) / 8) of k-step at / 32, dim block d / 16.
-            const uint64_t off = a.dt_tiled ? (((uint64_t)(at / 32) * (HD / 16) + (uint32_t)d / 16) * 64 +
-                                               ((at % 32) / 8) * 16 + (uint32_t)d % 16) * 8
-                                            : (uint64_t)d * a.dt_pitch + at;
-            *(uint4_t*)(dt + off) = (uint4_t){w[0], w[1], w[2], w[3]};
-        }
-    }
+    write_dt<HD, TA, kProjThreads>(a, sd, P, group, atom0);
     if (a.qlf != nullptr) {
         // fp32 rows straight from the accumulators: a lane holds atoms 4*lg .. +3
         // of row li of each tile (16 contiguous bytes; A % 16 == 0).
@@ -358,6 +365,89 @@ __global__ __launch_bounds__(kProjThreads) void project_kernel(ProjArgs a) {
                 *(uint4_t*)(a.ql + qrow_of(i) * A + ao) = *(const uint4_t*)(so + r * OP + 8 * c);
         }
     }
+}
+
+// ------------------------------------------------------ q . D^T (VALU)
+//
+// The same projection on the vector ALUs, for few rows per dictionary group.
+// Work-group = TA atoms (one per thread) x RB rows: the atoms' dictionary
+// rows and the RB q rows are staged in LDS (the same loads-then-stores
+// pattern), then each thread forms its atom's RB dot products with
+// v_dot2_f32_f16 (two f16 products per instruction, fp32 sums in dim order)
+// and writes one value per row: consecutive threads, consecutive atoms, so the
+// stores of a row are contiguous.  D^T is written as by project_kernel.
+inline size_t project_valu_smem_bytes(int HD, int TA, int RB) {
+    return ((size_t)TA * kProjPitch(HD) + (size_t)RB * HD) * 2;
+}
+
+template <int HD, int TA, int RB>
+__global__ __launch_bounds__(TA) void project_valu_kernel(ProjArgs a) {
+    constexpr int P = kProjPitch(HD), PR = HD / 8;
+    constexpr int PIECES = (TA + RB) * PR, PT = (PIECES + TA - 1) / TA;
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    _Float16* sd = (_Float16*)smem; // [TA][P] dictionary atoms
+    _Float16* sq = sd + TA * P;     // [RB][HD] query rows
+    const int tid = threadIdx.x;
+    const uint32_t group = blockIdx.z;
+    const uint32_t l = group / a.dict_heads, dg = group % a.dict_heads;
+    const uint32_t atom0 = blockIdx.x * TA, row0 = blockIdx.y * RB;
+    const uint32_t A = a.dict_size;
+    const uint16_t* dict = a.dict + l * a.dict_layer + (uint64_t)dg * A * HD;
+    const bool shared = a.dict_heads == 1;
+    auto qrow_of = [&](uint32_t i) -> uint64_t {
+        i = min(i, a.rows_per_group - 1u);
+        if (shared) return (uint64_t)l * a.rows_per_group + i;
+        const uint32_t bq = i / a.gqa, hh = i % a.gqa;
+        return ((uint64_t)l * a.batch * a.queries + bq) * a.q_heads + dg * a.gqa + hh;
+    };
+    {
+        uint4_t v[PT];
+#pragma unroll
+        for (int k = 0; k < PT; ++k) {
+            const int p = min(tid + k * TA, PIECES - 1);
+            const int r = p / PR, c = p % PR;
+            const uint16_t* src = r < TA ? dict + (uint64_t)min(atom0 + (uint32_t)r, A - 1u) * HD
+                                         : a.q + qrow_of(row0 + (uint32_t)(r - TA)) * HD;
+            v[k] = *(const uint4_t*)(src + 8 * c);
+        }
+#pragma unroll
+        for (int k = 0; k < PT; ++k) {
+            const int p = tid + k * TA;
+            if (p >= PIECES) continue;
+            const int r = p / PR, c = p % PR;
+            *(uint4_t*)(r < TA ? sd + r * P + 8 * c : sq + (r - TA) * HD + 8 * c) = v[k];
+        }
+    }
+    __syncthreads();
+    const bool want = a.ql != nullptr || a.qlf != nullptr;
+    if (want) {
+        float acc[RB];
+#pragma unroll
+        for (int r = 0; r < RB; ++r) acc[r] = 0.0f;
+#pragma unroll 4
+        for (int c = 0; c < PR; ++c) {
+            const half8_t dv = *(const half8_t*)(sd + tid * P + 8 * c);
+#pragma unroll
+            for (int r = 0; r < RB; ++r) {
+                const half8_t qv = *(const half8_t*)(sq + r * HD + 8 * c); // one address: a broadcast
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    acc[r] = __builtin_amdgcn_fdot2((half2_t){dv[2 * e], dv[2 * e + 1]},
+                                                    (half2_t){qv[2 * e], qv[2 * e + 1]}, acc[r], false);
+            }
+        }
+        const uint32_t at = atom0 + (uint32_t)tid;
+        if (at < A) {
+#pragma unroll
+            for (int r = 0; r < RB; ++r) {
+                const uint32_t i = row0 + (uint32_t)r;
+                if (i >= a.rows_per_group) break;
+                if (a.qlf != nullptr) a.qlf[qrow_of(i) * A + at] = acc[r];
+                else a.ql[qrow_of(i) * A + at] = __builtin_bit_cast(uint16_t, (_Float16)acc[r]);
+            }
+        }
+    }
+    write_dt<HD, TA, TA>(a, sd, P, group, atom0);
 }
 
 // ------------------------------------------------- hot pool, split-K (MFMA)

@@ -297,6 +297,11 @@ class WeaverEngine:
         pipeline; 2: event-time each kernel with the stages serialized."""
         self._check(self._lib.aw_engine_set_profiling(self._h, int(mode)), "set_profiling")
 
+    def set_projection(self, mode) -> None:
+        """Kernel of q_latent = q . D^T: 0 the planner's choice (MFMA), 1 MFMA
+        tiles, 2 the VALU kernel (AW_PROJECT_*)."""
+        self._check(self._lib.aw_engine_set_projection(self._h, int(mode)), "set_projection")
+
     def reset_stage_stats(self) -> None:
         self._check(self._lib.aw_engine_reset_stage_stats(self._h), "reset_stage_stats")
 

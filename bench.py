@@ -83,6 +83,8 @@ def parse():
                    help="print HBM traffic per launch from a FETCH_SIZE and a WRITE_SIZE rocprofv3 database and exit")
     p.add_argument("--traffic-command", default="", help="command line recorded in --traffic-summary output")
     p.add_argument("--traffic-title", default="", help="workload named in --traffic-summary output")
+    p.add_argument("--only-projection", action="store_true",
+                   help="time only q . D^T on MFMA and on the VALU at several row counts and print them")
     p.add_argument("--only-attention", action="store_true",
                    help="time only the inference attention (dense and tiered caches) and print it")
     return p.parse_args()
@@ -359,6 +361,63 @@ def config_line(engine, key: str, args) -> dict:
 
 VALU_FP32_FMA_TFLOPS = 78.6  # 256 CUs x 128 fp32 FMA lanes x 2.4 GHz x 2 (no packed fp32 here)
 MFMA_F16_TFLOPS = 2500.0     # dense f16 MFMA
+VALU_DOT2_F16_TFLOPS = 157.3  # v_dot2_f32_f16: two f16 products per lane and cycle
+
+
+def projection_table(engine, seed, steps=50):
+    """q_latent = q . D^T (YELLOWPAPER.md:86-92) on MFMA tiles (project_kernel)
+    and on the vector ALUs (project_valu_kernel), serialized stage time of each
+    path over `steps` decodes, at several rows per dictionary group; `planner`
+    is the path aw_engine_set_projection(AUTO) takes there."""
+    import torch
+    from aether_nexus_amd import workloads as W
+    from aether_nexus_amd.types import AW_PROJECT_AUTO, AW_PROJECT_MFMA, AW_PROJECT_VALU
+    from aether_nexus_amd.weaver import plan
+    cases = [("4 rows per group: one query, 8 per-kv-head dictionaries of 512 atoms",
+              W.hot_cold(batch=1, dict_size=512, dict_heads=8)),
+             ("16 rows per group: 4 queries, 8 per-kv-head dictionaries of 512 atoms",
+              W.hot_cold(batch=1, queries=4, causal=True, dict_size=512, dict_heads=8)),
+             ("32 rows: B = 1, shared 4096-atom dictionary", W.sweep(1)),
+             ("256 rows: B = 8, shared 4096-atom dictionary", W.sweep(8)),
+             ("2048 rows: B = 64, shared 4096-atom dictionary", W.sweep(64))]
+    st = torch.cuda.current_stream().cuda_stream
+    rows = []
+    try:
+        for name, geom in cases:
+            wl = W.generate(geom, seed=seed, device="cuda:0")
+            out = torch.empty(wl.out_shape(), dtype=torch.float16, device="cuda:0")
+            desc = W.device_desc(wl, out)
+            per_group = geom.batch * geom.queries * (geom.q_heads if geom.dict_heads == 1 else
+                                                       geom.q_heads // geom.kv_heads)
+            flops = 2.0 * geom.layers * geom.batch * geom.queries * geom.q_heads * geom.dict_size * geom.head_dim
+            row = {"case": name, "rows_per_group": per_group, "groups": geom.layers * geom.dict_heads,
+                   "atoms": geom.dict_size, "gflop": round(flops / 1e9, 4)}
+            for key, mode in (("mfma", AW_PROJECT_MFMA), ("valu", AW_PROJECT_VALU)):
+                engine.set_projection(mode)
+                engine.decode_device(desc, stream=st)
+                engine.reset_stage_stats()
+                engine.set_profiling(2)
+                for _ in range(steps):
+                    engine.decode_device(desc, stream=st)
+                torch.cuda.synchronize()
+                engine.set_profiling(0)
+                ms, n = engine.stage_stats()["project"]
+                us = ms / n * 1e3
+                tf = flops / (us * 1e-6) / 1e12
+                peak = MFMA_F16_TFLOPS if key == "mfma" else VALU_DOT2_F16_TFLOPS
+                row[key] = {"us": round(us, 2), "tflops": round(tf, 2), "frac_of_peak": round(tf / peak, 4),
+                            "peak_tflops": peak}
+            row["planner"] = "valu" if plan(desc).projection == AW_PROJECT_VALU else "mfma"
+            rows.append(row)
+            log(json.dumps(row))
+            del wl, out, desc
+            torch.cuda.empty_cache()
+    finally:
+        engine.set_projection(AW_PROJECT_AUTO)
+        engine.set_profiling(0)
+    return {"note": "serialized stage time (HIP events) of the projection alone; peaks: f16 MFMA dense for "
+                    "project_kernel, v_dot2_f32_f16 on every lane for project_valu_kernel",
+            "rows": rows}
 
 
 def encoder_bench(engine, seed, reps, cpu_blocks):
@@ -1054,6 +1113,11 @@ def main():
         engine.close()
         print(json.dumps({"configs": rows}), flush=True)
         return 0
+    if args.only_projection:
+        out = projection_table(engine, args.seed)
+        engine.close()
+        print(json.dumps({"projection_paths": out}), flush=True)
+        return 0
     if args.only_attention:
         out = attention_bench(engine, args.seed, 20, 0.5 if args.no_cpu else 3.0)
         engine.close()
@@ -1127,6 +1191,7 @@ def main():
         if serial[k][0]:
             tf = fl / (serial[k][0] * 1e-3) / 1e12
             mfma[k] = {"gflop": round(fl / 1e9, 3), "tflops": round(tf, 1), "frac": round(tf / MFMA_F16_TFLOPS, 4)}
+    proj_paths = projection_table(engine, args.seed)
     copy_peak = hbm_copy_peak()
     read_peak = hbm_read_peak(engine)
     log(json.dumps({"hbm_read_peak": read_peak}))
@@ -1209,6 +1274,7 @@ def main():
         "hbm_gather_peak": gather_peak,
         "configs": configs,
         "mfma_kernels": mfma,
+        "projection_paths": proj_paths,
         "other_cold_layout": alt,
         "encoder": enc,
         "fabric": fab,

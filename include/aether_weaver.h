@@ -165,7 +165,7 @@ typedef struct aw_decode_plan_info {
     uint32_t cold_tokens_per_split;
     uint32_t cold_row_chunk;     /* query rows binned together in one cold work-group */
     uint32_t computes_q_latent;  /* 1 when q . D^T runs on the device */
-    uint32_t _reserved;
+    uint32_t projection;         /* its kernel by the planner's choice: AW_PROJECT_MFMA or _VALU (0: none) */
     uint64_t workspace_bytes;    /* device scratch this request needs */
 } aw_decode_plan_info;
 
@@ -428,6 +428,19 @@ int aw_debug_read_pools(aw_engine* engine, const aw_decode_desc* desc, uint32_t*
 #define AW_PROFILE_ON 1
 #define AW_PROFILE_SERIAL 2
 int aw_engine_set_profiling(aw_engine* engine, int mode);
+
+/* Which kernel computes q_latent = q . D^T (spec YELLOWPAPER.md:86-92; the
+ * reference's caller supplies it, weaver_kernel.metal:111).  AW_PROJECT_AUTO
+ * is the planner's choice by rows per dictionary group: MFMA tiles at every
+ * row count, the VALU kernel having measured slower at each one (4 rows per
+ * group with 512 atoms: 10.9 against 6.6 us; 32 rows with 4096 atoms: 9.0
+ * against 6.5; 2048 rows: 56 against 12.3).  AW_PROJECT_MFMA and
+ * AW_PROJECT_VALU force one path, for measuring the other.  No reference
+ * counterpart. */
+#define AW_PROJECT_AUTO 0
+#define AW_PROJECT_MFMA 1
+#define AW_PROJECT_VALU 2
+int aw_engine_set_projection(aw_engine* engine, int mode);
 int aw_engine_stage_stats(aw_engine* engine, int stage, double* total_ms, uint64_t* launches);
 int aw_engine_reset_stage_stats(aw_engine* engine);
 

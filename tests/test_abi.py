@@ -13,7 +13,7 @@ import pytest
 
 from aether_nexus_amd import _lib
 from aether_nexus_amd import workloads as W
-from aether_nexus_amd.types import (AW_E_ALIGN, AW_E_INVALID_ARG, AW_E_OOB, AW_E_UNSUPPORTED, SPARSE_CODE_DTYPE,
+from aether_nexus_amd.types import (AW_E_ALIGN, AW_PROJECT_AUTO, AW_PROJECT_MFMA, AW_PROJECT_VALU, AW_E_INVALID_ARG, AW_E_OOB, AW_E_UNSUPPORTED, SPARSE_CODE_DTYPE,
                                     STRUCT_SIZES, DecodeDesc, PlanInfo, WeaverParams)
 from aether_nexus_amd.weaver import WeaverError, plan, validate_params
 
@@ -276,9 +276,10 @@ def test_headers_compile_as_c_and_match_the_library(tmp_path):
 int main(void) {
     size_t s[4];
     aw_abi_struct_sizes(s);
-    printf("%zu %zu %zu %zu %zu %zu %zu %u\\n", sizeof(aw_sparse_code), sizeof(aw_weaver_params),
+    printf("%zu %zu %zu %zu %zu %zu %zu %u %d %d %d\\n", sizeof(aw_sparse_code), sizeof(aw_weaver_params),
            sizeof(aw_decode_desc), sizeof(aw_decode_plan_info), offsetof(aw_decode_desc, hot_tokens),
-           offsetof(aw_decode_desc, q), offsetof(aw_decode_desc, out), aw_abi_version());
+           offsetof(aw_decode_desc, q), offsetof(aw_decode_desc, out), aw_abi_version(), AW_PROJECT_AUTO,
+           AW_PROJECT_MFMA, AW_PROJECT_VALU);
     return !(s[0] == sizeof(aw_sparse_code) && s[1] == sizeof(aw_weaver_params) && s[2] == sizeof(aw_decode_desc) &&
              s[3] == sizeof(aw_decode_plan_info));
 }
@@ -295,6 +296,7 @@ int main(void) {
     assert vals[:4] == list(STRUCT_SIZES)
     assert vals[4:7] == [DecodeDesc.hot_tokens.offset, DecodeDesc.q.offset, DecodeDesc.out.offset]
     assert vals[7] == lib_abi_version()
+    assert vals[8:11] == [AW_PROJECT_AUTO, AW_PROJECT_MFMA, AW_PROJECT_VALU]
 
 
 def lib_abi_version() -> int:

@@ -155,9 +155,11 @@ PROJECTIONS = {
 }
 
 
+@pytest.mark.parametrize("path", ["mfma", "valu"])
 @pytest.mark.parametrize("name", list(PROJECTIONS))
-def test_projection_q_latent_direct(engine, stream, name):
-    """q_latent = q . D^T on the device (project_kernel, MFMA f16 x f16 -> fp32),
+def test_projection_q_latent_direct(engine, stream, name, path):
+    """q_latent = q . D^T on the device (project_kernel, MFMA f16 x f16 -> fp32,
+    the planner's path; and project_valu_kernel, v_dot2_f32_f16 on the VALU),
     checked directly against the float64 projection: the f16 result is the
     float64 value rounded to f16 for all but entries within the fp32
     accumulation error of a rounding boundary (those are one f16 ulp off); the
@@ -174,8 +176,13 @@ def test_projection_q_latent_direct(engine, stream, name):
     out = torch.empty(dev.out_shape(), dtype=torch.float16, device="cuda:0")
     desc = W.device_desc(dev, out, q_latent_f32=f32)
     ql = torch.empty(ref.shape, dtype=torch.float32 if f32 else torch.float16, device="cuda:0")
-    engine.project(desc, ql, stream=stream)
-    torch.cuda.synchronize()
+    from aether_nexus_amd.types import AW_PROJECT_AUTO, AW_PROJECT_MFMA, AW_PROJECT_VALU
+    engine.set_projection(AW_PROJECT_VALU if path == "valu" else AW_PROJECT_MFMA)
+    try:
+        engine.project(desc, ql, stream=stream)
+        torch.cuda.synchronize()
+    finally:
+        engine.set_projection(AW_PROJECT_AUTO)
     got = ql.cpu().numpy().astype(np.float64)
     q = oracle.h2f(a["q"]).astype(np.float64).reshape(geom.layers, geom.batch, geom.queries, geom.q_heads, -1)
     dic = oracle.h2f(a["dictionary"]).astype(np.float64).reshape(geom.layers, geom.dict_heads, geom.dict_size, -1)
@@ -265,3 +272,20 @@ def test_peaked_softmax_device_q_latent(engine, stream, hot_count, batch):
 def test_cold_many_tiles_small_coefficients(engine, stream):
     check(engine, stream, W.hot_cold(batch=2, hot_count=8, cold_count=2048, coef_std=0.05), seed=12,
           what="hot+cold, coef std 0.05")
+
+
+@pytest.mark.parametrize("geom", [W.hot_cold(batch=2, hot_count=4, cold_count=64, dict_size=512, dict_heads=8,
+                                             queries=2, causal=True),
+                                  W.hot_cold(batch=1, hot_count=8, cold_count=128)],
+                         ids=["per_head_512_b2_q2", "shared_4096_b1"])
+def test_decode_with_valu_projection(engine, stream, geom):
+    """The whole decode with q_latent from the VALU kernel (forced; the planner
+    takes MFMA tiles at every size) against the fp64 oracle."""
+    from aether_nexus_amd.types import AW_PROJECT_AUTO, AW_PROJECT_VALU
+    wl = W.generate(geom, seed=81)
+    engine.set_projection(AW_PROJECT_VALU)
+    try:
+        got = run_gpu(engine, wl, stream)
+    finally:
+        engine.set_projection(AW_PROJECT_AUTO)
+    assert_close(got, oracle.decode_f64(geom, W.host_arrays(wl)), "decode, VALU projection")
