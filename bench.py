@@ -57,6 +57,9 @@ def parse():
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--batches", default="1,2,4,8,16,32,64")
     p.add_argument("--no-graph", action="store_true", help="launch each step from the host (no HIP graph)")
+    p.add_argument("--steps-per-graph", type=int, default=8,
+                   help="decode steps captured in one HIP graph for the timed replays (1: a graph per step, "
+                        "whose host launch cost then bounds short steps)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--seed", type=int, default=0)
@@ -98,7 +101,7 @@ def copies_for(geom) -> int:
 class Runner:
     """One workload resident on the GPU, its descriptors and (optionally) graphs."""
 
-    def __init__(self, engine, geom, seed, use_graph, wl=None, cold_head_blocked=False):
+    def __init__(self, engine, geom, seed, use_graph, wl=None, cold_head_blocked=False, steps_per_graph=1):
         import torch
         from aether_nexus_amd import workloads as W
         self.torch = torch
@@ -126,6 +129,20 @@ class Runner:
                 with torch.cuda.graph(g, stream=self.stream):
                     engine.decode_device(d, stream=torch.cuda.current_stream().cuda_stream)
                 self.graphs.append(g)
+        # Graphs of m consecutive steps (copies in rotation), the way a serving
+        # loop captures a whole decode step: a replay's host launch cost is paid
+        # once per m steps, so a short step is timed on the GPU, not on the host.
+        self.m = steps_per_graph if use_graph else 1
+        self.multi = []
+        if self.m > 1:
+            C = len(self.descs)
+            for k in range(max(1, C // self.m)):
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g, stream=self.stream):
+                    for j in range(self.m):
+                        engine.decode_device(self.descs[(k * self.m + j) % C],
+                                             stream=torch.cuda.current_stream().cuda_stream)
+                self.multi.append(g)
 
     def step(self, i):
         if self.graphs is not None:
@@ -133,16 +150,24 @@ class Runner:
         else:
             self.engine.decode_device(self.descs[i % len(self.descs)], stream=self.stream.cuda_stream)
 
-    def time_steps(self, steps, warmup):
+    def time_steps(self, steps, warmup, one_step_graphs=False):
+        """ms per step over exactly `steps` decode steps after `warmup` untimed
+        ones: replays of the m-step graphs (and one-step graphs for a remainder),
+        or of one-step graphs only."""
         torch = self.torch
+        m = 1 if one_step_graphs or not self.multi else self.m
         with torch.cuda.stream(self.stream):
             for i in range(warmup):
                 self.step(i)
+            for g in self.multi:
+                g.replay()
             torch.cuda.synchronize()
             a = torch.cuda.Event(enable_timing=True)
             b = torch.cuda.Event(enable_timing=True)
             a.record(self.stream)
-            for i in range(steps):
+            for k in range(steps // m if m > 1 else 0):
+                self.multi[k % len(self.multi)].replay()
+            for i in range(steps % m if m > 1 else steps):
                 self.step(warmup + i)
             b.record(self.stream)
             torch.cuda.synchronize()
@@ -186,6 +211,7 @@ def cpu_baseline(seconds: float, seed: int):
     import numpy as np
     from aether_nexus_amd import workloads as W
     from oracle import oracle
+    build = native_oracle()
     geom = W.hot_cold(batch=1)
     wl = W.generate(geom, seed=seed, device="cpu")
     arrs = W.host_arrays(wl)
@@ -212,17 +238,46 @@ def cpu_baseline(seconds: float, seed: int):
                       f"computed on the CPU) in {el:.1f} s, fp32 restatement of weaver_kernel.metal, "
                       f"{threads} threads",
             "single_thread_value": round(n1 / el1, 3), "cpu_model": cpu_model(),
-            "host_cpus": os.cpu_count()}
+            "host_cpus": os.cpu_count(), "build": build}
+
+
+_NATIVE = {}
+
+
+def native_oracle() -> str:
+    """The timed CPU port built for this host (-O3 -march=native) into a scratch
+    directory and bound in place of the shipped portable build (x86-64-v3, used
+    by the tests); the shipped build is kept if no compiler is here."""
+    if "build" not in _NATIVE:
+        import tempfile
+        from oracle import oracle
+        try:
+            out = Path(tempfile.mkdtemp(prefix="weaver_oracle_")) / "libweaver_oracle_native.so"
+            oracle.use_lib(oracle.build_native(out))
+            _NATIVE["build"] = "gcc -O3 -march=native -ffp-contract=off, built on this host"
+        except Exception as exc:  # no gcc/make on the host: the portable build times it
+            _NATIVE["build"] = f"gcc -O3 -march=x86-64-v3 -ffp-contract=off (shipped; native build failed: {exc})"
+    return _NATIVE["build"]
 
 
 def cpu_model() -> str:
+    """The host CPU as /proc/cpuinfo names it, with its family/model/stepping and
+    widest vector extension (a virtualised host may report only the brand)."""
+    info = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            if ":" in line:
+                k, v = (x.strip() for x in line.split(":", 1))
+                info.setdefault(k, v)
+            elif info:
+                break  # first processor only
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    flags = set(info.get("flags", "").split())
+    isa = next((f for f in ("avx512f", "avx2", "avx") if f in flags), "sse")
+    return (f"{info.get('model name', 'unknown')} (vendor {info.get('vendor_id', '?')}, family "
+            f"{info.get('cpu family', '?')}, model {info.get('model', '?')}, stepping {info.get('stepping', '?')}, "
+            f"{isa})")
 
 
 def hbm_copy_peak(mib: int = 1024, reps: int = 10) -> dict:
@@ -332,8 +387,9 @@ def config_line(engine, key: str, args) -> dict:
     g0 = config_geom(key)
     geom = replace(g0, copies=copies_for(g0))
     hb = args.cold_layout == "head_blocked" and g0.cold_count > 0
-    r = Runner(engine, geom, args.seed, not args.no_graph, cold_head_blocked=hb)
+    r = Runner(engine, geom, args.seed, not args.no_graph, cold_head_blocked=hb, steps_per_graph=args.steps_per_graph)
     ms = r.time_steps(args.steps, args.warmup)
+    ms_1g = r.time_steps(args.steps, args.warmup, one_step_graphs=True)
     ab = geom.algorithmic_bytes()["total"]
     gbps = ab / (ms * 1e-3) / 1e9
     stages = r.stage_times(args.steps, mode=1)
@@ -343,6 +399,7 @@ def config_line(engine, key: str, args) -> dict:
     pipe, alone = stages[dom][0], serial[dom][0]
     row = {"config": key, "workload": CONFIGS[key], "layers": geom.layers, "batch": geom.batch,
            "queries": geom.queries, "tokens_per_step": geom.tokens, "ms_per_step": round(ms, 5),
+           "ms_per_step_graph_per_step": round(ms_1g, 5), "steps_per_graph": r.m,
            "tokens_per_s": round(geom.tokens / (ms * 1e-3), 1), "alg_bytes_per_step": int(ab),
            "achieved_gbps": round(gbps, 1), "frac_of_peak": round(gbps / PEAK_HBM_GBPS, 4),
            "cold_layout": ("head_blocked" if hb else "reference") if g0.cold_count else None,
@@ -481,6 +538,7 @@ def encoder_bench(engine, seed, reps, cpu_blocks):
                           "valu_frac": round(scan_tf / VALU_FP32_FMA_TFLOPS, 4), "valu_peak_tflops": VALU_FP32_FMA_TFLOPS,
                           "note": "AW_F_ENCODE_FULL_SCAN: one exact fp32 FMA per (token, kv head, atom, dim); same codes"},
             "cpu_baseline": {"value": round(cpu_blocks / cpu_s, 2), "unit": "blocks/s", "cores": 1, "kind": "port",
+                             "build": native_oracle(),
                              "sample": f"{cpu_blocks} blocks through the oracle's restatement of distiller.rs:171-246"},
             "codes_match_cpu": same}
 
@@ -550,7 +608,7 @@ def attention_bench(engine, seed, reps, cpu_seconds):
         if el >= cpu_seconds or n >= 2000:
             break
     res["cpu_baseline"] = {"value": round(n / el / layers, 3), "unit": "decode forwards/s (32 layers)",
-                           "cores": threads, "kind": "port",
+                           "cores": threads, "kind": "port", "build": native_oracle(),
                            "sample": f"{n} single-layer decode attentions ({kv_len} cached tokens) through the "
                                      f"oracle's fp32 restatement in {el:.1f} s, {threads} threads"}
     res["gpu_forwards_per_s"] = round(1e3 / res["decode"]["ms_per_forward"], 1)
@@ -898,6 +956,7 @@ def fabric_bench(engine, seed, cpu_blocks):
             "distill_cycle_ms": round(cycle * 1e3, 2), "distilled_blocks": int(n),
             "distill_blocks_per_s": round(n / cycle, 1),
             "cpu_baseline": {"value": round(cpu_blocks / cpu_s, 2), "unit": "blocks/s", "cores": 1, "kind": "port",
+                             "build": native_oracle(),
                              "sample": f"entropy proxy and encoding of hot blocks 0..{cpu_blocks - 1} "
                                        "through the oracle (distiller.rs:97-246)"},
             "cycle_matches_cpu": same}
@@ -1096,6 +1155,8 @@ def main():
     from aether_nexus_amd.weaver import WeaverEngine
 
     batches = [int(x) for x in args.batches.split(",") if x]
+    if not args.no_cpu:
+        log(f"CPU port: {native_oracle()}")
     engine = WeaverEngine()
     log(f"device: {engine.device_name()}")
     config_keys = [k for k in args.configs.split(",") if k]
@@ -1134,11 +1195,14 @@ def main():
     for B in batches:
         g0 = W.sweep(B)
         geom = W.sweep(B, copies=copies_for(g0))
-        r = Runner(engine, geom, args.seed, not args.no_graph, cold_head_blocked=args.cold_layout == "head_blocked")
+        r = Runner(engine, geom, args.seed, not args.no_graph, cold_head_blocked=args.cold_layout == "head_blocked",
+                   steps_per_graph=args.steps_per_graph)
         ms = r.time_steps(args.steps, args.warmup)
+        ms_1g = r.time_steps(args.steps, args.warmup, one_step_graphs=True)
         ab = geom.algorithmic_bytes()["total"]
         gbps = ab / (ms * 1e-3) / 1e9
-        row = {"batch": B, "ms_per_step": round(ms, 5), "tokens_per_s": round(B / (ms * 1e-3), 1),
+        row = {"batch": B, "ms_per_step": round(ms, 5), "ms_per_step_graph_per_step": round(ms_1g, 5),
+               "steps_per_graph": r.m, "tokens_per_s": round(B / (ms * 1e-3), 1),
                "alg_bytes_per_step": int(ab), "achieved_gbps": round(gbps, 1),
                "frac_of_peak": round(gbps / PEAK_HBM_GBPS, 4), "copies": geom.copies}
         if args.stage_sweep:
@@ -1206,7 +1270,8 @@ def main():
     alt = None
     if not args.skip_alt_layout:
         other = "head_blocked" if args.cold_layout == "reference" else "reference"
-        rh = Runner(engine, geom, args.seed, not args.no_graph, wl=r.wl, cold_head_blocked=other == "head_blocked")
+        rh = Runner(engine, geom, args.seed, not args.no_graph, wl=r.wl, cold_head_blocked=other == "head_blocked",
+                    steps_per_graph=args.steps_per_graph)
         ms_hb = rh.time_steps(args.steps, args.warmup)
         same = bool(torch.equal(rh.out.view(torch.int16), r.out.view(torch.int16)))
         gb_hb = geom.algorithmic_bytes()["total"] / (ms_hb * 1e-3) / 1e9
@@ -1260,7 +1325,8 @@ def main():
                                f"one query token, scale 1/sqrt(128), cold pool {args.cold_layout} in HBM",
                    "batch": geom.batch, "hot_tokens": geom.hot_count * 16, "cold_tokens": geom.cold_count * 16,
                    "q_heads": geom.q_heads, "kv_heads": geom.kv_heads, "head_dim": geom.head_dim,
-                   "dict_atoms": geom.dict_size, "cold_layout": args.cold_layout, "hip_graph": not args.no_graph},
+                   "dict_atoms": geom.dict_size, "cold_layout": args.cold_layout, "hip_graph": not args.no_graph,
+                   "steps_per_graph": r.m},
         "achieved_gbps": row["achieved_gbps"],
         "frac_of_peak": row["frac_of_peak"],
         "frac_of_copy_peak": round(row["achieved_gbps"] / copy_peak["gbps"], 4),

@@ -30,33 +30,51 @@ def build() -> Path:
     return LIB
 
 
+def build_native(out: Path) -> Path:
+    """Compile the same source for the host that runs it (-O3 -march=native,
+    fp contraction off) into `out`: the timed CPU baseline's build."""
+    subprocess.run(["make", "-s", "-C", str(HERE), "native", f"NATIVE_OUT={out}"], check=True,
+                   stdout=subprocess.DEVNULL)
+    return out
+
+
+def use_lib(path: Path) -> None:
+    """Bind the oracle functions to another build of the same source."""
+    global _lib
+    _lib = _bind(ctypes.CDLL(str(path)))
+
+
 def lib() -> ctypes.CDLL:
     global _lib
     if _lib is None:
         if not LIB.is_file():
             build()
-        l = ctypes.CDLL(str(LIB))
-        vp, u64 = ctypes.c_void_p, ctypes.c_uint64
-        l.or_h2f.restype = ctypes.c_float
-        l.or_h2f.argtypes = [ctypes.c_uint16]
-        l.or_f2h.restype = ctypes.c_uint16
-        l.or_f2h.argtypes = [ctypes.c_float]
-        l.or_h2f_array.argtypes = [vp, vp, ctypes.c_size_t]
-        l.or_f2h_array.argtypes = [vp, vp, ctypes.c_size_t]
-        l.or_decode_ref32.argtypes = [vp, ctypes.c_int]
-        l.or_decode_ref32_rows.argtypes = [vp, vp, u64, vp, ctypes.c_int]
-        l.or_decode_f64.argtypes = [vp, vp, u64, vp, ctypes.c_int]
-        l.or_qlatent_f64.argtypes = [vp, vp]
-        l.or_gather_codes.argtypes = [vp, u64, vp, ctypes.c_uint32, ctypes.c_uint32, vp, vp, vp]
-        l.or_encode_blocks.argtypes = [vp, u64, ctypes.c_uint32, ctypes.c_uint32, vp, ctypes.c_uint32, ctypes.c_uint32,
-                                       vp, vp, ctypes.c_uint32, vp, u64, ctypes.c_int, vp]
-        l.or_block_entropy.argtypes = [vp, u64]
-        l.or_block_entropy.restype = ctypes.c_float
-        for f in ("or_decode_ref32", "or_decode_ref32_rows", "or_decode_f64", "or_qlatent_f64", "or_gather_codes",
-                  "or_encode_blocks"):
-            getattr(l, f).restype = ctypes.c_int
-        _lib = l
+        _lib = _bind(ctypes.CDLL(str(LIB)))
     return _lib
+
+
+def _bind(l: ctypes.CDLL) -> ctypes.CDLL:
+    """Argument and result types of the exported functions."""
+    vp, u64 = ctypes.c_void_p, ctypes.c_uint64
+    l.or_h2f.restype = ctypes.c_float
+    l.or_h2f.argtypes = [ctypes.c_uint16]
+    l.or_f2h.restype = ctypes.c_uint16
+    l.or_f2h.argtypes = [ctypes.c_float]
+    l.or_h2f_array.argtypes = [vp, vp, ctypes.c_size_t]
+    l.or_f2h_array.argtypes = [vp, vp, ctypes.c_size_t]
+    l.or_decode_ref32.argtypes = [vp, ctypes.c_int]
+    l.or_decode_ref32_rows.argtypes = [vp, vp, u64, vp, ctypes.c_int]
+    l.or_decode_f64.argtypes = [vp, vp, u64, vp, ctypes.c_int]
+    l.or_qlatent_f64.argtypes = [vp, vp]
+    l.or_gather_codes.argtypes = [vp, u64, vp, ctypes.c_uint32, ctypes.c_uint32, vp, vp, vp]
+    l.or_encode_blocks.argtypes = [vp, u64, ctypes.c_uint32, ctypes.c_uint32, vp, ctypes.c_uint32, ctypes.c_uint32,
+                                   vp, vp, ctypes.c_uint32, vp, u64, ctypes.c_int, vp]
+    l.or_block_entropy.argtypes = [vp, u64]
+    l.or_block_entropy.restype = ctypes.c_float
+    for f in ("or_decode_ref32", "or_decode_ref32_rows", "or_decode_f64", "or_qlatent_f64", "or_gather_codes",
+              "or_encode_blocks"):
+        getattr(l, f).restype = ctypes.c_int
+    return l
 
 
 class OracleError(RuntimeError):
