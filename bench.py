@@ -71,6 +71,7 @@ def parse():
     p.add_argument("--skip-fabric", action="store_true", help="skip the .aether fabric residency measurement")
     p.add_argument("--skip-attention", action="store_true", help="skip the inference-attention measurement")
     p.add_argument("--skip-ops", action="store_true", help="skip the dense-ops measurement (products, decode forward)")
+    p.add_argument("--skip-projection", action="store_true", help="skip the projection-path table (MFMA vs VALU)")
     p.add_argument("--only-ops", action="store_true", help="time only the dense ops and print them")
     p.add_argument("--configs", default="2,4,5",
                    help="BASELINE configurations timed beside the sweep (comma list of 2, 4, 5; empty for none)")
@@ -90,6 +91,9 @@ def parse():
                    help="time only q . D^T on MFMA and on the VALU at several row counts and print them")
     p.add_argument("--only-attention", action="store_true",
                    help="time only the inference attention (dense and tiered caches) and print it")
+    p.add_argument("--trace-phase", choices=("all", "pipeline", "serial"), default="all",
+                   help="for kernel traces: 'pipeline' launches only the concurrent pipeline (no per-kernel "
+                        "event timing), 'serial' runs every decode with its kernels one at a time and no graph")
     return p.parse_args()
 
 
@@ -191,6 +195,15 @@ class Runner:
         finally:
             eng.set_profiling(0)
         return {k: (ms / n if n else None, n) for k, (ms, n) in st.items()}
+
+
+def stage_pair(r, args):
+    """Per-kernel event times in the pipeline and serialized, or none (a kernel
+    trace of one phase: --trace-phase pipeline / serial)."""
+    if args.trace_phase != "all":
+        none = {k: (None, 0) for k in ("project", "hot", "cold", "finish", "merge")}
+        return none, dict(none)
+    return r.stage_times(args.steps, mode=1), r.stage_times(args.steps, mode=2)
 
 
 def kernel_bytes(geom) -> dict:
@@ -392,11 +405,10 @@ def config_line(engine, key: str, args) -> dict:
     ms_1g = r.time_steps(args.steps, args.warmup, one_step_graphs=True)
     ab = geom.algorithmic_bytes()["total"]
     gbps = ab / (ms * 1e-3) / 1e9
-    stages = r.stage_times(args.steps, mode=1)
-    serial = r.stage_times(args.steps, mode=2)
+    stages, serial = stage_pair(r, args)
     kb = kernel_bytes(geom)
-    dom = max((k for k in ("hot", "cold") if serial[k][0]), key=lambda k: serial[k][0])
-    pipe, alone = stages[dom][0], serial[dom][0]
+    dom = max((k for k in ("hot", "cold") if serial[k][0]), key=lambda k: serial[k][0], default="hot")
+    pipe, alone = stages[dom][0] or math.nan, serial[dom][0] or math.nan
     row = {"config": key, "workload": CONFIGS[key], "layers": geom.layers, "batch": geom.batch,
            "queries": geom.queries, "tokens_per_step": geom.tokens, "ms_per_step": round(ms, 5),
            "ms_per_step_graph_per_step": round(ms_1g, 5), "steps_per_graph": r.m,
@@ -997,13 +1009,19 @@ def rocpd_summary(db: str, name_filter: str) -> str:
     c = sqlite3.connect(db)
     lines = []
     dur = collections.defaultdict(list)
-    for name, d, gx, gy, wgx, vg, ag, lds in c.execute(
-            "select name, duration, grid_x, grid_y, workgroup_x, vgpr_count, accum_vgpr_count, lds_size from kernels"):
+    try:  # grid_z separates launches that differ only in layers x dictionary groups
+        rows = c.execute("select name, duration, grid_x, grid_y, grid_z, workgroup_x, vgpr_count, accum_vgpr_count, "
+                         "lds_size from kernels").fetchall()
+    except sqlite3.Error:
+        rows = [(n, d, gx, gy, 1, w, v, a, l) for n, d, gx, gy, w, v, a, l in c.execute(
+            "select name, duration, grid_x, grid_y, workgroup_x, vgpr_count, accum_vgpr_count, lds_size from kernels")]
+    for name, d, gx, gy, gz, wgx, vg, ag, lds in rows:
         if name_filter in name:
-            dur[(name, gx, gy, wgx, vg, ag, lds)].append(d / 1e3)
+            dur[(name, gx, gy, gz, wgx, vg, ag, lds)].append(d / 1e3)
     lines.append("kernel | grid | wg | vgpr | agpr | lds | launches | avg_us | min_us | max_us")
     for k, v in sorted(dur.items(), key=lambda x: -sum(x[1])):
-        lines.append(f"{k[0][:60]} | {k[1]}x{k[2]} | {k[3]} | {k[4]} | {k[5]} | {k[6]} | {len(v)} | "
+        grid = f"{k[1]}x{k[2]}" + (f"x{k[3]}" if k[3] != 1 else "")
+        lines.append(f"{k[0][:60]} | {grid} | {k[4]} | {k[5]} | {k[6]} | {k[7]} | {len(v)} | "
                      f"{sum(v) / len(v):.2f} | {min(v):.2f} | {max(v):.2f}")
     try:
         rows = list(c.execute("select kernel_name, grid_size, dispatch_id, counter_name, value from counters_collection"))
@@ -1158,6 +1176,9 @@ def main():
     if not args.no_cpu:
         log(f"CPU port: {native_oracle()}")
     engine = WeaverEngine()
+    if args.trace_phase == "serial":
+        engine.set_profiling(2)  # every decode's kernels one at a time on the caller's stream
+        args.no_graph = True
     log(f"device: {engine.device_name()}")
     config_keys = [k for k in args.configs.split(",") if k]
     for k in config_keys:
@@ -1219,8 +1240,10 @@ def main():
     geom, r, row = head
     # Per-kernel durations over the same steps, launched from the host with
     # events around each kernel on its own stream (pipeline unchanged).
-    stages = r.stage_times(args.steps, mode=1)
-    serial = r.stage_times(args.steps, mode=2)
+    stages, serial = stage_pair(r, args)
+    if serial["cold"][0] is None:  # a kernel trace of one phase: nothing timed per kernel
+        serial = {k: (v or math.nan, n) for k, (v, n) in serial.items()}
+        stages = {k: (v or math.nan, n) for k, (v, n) in stages.items()}
     kb_per_launch = kernel_bytes(geom)
     # Dominant of the two bandwidth-bound kernels by its own (serialized) cost; its
     # duration in the pipeline of the timed steps (where the hot kernel runs
@@ -1255,7 +1278,7 @@ def main():
         if serial[k][0]:
             tf = fl / (serial[k][0] * 1e-3) / 1e12
             mfma[k] = {"gflop": round(fl / 1e9, 3), "tflops": round(tf, 1), "frac": round(tf / MFMA_F16_TFLOPS, 4)}
-    proj_paths = projection_table(engine, args.seed)
+    proj_paths = None if args.skip_projection else projection_table(engine, args.seed)
     copy_peak = hbm_copy_peak()
     read_peak = hbm_read_peak(engine)
     log(json.dumps({"hbm_read_peak": read_peak}))
