@@ -2,6 +2,7 @@
 // aw_engine, whose definition stays private to weaver_engine.hip.
 #pragma once
 
+#include <stddef.h>
 #include <stdint.h>
 
 #include "../../include/aether_weaver.h"
@@ -17,5 +18,9 @@ uint32_t compute_units(const aw_engine* e);
 uint32_t* error_word(const aw_engine* e); // device address of the error word
 // Records the message as the engine's last error and returns `code`.
 int fail(aw_engine* e, int code, const char* fmt, ...) __attribute__((format(printf, 3, 4)));
+
+// Lets the dense-ops kernels that stage more than 64 KiB of LDS use `max_lds`
+// bytes (ops.hip); false when the runtime refuses.
+bool ops_set_lds_limits(size_t max_lds);
 
 } // namespace aw_engine_internal

@@ -98,10 +98,20 @@ int launch_products(aw_engine* e, const char* what, const uint16_t* a, const Pro
             awo::GemmArgs t = g;
             t.g[0] = g.g[i];
             t.groups = 1;
-            const dim3 grid((uint32_t)cdiv64(t.g[0].N, awo::kTileN), (uint32_t)cdiv64(m, awo::kTileM));
+            // 256 x 128 tiles when they fill the CUs at least once (16-byte rows, each
+            // operand below 4 GiB - 64 KiB for the buffer loads), else 128 x 128.
+            const dim3 wgrid((uint32_t)cdiv64(t.g[0].N, awo::kWideN), (uint32_t)cdiv64(m, awo::kWideM));
+            const uint64_t lim = (1ull << 32) - 65536;
+            const bool wide = vec && (uint64_t)wgrid.x * wgrid.y >= ei::compute_units(e) &&
+                              (uint64_t)t.g[0].N * k * 2 < lim && (uint64_t)m * k * 2 < lim;
+            const dim3 grid = wide ? wgrid : dim3((uint32_t)cdiv64(t.g[0].N, awo::kTileN), (uint32_t)cdiv64(m, awo::kTileM));
             if (grid.y > 65535u) return ei::fail(e, AW_E_UNSUPPORTED, "%s: m = %u rows exceed the grid", what, m);
             if constexpr (EPI != awo::Epi::SiluGate) {
-                if (vec)
+                if (wide && k % awo::kWideK != 0)
+                    hipLaunchKernelGGL((awo::gemm_wide_kernel<true, F32, EPI>), grid, dim3(awo::kWideThreads), awo::kWideLdsBytes, st, t);
+                else if (wide)
+                    hipLaunchKernelGGL((awo::gemm_wide_kernel<false, F32, EPI>), grid, dim3(awo::kWideThreads), awo::kWideLdsBytes, st, t);
+                else if (vec)
                     hipLaunchKernelGGL((awo::gemm_tiled_kernel<true, F32, EPI>), grid, dim3(256), 0, st, t);
                 else
                     hipLaunchKernelGGL((awo::gemm_tiled_kernel<false, F32, EPI>), grid, dim3(256), 0, st, t);
@@ -141,6 +151,27 @@ int launch_products(aw_engine* e, const char* what, const uint16_t* a, const Pro
 }
 
 } // namespace
+
+namespace aw_engine_internal {
+
+bool ops_set_lds_limits(size_t max_lds) {
+    // <MASK, F32, EPI> of the products that take the wide tiles.
+    const void* fns[] = {(const void*)awo::gemm_wide_kernel<true, false, awo::Epi::Store>,
+                         (const void*)awo::gemm_wide_kernel<false, false, awo::Epi::Store>,
+                         (const void*)awo::gemm_wide_kernel<true, true, awo::Epi::Store>,
+                         (const void*)awo::gemm_wide_kernel<false, true, awo::Epi::Store>,
+                         (const void*)awo::gemm_wide_kernel<true, false, awo::Epi::Residual>,
+                         (const void*)awo::gemm_wide_kernel<false, false, awo::Epi::Residual>};
+    bool ok = true;
+    for (const void* f : fns)
+        if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)max_lds) != hipSuccess) {
+            ok = false;
+            (void)hipGetLastError();
+        }
+    return ok && max_lds >= awo::kWideLdsBytes;
+}
+
+} // namespace aw_engine_internal
 
 extern "C" {
 

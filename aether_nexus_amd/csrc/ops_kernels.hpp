@@ -485,4 +485,157 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(GemmArgs a) {
                              a.g[0].vec_out);
 }
 
+// Large products (many 256 x 128 tiles): 256 weight rows x 128 activation rows
+// per work-group of 8 waves, each 64 x 64 (4 x 4 MFMA tiles), two waves per
+// SIMD (one wave per SIMD does not issue its MFMAs back to back).  The operands
+// go from memory straight into LDS (buffer loads with the LDS flag), in LDS
+// stages of 64 k: each row of a stage is 128 contiguous bytes, so a wave's load
+// instruction (64 lanes x 16 bytes) covers 8 rows x 128 bytes.  Loads of 16
+// rows x 64 bytes, the shape of 32-k stages, move about 40 GB/s per CU (also
+// measured here); 128-byte runs move more.
+//   - Stages rotate through three LDS buffers: stage s + 2's loads are issued
+//     during stage s, into the buffer stage s - 1 used, and waited for (s_waitcnt
+//     vmcnt, each wave its own) at the end of stage s + 1, before the barrier
+//     that publishes them.
+//   - A stage's fragments are read at its start; the other wave of the SIMD
+//     covers their latency.
+// Staged rows are 128 bytes (eight 16-byte chunks) with chunk c of row r stored
+// at c ^ (r & 7): the 8 lanes that one 128-byte LDS cycle serves, rows r .. r + 7
+// at one chunk, hit 8 distinct 16-byte slots; a load instruction writes 64
+// consecutive slots, so each lane fetches the chunk its slot holds.  The 32-k
+// MFMA steps are summed in the same order as gemm_tiled_kernel, so both give the
+// same bits.
+constexpr int kWideN = 256, kWideM = 128, kWideBufs = 3, kWideThreads = 512, kWideK = 64;
+
+__device__ inline uint32_t wide_slot(uint32_t row, uint32_t chunk) { // halves
+    return row * 64u + ((chunk ^ (row & 7u)) << 3);
+}
+
+// gfx9 buffer resource word 3 (32-bit data format) of the wide kernel's operand loads.
+constexpr uint32_t kWideRsrcWord3 = 0x00020000u;
+// A buffer offset past any operand (at most 4 GiB - 64 KiB): the load returns zeros.
+constexpr uint32_t kWideOutOfRange = 0xFFFFFFF0u;
+
+// The wide kernel's work-group barrier: s_barrier alone, with compiler barriers
+// on both sides so no memory access moves across it.  No hardware wait: the
+// kernel writes LDS only through its loads, and waits for each wave's own with
+// s_waitcnt vmcnt (as many as it needs) before the barrier that publishes them;
+// a fence here would wait for every load in flight (vmcnt(0)), also those
+// issued for later stages.  LDS reads complete in order, before their registers
+// are used, before the barrier after which another load may overwrite them.
+__device__ inline void lds_barrier() {
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");
+}
+
+// MASK: K % 64 != 0, so the last stage's chunks past K load zeros.  Operands:
+// 16-byte aligned rows with K % 8 == 0, each below 4 GiB - 64 KiB (buffer loads
+// with 32-bit offsets, range-checked).
+template <bool MASK, bool F32, Epi EPI>
+__global__ __launch_bounds__(kWideThreads) __attribute__((amdgpu_waves_per_eu(2))) void gemm_wide_kernel(GemmArgs a) {
+    static_assert(EPI != Epi::SiluGate, "one weight matrix");
+    constexpr uint32_t SB = kWideN * kWideK, SA = kWideM * kWideK; // halves per buffer: weights, activations
+    constexpr int LPT = (kWideN + kWideM) * (kWideK / 8) / kWideThreads; // loads per thread and stage: 4 + 2
+    extern __shared__ __attribute__((aligned(16))) _Float16 wide_lds[]; // [kWideBufs][SB + SA]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, li = lane & 15, lg = lane >> 4;
+    const int wn = wave & 3, wm = wave >> 2; // 4 x 64 weight rows, 2 x 64 activation rows
+    const uint32_t n0 = blockIdx.x * kWideN, m0 = blockIdx.y * kWideM;
+    const uint32_t N = a.g[0].N, K = a.K;
+    const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc((void*)a.g[0].B, (short)0,
+                                                                        (int)(uint32_t)((uint64_t)N * K * 2u),
+                                                                        (int)kWideRsrcWord3);
+    const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc((void*)a.A, (short)0,
+                                                                        (int)(uint32_t)((uint64_t)a.M * K * 2u),
+                                                                        (int)kWideRsrcWord3);
+    // Load instruction j (0-3 weights, 4-5 activations) of this thread fills LDS
+    // slot q = tid + 512 * (j % 4) of its region: row q >> 3, chunk (q & 7) ^
+    // (row & 7).  off: that chunk's byte offset at k = 0 (rows clamped).
+    uint32_t off[LPT];
+    bool cin[LPT]; // MASK: the chunk holds k < K in the last stage
+#pragma unroll
+    for (int j = 0; j < LPT; ++j) {
+        const uint32_t q = (uint32_t)tid + (uint32_t)kWideThreads * (uint32_t)(j < 4 ? j : j - 4);
+        const uint32_t row = q >> 3, chunk = (q & 7u) ^ (row & 7u);
+        const uint32_t r = j < 4 ? min(n0 + row, N - 1u) : min(m0 + row, a.M - 1u);
+        off[j] = (r * K + 8u * chunk) * 2u;
+        cin[j] = true;
+        if constexpr (MASK) cin[j] = 8u * chunk < K % (uint32_t)kWideK;
+    }
+    const uint32_t n_stages = (K + kWideK - 1u) / kWideK;
+    const uint32_t last = n_stages - 1u;
+    // Stage `st`'s operands into LDS buffer `buf` (LPT loads per thread, always:
+    // the waits below count them).
+    auto issue = [&](uint32_t st, uint32_t buf) {
+        _Float16* base = wide_lds + buf * (SB + SA);
+#pragma unroll
+        for (int j = 0; j < LPT; ++j) {
+            const uint32_t slot0 = (uint32_t)wave * 64u + (uint32_t)kWideThreads * (uint32_t)(j < 4 ? j : j - 4);
+            _Float16* dst = base + (j < 4 ? 0u : SB) + slot0 * 8u; // wave-uniform
+            uint32_t v = off[j] + st * (uint32_t)(kWideK * 2);
+            if constexpr (MASK) v = (st < last || cin[j]) ? v : kWideOutOfRange;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(j < 4 ? rB : rA, (__attribute__((address_space(3))) void*)dst,
+                                                     16, (int)v, 0, 0, 0);
+        }
+    };
+    float4_t acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = (float4_t)0.0f;
+    // One stage's products: two 32-k MFMA steps, each over the 4 activation and
+    // 4 weight fragments of chunks 4 * ks + lg.
+    auto products = [&](uint32_t buf) {
+        const _Float16* sb = wide_lds + buf * (SB + SA);
+#pragma unroll
+        for (int ks = 0; ks < kWideK / 32; ++ks) {
+            half8_t ao[4], bo[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                ao[j] = *(const half8_t*)(sb + SB + wide_slot(wm * 64 + j * 16 + li, 4 * ks + lg));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) bo[i] = *(const half8_t*)(sb + wide_slot(wn * 64 + i * 16 + li, 4 * ks + lg));
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = mfma(bo[i], ao[j], acc[i][j]);
+        }
+    };
+    // Loads allowed still in flight at a stage's end: the next stage's LPT.
+    // s_waitcnt immediate (gfx9): vmcnt in bits 3:0 and 15:14, no expcnt (6:4) or
+    // lgkmcnt (11:8) wait.
+    constexpr uint32_t kInFlight = (uint32_t)LPT;
+    constexpr short kWaitLoads = (short)((kInFlight & 15u) | ((kInFlight >> 4) << 14) | 0x0F70u);
+    if (K > 0) {
+        issue(0, 0);
+        issue(min(1u, last), 1);
+        __builtin_amdgcn_s_waitcnt(kWaitLoads); // stage 0 is in LDS
+        lds_barrier();
+        // Stage s (buffer s % 3): stage s + 2's loads into buffer (s + 2) % 3, the
+        // one stage s - 1 read before the previous barrier; the products; this
+        // wave's stage s + 1 loads waited for; the barrier.  Loads past the last
+        // stage re-read it (unconditional, so the wait counts stay exact; nothing
+        // reads them).
+        uint32_t b = 0;
+        for (uint32_t s = 0; s < n_stages; ++s) {
+            issue(min(s + 2u, last), b == 0u ? 2u : b - 1u);
+            products(b);
+            __builtin_amdgcn_s_waitcnt(kWaitLoads);
+            lds_barrier();
+            b = b == 2u ? 0u : b + 1u;
+        }
+        __builtin_amdgcn_s_waitcnt(0); // no load still writing LDS when the wave ends
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            store4<EPI, F32>(a.g[0].C, a.M, N, m0 + (uint32_t)(wm * 64 + j * 16 + li),
+                             n0 + (uint32_t)(wn * 64 + i * 16 + 4 * lg), acc[i][j], acc[i][j], a.scale,
+                             a.g[0].vec_out);
+}
+
+// Dynamic LDS of gemm_wide_kernel.
+constexpr size_t kWideLdsBytes = (size_t)kWideBufs * (kWideN + kWideM) * kWideK * 2;
+
 } // namespace awo

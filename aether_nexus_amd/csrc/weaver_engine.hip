@@ -1080,6 +1080,7 @@ int aw_engine_create(int device, aw_engine** out) {
                               (const void*)aw::project_valu_kernel<128, kProjValuTa, kProjValuRb>,
                               (const void*)aw::project_valu_kernel<64, kProjValuTa, kProjValuRb>};
         for (const void* f : proj) set_lds(f);
+        if (!aw_engine_internal::ops_set_lds_limits(e->max_lds)) attr_ok = false;
     }
     if (!attr_ok) {
         aw_engine_destroy(e);

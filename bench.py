@@ -73,6 +73,8 @@ def parse():
     p.add_argument("--skip-ops", action="store_true", help="skip the dense-ops measurement (products, decode forward)")
     p.add_argument("--skip-projection", action="store_true", help="skip the projection-path table (MFMA vs VALU)")
     p.add_argument("--only-ops", action="store_true", help="time only the dense ops and print them")
+    p.add_argument("--only-products", action="store_true",
+                   help="time only the dense products (no decode forwards: short enough for counter runs)")
     p.add_argument("--configs", default="2,4,5",
                    help="BASELINE configurations timed beside the sweep (comma list of 2, 4, 5; empty for none)")
     p.add_argument("--only-configs", action="store_true",
@@ -731,7 +733,7 @@ def _graph_time(fn, st, reps):
     return ms
 
 
-def ops_bench(engine, seed, read_peak_gbps, reps=10):
+def ops_bench(engine, seed, read_peak_gbps, reps=10, forwards=True):
     """The dense ops (ops.metal:16-635) on MI355X at Llama-3.1-8B shapes.
 
     * Each product of a layer, one launch at a time: decode (M = 1) and verify
@@ -802,6 +804,8 @@ def ops_bench(engine, seed, read_peak_gbps, reps=10):
         torch.cuda.empty_cache()
     res = {"workload": "Llama-3.1-8B shapes: hidden 4096, 32q/8kv heads x 128, MLP 14336, vocab 128256",
            "products": products}
+    if not forwards:
+        return res
 
     # One decode forward of 32 layers.
     L, hq, hkv, hd, S = c["layers"], c["q_heads"], c["kv_heads"], c["head_dim"], c["max_seq"]
@@ -1214,9 +1218,9 @@ def main():
         engine.close()
         print(json.dumps({"inference_attention": out}), flush=True)
         return 0
-    if args.only_ops:
+    if args.only_ops or args.only_products:
         rp = hbm_read_peak(engine)
-        out = ops_bench(engine, args.seed, rp["gbps"])
+        out = ops_bench(engine, args.seed, rp["gbps"], forwards=not args.only_products)
         engine.close()
         print(json.dumps({"hbm_read_peak": rp, "dense_ops": out}), flush=True)
         return 0

@@ -185,8 +185,11 @@ def test_rope(ops, tokens, hq, hkv, hd, start):
 
 # M <= 16, 32, 64 take the skinny kernel with 1, 2, 4 row tiles (16 waves up to 4 weight tiles per CU, 8
 # beyond: N = 20000 and 49155), larger M the tiled one; K % 8 != 0 the element-wise loads.
+# 256 x 128 tiles where they fill the CUs: 1000 x 8200 x 520 (ragged M, N and a partial
+# last k-step); 300 x 33000 x 517 (K % 8 != 0) stays on the 128 x 128 tiles.
 SHAPES = [(1, 1, 1), (1, 5, 7), (1, 1000, 4096), (3, 33, 64), (16, 1024, 4096), (17, 100, 200), (20, 20000, 64),
-          (64, 256, 520), (65, 130, 96), (200, 300, 520), (256, 1024, 4096), (130, 77, 13)]
+          (64, 256, 520), (65, 130, 96), (200, 300, 520), (256, 1024, 4096), (130, 77, 13), (1000, 8200, 520),
+          (300, 33000, 517)]
 
 
 def check_product(got, a, b, k, what, scale=1.0, f16_out=True):
@@ -301,6 +304,35 @@ def test_fused_products_match_the_separate_calls(ops, m):
     ops.matmul_qkv(a, bq, bk, bv, *fused, m, n, nkv, k)
     for s_, f_ in zip(sep, fused):
         assert torch.equal(s_.view(torch.int16), f_.view(torch.int16)), "qkv"
+
+
+@pytest.mark.parametrize("k", [520, 517])
+def test_wide_and_tiled_products_same_bits(ops, k):
+    """Products with many 256 x 128 tiles take gemm_wide_kernel (K % 8 == 0),
+    smaller ones the 128 x 128 tiles; both sum the same k-steps of 32 in the same
+    order, so the columns a small product shares with a large one have the same
+    bits, for the f16 store, the residual form and the scaled fp32 store (K = 520:
+    a partial last k-step; K = 517: both on the 128 x 128 tiles)."""
+    import torch
+    rng = np.random.default_rng(k)
+    m, n, ns = 1000, 8200, 96  # 33 x 8 = 264 wide tiles; 96 columns: 8 tiles of 128 x 128
+    a = dev(f16(rng, m, k))
+    b = f16(rng, n, k, scale=0.05)
+    bb, bs = dev(b), dev(b[:ns])
+    big, small = torch.zeros((m, n), dtype=torch.float16, device="cuda:0"), torch.zeros((m, ns), dtype=torch.float16, device="cuda:0")
+    ops.matmul(a, bb, big, m, n, k)
+    ops.matmul(a, bs, small, m, ns, k)
+    assert torch.equal(big[:, :ns].contiguous().view(torch.int16), small.view(torch.int16)), "store"
+    x0 = f16(rng, m, n)
+    xb, xs = dev(x0), dev(np.ascontiguousarray(x0[:, :ns]))
+    ops.matmul_add_residual(a, bb, xb, m, n, k, 0.5)
+    ops.matmul_add_residual(a, bs, xs, m, ns, k, 0.5)
+    assert torch.equal(xb[:, :ns].contiguous().view(torch.int16), xs.view(torch.int16)), "residual"
+    fb = torch.zeros((m, n), dtype=torch.float32, device="cuda:0")
+    fs = torch.zeros((m, ns), dtype=torch.float32, device="cuda:0")
+    ops.matmul_scaled(a, bb, fb, m, n, k, 0.25)
+    ops.matmul_scaled(a, bs, fs, m, ns, k, 0.25)
+    assert torch.equal(fb[:, :ns].contiguous().view(torch.int32), fs.view(torch.int32)), "scaled"
 
 
 def test_product_bits_do_not_depend_on_the_wave_count(ops):
