@@ -45,6 +45,7 @@ SIGNATURES = {
     "aw_debug_gather_codes": (_c_int, [_vp, _vp, _sz, _vp, _u32, _u32, _vp, _vp, _vp, _vp]),
     "aw_engine_set_profiling": (_c_int, [_vp, _c_int]),
     "aw_engine_set_projection": (_c_int, [_vp, _c_int]),
+    "aw_engine_set_cold_output": (_c_int, [_vp, _c_int]),
     "aw_engine_stage_stats": (_c_int, [_vp, _c_int, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_u64)]),
     "aw_engine_reset_stage_stats": (_c_int, [_vp]),
     "aw_abi_encode_desc_size": (_sz, []),

@@ -107,6 +107,9 @@ struct Layout {
     uint32_t atoms_per_range = 0;
     uint32_t tiles_per_group = 0, rows_per_group = 0, n_groups = 0;
     bool qf32 = false;     // q_latent computed on the device, kept in fp32
+    bool cold_out = false; // the cold kernel writes value partials for the merge (no bins, no finish)
+    size_t cold_smem = 0, w_lds_off = 0; // the cold kernel's LDS bytes; with cold_out, where its W staging starts
+    uint32_t part_splits = 0; // partials per row in the hot arrays: hot splits (+ cold splits when cold_out)
     size_t off_ql = 0, off_dt = 0, off_hm = 0, off_hl = 0, off_ho = 0;
     size_t off_cm = 0, off_cl = 0, off_ca = 0, off_cw = 0, off_ocp = 0;
 };
@@ -118,6 +121,10 @@ bool supported_head_dim(uint32_t d) { return d == 64 || d == 128; }
 constexpr uint32_t kSepMergeRows = 16;
 // Cold splits per row before the row chunk is halved instead.
 constexpr uint64_t kColdSplitsBeforeRc = 8;
+// Largest dictionary head (bytes of f16) for which the cold kernel writes value
+// partials (AW_COLD_OUT_VALUES): every work item reads its head's dictionary from
+// L2 once, in place of the bins' round trip through HBM and the finish kernel.
+constexpr uint64_t kColdOutMaxDictBytes = 128u << 10;
 
 // q . D^T on the vector ALUs (project_valu_kernel: kProjValuTa atoms x
 // kProjValuRb rows per work-group) for groups of at most kProjValuRows rows
@@ -137,6 +144,13 @@ constexpr uint32_t kProjValuRows = 0;
 uint32_t dt_pitch(uint32_t A) { return A + 64; }
 uint32_t w_pitch(uint32_t A) { return A + 32; }
 
+// Buffer loads cover the codes when a layer's pool fits the resource window and
+// the largest in-block token offset added to the "no code" offset stays below 2^32.
+bool cold_uses_buffer(const aw_decode_desc* d) {
+    const uint64_t blk_bytes = (uint64_t)kBlock * d->kv_heads * 16u;
+    return d->kv_heads <= 256 && d->cold_blocks * blk_bytes <= aw::kColdWindow;
+}
+
 // Largest cold row chunk (1, 2 or 4) whose LDS tables fit (with at least one
 // 1024-token split's block refs), for a q_latent table of qbytes per entry.
 uint32_t pick_rc(uint32_t R, uint32_t A, size_t max_lds, uint32_t qbytes) {
@@ -146,8 +160,9 @@ uint32_t pick_rc(uint32_t R, uint32_t A, size_t max_lds, uint32_t qbytes) {
 }
 
 // hot_waves_per_cu[rt]: resident hot waves per CU for RT = 1, 2, 4 row tiles (0, 1, 2).
-int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, const uint32_t hot_waves_per_cu[3], Layout* L,
-         char* msg, size_t mlen) {
+// cold_out_mode: AW_COLD_OUT_* (the engine's setting; AUTO for aw_decode_plan).
+int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, const uint32_t hot_waves_per_cu[3], int cold_out_mode,
+         Layout* L, char* msg, size_t mlen) {
     if (!d) {
         put_msg(msg, mlen, "null descriptor");
         return AW_E_INVALID_ARG;
@@ -314,7 +329,22 @@ int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, const uint32_t 
         // kernel, ends after it (32-layer verify, R = 32: 4.97 against 4.70 ms), so
         // the finish does not merge and wait for it; a merge kernel follows.
         o.sep_merge = o.n_ar > 1 || (R >= kSepMergeRows && o.info.hot_splits > 0);
+        // Value partials from the cold kernel: small dictionary heads, and room for
+        // the cold splits beside the hot ones in the merge's partials.
+        o.cold_out = cold_out_mode != AW_COLD_OUT_BINS && (uint64_t)A * HD * 2 <= kColdOutMaxDictBytes && A % 32 == 0 &&
+                     (uint64_t)o.info.hot_splits + o.info.cold_splits <= (uint64_t)aw::kMaxSplits &&
+                     cold_uses_buffer(d);
+        o.info.cold_output = o.cold_out ? AW_COLD_OUT_VALUES : AW_COLD_OUT_BINS;
+        o.cold_smem = aw::cold_smem_bytes(A, (int)o.rc, o.info.cold_tokens_per_split, qbytes);
+        if (o.cold_out) { // the bins' f16 hi + lo terms staged after the tables (A * rc * 4 bytes)
+            o.w_lds_off = align_up(o.cold_smem, 16);
+            o.cold_smem = o.w_lds_off + (size_t)A * o.rc * 4;
+            if (o.cold_smem > max_lds) o.cold_out = false;
+            o.info.cold_output = o.cold_out ? AW_COLD_OUT_VALUES : AW_COLD_OUT_BINS;
+            if (!o.cold_out) o.cold_smem = aw::cold_smem_bytes(A, (int)o.rc, o.info.cold_tokens_per_split, qbytes);
+        }
     }
+    o.part_splits = o.info.hot_splits + (o.cold_out ? o.info.cold_splits : 0u);
 
     // Workspace layout.
     size_t off = 0;
@@ -325,13 +355,13 @@ int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, const uint32_t 
     };
     if (o.info.computes_q_latent) o.off_ql = take((uint64_t)d->layers * d->batch * d->queries * d->q_heads * A * qbytes);
     if (d->cold_count > 0) o.off_dt = take((uint64_t)d->layers * d->dict_heads * dt_pitch(A) * HD * 2);
-    if (o.info.hot_splits) {
-        const uint64_t n = n_lbg * o.info.hot_splits * R;
+    if (o.part_splits) {
+        const uint64_t n = n_lbg * o.part_splits * R;
         o.off_hm = take(n * 4);
         o.off_hl = take(n * 4);
         o.off_ho = take(n * HD * 4);
     }
-    if (o.info.cold_splits) {
+    if (o.info.cold_splits && !o.cold_out) {
         const uint64_t n = n_lbg * o.info.cold_splits * R;
         o.off_cm = take(n * 4);
         o.off_cl = take(n * 4);
@@ -404,6 +434,7 @@ struct aw_engine {
     uint32_t* err = nullptr;                  // device error word
     int profiling = 0; // AW_PROFILE_*
     int projection = AW_PROJECT_AUTO;
+    int cold_output = AW_COLD_OUT_AUTO;
     struct Pending {
         int stage;
         hipEvent_t a, b;
@@ -489,7 +520,7 @@ int launch_project(aw_engine* e, const aw_decode_desc* d, const Layout& o, char*
     a.qlf = o.qf32 ? (float*)(ws + o.off_ql) : nullptr;
     a.dt = (uint16_t*)(ws + o.off_dt);
     a.dt_pitch = dt_pitch(d->dict_size);
-    a.dt_tiled = o.fin_rows ? 1u : 0u;
+    a.dt_tiled = o.fin_rows || o.cold_out ? 1u : 0u; // the row-tile finish's and the value partials' A operand
     a.batch = d->batch;
     a.queries = d->queries;
     a.q_heads = d->q_heads;
@@ -554,6 +585,7 @@ int launch_hot(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* ws,
     a.hot_count = d->hot_count;
     a.refs_stride = d->refs_stride;
     a.splits = o.info.hot_splits;
+    a.part_splits = o.part_splits;
     a.tokens_per_split = o.info.hot_tokens_per_split;
     a.refs_cap = (uint32_t)align_up(cdiv(a.tokens_per_split, kBlock), 4);
     // The engine's identity table (contiguous caches, one sequence): the kernel
@@ -592,26 +624,21 @@ constexpr int kColdCPT = 2;
 constexpr int kColdPD = 4;
 
 // cold_kernel instance for a row chunk of 1, 2 or 4, a power-of-two dictionary
-// or not, an f16 or fp32 q_latent table, and buffer loads (a layer's pool within
-// aw::kColdWindow bytes) or 64-bit addresses.
-const void* cold_kernel_fn(uint32_t rc, bool pow2, bool qf32, bool buf) {
-#define AW_COLD_B(RCV, P2)                                                                    \
-    { {(const void*)aw::cold_kernel<RCV, kColdCPT, kColdPD, P2, false, false>,              \
-       (const void*)aw::cold_kernel<RCV, kColdCPT, kColdPD, P2, false, true>},              \
-      {(const void*)aw::cold_kernel<RCV, kColdCPT, kColdPD, P2, true, false>,               \
-       (const void*)aw::cold_kernel<RCV, kColdCPT, kColdPD, P2, true, true>} }
-#define AW_COLD(RCV) {AW_COLD_B(RCV, false), AW_COLD_B(RCV, true)}
-    static const void* const table[3][2][2][2] = {AW_COLD(1), AW_COLD(2), AW_COLD(4)};
+// or not, an f16 or fp32 q_latent table, buffer loads (a layer's pool within
+// aw::kColdWindow bytes) or 64-bit addresses, and bins or value partials out
+// (value partials with buffer loads only).
+const void* cold_kernel_fn(uint32_t rc, bool pow2, bool qf32, bool buf, bool out) {
+#define AW_COLD_B(RCV, P2, OUT)                                                                  \
+    { {(const void*)aw::cold_kernel<RCV, kColdCPT, kColdPD, P2, false, false, false>,          \
+       (const void*)aw::cold_kernel<RCV, kColdCPT, kColdPD, P2, false, true, OUT>},            \
+      {(const void*)aw::cold_kernel<RCV, kColdCPT, kColdPD, P2, true, false, false>,           \
+       (const void*)aw::cold_kernel<RCV, kColdCPT, kColdPD, P2, true, true, OUT>} }
+#define AW_COLD(RCV) {{AW_COLD_B(RCV, false, false), AW_COLD_B(RCV, true, false)}, \
+                      {AW_COLD_B(RCV, false, true), AW_COLD_B(RCV, true, true)}}
+    static const void* const table[3][2][2][2][2] = {AW_COLD(1), AW_COLD(2), AW_COLD(4)};
 #undef AW_COLD
 #undef AW_COLD_B
-    return table[rc == 4 ? 2 : (rc == 2 ? 1 : 0)][pow2 ? 1 : 0][qf32 ? 1 : 0][buf ? 1 : 0];
-}
-
-// Buffer loads cover the codes when a layer's pool fits the resource window and
-// the largest in-block token offset added to the "no code" offset stays below 2^32.
-bool cold_uses_buffer(const aw_decode_desc* d) {
-    const uint64_t blk_bytes = (uint64_t)kBlock * d->kv_heads * 16u;
-    return d->kv_heads <= 256 && d->cold_blocks * blk_bytes <= aw::kColdWindow;
+    return table[rc == 4 ? 2 : (rc == 2 ? 1 : 0)][out ? 1 : 0][pow2 ? 1 : 0][qf32 ? 1 : 0][buf ? 1 : 0];
 }
 
 int launch_cold(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* ws, hipStream_t st) {
@@ -665,13 +692,23 @@ int launch_cold(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* ws
     a.s_q = (uint64_t)d->q_heads * A;
     a.s_j = A;
     a.s_a = 1;
-    (void)HD;
+    if (o.cold_out) {
+        a.dt = (const uint16_t*)(ws + o.off_dt);
+        a.dict_heads = d->dict_heads;
+        a.head_dim = HD;
+        a.out_splits = o.part_splits;
+        a.out_split0 = o.info.hot_splits;
+        a.w_lds_off = (uint32_t)o.w_lds_off;
+        a.out_m = (float*)(ws + o.off_hm);
+        a.out_l = (float*)(ws + o.off_hl);
+        a.out_o = (float*)(ws + o.off_ho);
+    }
     const uint64_t n_wg = (uint64_t)cdiv(a.n_units, 8) * 8 * (a.chunk_xcd ? o.n_chunks : d->kv_heads);
     if (n_wg > 0x7FFFFFFFull) return fail(e, AW_E_UNSUPPORTED, "cold grid too large");
     a.n_wg = (uint32_t)n_wg;
-    const size_t smem = aw::cold_smem_bytes(A, (int)o.rc, a.tokens_per_split, o.qf32 ? 4u : 2u);
+    const size_t smem = o.cold_smem;
     const bool pow2 = (A & (A - 1u)) == 0u;
-    const void* fn = cold_kernel_fn(o.rc, pow2, o.qf32, cold_uses_buffer(d));
+    const void* fn = cold_kernel_fn(o.rc, pow2, o.qf32, cold_uses_buffer(d), o.cold_out);
     // One resident round of work-groups (a multiple of 8: each keeps its XCD).
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, aw::kColdThreads, smem) != hipSuccess || per_cu < 1)
@@ -746,12 +783,12 @@ int launch_finish(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* 
 template <int HD>
 int launch_merge(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* ws, hipStream_t st) {
     aw::MergeArgs a{};
-    const bool cold = o.info.cold_splits > 0;
+    const bool cold = o.info.cold_splits > 0 && !o.cold_out; // value partials come in as splits of the hot arrays
     a.cold_m = cold ? (const float*)(ws + o.off_cm) : nullptr;
     a.cold_l = cold ? (const float*)(ws + o.off_cl) : nullptr;
     a.cold_amax = cold ? (const float*)(ws + o.off_ca) : nullptr;
     a.ocp = cold ? (const float*)(ws + o.off_ocp) : nullptr;
-    if (o.info.hot_splits) {
+    if (o.part_splits) {
         a.hot_m = (const float*)(ws + o.off_hm);
         a.hot_l = (const float*)(ws + o.off_hl);
         a.hot_o = (const float*)(ws + o.off_ho);
@@ -763,9 +800,9 @@ int launch_merge(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* w
     a.kv_heads = d->kv_heads;
     a.gqa = d->q_heads / d->kv_heads;
     a.rows_r = o.info.rows_per_kv_head;
-    a.cold_splits = o.info.cold_splits;
-    a.hot_splits = o.info.hot_splits;
-    a.n_ar = o.n_ar;
+    a.cold_splits = cold ? o.info.cold_splits : 0u;
+    a.hot_splits = o.part_splits;
+    a.n_ar = cold ? o.n_ar : 0u;
     a.total_rows = (uint64_t)d->layers * d->batch * d->kv_heads * a.rows_r;
     const uint64_t gx = cdiv(a.total_rows, 4);
     if (gx > 0x7FFFFFFFull) return fail(e, AW_E_UNSUPPORTED, "merge grid too large");
@@ -785,7 +822,8 @@ int launch_merge(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* w
     return AW_OK;
 }
 
-// Stage order on `st`: [q.D^T] -> cold -> finish [-> merge].  The hot kernel
+// Stage order on `st`: [q.D^T] -> cold -> finish [-> merge], or [q.D^T] ->
+// cold -> merge when the cold kernel writes value partials.  The hot kernel
 // (HBM-bound) runs on the engine's side stream, forked after q.D^T, so it starts
 // together with the cold kernel (bound by L2 requests: one per 16-byte code, one
 // resident work-group per CU) and fills the resources the cold work-groups leave
@@ -814,6 +852,10 @@ int run_pipeline(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* w
         if ((rc = launch_hot<HD>(e, d, o, ws, e->side))) return rc;
         AW_HIP(e, hipEventRecord(e->ev_join, e->side));
     }
+    if (o.cold_out) { // value partials: the merge reads the hot and cold splits alike
+        if (fork) AW_HIP(e, hipStreamWaitEvent(st, e->ev_join, 0));
+        return launch_merge<HD>(e, d, o, ws, st);
+    }
     const bool merge = o.sep_merge; // otherwise the finish merges
     if (fork && !merge) AW_HIP(e, hipStreamWaitEvent(st, e->ev_join, 0));
     if ((rc = launch_finish<HD>(e, d, o, ws, st))) return rc;
@@ -829,7 +871,7 @@ int run_pipeline(aw_engine* e, const aw_decode_desc* d, const Layout& o, char* w
 int decode_device(aw_engine* e, const aw_decode_desc* d, hipStream_t st, bool no_alloc = false) {
     Layout o;
     char msg[256] = {0};
-    int rc = plan(d, e->max_lds, e->n_cu, e->hot_wpc, &o, msg, sizeof msg);
+    int rc = plan(d, e->max_lds, e->n_cu, e->hot_wpc, e->cold_output, &o, msg, sizeof msg);
     if (rc) return fail(e, rc, "%s", msg);
     if (!d->out || !d->q) return fail(e, AW_E_INVALID_ARG, "q and out are required");
     if (d->hot_count && (!d->hot_k || !d->refs)) return fail(e, AW_E_INVALID_ARG, "hot_k and refs are required");
@@ -1007,7 +1049,7 @@ int aw_decode_plan(const aw_decode_desc* desc, aw_decode_plan_info* info, char* 
     Layout o;
     // Host-side planning assumes the MI355X limits: 160 KiB LDS per work-group, 256 CUs.
     const uint32_t wpc[3] = {12, 4, 4}; // gfx950 residency of the hot kernel variants
-    int rc = plan(desc, 160 * 1024, 256, wpc, &o, msg, mlen);
+    int rc = plan(desc, 160 * 1024, 256, wpc, AW_COLD_OUT_AUTO, &o, msg, mlen);
     if (rc == AW_OK && info) *info = o.info;
     return rc;
 }
@@ -1035,7 +1077,7 @@ int aw_engine_create(int device, aw_engine** out) {
     e->n_cu = (uint32_t)prop.multiProcessorCount;
     int rc = AW_OK;
     if (!rc) rc = check_kernel(e, aw::hot_kernel<128, 1, false>, "hot_kernel");
-    if (!rc) rc = check_kernel(e, aw::cold_kernel<4, kColdCPT, kColdPD, true, false, true>, "cold_kernel");
+    if (!rc) rc = check_kernel(e, aw::cold_kernel<4, kColdCPT, kColdPD, true, false, true, false>, "cold_kernel");
     if (!rc) rc = check_kernel(e, aw::finish_kernel<128, true>, "finish_kernel");
     if (rc) {
         delete e;
@@ -1067,7 +1109,7 @@ int aw_engine_create(int device, aw_engine** out) {
             for (bool p2 : {false, true})
                 for (bool qf : {false, true})
                     for (bool bf : {false, true})
-                        set_lds(cold_kernel_fn(rcv, p2, qf, bf));
+                        for (bool out : {false, true}) set_lds(cold_kernel_fn(rcv, p2, qf, bf, out));
         const void* fin[] = {(const void*)aw::finish_kernel<128, true>, (const void*)aw::finish_kernel<128, false>,
                              (const void*)aw::finish_kernel<64, true>, (const void*)aw::finish_kernel<64, false>};
         for (const void* f : fin) set_lds(f);
@@ -1497,7 +1539,7 @@ int aw_debug_project(aw_engine* e, const aw_decode_desc* d, void* q_latent, void
     if (!d || !q_latent) return fail(e, AW_E_INVALID_ARG, "desc and q_latent are required");
     Layout o;
     char msg[256] = {0};
-    int rc = plan(d, e->max_lds, e->n_cu, e->hot_wpc, &o, msg, sizeof msg);
+    int rc = plan(d, e->max_lds, e->n_cu, e->hot_wpc, e->cold_output, &o, msg, sizeof msg);
     if (rc) return fail(e, rc, "%s", msg);
     if (!o.info.computes_q_latent)
         return fail(e, AW_E_INVALID_ARG, "the request does not compute q_latent (it needs a cold pool and q_latent NULL)");
@@ -1557,6 +1599,13 @@ int aw_engine_set_projection(aw_engine* e, int mode) {
     if (!e) return AW_E_INVALID_ARG;
     if (mode < AW_PROJECT_AUTO || mode > AW_PROJECT_VALU) return fail(e, AW_E_INVALID_ARG, "projection mode %d", mode);
     e->projection = mode;
+    return AW_OK;
+}
+
+int aw_engine_set_cold_output(aw_engine* e, int mode) {
+    if (!e) return AW_E_INVALID_ARG;
+    if (mode < AW_COLD_OUT_AUTO || mode > AW_COLD_OUT_VALUES) return fail(e, AW_E_INVALID_ARG, "cold output mode %d", mode);
+    e->cold_output = mode;
     return AW_OK;
 }
 

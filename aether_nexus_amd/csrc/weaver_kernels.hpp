@@ -91,7 +91,6 @@ __device__ inline float wave_reduce(float v) {
 }
 __device__ inline float wave_max(float v) { return wave_reduce<true>(v); }
 __device__ inline float wave_sum(float v) { return wave_reduce<false>(v); }
-
 // Log-sum-exp combination of one row's splits, one wave, lane = split
 // (S <= 64; lanes past S pass l = 0).  Empty splits (l == 0) get factor 0.
 // Returns the row maximum M, the combined sum L, and this lane's factor
@@ -110,7 +109,7 @@ struct ProjArgs {
     const uint16_t* dict; // [L][dict_heads][A][HD]
     uint16_t* ql;         // [L][B][Q][Hq][A] f16, or null
     float* qlf;           // [L][B][Q][Hq][A] fp32, or null (both null: transpose only)
-    uint16_t* dt;         // [L][dict_heads][HD][dt_pitch] f16: D^T for the finish (or tiled, below)
+    uint16_t* dt;         // [L][dict_heads][HD][dt_pitch] f16: D^T for the finish (or tiled, below); null: none
     uint32_t dt_pitch;    // A + padding: rows of D^T do not alias one L2 channel
     uint32_t dt_tiled;    // D^T as [group][A/32][HD/16][64 lanes][8 atoms] (finish_rows_kernel's A operand)
     uint32_t batch, queries, q_heads, kv_heads, gqa, rows_r;
@@ -131,6 +130,7 @@ struct HotArgs {
     uint32_t* err;
     uint32_t batch, queries, q_heads, kv_heads, gqa, rows_r;
     uint32_t hot_count, refs_stride, splits, tokens_per_split, causal;
+    uint32_t part_splits; // S of the partial arrays: splits, plus the cold splits when they write values here
     uint32_t refs_cap;   // block refs the launch's LDS holds per split (>= tokens_per_split / 16)
     uint32_t refs_identity; // refs[i] == i for every sequence (a contiguous cache): refs are not read
     uint32_t n_tok_max;  // hot tokens of a sequence (hot_count * 16 unless the request gives fewer)
@@ -168,6 +168,17 @@ struct ColdArgs {
     uint64_t cold_blocks, cold_layer, refs_layer;
     // q_latent element (lb, g, q, j, a) = ql[lb*s_lb + g*s_g + q*s_q + j*s_j + a*s_a]
     uint64_t s_lb, s_g, s_q, s_j, s_a;
+    // Value partials instead of bins (OUT, dictionaries of at most 64 Ki elements
+    // per head, A % 32 == 0): each split's sum_a bin[a][r] * D[a] goes out with its
+    // m and l in the hot kernel's partial layout, as split out_split0 + s of
+    // out_splits, for the merge.  D^T comes from the projection in the row-tile
+    // finish's order ([L][dict_heads] groups of [A/32][head_dim/16][64 lanes][8
+    // atoms]); the bins' f16 hi + lo terms are staged in LDS at byte w_lds_off.
+    const uint16_t* dt;
+    uint32_t dict_heads, head_dim, out_splits, out_split0, w_lds_off;
+    float* out_m;
+    float* out_l;
+    float* out_o;
 };
 
 struct FinishArgs {
@@ -244,6 +255,7 @@ inline size_t project_smem_bytes(int HD, int TR, int TA) {
 template <int HD, int TA, int NTH>
 __device__ __forceinline__ void write_dt(const ProjArgs& a, const _Float16* sd, int P, uint32_t group, uint32_t atom0) {
     const uint32_t A = a.dict_size;
+    if (a.dt == nullptr) return; // no finish reads D^T (the cold kernel writes value partials)
     const uint32_t nrb = gridDim.y, y = blockIdx.y;
     const int d0 = (int)((y * (uint32_t)HD) / nrb), nd = (int)(((y + 1) * (uint32_t)HD) / nrb) - d0;
     const int TP = nd * (TA / 8);
@@ -659,7 +671,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu((RT == 1 && 
     }
     if (bad) flag_error(a.err, kErrHotRef);
 
-    const uint64_t pbase = ((uint64_t)lbg * a.splits + s) * R;
+    const uint64_t pbase = ((uint64_t)lbg * a.part_splits + s) * R;
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
         float lt = l_run[rt] + __shfl_xor(l_run[rt], 16);
@@ -785,8 +797,9 @@ constexpr float kBinLimit = 2013265920.0f;
 // Tokens are dealt to waves in wave tiles of 64*CPT consecutive tokens: wave w
 // takes tiles w, w + NW, w + 2*NW, ... (so the first NW tiles, the planning
 // sample, cover the split's first NT*CPT tokens).  The assignment is static, so
-// every float sum runs in the same order on every call.
-template <int RC, int CPT, int PD, bool POW2, bool QF32, bool BUF>
+// every float sum runs in the same order on every call.  OUT: value partials
+// (a.out_*) instead of bins.
+template <int RC, int CPT, int PD, bool POW2, bool QF32, bool BUF, bool OUT>
 __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
     using QT = std::conditional_t<QF32, float, _Float16>; // q_latent table element
     constexpr int NT = kColdThreads, NW = NT / 64, NP = (RC + 1) / 2;
@@ -833,13 +846,20 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
     const uint32_t t_end = min(t_begin + a.tokens_per_split, n_tok);
     const uint64_t pbase = (lbg * a.splits + s) * R;
 
+    // Value partials: split out_split0 + s of the merge's partial arrays.
+    const uint64_t obase = (lbg * a.out_splits + a.out_split0 + s) * R;
     if (t_begin >= t_end) {
         if (tid < RC) {
             const uint32_t r = c * RC + tid;
             if (r < R) {
-                a.part_m[pbase + r] = -INFINITY;
-                a.part_l[pbase + r] = 0.0f;
-                a.part_amax[pbase + r] = 0.0f;
+                if constexpr (OUT) {
+                    a.out_m[obase + r] = -INFINITY;
+                    a.out_l[obase + r] = 0.0f;
+                } else {
+                    a.part_m[pbase + r] = -INFINITY;
+                    a.part_l[pbase + r] = 0.0f;
+                    a.part_amax[pbase + r] = 0.0f;
+                }
             }
         }
         return;
@@ -1482,88 +1502,159 @@ __device__ __forceinline__ void cold_unit(const ColdArgs& a, uint32_t wg) {
     float inv[RC];
 #pragma unroll
     for (int rr = 0; rr < RC; ++rr) inv[rr] = pow2f(-F[rr]);
-    // 2^-F_rr for a row index known only at run time, by arithmetic: selects over
-    // the array would be folded into an indexed load from scratch memory.
-    auto inv_of = [&](int rr) -> float {
-        int f = 0;
+    if constexpr (OUT) {
+        // Value partials: O^T[d][r] = sum_a D^T[d][a] * W[a][r] on MFMA, so no bins
+        // leave the work-group and no finish runs.  W = bins * 2^-16 as f16 hi + lo
+        // (|bin| < 2^31, so both terms stay inside f16: ~22 significant bits, the
+        // finish's split), staged in LDS as [A/32 k-steps][4 lg][RC rows][8 atoms],
+        // hi then lo: the MFMA B operand of lane (row li, lg) is one 16-byte read.
+        // The A operand, D^T, is the projection's tiled copy: a wave's 16-byte loads
+        // cover 1 KiB.  Wave w takes dim block w (16 dims) over every atom; lanes
+        // with li >= RC carry zero rows.  Output: lane (li, lg) holds dims
+        // 16 w + 4 lg .. +3 of row li, scaled back by 2^(16 - F_li).
+        const uint32_t HD = a.head_dim, nkb = A / 32u, ndb = HD / 16u;
+        _Float16* wl = (_Float16*)(smem + a.w_lds_off);
+        const uint32_t wlo = nkb * 4u * RC * 8u; // halves of the hi plane
+        for (uint32_t i = tid; i < (A / 8u) * RC; i += NT) {
+            const uint32_t rr = i % RC, a8 = i / RC; // atoms 8 a8 .. +7 of row rr: k-step a8 / 4, lg a8 % 4
+            half8_t hi, lo;
 #pragma unroll
-        for (int k = 0; k < RC; ++k) f += F[k] * (int)(rr == k);
-        return pow2f(-f);
-    };
-    float amax[RC];
-#pragma unroll
-    for (int rr = 0; rr < RC; ++rr) amax[rr] = 0.0f;
-    // The bin of row rr at atom `at` as a float.
-    auto bin_value = [&](uint32_t at, int rr) -> float {
-        const uint64_t wv = *binp(at, rr / 2);
-        const int32_t v0 = (int32_t)(uint32_t)wv;
-        const int32_t v1 = (int32_t)((uint32_t)(wv >> 32) + (v0 < 0 ? 1u : 0u));
-        return (float)((rr & 1) ? v1 : v0) * inv_of(rr);
-    };
-    if (a.w_tiled) {
-        // Thread -> (group of 4 atoms, row): 16-byte pieces, the rows of one piece
-        // position adjacent in the tile (64-byte runs for 4 rows).
-        const uint32_t l_in = lb / a.batch, b_in = lb % a.batch;
-        const uint32_t grp = a.w_dict_heads == 1 ? l_in : l_in * a.kv_heads + g;
-        const uint32_t tiles = (a.w_rows_per_group + 15) / 16, nk = A / 32;
-        for (uint32_t i = tid; i < (A / 4) * RC; i += NT) {
-            const int rr = (int)(i % RC);
-            const uint32_t a4 = i / RC, r = c * RC + (uint32_t)rr;
-            float4_t v;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = bin_value(4 * a4 + e, rr);
-            amax[rr] = fmaxf(amax[rr], fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
-            if (r >= R) continue;
-            const uint32_t grow = a.w_dict_heads == 1 ? (b_in * a.kv_heads + g) * R + r : b_in * R + r;
-            const uint32_t at = 4 * a4, kk = at / 32, lgv = (at % 32) / 8, h = (at % 8) / 4;
-            const uint64_t off = ((((uint64_t)grp * tiles + grow / 16) * nk + kk) * 2 + h) * 64 + lgv * 16 + grow % 16;
-            *(float4_t*)(a.part_w + off * 4) = v;
+            for (int e = 0; e < 8; ++e) {
+                const uint64_t wv = *binp(a8 * 8u + (uint32_t)e, (int)(rr >> 1));
+                const int32_t v0 = (int32_t)(uint32_t)wv;
+                const int32_t v1 = (int32_t)((uint32_t)(wv >> 32) + (v0 < 0 ? 1u : 0u));
+                const float x = (float)((rr & 1u) ? v1 : v0) * 1.52587890625e-05f; // 2^-16
+                hi[e] = (_Float16)x;
+                lo[e] = (_Float16)(x - (float)hi[e]);
+            }
+            *(half8_t*)(wl + (a8 * RC + rr) * 8u) = hi;
+            *(half8_t*)(wl + wlo + (a8 * RC + rr) * 8u) = lo;
         }
-    } else
-    for (uint32_t at = tid; at < A; at += NT) {
+        __syncthreads(); // W staged
+        const uint32_t li = (uint32_t)lane & 15u, lg = (uint32_t)lane >> 4;
+        if ((uint32_t)wave < ndb) {
+            const uint32_t grp = a.dict_heads == 1 ? l : l * a.kv_heads + g;
+            const uint4_t* dtp = (const uint4_t*)(a.dt + (uint64_t)grp * HD * A) + (uint32_t)wave * 64u + (uint32_t)lane;
+            const bool rowl = li < (uint32_t)RC;
+            const _Float16* wrow = wl + (lg * RC + (rowl ? li : 0u)) * 8u;
+            float4_t acc = (float4_t)0.0f;
+            constexpr int KB = 8; // k-steps of D^T loads in flight
+            for (uint32_t k0 = 0; k0 < nkb; k0 += KB) {
+                uint4_t av[KB];
 #pragma unroll
-        for (int pp = 0; pp < NP; ++pp) {
-            const uint64_t wv = *binp(at, pp);
+                for (int j = 0; j < KB; ++j) av[j] = dtp[(uint64_t)min(k0 + (uint32_t)j, nkb - 1u) * ndb * 64u];
+#pragma unroll
+                for (int j = 0; j < KB; ++j) {
+                    if (k0 + (uint32_t)j >= nkb) break;
+                    const uint32_t ko = (k0 + (uint32_t)j) * 4u * RC * 8u;
+                    const half8_t bh = rowl ? *(const half8_t*)(wrow + ko) : (half8_t)(_Float16)0.0f;
+                    const half8_t bl = rowl ? *(const half8_t*)(wrow + wlo + ko) : (half8_t)(_Float16)0.0f;
+                    acc = mfma16x16x32(as_h8(av[j]), bh, acc);
+                    acc = mfma16x16x32(as_h8(av[j]), bl, acc);
+                }
+            }
+            const uint32_t r = c * RC + li;
+            if (rowl && r < R) {
+                int f = 0; // F of row li, by arithmetic (no register array indexed at run time)
+#pragma unroll
+                for (int k = 0; k < RC; ++k) f += F[k] * (int)(li == (uint32_t)k);
+                const float sc = pow2f(16 - f);
+                *(float4_t*)(a.out_o + (obase + r) * HD + 16u * (uint32_t)wave + 4u * lg) = acc * sc;
+            }
+        }
+#pragma unroll
+        for (int rr = 0; rr < RC; ++rr) // static indices: no register array indexed at run time
+            if (tid == rr) {
+                const uint32_t r = c * RC + rr;
+                if (r < R) {
+                    a.out_m[obase + r] = ref[rr];
+                    a.out_l[obase + r] = lpart[rr] * inv[rr];
+                }
+            }
+    } else {
+        // 2^-F_rr for a row index known only at run time, by arithmetic: selects over
+        // the array would be folded into an indexed load from scratch memory.
+        auto inv_of = [&](int rr) -> float {
+            int f = 0;
+#pragma unroll
+            for (int k = 0; k < RC; ++k) f += F[k] * (int)(rr == k);
+            return pow2f(-f);
+        };
+        float amax[RC];
+#pragma unroll
+        for (int rr = 0; rr < RC; ++rr) amax[rr] = 0.0f;
+        // The bin of row rr at atom `at` as a float.
+        auto bin_value = [&](uint32_t at, int rr) -> float {
+            const uint64_t wv = *binp(at, rr / 2);
             const int32_t v0 = (int32_t)(uint32_t)wv;
             const int32_t v1 = (int32_t)((uint32_t)(wv >> 32) + (v0 < 0 ? 1u : 0u));
+            return (float)((rr & 1) ? v1 : v0) * inv_of(rr);
+        };
+        if (a.w_tiled) {
+            // Thread -> (group of 4 atoms, row): 16-byte pieces, the rows of one piece
+            // position adjacent in the tile (64-byte runs for 4 rows).
+            const uint32_t l_in = lb / a.batch, b_in = lb % a.batch;
+            const uint32_t grp = a.w_dict_heads == 1 ? l_in : l_in * a.kv_heads + g;
+            const uint32_t tiles = (a.w_rows_per_group + 15) / 16, nk = A / 32;
+            for (uint32_t i = tid; i < (A / 4) * RC; i += NT) {
+                const int rr = (int)(i % RC);
+                const uint32_t a4 = i / RC, r = c * RC + (uint32_t)rr;
+                float4_t v;
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int rr = 2 * pp + h;
-                if (rr >= RC) continue;
-                const float v = (float)(h ? v1 : v0) * inv[rr];
-                amax[rr] = fmaxf(amax[rr], fabsf(v));
+                for (int e = 0; e < 4; ++e) v[e] = bin_value(4 * a4 + e, rr);
+                amax[rr] = fmaxf(amax[rr], fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+                if (r >= R) continue;
+                const uint32_t grow = a.w_dict_heads == 1 ? (b_in * a.kv_heads + g) * R + r : b_in * R + r;
+                const uint32_t at = 4 * a4, kk = at / 32, lgv = (at % 32) / 8, h = (at % 8) / 4;
+                const uint64_t off = ((((uint64_t)grp * tiles + grow / 16) * nk + kk) * 2 + h) * 64 + lgv * 16 + grow % 16;
+                *(float4_t*)(a.part_w + off * 4) = v;
+            }
+        } else
+        for (uint32_t at = tid; at < A; at += NT) {
+#pragma unroll
+            for (int pp = 0; pp < NP; ++pp) {
+                const uint64_t wv = *binp(at, pp);
+                const int32_t v0 = (int32_t)(uint32_t)wv;
+                const int32_t v1 = (int32_t)((uint32_t)(wv >> 32) + (v0 < 0 ? 1u : 0u));
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int rr = 2 * pp + h;
+                    if (rr >= RC) continue;
+                    const float v = (float)(h ? v1 : v0) * inv[rr];
+                    amax[rr] = fmaxf(amax[rr], fabsf(v));
+                    const uint32_t r = c * RC + rr;
+                    if (r < R) a.part_w[(pbase + r) * a.w_pitch + at] = v;
+                }
+            }
+        }
+        float v[NB];
+        bool is_max[NB];
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            v[i] = i < RC ? amax[i] : 0.0f;
+            is_max[i] = true;
+        }
+        wg_reduce(v, is_max);
+#pragma unroll
+        for (int rr = 0; rr < RC; ++rr) // static indices: no register array indexed at run time
+            if (tid == rr) {
                 const uint32_t r = c * RC + rr;
-                if (r < R) a.part_w[(pbase + r) * a.w_pitch + at] = v;
+                if (r < R) {
+                    a.part_m[pbase + r] = ref[rr];
+                    a.part_l[pbase + r] = lpart[rr] * inv[rr]; // sum of p, back from units of 2^-F_r
+                    a.part_amax[pbase + r] = v[rr];
+                }
             }
-        }
     }
-    float v[NB];
-    bool is_max[NB];
-#pragma unroll
-    for (int i = 0; i < NB; ++i) {
-        v[i] = i < RC ? amax[i] : 0.0f;
-        is_max[i] = true;
-    }
-    wg_reduce(v, is_max);
-#pragma unroll
-    for (int rr = 0; rr < RC; ++rr) // static indices: no register array indexed at run time
-        if (tid == rr) {
-            const uint32_t r = c * RC + rr;
-            if (r < R) {
-                a.part_m[pbase + r] = ref[rr];
-                a.part_l[pbase + r] = lpart[rr] * inv[rr]; // sum of p, back from units of 2^-F_r
-                a.part_amax[pbase + r] = v[rr];
-            }
-        }
 }
 
 // Persistent: work-group i takes work items i, i + gridDim.x, ... (gridDim.x a
 // multiple of 8, so each keeps its XCD), so the grid is one resident round and
 // the hot kernel can run beside it in the resources it leaves free.
-template <int RC, int CPT, int PD, bool POW2, bool QF32, bool BUF>
+template <int RC, int CPT, int PD, bool POW2, bool QF32, bool BUF, bool OUT>
 __global__ __launch_bounds__(kColdThreads) void cold_kernel(ColdArgs a) {
     for (uint32_t wg = blockIdx.x; wg < a.n_wg; wg += gridDim.x) {
-        cold_unit<RC, CPT, PD, POW2, QF32, BUF>(a, wg);
+        cold_unit<RC, CPT, PD, POW2, QF32, BUF, OUT>(a, wg);
         __syncthreads(); // the next item rewrites the LDS tables
     }
 }

@@ -177,6 +177,7 @@ AW_F_SEQ_HOT_TOKENS = 8
 AW_F_QLATENT_F32 = 16
 AW_NOALLOC_SCRATCH_BYTES = 96 << 20  # scratch of aw_decode_device_noalloc
 AW_PROJECT_AUTO, AW_PROJECT_MFMA, AW_PROJECT_VALU = 0, 1, 2  # aw_engine_set_projection
+AW_COLD_OUT_AUTO, AW_COLD_OUT_BINS, AW_COLD_OUT_VALUES = 0, 1, 2  # aw_engine_set_cold_output
 
 AW_OK = 0
 AW_E_INVALID_ARG = -1
@@ -236,7 +237,7 @@ class PlanInfo(ctypes.Structure):
         ("hot_tokens_per_split", ctypes.c_uint32), ("cold_splits", ctypes.c_uint32),
         ("cold_tokens_per_split", ctypes.c_uint32), ("cold_row_chunk", ctypes.c_uint32),
         ("computes_q_latent", ctypes.c_uint32), ("projection", ctypes.c_uint32),
-        ("workspace_bytes", ctypes.c_uint64),
+        ("workspace_bytes", ctypes.c_uint64), ("cold_output", ctypes.c_uint32), ("reserved", ctypes.c_uint32),
     ]
 
 

@@ -302,6 +302,12 @@ class WeaverEngine:
         tiles, 2 the VALU kernel (AW_PROJECT_*)."""
         self._check(self._lib.aw_engine_set_projection(self._h, int(mode)), "set_projection")
 
+    def set_cold_output(self, mode) -> None:
+        """What the cold kernel hands on (AW_COLD_OUT_*): 0 the planner's choice,
+        1 per-atom bins for the finish kernel, 2 value partials for the merge
+        (dictionary heads of at most 128 KiB; bins elsewhere)."""
+        self._check(self._lib.aw_engine_set_cold_output(self._h, int(mode)), "set_cold_output")
+
     def reset_stage_stats(self) -> None:
         self._check(self._lib.aw_engine_reset_stage_stats(self._h), "reset_stage_stats")
 

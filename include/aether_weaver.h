@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define AW_ABI_VERSION 1u
+#define AW_ABI_VERSION 2u
 
 /* ---- status codes -------------------------------------------------------- */
 #define AW_OK             0
@@ -167,6 +167,8 @@ typedef struct aw_decode_plan_info {
     uint32_t computes_q_latent;  /* 1 when q . D^T runs on the device */
     uint32_t projection;         /* its kernel by the planner's choice: AW_PROJECT_MFMA or _VALU (0: none) */
     uint64_t workspace_bytes;    /* device scratch this request needs */
+    uint32_t cold_output;        /* what the cold kernel writes: AW_COLD_OUT_BINS or _VALUES (0: no cold pool) */
+    uint32_t reserved;
 } aw_decode_plan_info;
 
 /* Kernel stages, for aw_engine_stage_stats. */
@@ -441,6 +443,22 @@ int aw_engine_set_profiling(aw_engine* engine, int mode);
 #define AW_PROJECT_MFMA 1
 #define AW_PROJECT_VALU 2
 int aw_engine_set_projection(aw_engine* engine, int mode);
+
+/* What the cold kernel hands on (weaver_kernel.metal:206-222 forms the cold
+ * output per token; here it is formed per atom).  AW_COLD_OUT_BINS: per-atom
+ * softmax-weight bins, which a finish kernel multiplies by the dictionary on
+ * MFMA before the merge.  AW_COLD_OUT_VALUES: each work item multiplies its own
+ * bins by the dictionary on MFMA (D^T read from L2) and hands value partials
+ * straight to the merge, so no bins reach HBM and no finish runs; only for
+ * dictionaries of at most 128 KiB per head with a multiple of 32 atoms (512
+ * atoms at head_dim 128), elsewhere bins.  AW_COLD_OUT_AUTO is the planner's
+ * choice (values wherever allowed).  Both forms are exact rewrites of the same
+ * sums, with the same f16 hi + lo split of the bins.  No reference
+ * counterpart. */
+#define AW_COLD_OUT_AUTO 0
+#define AW_COLD_OUT_BINS 1
+#define AW_COLD_OUT_VALUES 2
+int aw_engine_set_cold_output(aw_engine* engine, int mode);
 int aw_engine_stage_stats(aw_engine* engine, int stage, double* total_ms, uint64_t* launches);
 int aw_engine_reset_stage_stats(aw_engine* engine);
 

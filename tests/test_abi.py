@@ -44,7 +44,7 @@ def test_struct_sizes_match():
     sizes = (ctypes.c_size_t * 4)()
     lib.aw_abi_struct_sizes(sizes)
     assert tuple(sizes) == STRUCT_SIZES == (16, 48, ctypes.sizeof(DecodeDesc), ctypes.sizeof(PlanInfo))
-    assert lib.aw_abi_version() == 1
+    assert lib.aw_abi_version() == 2
     assert lib.aw_status_string(AW_E_OOB).decode().startswith("block ref")
 
 
@@ -195,6 +195,37 @@ def test_plan_full_hot_region():
                        dict_heads=1, hot_count=top + 1, cold_count=0, refs_stride=top + 1, hot_blocks=top + 1,
                        cold_blocks=0, q=1, out=1))
     assert e.value.status == AW_E_UNSUPPORTED and "4096 blocks" in str(e.value)
+
+
+def test_plan_cold_output():
+    """The cold kernel writes value partials for dictionary heads of at most
+    128 KiB of f16 (512 atoms at head_dim 128, 1024 at 64) and bins elsewhere; the
+    value path's workspace holds no bins and no D^T, its hot partial arrays hold
+    the cold splits too, and a pool past the buffer-load window keeps bins."""
+    from aether_nexus_amd.types import AW_COLD_OUT_BINS, AW_COLD_OUT_VALUES
+    from aether_nexus_amd.weaver import make_desc
+
+    def info(A, hd=128, dh=8, B=1, cold_blocks=None, hot=128, cold=2048):
+        return plan(make_desc(layers=1, batch=B, queries=1, q_heads=32, kv_heads=8, head_dim=hd, dict_size=A,
+                              dict_heads=dh, hot_count=hot, cold_count=cold, refs_stride=hot + cold,
+                              hot_blocks=hot * B, cold_blocks=cold_blocks or cold * B, q=1, out=1))
+    v, b = info(512), info(4096, dh=1)
+    assert v.cold_output == AW_COLD_OUT_VALUES and b.cold_output == AW_COLD_OUT_BINS
+    assert info(1024, hd=64).cold_output == AW_COLD_OUT_VALUES
+    assert info(1024).cold_output == AW_COLD_OUT_BINS and info(528).cold_output == AW_COLD_OUT_BINS
+    assert info(512, B=64).cold_output == AW_COLD_OUT_VALUES
+    # Same splits either way; the value path's scratch: q_latent (f16), D^T, and the partials
+    # of every hot and cold split (m, l, 128 floats per row).
+    assert (v.cold_splits, v.hot_splits) == (8, 16)
+    rows = 8 * 4
+    parts = rows * (v.hot_splits + v.cold_splits)
+    assert v.workspace_bytes <= 32 * 512 * 2 + 8 * (512 + 64) * 128 * 2 + parts * (2 * 4 + 128 * 4) + 5 * 4096
+    # A dictionary size that is not a multiple of 32 atoms keeps bins (the product's k-steps).
+    assert info(496).cold_output == AW_COLD_OUT_BINS and info(480).cold_output == AW_COLD_OUT_VALUES
+    # A cold pool over the 4 GiB window of buffer loads (2^21 blocks x 8 kv heads x 16 codes x 16 B).
+    assert info(512, cold_blocks=1 << 21).cold_output == AW_COLD_OUT_BINS
+    # No cold pool: neither.
+    assert info(0, dh=1, cold=0).cold_output == 0
 
 
 def test_plan_flags():

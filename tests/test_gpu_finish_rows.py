@@ -35,6 +35,16 @@ CASES = {
 }
 
 
+@pytest.fixture(autouse=True)
+def _bins(engine):
+    """These shapes are the finish kernel's: the cold kernel writes bins for it,
+    also where its dictionary is small enough for value partials."""
+    from aether_nexus_amd.types import AW_COLD_OUT_AUTO, AW_COLD_OUT_BINS
+    engine.set_cold_output(AW_COLD_OUT_BINS)
+    yield
+    engine.set_cold_output(AW_COLD_OUT_AUTO)
+
+
 def sample_rows(geom, n=160, seed=0):
     total = geom.layers * geom.batch * geom.queries * geom.q_heads
     rng = np.random.default_rng(seed)
