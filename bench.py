@@ -643,8 +643,10 @@ def tiered_attention_bench(engine, seed, reps, layers=32, hot=2048, cold=32768):
     2048 exact K and V tokens plus 32768 cold tokens distilled into SparseCodes of
     the layer's 512-atom per-kv-head dictionaries (the reference's Llama8B
     geometry), one hot+cold aw_decode_device per layer with q_latent computed on
-    the device, the 32 layers captured in a HIP graph.  Algorithmic bytes per
-    layer: hot K and V rows, cold codes, the dictionary, block refs, q and out."""
+    the device, the 32 layers captured in a HIP graph; the cold kernel's value
+    partials (the planner's path here) and its bins + finish path, each timed.
+    Algorithmic bytes per layer: hot K and V rows, cold codes, the dictionary,
+    block refs, q and out."""
     import torch
     from aether_nexus_amd.inference import WeaverKvCache
     hq, hkv, hd, atoms = 32, 8, 128, 512
@@ -665,6 +667,7 @@ def tiered_attention_bench(engine, seed, reps, layers=32, hot=2048, cold=32768):
                        f"heads, head_dim {hd}",
            "cold_tokens": cache.cold_tokens, "hot_tokens": cache.hot_tokens()}
     p0 = cache.position
+    from aether_nexus_amd.types import AW_COLD_OUT_AUTO, AW_COLD_OUT_BINS
     for name, nq in (("decode", 1), ("verify_3_drafts", 4)):
         q = torch.randn((nq, hq, hd), generator=g, device="cuda:0").to(torch.float16)
         rows = torch.randn((nq, hkv, hd), generator=g, device="cuda:0").to(torch.float16)
@@ -673,32 +676,43 @@ def tiered_attention_bench(engine, seed, reps, layers=32, hot=2048, cold=32768):
             for l in range(layers):
                 cache.append(l, rows, rows)
 
-            def forward(s):
-                for l in range(layers):
-                    cache.attend(engine, l, q, outs[l], stream=s)
-            forward(st.cuda_stream)  # sizes the workspace and the block table before capture
-            engine.check_device_errors(st.cuda_stream)
-            graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graph, stream=st):
-                forward(torch.cuda.current_stream().cuda_stream)
-            for _ in range(3):
-                graph.replay()
-            ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
-            ev[0].record(st)
-            for _ in range(reps):
-                graph.replay()
-            ev[1].record(st)
-        torch.cuda.synchronize()
-        ms = ev[0].elapsed_time(ev[1]) / reps
+        def forward(s):
+            for l in range(layers):
+                cache.attend(engine, l, q, outs[l], stream=s)
+        # The planner's path (value partials at these 512-atom heads), then the
+        # bins + finish path on the same cache for comparison.
+        by_mode = {}
+        for mode in (AW_COLD_OUT_AUTO, AW_COLD_OUT_BINS):
+            engine.set_cold_output(mode)
+            try:
+                with torch.cuda.stream(st):
+                    forward(st.cuda_stream)  # sizes the workspace and the block table before capture
+                    engine.check_device_errors(st.cuda_stream)
+                    graph = torch.cuda.CUDAGraph()
+                    with torch.cuda.graph(graph, stream=st):
+                        forward(torch.cuda.current_stream().cuda_stream)
+                    for _ in range(3):
+                        graph.replay()
+                    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+                    ev[0].record(st)
+                    for _ in range(reps):
+                        graph.replay()
+                    ev[1].record(st)
+                torch.cuda.synchronize()
+            finally:
+                engine.set_cold_output(AW_COLD_OUT_AUTO)
+            by_mode[mode] = ev[0].elapsed_time(ev[1]) / reps
+            del graph
+        ms = by_mode[AW_COLD_OUT_AUTO]
         n_hot = hot + nq
         alg = layers * (n_hot * hkv * hd * 2 * 2 + cold * hkv * 16 + hkv * atoms * hd * 2
                         + (-(-n_hot // 16) + cold // 16) * 4 + 2 * nq * hq * hd * 2)
         gbps = alg / (ms * 1e-3) / 1e9
         res[name] = {"new_tokens": nq, "ms_per_forward": round(ms, 4), "us_per_layer": round(ms * 1e3 / layers, 2),
                      "alg_bytes_per_forward": alg, "achieved_gbps": round(gbps, 1),
-                     "frac_of_peak": round(gbps / PEAK_HBM_GBPS, 4)}
+                     "frac_of_peak": round(gbps / PEAK_HBM_GBPS, 4),
+                     "bins_path_us_per_layer": round(by_mode[AW_COLD_OUT_BINS] * 1e3 / layers, 2)}
         cache.pop_loom(p0)
-        del graph
     del cache
     torch.cuda.empty_cache()
     return res
