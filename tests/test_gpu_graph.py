@@ -1,7 +1,9 @@
 """Decode captured in a HIP graph (as the benchmark replays it): every replay
 gives the eager call's output bits, with other eager decodes, torch work and
 synchronisations between the replays.  The capture holds the engine's
-stream fork / join (hot kernel on its side stream beside the cold kernel)."""
+stream fork / join (hot kernel on its side stream beside the cold kernel);
+the last case is one sequence over 512-atom per-kv-head dictionaries, where
+the cold kernel hands value partials to the merge."""
 from __future__ import annotations
 
 import pytest
@@ -17,7 +19,8 @@ pytestmark = pytest.mark.gpu
     (W.hot_cold(batch=4), True),
     (W.spec_verify(layers=2, batch=2), False),
     (W.hot_cold(batch=1), False),
-], ids=["hot_cold_b4", "hot_cold_b4_head_blocked", "spec_verify_l2_b2", "hot_cold_b1"])
+    (W.hot_cold(batch=1, dict_size=512, dict_heads=8, separate_v=True, causal=True), True),
+], ids=["hot_cold_b4", "hot_cold_b4_head_blocked", "spec_verify_l2_b2", "hot_cold_b1", "value_partials_b1"])
 def test_graph_replays_match_eager(engine, geom, hb):
     wl = W.generate(geom, seed=21, device="cuda:0")
     other = W.generate(W.hot_cold(batch=2), seed=22, device="cuda:0")
