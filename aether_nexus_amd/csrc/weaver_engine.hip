@@ -122,8 +122,9 @@ constexpr uint32_t kSepMergeRows = 16;
 // Cold splits per row before the row chunk is halved instead.
 constexpr uint64_t kColdSplitsBeforeRc = 8;
 // Largest dictionary head (bytes of f16) for which the cold kernel writes value
-// partials (AW_COLD_OUT_VALUES): every work item reads its head's dictionary from
-// L2 once, in place of the bins' round trip through HBM and the finish kernel.
+// partials (AW_COLD_OUT_VALUES): every work item reads its head's D^T (the
+// projection's tiled copy) from L2 once, in place of the bins' round trip through
+// HBM and the finish kernel.
 constexpr uint64_t kColdOutMaxDictBytes = 128u << 10;
 
 // q . D^T on the vector ALUs (project_valu_kernel: kProjValuTa atoms x
