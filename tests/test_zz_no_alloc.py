@@ -32,8 +32,14 @@ def decode_both(engine, stream, geom, seed):
 def test_noalloc_matches_decode_device(engine, stream):
     # 64 sequences at hot 2048 + cold 32768 tokens (55.1 MiB of scratch), then a
     # smaller ragged request: the second call reuses the array the first left behind.
+    # The second one's 256-atom dictionary takes the cold kernel's value partials
+    # (their cold splits in the hot partial arrays), the first the bins and a finish.
+    from aether_nexus_amd.types import AW_COLD_OUT_BINS, AW_COLD_OUT_VALUES
     big = W.sweep(64)
     small = W.hot_cold(batch=3, hot_count=5, cold_count=40, dict_size=256, queries=2, causal=True)
+    for geom, path in ((big, AW_COLD_OUT_BINS), (small, AW_COLD_OUT_VALUES)):
+        wl = W.generate(geom, seed=0)
+        assert plan(W.device_desc(wl, torch.empty(wl.out_shape(), dtype=torch.float16))).cold_output == path
     decode_both(engine, stream, big, seed=71)
     decode_both(engine, stream, small, seed=72)
 
