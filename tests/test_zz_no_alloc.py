@@ -19,14 +19,16 @@ def decode_both(engine, stream, geom, seed):
     wl = W.generate(geom, seed=seed, device="cuda:0")
     ref = torch.full(wl.out_shape(), float("nan"), dtype=torch.float16, device="cuda:0")
     out = torch.full(wl.out_shape(), float("nan"), dtype=torch.float16, device="cuda:0")
+    info = plan(W.device_desc(wl, out))
     print(f"no-alloc: {geom.batch} seq, hot {geom.hot_count} + cold {geom.cold_count} blocks, "
-          f"scratch {plan(W.device_desc(wl, out)).workspace_bytes} bytes", flush=True)
+          f"scratch {info.workspace_bytes} bytes", flush=True)
     engine.decode_device_noalloc(W.device_desc(wl, out), stream=stream)
     engine.check_device_errors(stream)
     engine.decode_device(W.device_desc(wl, ref), stream=stream)
     engine.check_device_errors(stream)
     assert torch.isfinite(out.float()).all()
     assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+    return info.cold_output
 
 
 def test_noalloc_matches_decode_device(engine, stream):
@@ -37,11 +39,8 @@ def test_noalloc_matches_decode_device(engine, stream):
     from aether_nexus_amd.types import AW_COLD_OUT_BINS, AW_COLD_OUT_VALUES
     big = W.sweep(64)
     small = W.hot_cold(batch=3, hot_count=5, cold_count=40, dict_size=256, queries=2, causal=True)
-    for geom, path in ((big, AW_COLD_OUT_BINS), (small, AW_COLD_OUT_VALUES)):
-        wl = W.generate(geom, seed=0)
-        assert plan(W.device_desc(wl, torch.empty(wl.out_shape(), dtype=torch.float16))).cold_output == path
-    decode_both(engine, stream, big, seed=71)
-    decode_both(engine, stream, small, seed=72)
+    assert decode_both(engine, stream, big, seed=71) == AW_COLD_OUT_BINS
+    assert decode_both(engine, stream, small, seed=72) == AW_COLD_OUT_VALUES
 
 
 @pytest.mark.parametrize("layers", [2, 4])
