@@ -614,6 +614,7 @@ def attention_bench(engine, seed, reps, cpu_seconds):
                      "frac_of_peak": round(gbps / PEAK_HBM_GBPS, 4)}
         del graph
     res["tiered"] = tiered_attention_bench(engine, seed, reps)
+    res["dense_at_tiered_length"] = dense_attention_at(engine, seed, reps, kv_len=2048 + 32768)
     # CPU: the oracle's fp32 restatement of the same attention (a hot pool of
     # 16-token blocks, identity block table, causal) on one layer of the decode step.
     from oracle import oracle
@@ -636,6 +637,36 @@ def attention_bench(engine, seed, reps, cpu_seconds):
                                      f"oracle's fp32 restatement in {el:.1f} s, {threads} threads"}
     res["gpu_forwards_per_s"] = round(1e3 / res["decode"]["ms_per_forward"], 1)
     return res
+
+
+def dense_attention_at(engine, seed, reps, kv_len, layers=32, distinct=8):
+    """The contiguous-cache attention (multihead_attention, one decode token) at the
+    tiered cache's total length: what the same 32 layers cost when every token
+    stays exact f16 K and V (8 distinct caches of 143 MB rotated over the layers,
+    so no layer finds the previous one's in the MALL)."""
+    import torch
+    hq, hkv, hd = 32, 8, 128
+    g = torch.Generator(device="cuda:0").manual_seed(seed + 2)
+    kc = [torch.randn((kv_len, hkv, hd), generator=g, device="cuda:0").to(torch.float16) for _ in range(distinct)]
+    vc = [torch.randn((kv_len, hkv, hd), generator=g, device="cuda:0").to(torch.float16) for _ in range(distinct)]
+    q = torch.randn((1, hq, hd), generator=g, device="cuda:0").to(torch.float16)
+    outs = [torch.empty((1, hq, hd), dtype=torch.float16, device="cuda:0") for _ in range(layers)]
+    st = torch.cuda.Stream()
+
+    def forward(s):
+        for l in range(layers):
+            engine.multihead_attention(q, kc[l % distinct], vc[l % distinct], outs[l], kv_len, hd, hq, hkv, 1,
+                                       cache_tokens=kv_len, stream=s)
+    ms = _graph_time(forward, st, reps)
+    alg = layers * (kv_len * hkv * hd * 2 * 2 + 2 * hq * hd * 2)
+    gbps = alg / (ms * 1e-3) / 1e9
+    del kc, vc
+    torch.cuda.empty_cache()
+    return {"workload": f"{layers} layers x multihead_attention, one decode token over contiguous K and V caches of "
+                        f"{kv_len} tokens ({distinct} distinct caches rotated), 32q/8kv heads, head_dim 128",
+            "us_per_layer": round(ms * 1e3 / layers, 2), "alg_bytes_per_forward": alg,
+            "achieved_gbps": round(gbps, 1), "frac_of_peak": round(gbps / PEAK_HBM_GBPS, 4),
+            "cache_bytes_per_token_and_layer": hkv * hd * 2 * 2}
 
 
 def tiered_attention_bench(engine, seed, reps, layers=32, hot=2048, cold=32768):
