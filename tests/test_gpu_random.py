@@ -1,10 +1,11 @@
 """Seeded random geometries through aw_decode_device against the fp64 oracle:
 kv heads 1-8, GQA groups 1-7, 1-4 query tokens (causal or not), head_dim 64
-or 128, dictionaries of 16-1008 atoms shared or per kv head, 0-9 hot and 0-39
-cold blocks per sequence, ragged per-sequence counts, separate V, bit 31 on
-refs, uniform or Zipf atom indices, either cold pool order, 1-2 layers.  Each
-case draws its geometry from its own seed, so a failure names a reproducible
-shape."""
+or 128, dictionaries of 16-1024 atoms shared or per kv head (those of at most
+128 KiB per head with a multiple of 32 atoms take the cold kernel's value
+partials, the others its bins), 0-9 hot and 0-39 cold blocks per sequence,
+ragged per-sequence counts, separate V, bit 31 on refs, uniform or Zipf atom
+indices, either cold pool order, 1-2 layers.  Each case draws its geometry
+from its own seed, so a failure names a reproducible shape."""
 from __future__ import annotations
 
 import numpy as np
@@ -27,7 +28,8 @@ def draw(seed: int):
     hot, cold = int(rng.integers(0, 10)), int(rng.integers(0, 40))
     geom = W.Geometry(layers=int(rng.integers(1, 3)), batch=int(rng.integers(1, 6)), queries=queries,
                       q_heads=kv * g, kv_heads=kv, head_dim=int(rng.choice([64, 128])),
-                      dict_size=int(rng.choice([16, 48, 256, 512, 1008])), dict_heads=1 if rng.random() < 0.5 else kv,
+                      dict_size=int(rng.choice([16, 48, 96, 256, 512, 1008, 1024])),
+                      dict_heads=1 if rng.random() < 0.5 else kv,
                       hot_count=hot, cold_count=cold, scale=float(rng.uniform(0.05, 0.5)),
                       causal=bool(rng.random() < 0.5), separate_v=bool(hot and rng.random() < 0.3),
                       zipf=1.1 if rng.random() < 0.3 else None, tag_bit31=bool(rng.random() < 0.5))
