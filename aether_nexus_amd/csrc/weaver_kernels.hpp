@@ -58,6 +58,14 @@ __device__ inline float4_t mfma16x16x32(half8_t a, half8_t b, float4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 __device__ inline half8_t as_h8(uint4_t v) { return __builtin_bit_cast(half8_t, v); }
+
+typedef short short4_t __attribute__((ext_vector_type(4)));
+// ds_read_b64_tr_b16 (gfx950): in each group of 16 lanes, lane 4*r + c supplies the
+// LDS address of 4 consecutive halves (row r, columns 4c..4c+3 of a 4 x 16 block);
+// lane j of the group receives column j, rows 0..3.  p must be 8-byte aligned.
+__device__ __forceinline__ short4_t lds_read_tr16(const _Float16* p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4_t*)p);
+}
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 // e with 2^(e-1) <= x < 2^e for finite x > 0 (v_frexp_exp_i32_f32), and x * 2^e (v_ldexp_f32).
 __device__ inline int exp_of(float x) { return __builtin_amdgcn_frexp_expf(x); }
@@ -472,9 +480,13 @@ __global__ __launch_bounds__(TA) void project_valu_kernel(ProjArgs a) {
 //      the P^T operand of the second product is already in the lane:
 //      k-index 8*lg+e' <-> token 4*lg+e' (e'<4) / 16+4*lg+(e'-4) (e'>=4).
 //   O^T[dim][row] += V^T P^T: A = V^T (lane: dim 16*nb+li, the 8 tokens above),
-//      gathered from the chunk staged in LDS.
-// LDS pitch HD+4 halves (66 words at HD=128) puts the four token rows 4*lg+e'
-// of one read on disjoint 8-bank groups.
+//      read from the chunk staged in LDS as [token][dim] by transposing loads:
+//      ds_read_b64_tr_b16 gives lane li of each 16-lane group one column (dim
+//      16*nb+li) of the 4 x 16 block whose rows (tokens 4*lg..4*lg+3, then
+//      16+4*lg..) its lanes address, 8 bytes each: 2 loads per 16 dims.
+// LDS pitch HD+16 halves (72 words at HD=128, 40 at 64): 16-byte aligned rows for
+// the staging stores, and the 16 token rows of one transposing load start on
+// 8-word bank groups that cover the 64 banks twice.
 //
 // A split holds at most kMaxHotSplitBlocks blocks; their refs are staged in
 // (dynamic) LDS once.  Every global load of the loop is unconditional (a bad
@@ -482,7 +494,7 @@ __global__ __launch_bounds__(TA) void project_valu_kernel(ProjArgs a) {
 // next chunk's loads really stay in flight while the current chunk is computed.
 template <int HD, int RT, bool SEPV>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu((RT == 1 && !SEPV) ? 3 : 1))) void hot_kernel(HotArgs a) {
-    constexpr int KS = HD / 32, NB = HD / 16, P = HD + 4;
+    constexpr int KS = HD / 32, NB = HD / 16, P = HD + 16;
     __shared__ __attribute__((aligned(16))) _Float16 lds[32 * P];
     const int lane = threadIdx.x, li = lane & 15, lg = lane >> 4;
     const uint32_t s = blockIdx.x % a.splits, lbg = blockIdx.x / a.splits;
@@ -602,10 +614,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu((RT == 1 && 
         for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
             for (int j = 0; j < KS; ++j) {
-                const uint4_t v = SEPV ? vcur[tb][j] : kcur[tb][j];
-                _Float16* dst = lds + (16 * tb + li) * P + 32 * j + 8 * lg;
-                *(uint2_t*)dst = (uint2_t){v[0], v[1]};
-                *(uint2_t*)(dst + 4) = (uint2_t){v[2], v[3]};
+                *(uint4_t*)(lds + (16 * tb + li) * P + 32 * j + 8 * lg) = SEPV ? vcur[tb][j] : kcur[tb][j];
             }
         __syncthreads();
 
@@ -646,15 +655,14 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu((RT == 1 && 
             for (int nb = 0; nb < NB; ++nb) oacc[rt][nb] *= alpha;
         }
 
-        // O^T += V^T P^T
+        // O^T += V^T P^T; lane li + 16*lg addresses token 4*lg + li/4, dims 4*(li%4)..+3
+        // of each 16-dim block, and receives tokens 4*lg..+3 (then 16+4*lg..+3) of dim 16*nb+li.
+        const _Float16* vrow = lds + (4 * lg + (li >> 2)) * P + 4 * (li & 3);
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
-            half8_t vop;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int row = e < 4 ? 4 * lg + e : 16 + 4 * lg + (e - 4);
-                vop[e] = lds[row * P + 16 * nb + li];
-            }
+            const half8_t vop = __builtin_bit_cast(
+                half8_t, __builtin_shufflevector(lds_read_tr16(vrow + 16 * nb), lds_read_tr16(vrow + 16 * P + 16 * nb),
+                                                 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
             for (int rt = 0; rt < RT; ++rt) oacc[rt][nb] = mfma16x16x32(vop, pop[rt], oacc[rt][nb]);
         }
