@@ -612,9 +612,11 @@ def attention_bench(engine, seed, reps, cpu_seconds):
         res[name] = {"new_tokens": nq, "ms_per_forward": round(ms, 4), "us_per_layer": round(ms * 1e3 / layers, 2),
                      "alg_bytes_per_forward": alg, "achieved_gbps": round(gbps, 1),
                      "frac_of_peak": round(gbps / PEAK_HBM_GBPS, 4)}
+        log(f"attention: {name} {res[name]['us_per_layer']} us per layer")
         del graph
     res["tiered"] = tiered_attention_bench(engine, seed, reps)
     res["dense_at_tiered_length"] = dense_attention_at(engine, seed, reps, kv_len=2048 + 32768)
+    log(f"attention: dense cache of {2048 + 32768} tokens {res['dense_at_tiered_length']['us_per_layer']} us per layer")
     # CPU: the oracle's fp32 restatement of the same attention (a hot pool of
     # 16-token blocks, identity block table, causal) on one layer of the decode step.
     from oracle import oracle
@@ -693,6 +695,7 @@ def tiered_attention_bench(engine, seed, reps, layers=32, hot=2048, cold=32768):
         cache.extend(engine, ks, ks, stream=st.cuda_stream)
     torch.cuda.synchronize()
     del ks
+    log(f"tiered: prompt of {n} tokens per layer loaded ({cache.cold_tokens} cold)")
     res = {"workload": f"{layers} layers x Weaver attention over a hot window of {hot} f16 K/V tokens + {cold} "
                        f"cold SparseCodes per kv head ({atoms}-atom per-kv-head dictionaries), {hq}q/{hkv}kv "
                        f"heads, head_dim {hd}",
@@ -733,6 +736,8 @@ def tiered_attention_bench(engine, seed, reps, layers=32, hot=2048, cold=32768):
             finally:
                 engine.set_cold_output(AW_COLD_OUT_AUTO)
             by_mode[mode] = ev[0].elapsed_time(ev[1]) / reps
+            log(f"tiered: {name}, cold output {'auto' if mode == AW_COLD_OUT_AUTO else 'bins'}: "
+                f"{by_mode[mode] * 1e3 / layers:.2f} us per layer")
             del graph
         ms = by_mode[AW_COLD_OUT_AUTO]
         n_hot = hot + nq
