@@ -282,10 +282,14 @@ int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, const uint32_t 
         // their factors and bins), so while the row chunk can still shrink, at most
         // kColdSplitsBeforeRc splits: a one-sequence decode over 512-atom per-kv-head
         // dictionaries measured 51.6 us with rc 4 x 32 splits, 44.9 with 4 x 16,
-        // 38.1 with 2 x 8 and 35.3 with 1 x 8.
+        // 38.1 with 2 x 8 and 35.3 with 1 x 8.  One-row chunks take half a round of
+        // work-groups, each with twice the tokens: the cache's one-sequence decode over
+        // those dictionaries 30.6 -> 28.5 us per layer, the B = 1 step over a shared
+        // 4096-atom dictionary 36.8 -> 35.5 us (a quarter of a round: 32.1 and 39.8;
+        // the sweep's batches of 2-64 sequences keep chunks of 2 or 4 rows).
         auto splits_for = [&](uint32_t rc) {
             const uint64_t items = n_lbg * cdiv(R, rc);
-            const uint64_t want = cdiv((uint64_t)n_cu, items);
+            const uint64_t want = std::max<uint64_t>(1, cdiv((uint64_t)n_cu, items) / (rc == 1 ? 2u : 1u));
             const uint64_t cap = std::max<uint64_t>(
                 1, std::min<uint64_t>(cdiv(n_tok, 1024), (n_tok * 16) / ((uint64_t)A * rc * 4 * 2)));
             const uint64_t lim = rc > 1 ? kColdSplitsBeforeRc : (uint64_t)aw::kMaxSplits;
