@@ -299,7 +299,12 @@ int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, const uint32_t 
         // the codes again, but does less work per token and allows more splits).
         while (o.rc > 1 && n_lbg * cdiv(R, o.rc) * splits_for(o.rc) < (uint64_t)n_cu) o.rc /= 2;
         o.n_chunks = cdiv(R, o.rc);
-        uint64_t S = splits_for(o.rc);
+        // Splits of at least 8192 tokens once the chunk is chosen: each split's set-up,
+        // plan, reductions and write-out are paid per item (B = 2, 2-row chunks: 8 -> 4
+        // splits, 42.4 -> 40.5 us; the cache's verify step, 4-row chunks: 8 -> 4 splits,
+        // 41.7 -> 39.0 us per layer; batches whose splits already hold 8192 tokens or more
+        // unchanged, and halving those was slower: B = 8 53.5 -> 57.7 us, B = 16 66.5 -> 76.6).
+        uint64_t S = std::min<uint64_t>(splits_for(o.rc), std::max<uint64_t>(1, n_tok / 8192));
         uint64_t tps = align_up(cdiv(n_tok, S), 16);
         // The split's block refs live in LDS too: shorten splits until they fit.
         while (tps > 1024 && aw::cold_smem_bytes(A, (int)o.rc, (uint32_t)tps, qbytes) > max_lds) {
