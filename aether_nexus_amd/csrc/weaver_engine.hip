@@ -232,11 +232,9 @@ int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, const uint32_t 
     }
     const uint32_t qbytes = o.qf32 ? 4u : 2u;
 
-    // Hot: one round of waves filling the resident capacity, splits <= kMaxSplits,
-    // of at least min_tok tokens each.
-    const uint64_t n_hot_tok = d->hot_tokens ? d->hot_tokens : (uint64_t)d->hot_count * kBlock;
-    auto hot_splits_for = [&](uint64_t min_tok) -> uint64_t {
-        const uint64_t n_tok = n_hot_tok;
+    // Hot: one round of waves filling the resident capacity, splits <= kMaxSplits.
+    if (d->hot_count > 0) {
+        const uint64_t n_tok = d->hot_tokens ? d->hot_tokens : (uint64_t)d->hot_count * kBlock;
         // Beside the cold kernel (one 8-wave work-group per CU) one hot wave per SIMD fits.
         uint32_t wpc = hot_waves_per_cu[R <= 16 ? 0 : (R <= 32 ? 1 : 2)];
         if (d->cold_count > 0) wpc = std::min(wpc, 4u);
@@ -244,14 +242,12 @@ int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, const uint32_t 
         // Beside the cold kernel, splits of at most ~512 tokens (B = 64 sweep: 4 splits of
         // 512 tokens 0.159 ms, 2 of 1024 0.164 ms; B = 32: 4 of 512 0.089 ms, 8 of 256 0.092 ms).
         if (d->cold_count > 0) want = std::max<uint64_t>(want, cdiv(n_tok, 512));
-        const uint64_t cap = std::max<uint64_t>(1, cdiv(n_tok, min_tok));
-        return std::max<uint64_t>(1, std::min<uint64_t>({want, cap, (uint64_t)aw::kMaxSplits}));
-    };
-    if (d->hot_count > 0) {
-        const uint64_t n_tok = n_hot_tok;
-        // >= 128 tokens per wave beside the cold kernel's bins (64: B <= 4 steps 1-3% slower);
-        // >= 64 alone (one-sequence attention 11.9 -> 11.1 us per layer against 128).
-        const uint64_t S = hot_splits_for(d->cold_count > 0 ? 128 : 64);
+        // >= 64 tokens per wave: alone, one-sequence attention 11.9 -> 11.1 us per layer
+        // against 128; beside the cold kernel's value partials the cache's decode 31.05 ->
+        // 30.6 us per layer and verify 43.5 -> 41.9, beside its bins B = 2 40.6 -> 39.9 us
+        // and B = 4 44.9 -> 44.4 (other batches unchanged).
+        const uint64_t cap = std::max<uint64_t>(1, cdiv(n_tok, 64));
+        const uint64_t S = std::max<uint64_t>(1, std::min<uint64_t>({want, cap, (uint64_t)aw::kMaxSplits}));
         // A split's block refs are staged in the hot kernel's LDS (4 bytes each,
         // sized per launch): at most kMaxHotSplitBlocks, so 64 splits cover
         // 64 * 4096 blocks = 4 Mi tokens per sequence.
@@ -358,20 +354,6 @@ int plan(const aw_decode_desc* d, size_t max_lds, uint32_t n_cu, const uint32_t 
             if (o.cold_smem > max_lds) o.cold_out = false;
             o.info.cold_output = o.cold_out ? AW_COLD_OUT_VALUES : AW_COLD_OUT_BINS;
             if (!o.cold_out) o.cold_smem = aw::cold_smem_bytes(A, (int)o.rc, o.info.cold_tokens_per_split, qbytes);
-        }
-    }
-    // With value partials the merge, not a finish, follows the cold kernel: hot splits of
-    // >= 64 tokens end sooner beside it (tiered cache, 2048 hot + 32768 cold tokens:
-    // decode 31.05 -> 30.6 us per layer, verify 43.5 -> 41.9), while hot and cold
-    // splits still fit the merge's partials.  (Smaller splits only lower the tokens
-    // per split, so the staged block refs stay within kMaxHotSplitBlocks.)
-    if (o.cold_out && o.info.hot_splits > 0) {
-        const uint64_t S = hot_splits_for(64);
-        const uint64_t tps = align_up(cdiv(n_hot_tok, S), 32);
-        const uint64_t hs = cdiv(n_hot_tok, tps);
-        if (hs + o.info.cold_splits <= (uint64_t)aw::kMaxSplits) {
-            o.info.hot_tokens_per_split = (uint32_t)tps;
-            o.info.hot_splits = (uint32_t)hs;
         }
     }
     o.part_splits = o.info.hot_splits + (o.cold_out ? o.info.cold_splits : 0u);

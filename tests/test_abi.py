@@ -215,10 +215,10 @@ def test_plan_cold_output():
     assert info(1024, hd=64).cold_output == AW_COLD_OUT_VALUES
     assert info(1024).cold_output == AW_COLD_OUT_BINS and info(528).cold_output == AW_COLD_OUT_BINS
     assert info(512, B=64).cold_output == AW_COLD_OUT_VALUES
-    # Beside value partials the hot splits hold >= 64 tokens (2048 hot tokens: 32 splits),
-    # beside bins >= 128 (16 splits).  The value path's scratch: q_latent (f16), D^T, and
-    # the partials of every hot and cold split (m, l, 128 floats per row).
-    assert (v.cold_splits, v.hot_splits) == (4, 32) and b.hot_splits == 16
+    # Hot splits hold >= 64 tokens (2048 hot tokens: 32 splits) beside either cold output.
+    # The value path's scratch: q_latent (f16), D^T, and the partials of every hot and
+    # cold split (m, l, 128 floats per row).
+    assert (v.cold_splits, v.hot_splits) == (4, 32) and b.hot_splits == 32
     rows = 8 * 4
     parts = rows * (v.hot_splits + v.cold_splits)
     assert v.workspace_bytes <= 32 * 512 * 2 + 8 * (512 + 64) * 128 * 2 + parts * (2 * 4 + 128 * 4) + 5 * 4096
